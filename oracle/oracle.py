@@ -1,0 +1,253 @@
+"""ctypes wrapper of the CPU oracle (oracle/liboracle.so).
+
+TEST INFRASTRUCTURE ONLY: imported by tests/, __graft_entry__.smoke() and the
+cpu_baseline leg of bench.py, always as the checker.  The product path
+(qengine_amd) never imports this module.
+
+Arrays are numpy; fp16 data travels as uint16 bit patterns (or numpy float16
+viewed as uint16).  Block arrays use the structured dtypes BLOCK_TQ3 (52 B)
+and BLOCK_Q8 (36 B), identical to the reference's block_tq3
+(turboquant.cuh:73-77) and block_q8_0_aligned (quant_gemv.cuh:19).
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import subprocess
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+_LIB_PATH = os.path.join(_HERE, "liboracle.so")
+
+BLOCK_TQ3 = np.dtype([("norm", "<f4"), ("qs", "u1", (48,))])
+BLOCK_Q8 = np.dtype([("qs", "i1", (32,)), ("pad", "<u2"), ("d", "<u2")])
+assert BLOCK_TQ3.itemsize == 52 and BLOCK_Q8.itemsize == 36
+
+KV_TQ3, KV_Q8, KV_F16 = 0, 1, 2
+
+_lib = None
+
+
+def build() -> None:
+    subprocess.run(["make", "-s", "-C", _HERE], check=True)
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(_LIB_PATH):
+            build()
+        _lib = ctypes.CDLL(_LIB_PATH)
+        _declare(_lib)
+    return _lib
+
+
+_P = ctypes.c_void_p
+_I = ctypes.c_int
+_I64 = ctypes.c_int64
+_F = ctypes.c_float
+
+
+def _declare(L):
+    L.or_f16_to_f32.restype = _F
+    L.or_f16_to_f32.argtypes = [ctypes.c_uint16]
+    L.or_f32_to_f16.restype = ctypes.c_uint16
+    L.or_f32_to_f16.argtypes = [_F]
+    L.or_f16_to_f32_n.argtypes = [_P, _P, _I64]
+    L.or_f32_to_f16_n.argtypes = [_P, _P, _I64]
+    L.or_tq3_signs.argtypes = [_P]
+    L.or_tq3_centroids.argtypes = [_P]
+    L.or_tq3_bounds.argtypes = [_P]
+    L.or_tq3_wht_scale.restype = _F
+    L.or_wht128.argtypes = [_P]
+    L.or_tq3_find_bin.restype = ctypes.c_uint8
+    L.or_tq3_find_bin.argtypes = [_F]
+    L.or_pack_3bit_8.argtypes = [_P, _P]
+    L.or_unpack_3bit_8.argtypes = [_P, _P]
+    L.or_tq3_encode.argtypes = [_P, _P, _I64, _I]
+    L.or_tq3_encode_rotated.argtypes = [_P, _P, _P, _I64]
+    L.or_tq3_decode.argtypes = [_P, _P, _I64, _I]
+    L.or_tq3_decode_f32.argtypes = [_P, _P, _I64]
+    L.or_q8_encode.argtypes = [_P, _P, _I64, _I]
+    L.or_q8_decode.argtypes = [_P, _P, _I64, _I]
+    L.or_attn_split.argtypes = [_I, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I,
+                                _F, _I, _I, _I, _P, _I]
+    L.or_attn_split_merge.argtypes = [_P, _P, _P, _P, _I, _I, _I, _I, _I, _I]
+    L.or_attn_ref_f64.argtypes = [_P, _P, _P, _P, _I, _I, _I, _I, _I, ctypes.c_double,
+                                  _I, _I, _P]
+    L.or_key_visible.restype = _I
+    L.or_key_visible.argtypes = [_I, _I, _I, _I, _I, _P]
+
+
+def _ptr(a):
+    return None if a is None else a.ctypes.data
+
+
+def _u16(a):
+    a = np.ascontiguousarray(a)
+    if a.dtype == np.float16:
+        a = a.view(np.uint16)
+    assert a.dtype == np.uint16, a.dtype
+    return a
+
+
+# ---- scalar / constants -------------------------------------------------
+
+def f16_to_f32(h: np.ndarray) -> np.ndarray:
+    h = _u16(h)
+    out = np.empty(h.shape, np.float32)
+    lib().or_f16_to_f32_n(_ptr(h), _ptr(out), h.size)
+    return out
+
+
+def f32_to_f16(f: np.ndarray) -> np.ndarray:
+    f = np.ascontiguousarray(f, dtype=np.float32)
+    out = np.empty(f.shape, np.uint16)
+    lib().or_f32_to_f16_n(_ptr(f), _ptr(out), f.size)
+    return out
+
+
+def tq3_signs() -> np.ndarray:
+    out = np.empty(128, np.float32)
+    lib().or_tq3_signs(_ptr(out))
+    return out
+
+
+def tq3_centroids() -> np.ndarray:
+    out = np.empty(8, np.float32)
+    lib().or_tq3_centroids(_ptr(out))
+    return out
+
+
+def tq3_bounds() -> np.ndarray:
+    out = np.empty(7, np.float32)
+    lib().or_tq3_bounds(_ptr(out))
+    return out
+
+
+def wht_scale() -> float:
+    return float(np.float32(lib().or_tq3_wht_scale()))
+
+
+def wht128(x: np.ndarray) -> np.ndarray:
+    x = np.array(x, dtype=np.float32, copy=True).reshape(-1, 128)
+    for row in x:
+        lib().or_wht128(row.ctypes.data)
+    return x
+
+
+def find_bin(v: np.ndarray) -> np.ndarray:
+    v = np.asarray(v, np.float32).ravel()
+    return np.array([lib().or_tq3_find_bin(float(x)) for x in v], np.uint8)
+
+
+def pack_3bit_8(idx8: np.ndarray) -> np.ndarray:
+    idx8 = np.ascontiguousarray(idx8, np.uint8)
+    out = np.zeros(3, np.uint8)
+    lib().or_pack_3bit_8(_ptr(out), _ptr(idx8))
+    return out
+
+
+def unpack_3bit_8(b3: np.ndarray) -> np.ndarray:
+    b3 = np.ascontiguousarray(b3, np.uint8)
+    out = np.zeros(8, np.uint8)
+    lib().or_unpack_3bit_8(_ptr(b3), _ptr(out))
+    return out
+
+
+# ---- codecs --------------------------------------------------------------
+
+def tq3_encode(x_f16: np.ndarray, nthreads: int = 0) -> np.ndarray:
+    x = _u16(x_f16).reshape(-1)
+    assert x.size % 128 == 0
+    n = x.size // 128
+    out = np.zeros(n, BLOCK_TQ3)
+    lib().or_tq3_encode(_ptr(x), _ptr(out), n, nthreads)
+    return out
+
+
+def tq3_encode_rotated(x_f16: np.ndarray):
+    x = _u16(x_f16).reshape(-1)
+    n = x.size // 128
+    out = np.zeros(n, BLOCK_TQ3)
+    rot = np.zeros((n, 128), np.float32)
+    lib().or_tq3_encode_rotated(_ptr(x), _ptr(out), _ptr(rot), n)
+    return out, rot
+
+
+def tq3_decode(blocks: np.ndarray, nthreads: int = 0) -> np.ndarray:
+    blocks = np.ascontiguousarray(blocks).view(BLOCK_TQ3).reshape(-1)
+    out = np.empty(blocks.size * 128, np.uint16)
+    lib().or_tq3_decode(_ptr(blocks), _ptr(out), blocks.size, nthreads)
+    return out
+
+
+def tq3_decode_f32(blocks: np.ndarray) -> np.ndarray:
+    blocks = np.ascontiguousarray(blocks).view(BLOCK_TQ3).reshape(-1)
+    out = np.empty(blocks.size * 128, np.float32)
+    lib().or_tq3_decode_f32(_ptr(blocks), _ptr(out), blocks.size)
+    return out
+
+
+def q8_encode(x_f16: np.ndarray, nthreads: int = 0) -> np.ndarray:
+    x = _u16(x_f16).reshape(-1)
+    assert x.size % 32 == 0
+    n = x.size // 32
+    out = np.zeros(n, BLOCK_Q8)
+    lib().or_q8_encode(_ptr(x), _ptr(out), n, nthreads)
+    return out
+
+
+def q8_decode(blocks: np.ndarray, nthreads: int = 0) -> np.ndarray:
+    blocks = np.ascontiguousarray(blocks).view(BLOCK_Q8).reshape(-1)
+    out = np.empty(blocks.size * 32, np.uint16)
+    lib().or_q8_decode(_ptr(blocks), _ptr(out), blocks.size, nthreads)
+    return out
+
+
+# ---- attention -------------------------------------------------------------
+
+def attn_split(kind, q, k, v, *, num_q, num_kv, hd, start_pos, sub_n, sub_n_max,
+               active_end_max, scale, k_splits, sink_tok=0, window_tok=0,
+               tree_mask=None, nthreads=0):
+    """attention.cuh:1905-2177 / 2633-2801.  Returns (part_m, part_l, part_o)."""
+    q = _u16(q)
+    k = np.ascontiguousarray(k)
+    v = np.ascontiguousarray(v)
+    pm = np.full((num_q, sub_n_max, k_splits), np.nan, np.float32)
+    pl = np.full((num_q, sub_n_max, k_splits), np.nan, np.float32)
+    po = np.full((num_q, sub_n_max, k_splits, hd), np.nan, np.float32)
+    tm = None if tree_mask is None else np.ascontiguousarray(tree_mask, np.uint32)
+    lib().or_attn_split(kind, _ptr(q), _ptr(k), _ptr(v), _ptr(pm), _ptr(pl), _ptr(po),
+                        num_q, num_kv, hd, start_pos, sub_n, sub_n_max, active_end_max,
+                        float(scale), k_splits, sink_tok, window_tok, _ptr(tm), nthreads)
+    return pm, pl, po
+
+
+def attn_split_merge(pm, pl, po, *, num_q, num_kv, hd, sub_n, sub_n_max, k_splits):
+    """attention.cuh:1837-1891.  Returns fp16 bits [sub_n][num_q][hd]."""
+    pm = np.ascontiguousarray(pm, np.float32)
+    pl = np.ascontiguousarray(pl, np.float32)
+    po = np.ascontiguousarray(po, np.float32)
+    out = np.zeros((sub_n, num_q, hd), np.uint16)
+    lib().or_attn_split_merge(_ptr(pm), _ptr(pl), _ptr(po), _ptr(out), num_q, num_kv, hd,
+                              sub_n, sub_n_max, k_splits)
+    return out
+
+
+def attn_ref_f64(q, k_f16, v_f16, *, num_q, num_kv, hd, start_pos, sub_n, scale,
+                 sink_tok=0, window_tok=0, tree_mask=None):
+    q = _u16(q)
+    k_f16 = _u16(k_f16)
+    v_f16 = _u16(v_f16)
+    out = np.zeros((sub_n, num_q, hd), np.float64)
+    tm = None if tree_mask is None else np.ascontiguousarray(tree_mask, np.uint32)
+    lib().or_attn_ref_f64(_ptr(q), _ptr(k_f16), _ptr(v_f16), _ptr(out), num_q, num_kv, hd,
+                          start_pos, sub_n, float(scale), sink_tok, window_tok, _ptr(tm))
+    return out
+
+
+def key_visible(key, start_pos, t_idx, sink_tok=0, window_tok=0, tree_mask=None):
+    tm = None if tree_mask is None else np.ascontiguousarray(tree_mask, np.uint32)
+    return bool(lib().or_key_visible(key, start_pos, t_idx, sink_tok, window_tok, _ptr(tm)))

@@ -1,0 +1,558 @@
+/*
+ * qkv_oracle.c -- CPU restatement of the reference's compressed-KV path.
+ *
+ * TEST INFRASTRUCTURE ONLY (see qkv_oracle.h).  Built with -ffp-contract=off
+ * and without fast-math so every float operation rounds exactly once, in the
+ * order the reference source writes it.
+ *
+ * Pinning (the independent check that fixes each function; tests/ file):
+ *   or_f16_to_f32 / or_f32_to_f16   numpy float16 casts, exhaustive over all
+ *                                   65536 halves + 2^20 random floats
+ *                                   (test_oracle_codec.py)
+ *   or_tq3_signs                    known answer: first 16 signs, 69 of 128
+ *                                   positive, LE mask words 0xfae78245 ...
+ *   or_tq3_centroids / bounds       bounds are centroid midpoints; centroids
+ *                                   are the 8-level Gaussian Lloyd-Max levels
+ *                                   times 1/sqrt(128)
+ *   or_wht128                       Sylvester Hadamard matrix from
+ *                                   scipy.linalg.hadamard, H*H = 128*I
+ *   or_tq3_find_bin                 numpy.searchsorted(bounds, v, 'left') on
+ *                                   random + all-boundary + signed-zero + NaN
+ *   or_pack/unpack_3bit_8           numpy bit-level packing (LE 3-bit stream)
+ *   or_tq3_encode                   fp64 rotation y = H*D*x/|x|/sqrt(128):
+ *                                   codes equal searchsorted(bounds, y) except
+ *                                   where |y - bound| < 4 ulp; norm equals the
+ *                                   sequential fp32 sum (numpy cumsum) sqrt;
+ *                                   zero-block rule
+ *   or_tq3_decode                   fp64 D*H*c*norm/sqrt(128) within fp16 ulp
+ *   or_q8_encode / decode           closed form: |x - q*d| <= d/2 (+fp16
+ *                                   rounding of d), amax=0 -> d=+0 and q=0,
+ *                                   ties to even, numpy rint cross-check
+ *   or_attn_split + merge           or_attn_ref_f64 (softmax in double) for
+ *                                   dense, causal-verify, tree, sink/window
+ *                                   inputs; split-count invariance
+ *   or_attn_ref_f64                 brute-force numpy softmax on tiny inputs
+ * No function is "parity unpinned".
+ */
+#include "qkv_oracle.h"
+
+#include <math.h>
+#include <stdlib.h>
+#include <string.h>
+#ifdef _OPENMP
+#include <omp.h>
+#endif
+
+/* ===================================================================== */
+/* fp16 <-> fp32 (IEEE binary16, round-to-nearest-even)                   */
+/* ===================================================================== */
+
+static inline float bits_f32(uint32_t u) { float f; memcpy(&f, &u, 4); return f; }
+static inline uint32_t f32_bits(float f) { uint32_t u; memcpy(&u, &f, 4); return u; }
+
+float or_f16_to_f32(uint16_t h) {
+    uint32_t sign = (uint32_t)(h & 0x8000u) << 16;
+    uint32_t exp = (h >> 10) & 0x1f;
+    uint32_t man = h & 0x3ffu;
+    if (exp == 0x1f) return bits_f32(sign | 0x7f800000u | (man << 13));
+    if (exp == 0) {
+        if (man == 0) return bits_f32(sign);
+        /* subnormal: value = man * 2^-24, exact in fp32 */
+        float v = (float)man * bits_f32(0x33800000u); /* 2^-24 */
+        return sign ? -v : v;
+    }
+    return bits_f32(sign | ((exp + 112u) << 23) | (man << 13));
+}
+
+uint16_t or_f32_to_f16(float f) {
+    uint32_t u = f32_bits(f);
+    uint16_t sign = (uint16_t)((u >> 16) & 0x8000u);
+    uint32_t a = u & 0x7fffffffu;
+    if (a >= 0x7f800000u) {                       /* inf / nan */
+        if (a > 0x7f800000u) return (uint16_t)(sign | 0x7e00u | ((a >> 13) & 0x3ffu));
+        return (uint16_t)(sign | 0x7c00u);
+    }
+    if (a >= 0x477ff000u) return (uint16_t)(sign | 0x7c00u); /* rounds to >= 65520 -> inf */
+    if (a >= 0x38800000u) {                       /* normal half range */
+        uint32_t exp = (a >> 23) - 112u;
+        uint32_t man = a & 0x7fffffu;
+        uint32_t h = (exp << 10) | (man >> 13);
+        uint32_t rem = man & 0x1fffu;
+        if (rem > 0x1000u || (rem == 0x1000u && (h & 1u))) h++;
+        return (uint16_t)(sign | h);
+    }
+    /* subnormal or zero in half: value / 2^-24 rounded to even integer */
+    {
+        float v = bits_f32(a) * bits_f32(0x4b800000u); /* * 2^24 (exact) */
+        /* v < 1024; round half to even */
+        float fl = floorf(v);
+        float r = v - fl;
+        uint32_t q = (uint32_t)fl;
+        if (r > 0.5f || (r == 0.5f && (q & 1u))) q++;
+        return (uint16_t)(sign | q);
+    }
+}
+
+void or_f16_to_f32_n(const uint16_t* h, float* f, int64_t n) {
+    for (int64_t i = 0; i < n; i++) f[i] = or_f16_to_f32(h[i]);
+}
+void or_f32_to_f16_n(const float* f, uint16_t* h, int64_t n) {
+    for (int64_t i = 0; i < n; i++) h[i] = or_f32_to_f16(f[i]);
+}
+
+/* ===================================================================== */
+/* Codec constants                                                         */
+/* ===================================================================== */
+
+/* turboquant.cuh:27-30 (data, kept identical) */
+static const float k_centroids[8] = {
+    -0.190303f, -0.118828f, -0.066847f, -0.021664f,
+     0.021664f,  0.066847f,  0.118828f,  0.190303f};
+/* turboquant.cuh:34-37 (data, kept identical) */
+static const float k_bounds[7] = {
+    -0.154566f, -0.092838f, -0.044256f, 0.000000f,
+     0.044256f,  0.092838f,  0.154566f};
+
+void or_tq3_centroids(float out[8]) { memcpy(out, k_centroids, sizeof(k_centroids)); }
+void or_tq3_bounds(float out[7]) { memcpy(out, k_bounds, sizeof(k_bounds)); }
+
+/* turboquant.cuh:61 rsqrtf(128.0f).  The correctly rounded value of
+ * 1/sqrt(128) is used (0x3DB504F3). */
+float or_tq3_wht_scale(void) { return bits_f32(0x3DB504F3u); }
+
+/* turboquant.cuh:288-302: xorshift64 from 0xCAFEF00D, bit 0 picks the sign. */
+void or_tq3_signs(float out[OR_TQ_BLOCK]) {
+    uint64_t s = 0xCAFEF00DULL;
+    for (int i = 0; i < OR_TQ_BLOCK; i++) {
+        s ^= s << 13;
+        s ^= s >> 7;
+        s ^= s << 17;
+        out[i] = (s & 1u) ? 1.0f : -1.0f;
+    }
+}
+
+static float g_signs[OR_TQ_BLOCK];
+static int g_signs_ready = 0;
+static const float* signs(void) {
+    if (!g_signs_ready) { or_tq3_signs(g_signs); g_signs_ready = 1; }
+    return g_signs;
+}
+
+/* ===================================================================== */
+/* Building blocks                                                         */
+/* ===================================================================== */
+
+/* turboquant.cuh:48-64: in-place Sylvester butterflies, strides 1..64,
+ * (a,b) -> (a+b, a-b), then every element times rsqrtf(128). */
+void or_wht128(float* x) {
+    for (int step = 1; step < OR_TQ_BLOCK; step <<= 1)
+        for (int i = 0; i < OR_TQ_BLOCK; i += 2 * step)
+            for (int j = i; j < i + step; j++) {
+                float a = x[j], b = x[j + step];
+                x[j] = a + b;
+                x[j + step] = a - b;
+            }
+    const float rs = or_tq3_wht_scale();
+    for (int i = 0; i < OR_TQ_BLOCK; i++) x[i] *= rs;
+}
+
+/* turboquant.cuh:79-87: idx = number of bounds strictly below v. */
+uint8_t or_tq3_find_bin(float v) {
+    uint8_t idx = 0;
+    for (int i = 0; i < 7; i++)
+        if (v > k_bounds[i]) idx = (uint8_t)(i + 1);
+    return idx;
+}
+
+/* turboquant.cuh:90-100 */
+void or_pack_3bit_8(uint8_t* dst, const uint8_t* idx8) {
+    uint32_t p = 0;
+    for (int i = 0; i < 8; i++) p |= ((uint32_t)idx8[i]) << (3 * i);
+    dst[0] = (uint8_t)(p & 0xff);
+    dst[1] = (uint8_t)((p >> 8) & 0xff);
+    dst[2] = (uint8_t)((p >> 16) & 0xff);
+}
+
+/* turboquant.cuh:103-108 */
+void or_unpack_3bit_8(const uint8_t* src, uint8_t* idx8) {
+    uint32_t p = (uint32_t)src[0] | ((uint32_t)src[1] << 8) | ((uint32_t)src[2] << 16);
+    for (int i = 0; i < 8; i++) idx8[i] = (uint8_t)((p >> (3 * i)) & 7u);
+}
+
+/* ===================================================================== */
+/* TQ3 encode / decode                                                     */
+/* ===================================================================== */
+
+/* turboquant.cuh:112-165, one block. */
+static void tq3_encode_one(const uint16_t* in, or_block_tq3* out, float* rot_out) {
+    const float* sg = signs();
+    float x[OR_TQ_BLOCK];
+    for (int i = 0; i < OR_TQ_BLOCK; i++) x[i] = or_f16_to_f32(in[i]);
+    float nsq = 0.0f;
+    for (int i = 0; i < OR_TQ_BLOCK; i++) nsq += x[i] * x[i];
+    float norm = sqrtf(nsq);
+    out->norm = norm;
+    if (norm < 1e-10f) {
+        memset(out->qs, 0, OR_TQ_QS_BYTES);
+        if (rot_out) memset(rot_out, 0, sizeof(float) * OR_TQ_BLOCK);
+        return;
+    }
+    float inv = 1.0f / norm;
+    for (int i = 0; i < OR_TQ_BLOCK; i++) x[i] *= inv;
+    for (int i = 0; i < OR_TQ_BLOCK; i++) x[i] *= sg[i];
+    or_wht128(x);
+    uint8_t idx[OR_TQ_BLOCK];
+    for (int i = 0; i < OR_TQ_BLOCK; i++) idx[i] = or_tq3_find_bin(x[i]);
+    for (int g = 0; g < OR_TQ_BLOCK / 8; g++) or_pack_3bit_8(&out->qs[3 * g], &idx[8 * g]);
+    if (rot_out) memcpy(rot_out, x, sizeof(float) * OR_TQ_BLOCK);
+}
+
+void or_tq3_encode(const uint16_t* in_f16, or_block_tq3* out, int64_t n_blocks, int nthreads) {
+#ifdef _OPENMP
+    if (nthreads <= 0) nthreads = omp_get_max_threads();
+#pragma omp parallel for schedule(static) num_threads(nthreads)
+#endif
+    for (int64_t b = 0; b < n_blocks; b++)
+        tq3_encode_one(in_f16 + b * OR_TQ_BLOCK, out + b, NULL);
+    (void)nthreads;
+}
+
+void or_tq3_encode_rotated(const uint16_t* in_f16, or_block_tq3* out, float* rot,
+                           int64_t n_blocks) {
+    for (int64_t b = 0; b < n_blocks; b++)
+        tq3_encode_one(in_f16 + b * OR_TQ_BLOCK, out + b, rot + b * OR_TQ_BLOCK);
+}
+
+/* turboquant.cuh:169-200 (and 253-284 when out_f32 != NULL). */
+static void tq3_decode_one(const or_block_tq3* in, uint16_t* out_f16, float* out_f32) {
+    const float* sg = signs();
+    float norm = in->norm;
+    float x[OR_TQ_BLOCK];
+    for (int g = 0; g < OR_TQ_BLOCK / 8; g++) {
+        uint8_t idx[8];
+        or_unpack_3bit_8(&in->qs[3 * g], idx);
+        for (int j = 0; j < 8; j++) x[8 * g + j] = k_centroids[idx[j]];
+    }
+    or_wht128(x);
+    for (int i = 0; i < OR_TQ_BLOCK; i++) x[i] *= sg[i];
+    for (int i = 0; i < OR_TQ_BLOCK; i++) {
+        float v = x[i] * norm;
+        if (out_f16) out_f16[i] = or_f32_to_f16(v);
+        if (out_f32) out_f32[i] = v;
+    }
+}
+
+void or_tq3_decode(const or_block_tq3* in, uint16_t* out_f16, int64_t n_blocks, int nthreads) {
+#ifdef _OPENMP
+    if (nthreads <= 0) nthreads = omp_get_max_threads();
+#pragma omp parallel for schedule(static) num_threads(nthreads)
+#endif
+    for (int64_t b = 0; b < n_blocks; b++)
+        tq3_decode_one(in + b, out_f16 + b * OR_TQ_BLOCK, NULL);
+    (void)nthreads;
+}
+
+void or_tq3_decode_f32(const or_block_tq3* in, float* out, int64_t n_blocks) {
+    for (int64_t b = 0; b < n_blocks; b++) tq3_decode_one(in + b, NULL, out + b * OR_TQ_BLOCK);
+}
+
+/* ===================================================================== */
+/* Q8_0 KV                                                                 */
+/* ===================================================================== */
+
+/* __float2int_rn: round half to even; NaN -> 0 (saturating convert). */
+static int f2i_rn(float v) {
+    if (v != v) return 0;
+    if (v >= 2147483648.0f) return 2147483647;
+    if (v <= -2147483648.0f) return (int)0x80000000u;
+    return (int)nearbyintf(v); /* default rounding mode: to nearest even */
+}
+
+/* attention.cuh:2587-2609, one block (pad is not written). */
+static void q8_encode_one(const uint16_t* in, or_block_q8* out) {
+    float v[OR_Q8_BLOCK];
+    float amax = 0.0f;
+    for (int i = 0; i < OR_Q8_BLOCK; i++) v[i] = or_f16_to_f32(in[i]);
+    /* fmaxf reduction over |v| (order is irrelevant for max; fmaxf drops NaN) */
+    amax = fabsf(v[0]);
+    for (int i = 1; i < OR_Q8_BLOCK; i++) amax = fmaxf(amax, fabsf(v[i]));
+    float scale = amax / 127.0f;
+    float inv = scale > 0.0f ? 1.0f / scale : 0.0f;
+    for (int i = 0; i < OR_Q8_BLOCK; i++) {
+        int q = f2i_rn(v[i] * inv);
+        if (q > 127) q = 127;
+        if (q < -128) q = -128;
+        out->qs[i] = (int8_t)q;
+    }
+    out->d = or_f32_to_f16(scale);
+}
+
+void or_q8_encode(const uint16_t* in_f16, or_block_q8* out, int64_t n_blocks, int nthreads) {
+#ifdef _OPENMP
+    if (nthreads <= 0) nthreads = omp_get_max_threads();
+#pragma omp parallel for schedule(static) num_threads(nthreads)
+#endif
+    for (int64_t b = 0; b < n_blocks; b++) q8_encode_one(in_f16 + b * OR_Q8_BLOCK, out + b);
+    (void)nthreads;
+}
+
+/* attention.cuh:2614-2626 */
+void or_q8_decode(const or_block_q8* in, uint16_t* out_f16, int64_t n_blocks, int nthreads) {
+#ifdef _OPENMP
+    if (nthreads <= 0) nthreads = omp_get_max_threads();
+#pragma omp parallel for schedule(static) num_threads(nthreads)
+#endif
+    for (int64_t b = 0; b < n_blocks; b++) {
+        float s = or_f16_to_f32(in[b].d);
+        for (int i = 0; i < OR_Q8_BLOCK; i++)
+            out_f16[b * OR_Q8_BLOCK + i] = or_f32_to_f16((float)in[b].qs[i] * s);
+    }
+    (void)nthreads;
+}
+
+/* ===================================================================== */
+/* Split-K flash decode                                                    */
+/* ===================================================================== */
+
+#define OR_BM 32
+
+int or_key_visible(int key, int start_pos, int t_idx, int sink_tok, int window_tok,
+                   const uint32_t* tree_mask) {
+    int active_end_t = start_pos + t_idx + 1;               /* attention.cuh:1941-1942 */
+    if (key < 0 || key >= active_end_t) return 0;
+    if (sink_tok > 0 || window_tok > 0) {                   /* attention.cuh:1983-1994 */
+        int ts = key & ~(OR_BM - 1);
+        int te = ts + OR_BM < active_end_t ? ts + OR_BM : active_end_t;
+        int win_lo = active_end_t - window_tok;
+        if (!(ts < sink_tok) && !(te > win_lo)) return 0;
+    }
+    if (tree_mask && key >= start_pos)                      /* attention.cuh:2101-2105 */
+        return (int)((tree_mask[t_idx] >> (key - start_pos)) & 1u);
+    return 1;
+}
+
+/* Decode one key or value row of one kv head into fp16 (the reference's smem
+ * tile contents): TQ3 per attention.cuh:2009-2072, Q8 per attention.cuh:2720-2729. */
+static void decode_row(int kind, const void* cache, int pos, int num_kv, int kv_head, int hd,
+                       uint16_t* dst) {
+    if (kind == OR_KV_TQ3) {
+        int bpk = hd / OR_TQ_BLOCK;
+        const or_block_tq3* b = (const or_block_tq3*)cache + ((int64_t)pos * num_kv + kv_head) * bpk;
+        for (int j = 0; j < bpk; j++) tq3_decode_one(b + j, dst + j * OR_TQ_BLOCK, NULL);
+    } else if (kind == OR_KV_Q8) {
+        int bpk = hd / OR_Q8_BLOCK;
+        const or_block_q8* b = (const or_block_q8*)cache + ((int64_t)pos * num_kv + kv_head) * bpk;
+        for (int j = 0; j < bpk; j++) {
+            float s = or_f16_to_f32(b[j].d);
+            for (int i = 0; i < OR_Q8_BLOCK; i++)
+                dst[j * OR_Q8_BLOCK + i] = or_f32_to_f16((float)b[j].qs[i] * s);
+        }
+    } else {
+        const uint16_t* src = (const uint16_t*)cache + ((int64_t)pos * num_kv + kv_head) * hd;
+        memcpy(dst, src, sizeof(uint16_t) * hd);
+    }
+}
+
+/* Score of one (q head, key row): the reference splits the HD-long dot product
+ * over 32 lanes (LANE_D = HD/32 consecutive elements each, accumulated as
+ * half2 pairs) and reduces with an xor butterfly (attention.cuh:2081-2095);
+ * this reproduces that association (lane 0's view of the butterfly). */
+static float score_dot(const float* qf, const float* kf, int hd) {
+    float part[32];
+    int lane_d = hd / 32;
+    for (int lane = 0; lane < 32; lane++) {
+        float p = 0.0f;
+        for (int i = 0; i < lane_d / 2; i++) {
+            int c = lane * lane_d + 2 * i;
+            p += qf[c] * kf[c] + qf[c + 1] * kf[c + 1];
+        }
+        part[lane] = p;
+    }
+    for (int off = 16; off > 0; off >>= 1) {
+        float nxt[32];
+        for (int lane = 0; lane < 32; lane++) nxt[lane] = part[lane] + part[lane ^ off];
+        memcpy(part, nxt, sizeof(part));
+    }
+    return part[0];
+}
+
+/* attention.cuh:1905-2177 / 2633-2801 for one (kv_head, t_idx, split). */
+static void split_one(int kind, const uint16_t* q, const void* k, const void* v,
+                      float* part_m, float* part_l, float* part_o, int num_q, int num_kv,
+                      int hd, int start_pos, int sub_n_max, int active_end_max, float scale,
+                      int k_splits, int sink_tok, int window_tok, const uint32_t* tree_mask,
+                      int kv_head, int t_idx, int split) {
+    const int gqa = num_q / num_kv;
+    const int abs_pos = start_pos + t_idx;
+    const int active_end_t = abs_pos + 1;
+    const int total_tiles = (active_end_max + OR_BM - 1) / OR_BM;
+    const int tps = (total_tiles + k_splits - 1) / k_splits;
+    const int tile_lo = split * tps * OR_BM;
+    int tile_hi = (split + 1) * tps * OR_BM;
+    if (tile_hi > active_end_t) tile_hi = active_end_t;
+
+    float* qf = (float*)malloc(sizeof(float) * gqa * hd);
+    float* acc = (float*)calloc((size_t)gqa * hd, sizeof(float));
+    float* m = (float*)malloc(sizeof(float) * gqa);
+    float* l = (float*)calloc(gqa, sizeof(float));
+    uint16_t* krow = (uint16_t*)malloc(sizeof(uint16_t) * OR_BM * hd);
+    uint16_t* vrow = (uint16_t*)malloc(sizeof(uint16_t) * OR_BM * hd);
+    float* kf = (float*)malloc(sizeof(float) * OR_BM * hd);
+    float* vf = (float*)malloc(sizeof(float) * OR_BM * hd);
+    float s[OR_BM], p[OR_BM];
+    for (int g = 0; g < gqa; g++) {
+        m[g] = -INFINITY;
+        int qh = kv_head * gqa + g;
+        for (int c = 0; c < hd; c++)
+            qf[g * hd + c] = or_f16_to_f32(q[((int64_t)t_idx * num_q + qh) * hd + c]);
+    }
+    const int sparse = (sink_tok > 0 || window_tok > 0);
+    const int win_lo = sparse ? active_end_t - window_tok : 0;
+    for (int ts = tile_lo; ts < tile_hi; ts += OR_BM) {
+        int te = ts + OR_BM < tile_hi ? ts + OR_BM : tile_hi;
+        int len = te - ts;
+        if (sparse && !(ts < sink_tok) && !(te > win_lo)) continue;
+        for (int r = 0; r < len; r++) {
+            decode_row(kind, k, ts + r, num_kv, kv_head, hd, krow + r * hd);
+            decode_row(kind, v, ts + r, num_kv, kv_head, hd, vrow + r * hd);
+        }
+        for (int i = 0; i < len * hd; i++) {
+            kf[i] = or_f16_to_f32(krow[i]);
+            vf[i] = or_f16_to_f32(vrow[i]);
+        }
+        for (int g = 0; g < gqa; g++) {
+            float mrow = -INFINITY;
+            for (int r = 0; r < OR_BM; r++) {
+                float val = -INFINITY;
+                if (r < len) {
+                    int key = ts + r;
+                    int vis = (key < start_pos) ||
+                              (tree_mask ? (int)((tree_mask[t_idx] >> (key - start_pos)) & 1u) : 1);
+                    if (vis) val = score_dot(qf + g * hd, kf + r * hd, hd) * scale;
+                }
+                s[r] = val;
+                mrow = fmaxf(mrow, val);
+            }
+            float mnew = fmaxf(m[g], mrow);
+            float corr = expf(m[g] - mnew);
+            float sum = 0.0f;
+            for (int r = 0; r < OR_BM; r++) { p[r] = expf(s[r] - mnew); }
+            /* xor-butterfly sum over 32 lanes (attention.cuh:2121-2123) */
+            {
+                float part[32];
+                for (int r = 0; r < 32; r++) part[r] = r < OR_BM ? p[r] : 0.0f;
+                for (int off = 16; off > 0; off >>= 1) {
+                    float nxt[32];
+                    for (int r = 0; r < 32; r++) nxt[r] = part[r] + part[r ^ off];
+                    memcpy(part, nxt, sizeof(part));
+                }
+                sum = part[0];
+            }
+            for (int c = 0; c < hd; c++) acc[g * hd + c] *= corr;
+            l[g] = l[g] * corr + sum;
+            for (int r = 0; r < len; r++)
+                for (int c = 0; c < hd; c++) acc[g * hd + c] += p[r] * vf[r * hd + c];
+            m[g] = mnew;
+        }
+    }
+    for (int g = 0; g < gqa; g++) {
+        int qh = kv_head * gqa + g;
+        int64_t ml = ((int64_t)qh * sub_n_max + t_idx) * k_splits + split;
+        part_m[ml] = m[g];
+        part_l[ml] = l[g];
+        memcpy(part_o + ml * hd, acc + g * hd, sizeof(float) * hd);
+    }
+    free(qf); free(acc); free(m); free(l); free(krow); free(vrow); free(kf); free(vf);
+}
+
+void or_attn_split(int kind, const uint16_t* q, const void* k, const void* v,
+                   float* part_m, float* part_l, float* part_o,
+                   int num_q, int num_kv, int hd, int start_pos, int sub_n,
+                   int sub_n_max, int active_end_max, float scale, int k_splits,
+                   int sink_tok, int window_tok, const uint32_t* tree_mask,
+                   int nthreads) {
+    int64_t n_items = (int64_t)num_kv * sub_n * k_splits;
+#ifdef _OPENMP
+    if (nthreads <= 0) nthreads = omp_get_max_threads();
+#pragma omp parallel for schedule(dynamic) num_threads(nthreads)
+#endif
+    for (int64_t it = 0; it < n_items; it++) {
+        int split = (int)(it % k_splits);
+        int t_idx = (int)((it / k_splits) % sub_n);
+        int kv_head = (int)(it / ((int64_t)k_splits * sub_n));
+        split_one(kind, q, k, v, part_m, part_l, part_o, num_q, num_kv, hd, start_pos,
+                  sub_n_max, active_end_max, scale, k_splits, sink_tok, window_tok,
+                  tree_mask, kv_head, t_idx, split);
+    }
+    (void)nthreads;
+}
+
+/* attention.cuh:1837-1891 */
+void or_attn_split_merge(const float* part_m, const float* part_l, const float* part_o,
+                         uint16_t* out, int num_q, int num_kv, int hd, int sub_n,
+                         int sub_n_max, int k_splits) {
+    (void)num_kv;
+    float* o = (float*)malloc(sizeof(float) * hd);
+    for (int t = 0; t < sub_n; t++)
+        for (int qh = 0; qh < num_q; qh++) {
+            int64_t base = ((int64_t)qh * sub_n_max + t) * k_splits;
+            float mg = -INFINITY;
+            for (int s = 0; s < k_splits; s++) mg = fmaxf(mg, part_m[base + s]);
+            float lg = 0.0f;
+            for (int c = 0; c < hd; c++) o[c] = 0.0f;
+            for (int s = 0; s < k_splits; s++) {
+                float ms = part_m[base + s], ls = part_l[base + s];
+                if (!isfinite(ms) || ls <= 0.0f) continue;
+                float w = expf(ms - mg);
+                lg += w * ls;
+                const float* op = part_o + (base + s) * hd;
+                for (int c = 0; c < hd; c++) o[c] += w * op[c];
+            }
+            float inv = lg > 0.0f ? 1.0f / lg : 0.0f;
+            for (int c = 0; c < hd; c++)
+                out[((int64_t)t * num_q + qh) * hd + c] = or_f32_to_f16(o[c] * inv);
+        }
+    free(o);
+}
+
+/* Independent fp64 reference (tools/dflash_attn_bench.cu:185-211 pattern). */
+void or_attn_ref_f64(const uint16_t* q, const uint16_t* k_f16, const uint16_t* v_f16,
+                     double* out, int num_q, int num_kv, int hd, int start_pos,
+                     int sub_n, double scale, int sink_tok, int window_tok,
+                     const uint32_t* tree_mask) {
+    const int gqa = num_q / num_kv;
+    for (int t = 0; t < sub_n; t++) {
+        int n_keys = start_pos + t + 1;
+        double* sc = (double*)malloc(sizeof(double) * (n_keys > 0 ? n_keys : 1));
+        for (int qh = 0; qh < num_q; qh++) {
+            int kvh = qh / gqa;
+            const uint16_t* qv = q + ((int64_t)t * num_q + qh) * hd;
+            double mx = -INFINITY;
+            for (int key = 0; key < n_keys; key++) {
+                if (!or_key_visible(key, start_pos, t, sink_tok, window_tok, tree_mask)) {
+                    sc[key] = -INFINITY;
+                    continue;
+                }
+                const uint16_t* kr = k_f16 + ((int64_t)key * num_kv + kvh) * hd;
+                double d = 0.0;
+                for (int c = 0; c < hd; c++)
+                    d += (double)or_f16_to_f32(qv[c]) * (double)or_f16_to_f32(kr[c]);
+                sc[key] = d * scale;
+                if (sc[key] > mx) mx = sc[key];
+            }
+            double den = 0.0;
+            double* o = out + ((int64_t)t * num_q + qh) * hd;
+            for (int c = 0; c < hd; c++) o[c] = 0.0;
+            if (mx == -INFINITY) continue;
+            for (int key = 0; key < n_keys; key++) {
+                if (sc[key] == -INFINITY) continue;
+                double w = exp(sc[key] - mx);
+                den += w;
+                const uint16_t* vr = v_f16 + ((int64_t)key * num_kv + kvh) * hd;
+                for (int c = 0; c < hd; c++) o[c] += w * (double)or_f16_to_f32(vr[c]);
+            }
+            for (int c = 0; c < hd; c++) o[c] /= den;
+        }
+        free(sc);
+    }
+}
