@@ -1,0 +1,160 @@
+/*
+ * qkv.h -- C ABI of the MI355X (gfx950) compressed KV-cache library libqkv.so.
+ *
+ * Drop-in for the reference's compressed-KV launches (Haru-neo/qengine,
+ * paths relative to its tree).  The reference launches CUDA kernels directly
+ * from QwenModel (src/model.cuh); every entry point below replaces one such
+ * launch and keeps its argument list, buffer layouts and stream ordering.
+ *
+ * Conventions
+ *  - fp16 tensors are passed as uint16_t bit patterns.
+ *  - The caller owns every buffer; no entry point allocates or frees device
+ *    memory.  Caches must be zero-initialised by the caller, as the reference
+ *    does (model.cuh:1914-1920).
+ *  - Every call is asynchronous on `stream` and never synchronises the host.
+ *  - Return value: QKV_OK (0) or a negative qkv_status.  Invalid arguments are
+ *    reported, never silently dropped (the reference returns void).
+ */
+#ifndef QKV_H
+#define QKV_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#include <hip/hip_runtime_api.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* turboquant.cuh:73-77  struct block_tq3 { float norm; uint8_t qs[48]; }  (52 B, align 4)
+ * 128 coordinates: L2 norm of the raw fp16 vector, then 3-bit Lloyd-Max codes of
+ * the rotated unit vector, element e at bits 3e..3e+2 of the little-endian stream. */
+typedef struct qkv_block_tq3 {
+  float norm;
+  uint8_t qs[48];
+} qkv_block_tq3;
+
+/* quant_gemv.cuh:19  block_q8_0_aligned { int8_t qs[32]; uint16_t pad; half d; }  (36 B) */
+typedef struct qkv_block_q8 {
+  int8_t qs[32];
+  uint16_t pad;
+  uint16_t d;
+} qkv_block_q8;
+
+typedef enum qkv_status {
+  QKV_OK = 0,
+  QKV_ERR_INVALID = -1,     /* bad size / shape / count                               */
+  QKV_ERR_NULL = -2,        /* required pointer is NULL                               */
+  QKV_ERR_UNSUPPORTED = -3, /* head_dim / GQA combination not compiled                */
+  QKV_ERR_ALIGN = -4,       /* pointer not aligned as documented                       */
+  QKV_ERR_DEVICE = -5,      /* no usable gfx950 device / HIP runtime error             */
+  QKV_ERR_LAUNCH = -6,      /* kernel launch failed                                    */
+  QKV_ERR_WORKSPACE = -7    /* workspace missing or smaller than the query says         */
+} qkv_status;
+
+/* Library version (major*10000 + minor*100 + patch). */
+int qkv_version(void);
+
+/* Static text for a status code. */
+const char* qkv_status_string(int status);
+
+/* ---------------------------------------------------------------------------
+ * TQ3 codec
+ * ------------------------------------------------------------------------- */
+
+/* Replaces tq3_init_signs(gpu) (turboquant.cuh:288-302).  The sign vector is a
+ * compile-time constant of this library (same seed and generator), so this call
+ * only validates `device` as a gfx950 GPU.  Idempotent; optional before the
+ * other calls. */
+int qkv_tq3_init(int device);
+
+/* Replaces tq3_quantize_kernel<<<(n+31)/32, 32, 0, stream>>>(in, out, n_blocks)
+ * (turboquant.cuh:112-165; launched at model.cuh:2329-2333, 5186-5190).
+ * in:  n_blocks*128 fp16, contiguous (16-byte aligned).
+ * out: n_blocks contiguous blocks (caller computes cache + (slot_off+pos)*bpt).
+ * Codes and norms are bit-identical to the reference encoder. */
+int qkv_tq3_append(const uint16_t* in_f16, qkv_block_tq3* out, int n_blocks,
+                   hipStream_t stream);
+
+/* K and V appends of one step in a single launch: equivalent to two
+ * qkv_tq3_append calls (model.cuh:2329-2333 issues them back to back). */
+int qkv_tq3_append_kv(const uint16_t* k_f16, const uint16_t* v_f16, qkv_block_tq3* k_out,
+                      qkv_block_tq3* v_out, int n_blocks, hipStream_t stream);
+
+/* Replaces tq3_dequantize_kernel (turboquant.cuh:169-200): fp16 output
+ * half(((H*c)*rs)*sign*norm), bit-identical to the reference. */
+int qkv_tq3_dequant(const qkv_block_tq3* in, uint16_t* out_f16, int n_blocks,
+                    hipStream_t stream);
+
+/* ---------------------------------------------------------------------------
+ * Q8_0 KV codec
+ * ------------------------------------------------------------------------- */
+
+/* Replaces quantize_kv_q8_0_kern<<<n_blocks, 32, 0, stream>>>(in, out, n_blocks)
+ * (attention.cuh:2587-2609; launched at model.cuh:2316-2317).  `pad` is not
+ * written.  in: n_blocks*32 fp16 (16-byte aligned). */
+int qkv_q8_append(const uint16_t* in_f16, qkv_block_q8* out, int n_blocks,
+                  hipStream_t stream);
+
+/* Replaces dequantize_kv_q8_0_kern (attention.cuh:2614-2626). */
+int qkv_q8_dequant(const qkv_block_q8* in, uint16_t* out_f16, int n_blocks,
+                   hipStream_t stream);
+
+/* ---------------------------------------------------------------------------
+ * Split-K flash decode over the packed caches
+ *
+ * Shapes: head_dim must be 256; GQA = num_q/num_kv in 1..8.
+ * q        [sub_n][num_q][256] fp16 (16-byte aligned); query t sits at absolute
+ *          position start_pos + t and attends keys [0, start_pos + t].
+ * k, v     slot-base caches, token-major [pos][num_kv][2] blocks.
+ * part_m/l [num_q][sub_n_max][k_splits] f32, part_o [..][k_splits][256] f32.
+ * sink_tok/window_tok: 0/0 = dense; otherwise the reference's 32-key tile
+ *          rule keeps tiles overlapping [0, sink) or the last `window` keys.
+ * tree_mask: NULL = chain; else bit j of tree_mask[t] lets query t see key
+ *          start_pos + j (sub_n <= 32).
+ * ------------------------------------------------------------------------- */
+
+/* Replaces flash_attn_chunk_fused_split_tq3<256, GQA, 32, 256, K_SPLITS>
+ * <<<(num_kv, sub_n, K_SPLITS), 256>>> (attention.cuh:1905-2177; launched at
+ * model.cuh:2472-2491 and 4663-4687).  Split z covers keys
+ * [z*tps*32, min((z+1)*tps*32, start_pos+t+1)), tps = ceil(ceil(active_end_max/32)/k_splits);
+ * writes the unnormalised partials (m, l, o) in the reference layout
+ * (o in the original, unrotated coordinates).  Outputs agree with the
+ * reference within the 2e-3 relative tolerance (fp32 accumulation). */
+int qkv_attn_split_tq3(const uint16_t* q, const qkv_block_tq3* k, const qkv_block_tq3* v,
+                       float* part_m, float* part_l, float* part_o, int num_q, int num_kv,
+                       int head_dim, int start_pos, int sub_n, int sub_n_max,
+                       int active_end_max, float scale, int k_splits, int sink_tok,
+                       int window_tok, const uint32_t* tree_mask, hipStream_t stream);
+
+/* Replaces flash_attn_split_merge<256, GQA, 256, K_SPLITS><<<(num_kv, sub_n), 256>>>
+ * (attention.cuh:1837-1891).  out [sub_n][num_q][256] fp16; may alias q of the
+ * preceding split call (model.cuh:2479-2482 merges in place). */
+int qkv_attn_split_merge(const float* part_m, const float* part_l, const float* part_o,
+                         uint16_t* out, int num_q, int num_kv, int head_dim, int sub_n,
+                         int sub_n_max, int k_splits, hipStream_t stream);
+
+/* Workspace bytes of qkv_decode_attn_tq3 for queries over up to
+ * n_keys = start_pos + sub_n keys. */
+size_t qkv_decode_attn_tq3_workspace_bytes(int num_q, int num_kv, int sub_n, int n_keys);
+
+/* Fast path for the same computation as qkv_attn_split_tq3 + qkv_attn_split_merge
+ * (model.cuh:2472-2491) in ONE launch: the key range is cut into chunks of
+ * 256*k keys, partials stay in rotated coordinates and are merged inside the
+ * kernel (the last-arriving workgroups do the merge), and each output row is
+ * rotated back once.  out [sub_n][num_q][256] fp16 (16-byte aligned).
+ * workspace: caller-owned device memory of at least
+ * qkv_decode_attn_tq3_workspace_bytes() bytes, 256-byte aligned, ZERO-FILLED
+ * before its first use; every completed call leaves it ready for the next
+ * one.  Calls sharing one workspace must be ordered (same stream). */
+int qkv_decode_attn_tq3(const uint16_t* q, const qkv_block_tq3* k, const qkv_block_tq3* v,
+                        uint16_t* out, int num_q, int num_kv, int head_dim, int start_pos,
+                        int sub_n, float scale, int sink_tok, int window_tok,
+                        const uint32_t* tree_mask, void* workspace, size_t workspace_bytes,
+                        hipStream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* QKV_H */

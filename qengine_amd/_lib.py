@@ -1,0 +1,79 @@
+"""ctypes binding of libqkv.so (the C ABI declared in include/qkv.h).
+
+The library is built in-tree (qengine_amd/libqkv.so) by __graft_entry__.build().
+There is no fallback: if the library is missing or fails to load, every call
+raises QKVError.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import re
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "libqkv.so")
+HEADER_PATH = os.path.join(os.path.dirname(_HERE), "include", "qkv.h")
+
+QKV_OK = 0
+STATUS_NAMES = {
+    0: "QKV_OK", -1: "QKV_ERR_INVALID", -2: "QKV_ERR_NULL", -3: "QKV_ERR_UNSUPPORTED",
+    -4: "QKV_ERR_ALIGN", -5: "QKV_ERR_DEVICE", -6: "QKV_ERR_LAUNCH", -7: "QKV_ERR_WORKSPACE",
+}
+
+
+class QKVError(RuntimeError):
+    def __init__(self, status: int, where: str = ""):
+        self.status = status
+        super().__init__(f"{where}: {STATUS_NAMES.get(status, status)} ({status})")
+
+
+_P = ctypes.c_void_p
+_I = ctypes.c_int
+_F = ctypes.c_float
+_SZ = ctypes.c_size_t
+
+# name -> (restype, argtypes); must cover every function declared in include/qkv.h
+SIGNATURES = {
+    "qkv_version": (_I, []),
+    "qkv_status_string": (ctypes.c_char_p, [_I]),
+    "qkv_tq3_init": (_I, [_I]),
+    "qkv_tq3_append": (_I, [_P, _P, _I, _P]),
+    "qkv_tq3_append_kv": (_I, [_P, _P, _P, _P, _I, _P]),
+    "qkv_tq3_dequant": (_I, [_P, _P, _I, _P]),
+    "qkv_q8_append": (_I, [_P, _P, _I, _P]),
+    "qkv_q8_dequant": (_I, [_P, _P, _I, _P]),
+    "qkv_attn_split_tq3": (_I, [_P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _F, _I, _I,
+                               _I, _P, _P]),
+    "qkv_attn_split_merge": (_I, [_P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _P]),
+    "qkv_decode_attn_tq3_workspace_bytes": (_SZ, [_I, _I, _I, _I]),
+    "qkv_decode_attn_tq3": (_I, [_P, _P, _P, _P, _I, _I, _I, _I, _I, _F, _I, _I, _P, _P, _SZ,
+                                _P]),
+}
+
+_lib = None
+
+
+def header_functions() -> list[str]:
+    """Names of the functions declared in include/qkv.h."""
+    text = open(HEADER_PATH).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(qkv_[a-z0-9_]+)\s*\(", text)))
+
+
+def lib() -> ctypes.CDLL:
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise QKVError(-5, f"{LIB_PATH} is not built (run __graft_entry__.build())")
+        L = ctypes.CDLL(LIB_PATH)
+        for name, (res, args) in SIGNATURES.items():
+            fn = getattr(L, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = L
+    return _lib
+
+
+def check(status: int, where: str) -> None:
+    if status != QKV_OK:
+        raise QKVError(status, where)

@@ -1,0 +1,99 @@
+// attn_common.h -- argument block and wave-level helpers shared by the
+// attention kernels (gfx950, wave64).
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace qkv {
+
+constexpr float kLn2 = 0.69314718055994531f;
+constexpr float kLog2e = 1.44269504088896341f;
+
+struct AttnArgs {
+  const uint16_t* q;        // [sub_n][num_q][256] fp16
+  const uint32_t* k;        // slot-base key cache (blocks viewed as dwords)
+  const uint32_t* v;        // slot-base value cache
+  uint32_t kv_bytes;        // readable bytes of each cache from its base (buffer range)
+  int num_q, num_kv;
+  int start_pos, sub_n, sub_n_max;
+  int active_end_max;       // reference split sizing (split API)
+  int k_splits;             // reference split count (split API)
+  int n_chunks;             // workgroups per (kv head, query): k_splits or key chunks
+  int chunk_keys;           // keys per fast-path chunk (multiple of 256)
+  int n_slots;              // fast-path records per (q head, query): n_chunks
+  float scale_log2;         // softmax scale * log2(e)
+  int sink_tok, window_tok;
+  const uint32_t* tree_mask;
+  // split API partials (reference layout)
+  float* part_m;
+  float* part_l;
+  float* part_o;
+  // fast-path workspace
+  float* ws_ml;             // [num_q][sub_n][n_slots][2] (m in log2 units, l)
+  float* ws_o;              // [num_q][sub_n][n_slots][256] rotated coordinates
+  int* tickets;             // [2]: records written, mergers finished (zero between calls)
+};
+
+// ---- DPP wave reductions (result broadcast through lane 63) -------------
+template <int CTRL, int ROW_MASK = 0xf>
+__device__ __forceinline__ float dpp_f(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(__builtin_bit_cast(int, v),
+                                                               __builtin_bit_cast(int, v), CTRL,
+                                                               ROW_MASK, 0xf, false));
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+  v = fmaxf(v, dpp_f<0xB1>(v));         // quad_perm [1,0,3,2]
+  v = fmaxf(v, dpp_f<0x4E>(v));         // quad_perm [2,3,0,1]
+  v = fmaxf(v, dpp_f<0x124>(v));        // row_ror:4
+  v = fmaxf(v, dpp_f<0x128>(v));        // row_ror:8
+  v = fmaxf(v, dpp_f<0x142, 0xa>(v));   // row_bcast:15
+  v = fmaxf(v, dpp_f<0x143, 0xc>(v));   // row_bcast:31
+  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
+}
+
+__device__ __forceinline__ float wave_sum(float v) {
+  v += dpp_f<0xB1>(v);
+  v += dpp_f<0x4E>(v);
+  v += dpp_f<0x124>(v);
+  v += dpp_f<0x128>(v);
+  v += dpp_f<0x142, 0xa>(v);
+  v += dpp_f<0x143, 0xc>(v);
+  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
+}
+
+// ---- 128-point Walsh-Hadamard pieces (butterflies (a,b) -> (a+b, a-b)) ----
+// Element e = part*8 + i of a 128-block lives in register i of lane `part`
+// (16 consecutive lanes per block).
+__device__ __forceinline__ void wht8_inreg(float (&x)[8]) {
+#pragma unroll
+  for (int step = 1; step < 8; step <<= 1)
+#pragma unroll
+    for (int i = 0; i < 8; i += 2 * step)
+#pragma unroll
+      for (int j = i; j < i + step; j++) {
+        const float a = x[j], b = x[j + step];
+        x[j] = a + b;
+        x[j + step] = a - b;
+      }
+}
+
+__device__ __forceinline__ void wht_xor_lanes16(float (&x)[8], int lane) {
+#pragma unroll
+  for (int m = 1; m < 16; m <<= 1) {
+    const bool upper = (lane & m) != 0;
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+      const float o = __shfl_xor(x[i], m);
+      x[i] = upper ? (o - x[i]) : (x[i] + o);
+    }
+  }
+}
+
+hipError_t launch_tq3_attn(const AttnArgs& a, int mode, uint16_t* out, hipStream_t stream);
+hipError_t launch_split_merge(const float* m, const float* l, const float* o, uint16_t* out,
+                              int num_q, int sub_n, int sub_n_max, int k_splits,
+                              hipStream_t stream);
+size_t tq3_attn_lds_bytes();
+
+}  // namespace qkv

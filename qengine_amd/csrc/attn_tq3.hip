@@ -1,0 +1,716 @@
+// attn_tq3.hip -- split-K flash decode over the packed TQ3 cache (gfx950).
+//
+// Reference semantics: flash_attn_chunk_fused_split_tq3 (attention.cuh:1905-2177)
+// and flash_attn_split_merge (attention.cuh:1837-1891).
+//
+// Design (not the reference's): attention runs in the rotated domain.  With
+// R = rs*H*D (orthogonal, D = signs, H = Sylvester Hadamard), a stored block
+// decodes to k = norm * R^T c[idx], so q.k = norm * (R q).c[idx]: the query is
+// rotated once per workgroup and keys are never inverse-transformed.  Values
+// accumulate sum_t p_t norm_t c[idx_t] in rotated coordinates and each output
+// row is rotated back once.
+//
+// Workgroup: 4 waves on one kv head; each wave takes 64-key tiles.  Per tile:
+//   scores  v_mfma_f32_16x16x32_f16, A = rotated query (rows = heads, held in
+//           32 VGPRs for the whole kernel), B = codes of 16 keys x 32 dims:
+//           lane (key, octet o) reads the 12 aligned bytes holding code groups
+//           4o..4o+3 of each 128-block and decodes centroid pairs through a
+//           64-entry LDS table.  One accumulator per 128-block, each scaled by
+//           its block norm.
+//   softmax online, per 16-lane row of the D layout (rows = heads), base 2.
+//   values  v_mfma_f32_16x16x32_f16, A = p*norm (fp16, LDS, rows = heads),
+//           B = codes of 32 keys x 16 dims.  The wave's value rows are loaded
+//           with aligned 16-byte loads (lane = key) and staged in LDS; lane
+//           (n, o) gathers dim group n of both blocks for 8 keys and pairs keys
+//           with v_perm.
+// Merging: the 4 waves merge in LDS.  Fast path: every workgroup writes one
+// record per q head {m, l, o[256]} (rotated) and counts itself in; the last
+// workgroups of the grid are designated mergers, one per (q head, query,
+// 128-block) unit: each waits for the full count (bounded poll), reads all of
+// its unit's records in one round of 16-byte loads, merges, rotates back and
+// stores fp16.  Only mergers wait, so progress does not depend on workgroup
+// co-residency.  Split API: one workgroup per reference split, written in the
+// reference partial layout.
+#include "qkv_device.h"
+#include "attn_common.h"
+
+namespace qkv {
+
+typedef _Float16 h8_t __attribute__((ext_vector_type(8)));
+typedef float f4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t u4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t u3_t __attribute__((ext_vector_type(3)));
+typedef uint32_t u2_t __attribute__((ext_vector_type(2)));
+
+// word 3 of a raw buffer resource on gfx9-family GPUs (32-bit data format)
+constexpr int kBufferRsrcWord3 = 0x00020000;
+
+constexpr int kTile = 64;
+constexpr int kWaves = 4;
+constexpr int kThreads = 64 * kWaves;
+constexpr int kHD = 256;
+constexpr int kRowDw = 26;        // one kv head of one key: 2 blocks x 13 dwords
+constexpr int kVPitchDw = 28;     // LDS pitch of a staged value row (conflict-free b128 writes)
+
+// LDS layout (bytes).  The merge area aliases the tile buffers (used after the loop).
+constexpr int kLdsLut = 0;                                   // 64 x u32 centroid pairs
+constexpr int kLdsW = 256;                                   // per wave [2][16][64] fp16
+constexpr int kLdsWBytes = 2 * 16 * kTile * 2;               // 4096
+constexpr int kLdsV = kLdsW + kWaves * kLdsWBytes;           // per wave [64][28] dwords
+constexpr int kLdsVBytes = kTile * kVPitchDw * 4;            // 7168
+constexpr int kLdsTileEnd = kLdsV + kWaves * kLdsVBytes;     // 45056
+constexpr int kLdsMergeO = kLdsW;                            // [4 waves][8 rows][256] f32
+constexpr int kLdsMergeML = kLdsMergeO + kWaves * 8 * kHD * 4;
+constexpr int kLdsFlag = kLdsMergeML + 256 * 4;
+constexpr int kLdsTotal = (kLdsFlag + 16 > kLdsTileEnd ? kLdsFlag + 16 : kLdsTileEnd);
+static_assert(kLdsV + 16 * 128 * 4 <= kLdsTileEnd, "query scratch must fit the value area");
+
+// merge-area float offsets (ML): m[w][8] 0, l[w][8] 32, M[8] 64, L[8] 72,
+// rescale[8] 80, weights[8][16] 96
+constexpr int kMlM = 64, kMlL = 72, kMlC = 80, kMlW = 96;
+
+__device__ __forceinline__ uint32_t lut_read(const uint8_t* lds, uint32_t addr) {
+  return *reinterpret_cast<const uint32_t*>(lds + addr);
+}
+
+// Centroid-pair table address of the 6-bit field at bit BIT of a 3-dword
+// code stream (the field lands at bits 2..7: byte offset of a 4-byte entry).
+template <int BIT>
+__device__ __forceinline__ uint32_t pair_addr3(const uint32_t (&q)[3]) {
+  if constexpr (BIT == 0) {
+    return (q[0] << 2) & 0xFCu;
+  } else {
+    constexpr int b = BIT - 2;
+    constexpr int w = b >> 5, sh = b & 31;
+    if constexpr (sh + 8 <= 32) {
+      return (q[w] >> sh) & 0xFCu;
+    } else {
+      return __builtin_amdgcn_alignbit(q[w + 1], q[w], sh) & 0xFCu;
+    }
+  }
+}
+
+// B operand for code group U (8 codes, bits 24U..24U+23) of a 3-dword stream.
+template <int U>
+__device__ __forceinline__ h8_t group_operand(const uint8_t* lds, const uint32_t (&q)[3]) {
+  u4_t v;
+  v[0] = lut_read(lds, kLdsLut + pair_addr3<24 * U + 0>(q));
+  v[1] = lut_read(lds, kLdsLut + pair_addr3<24 * U + 6>(q));
+  v[2] = lut_read(lds, kLdsLut + pair_addr3<24 * U + 12>(q));
+  v[3] = lut_read(lds, kLdsLut + pair_addr3<24 * U + 18>(q));
+  return __builtin_bit_cast(h8_t, v);
+}
+
+// Score MFMAs for one 16-key group: 4 slices per block, one accumulator per
+// block.  Slice U+1's table reads are issued before slice U's MFMAs.
+template <int U>
+__device__ __forceinline__ void score_group(const uint8_t* lds, const uint32_t (&k0)[3],
+                                            const uint32_t (&k1)[3], const h8_t (&qa)[8],
+                                            const h8_t& b0, const h8_t& b1, f4_t& a0, f4_t& a1) {
+  if constexpr (U < 4) {
+    h8_t n0, n1;
+    if constexpr (U < 3) {
+      n0 = group_operand<U + 1>(lds, k0);
+      n1 = group_operand<U + 1>(lds, k1);
+    }
+    a0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(qa[U], b0, a0, 0, 0, 0);
+    a1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(qa[4 + U], b1, a1, 0, 0, 0);
+    __builtin_amdgcn_sched_barrier(0);
+    if constexpr (U < 3) score_group<U + 1>(lds, k0, k1, qa, n0, n1, a0, a1);
+  }
+}
+
+// Values for one (32-key chunk, 128-block): centroid pair PP of the lane's
+// dim group gives tiles t0+2PP (low dim) and t0+2PP+1 (high dim).
+template <int PP>
+__device__ __forceinline__ void value_pipe(const uint8_t* lds, const uint32_t (&x)[8],
+                                           const h8_t& a, f4_t (&acc)[16], int t0) {
+  if constexpr (PP < 4) {
+    uint32_t cp[8];
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+      const uint32_t xi = x[i];
+      const uint32_t addr = (PP == 0) ? ((xi << 2) & 0xFCu) : ((xi >> (6 * PP - 2)) & 0xFCu);
+      cp[i] = lut_read(lds, kLdsLut + addr);
+    }
+#pragma unroll
+    for (int e = 0; e < 2; e++) {
+      u4_t bv;
+#pragma unroll
+      for (int k2 = 0; k2 < 4; k2++)
+        bv[k2] = __builtin_amdgcn_perm(cp[2 * k2 + 1], cp[2 * k2], e ? 0x07060302u : 0x05040100u);
+      const int tile = t0 + 2 * PP + e;
+      acc[tile] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, __builtin_bit_cast(h8_t, bv),
+                                                         acc[tile], 0, 0, 0);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    value_pipe<PP + 1>(lds, x, a, acc, t0);
+  }
+}
+
+// Registers of one 64-key tile.  Buffer loads: offsets are 32-bit and reads
+// past the cache extent (num_records) return zero, so partial tiles need no
+// branches; keys in [hi, extent) are read and masked out of the softmax.
+struct TileRegs {
+  u4_t vr[6];            // value row of key ts+lane (dwords 0..23)
+  u2_t vr6;              // dwords 24..25
+  uint32_t kq[4][2][3];  // key code groups 4*row..4*row+3, group g, block j
+  float kn[4][2];        // key block norms, group g, block j
+};
+
+__device__ __forceinline__ void load_tile(__amdgpu_buffer_rsrc_t rk, __amdgpu_buffer_rsrc_t rv,
+                                          int ts, int nkv, int h, int lane, int row, int col,
+                                          TileRegs& tr) {
+  const uint32_t vrow = (uint32_t)((ts + lane) * nkv + h) * 104u;
+#pragma unroll
+  for (int i = 0; i < 6; i++) tr.vr[i] = __builtin_amdgcn_raw_buffer_load_b128(rv, vrow + 16 * i, 0, 0);
+  tr.vr6 = __builtin_amdgcn_raw_buffer_load_b64(rv, vrow + 96, 0, 0);
+#pragma unroll
+  for (int g = 0; g < 4; g++) {
+    const uint32_t krow = (uint32_t)((ts + 16 * g + col) * nkv + h) * 104u;
+#pragma unroll
+    for (int j = 0; j < 2; j++) {
+      const u3_t c = __builtin_amdgcn_raw_buffer_load_b96(rk, krow + 52 * j + 4 + 12 * row, 0, 0);
+      tr.kq[g][j][0] = c[0];
+      tr.kq[g][j][1] = c[1];
+      tr.kq[g][j][2] = c[2];
+      tr.kn[g][j] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rk, krow + 52 * j, 0, 0));
+    }
+  }
+}
+
+struct KeyRule {
+  int start_pos, t_idx, sink, window;
+  const uint32_t* tree;
+  __device__ __forceinline__ bool visible(int key, int active_end) const {
+    if (sink > 0 || window > 0) {
+      const int ts = key & ~31;
+      const int te = min(ts + 32, active_end);
+      if (!(ts < sink) && !(te > active_end - window)) return false;
+    }
+    if (tree && key >= start_pos) return (tree[t_idx] >> (key - start_pos)) & 1u;
+    return true;
+  }
+};
+
+// max / sum inside each 16-lane row (all lanes of the row receive the result)
+__device__ __forceinline__ float row16_max(float v) {
+  v = fmaxf(v, dpp_f<0xB1>(v));
+  v = fmaxf(v, dpp_f<0x4E>(v));
+  v = fmaxf(v, dpp_f<0x124>(v));
+  v = fmaxf(v, dpp_f<0x128>(v));
+  return v;
+}
+__device__ __forceinline__ float row16_sum(float v) {
+  v += dpp_f<0xB1>(v);
+  v += dpp_f<0x4E>(v);
+  v += dpp_f<0x124>(v);
+  v += dpp_f<0x128>(v);
+  return v;
+}
+
+// Records move between workgroups (possibly on different XCDs, whose L2s are
+// not coherent with each other).  Writers store them with agent-scope atomic
+// stores, which gfx950 performs at the device coherence point (sc1), and wait
+// for completion (s_waitcnt vmcnt(0)) before counting themselves in; a merger
+// observes the full count, invalidates its caches once (agent-scope acquire)
+// and then reads the records with ordinary 16-byte loads.  Only the few merging
+// workgroups pay a cache invalidation, instead of an L2 write-back and
+// invalidate in every workgroup.
+__device__ __forceinline__ void coherent_store(float* p, float v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ int coherent_load_int(int* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Record index of (q head, query t, chunk) in the fast-path workspace.
+__device__ __forceinline__ long rec_index(const AttnArgs& p, int qh, int t, int chunk) {
+  return (long)(qh * p.sub_n + t) * p.n_slots + chunk;
+}
+
+// Spin limit of a merger waiting for the records of one launch (each poll
+// sleeps ~64 cycles; the limit is seconds, far beyond any legitimate wait).
+constexpr int kMergeSpinLimit = 1 << 24;
+
+// Merge all chunk records of one unit (q head qh, query t, 128-block blk) and
+// write its fp16 output: o = rs*D*H*(sum_c w_c o_c / sum_c w_c l_c).
+// Thread = (record slice sl = tid/32 of 8, dim quad dq = tid%32): records
+// sl, sl+8, ...; one round of 16-byte loads.
+__device__ void merge_unit(uint8_t* lds, const AttnArgs& p, int qh, int t, int blk,
+                           uint16_t* out) {
+  float* red = reinterpret_cast<float*>(lds + kLdsMergeO);   // [8 slices][128] + scalars
+  const int tid = threadIdx.x;
+  const int sl = tid >> 5, dq = tid & 31;
+  const int n = p.n_chunks;
+  const long base = rec_index(p, qh, t, 0);
+  constexpr int kMaxPer = 16;                                 // records per thread per pass
+  float M = -INFINITY;
+  // pass 1: global max of m over all records
+  for (int c = tid; c < n; c += kThreads) {
+    const float m = p.ws_ml[2 * (base + c)];
+    const float l = p.ws_ml[2 * (base + c) + 1];
+    if (l > 0.f) M = fmaxf(M, m);
+  }
+  M = fmaxf(M, __shfl_xor(M, 1));
+  M = fmaxf(M, __shfl_xor(M, 2));
+  M = fmaxf(M, __shfl_xor(M, 4));
+  M = fmaxf(M, __shfl_xor(M, 8));
+  M = fmaxf(M, __shfl_xor(M, 16));
+  M = fmaxf(M, __shfl_xor(M, 32));
+  if ((tid & 63) == 0) red[1024 + (tid >> 6)] = M;
+  __syncthreads();
+  M = fmaxf(fmaxf(red[1024], red[1025]), fmaxf(red[1026], red[1027]));
+  // pass 2: weighted sums (records sl, sl+8, ...), 16 loads in flight per batch
+  float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+  float L = 0.f;
+  for (int c0 = sl; c0 < n; c0 += 8 * kMaxPer) {
+    float4 v[kMaxPer];
+    float w[kMaxPer];
+#pragma unroll
+    for (int i = 0; i < kMaxPer; i++) {
+      const int c = c0 + 8 * i;
+      if (c < n) {
+        const float m = p.ws_ml[2 * (base + c)];
+        const float l = p.ws_ml[2 * (base + c) + 1];
+        w[i] = (l > 0.f) ? __builtin_amdgcn_exp2f(m - M) : 0.f;
+        L += (dq == 0) ? w[i] * l : 0.f;
+        v[i] = *reinterpret_cast<const float4*>(&p.ws_o[(base + c) * kHD + blk * 128 + 4 * dq]);
+      } else {
+        w[i] = 0.f;
+        v[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < kMaxPer; i++) {
+      acc.x += w[i] * v[i].x; acc.y += w[i] * v[i].y; acc.z += w[i] * v[i].z; acc.w += w[i] * v[i].w;
+    }
+  }
+  *reinterpret_cast<float4*>(&red[sl * 128 + 4 * dq]) = acc;
+  if (dq == 0) red[1032 + sl] = L;
+  __syncthreads();
+  // rotate back: 16 lanes x 8 elements (threads 0..15)
+  if (tid < 16) {
+    float Lt = 0.f;
+#pragma unroll
+    for (int i = 0; i < 8; i++) Lt += red[1032 + i];
+    const float inv = Lt > 0.f ? 1.0f / Lt : 0.f;
+    float x[8];
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+      float sum = 0.f;
+#pragma unroll
+      for (int k = 0; k < 8; k++) sum += red[k * 128 + tid * 8 + i];
+      x[i] = sum * inv;
+    }
+    wht8_inreg(x);
+    wht_xor_lanes16(x, tid);
+    const float rs = wht_scale();
+    uint32_t pk[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      float y[2];
+#pragma unroll
+      for (int e2 = 0; e2 < 2; e2++) {
+        const int e = tid * 8 + 2 * i + e2;
+        const bool pos = (kSignMask[e >> 5] >> (e & 31)) & 1u;
+        const float v = x[2 * i + e2] * rs;
+        y[e2] = pos ? v : -v;
+      }
+      pk[i] = f2h(y[0]) | (f2h(y[1]) << 16);
+    }
+    *reinterpret_cast<uint4*>(out + ((long)t * p.num_q + qh) * kHD + blk * 128 + tid * 8) =
+        make_uint4(pk[0], pk[1], pk[2], pk[3]);
+  }
+  __syncthreads();
+}
+
+// Store the merged rows in LDS as this workgroup's records (rotated).
+__device__ void store_record(const uint8_t* lds, const AttnArgs& p, int h, int t, int rows,
+                             int chunk) {
+  const float* mo = reinterpret_cast<const float*>(lds + kLdsMergeO);
+  const float* ml = reinterpret_cast<const float*>(lds + kLdsMergeML);
+  const int gqa = p.num_q / p.num_kv;
+  for (int idx = threadIdx.x; idx < rows * 64; idx += kThreads) {
+    const int r = idx >> 6, d4 = (idx & 63) * 4;
+    const long rec = rec_index(p, h * gqa + r, t, chunk);
+#pragma unroll
+    for (int i = 0; i < 4; i++) coherent_store(&p.ws_o[rec * kHD + d4 + i], mo[r * kHD + d4 + i]);
+    if (d4 == 0) {
+      coherent_store(&p.ws_ml[2 * rec], ml[kMlM + r]);
+      coherent_store(&p.ws_ml[2 * rec + 1], ml[kMlL + r]);
+    }
+  }
+}
+
+// Rotate the merged rows back (o = rs*D*H*o_rot per 128-block).  final: divide
+// by L and store fp16 rows [t][q_head][256]; otherwise store the unnormalised
+// f32 partial of reference split `split` (m in natural-log units).
+__device__ void finish_rows(const uint8_t* lds, const AttnArgs& p, int h, int t, int rows,
+                            bool final, int split, uint16_t* out) {
+  const float* mo = reinterpret_cast<const float*>(lds + kLdsMergeO);
+  const float* ml = reinterpret_cast<const float*>(lds + kLdsMergeML);
+  const int gqa = p.num_q / p.num_kv;
+  const int lane = threadIdx.x & 63;
+  for (int w0 = 0; w0 < rows * 2; w0 += kThreads / 16) {
+    const int wht = w0 + (threadIdx.x >> 4);
+    const int part = threadIdx.x & 15;
+    const int r = wht >> 1, blk = wht & 1;
+    const bool live = wht < rows * 2;
+    const float L = live ? ml[kMlL + r] : 0.f;
+    const float scale = final ? (L > 0.f ? 1.0f / L : 0.f) : 1.0f;
+    float x[8];
+#pragma unroll
+    for (int i = 0; i < 8; i++) x[i] = live ? mo[r * kHD + blk * 128 + part * 8 + i] * scale : 0.f;
+    wht8_inreg(x);
+    wht_xor_lanes16(x, lane);
+    if (!live) continue;
+    const float rs = wht_scale();
+    const int qh = h * gqa + r;
+    float y[8];
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+      const int e = part * 8 + i;
+      const bool pos = (kSignMask[e >> 5] >> (e & 31)) & 1u;
+      const float v = x[i] * rs;
+      y[i] = pos ? v : -v;
+    }
+    if (final) {
+      uint32_t pk[4];
+#pragma unroll
+      for (int i = 0; i < 4; i++) pk[i] = f2h(y[2 * i]) | (f2h(y[2 * i + 1]) << 16);
+      *reinterpret_cast<uint4*>(out + ((long)t * p.num_q + qh) * kHD + blk * 128 + part * 8) =
+          make_uint4(pk[0], pk[1], pk[2], pk[3]);
+    } else {
+      const long mlx = ((long)qh * p.sub_n_max + t) * p.k_splits + split;
+#pragma unroll
+      for (int i = 0; i < 8; i++) p.part_o[mlx * kHD + blk * 128 + part * 8 + i] = y[i];
+      if (blk == 0 && part == 0) {
+        const float M = ml[kMlM + r];
+        p.part_m[mlx] = (M == -INFINITY) ? -INFINITY : M * kLn2;
+        p.part_l[mlx] = ml[kMlL + r];
+      }
+    }
+  }
+}
+
+// MODE 0: fast path (final fp16 rows).  MODE 1: reference split partials.
+template <int MODE>
+__global__ __launch_bounds__(kThreads, 2) void tq3_attn_kernel(AttnArgs p, uint16_t* out) {
+  // static LDS: table and tile offsets fold into the instructions' offset field
+  __shared__ __attribute__((aligned(16))) uint8_t lds[kLdsTotal];
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int gqa = p.num_q / p.num_kv;
+
+  // ---- work id (XCD-aware: the num_kv workgroups of one (t, chunk) share an XCD)
+  int h, t_idx, chunk;
+  bool has_work;
+  {
+    const int L = blockIdx.x;
+    const int xcd = L & 7, r = L >> 3;
+    h = r % p.num_kv;
+    const int g = (r / p.num_kv) * 8 + xcd;
+    has_work = g < p.sub_n * p.n_chunks;
+    t_idx = has_work ? g / p.n_chunks : 0;
+    chunk = has_work ? g - t_idx * p.n_chunks : 0;
+  }
+  if (MODE == 1 && !has_work) return;
+  const int active_end = p.start_pos + t_idx + 1;
+  int lo = 0, hi = 0;
+  if (MODE == 0) {
+    if (has_work) {
+      lo = chunk * p.chunk_keys;
+      hi = min(lo + p.chunk_keys, active_end);
+    }
+  } else {
+    // reference split range (attention.cuh:1944-1951)
+    const int total_tiles = (p.active_end_max + 31) / 32;
+    const int tps = (total_tiles + p.k_splits - 1) / p.k_splits;
+    lo = chunk * tps * 32;
+    hi = min((chunk + 1) * tps * 32, active_end);
+  }
+  const KeyRule rule{p.start_pos, t_idx, p.sink_tok, p.window_tok, p.tree_mask};
+  const int row = lane >> 4;        // 16-lane row of the MFMA D layout
+  const int col = lane & 15;
+
+  // ---- first tile's loads go out before the setup work ----------------------
+  const __amdgpu_buffer_rsrc_t rk =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<uint32_t*>(p.k), 0, p.kv_bytes, kBufferRsrcWord3);
+  const __amdgpu_buffer_rsrc_t rv =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<uint32_t*>(p.v), 0, p.kv_bytes, kBufferRsrcWord3);
+  TileRegs tr;
+  if (lo + wave * kTile < hi) load_tile(rk, rv, lo + wave * kTile, p.num_kv, h, lane, row, col, tr);
+
+  // ---- setup: centroid-pair table; rotated query ---------------------------
+  if (threadIdx.x < 64) {
+    const uint32_t e = threadIdx.x;
+    *reinterpret_cast<uint32_t*>(lds + kLdsLut + 4 * e) =
+        f2h(kCentroids[e & 7]) | (f2h(kCentroids[e >> 3]) << 16);
+  }
+  {
+    // 16 WHTs of 128 (8 heads x 2 blocks), 16 lanes each; fp16 result in LDS
+    // scratch laid out [head][block][group u][octet o][8] so each lane's A
+    // operand slice is one 16-byte read.
+    uint16_t* qs = reinterpret_cast<uint16_t*>(lds + kLdsV);
+    const int wht = threadIdx.x >> 4;
+    const int part = threadIdx.x & 15;
+    const int hh = wht >> 1, blk = wht & 1;
+    if (hh < gqa) {
+      float x[8];
+      const uint16_t* qsrc =
+          p.q + ((long)t_idx * p.num_q + h * gqa + hh) * kHD + blk * 128 + part * 8;
+      const uint4 raw = *reinterpret_cast<const uint4*>(qsrc);
+      const uint32_t wv[4] = {raw.x, raw.y, raw.z, raw.w};
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        x[2 * i] = h2f(wv[i] & 0xffffu);
+        x[2 * i + 1] = h2f(wv[i] >> 16);
+      }
+#pragma unroll
+      for (int i = 0; i < 8; i++) {
+        const int e = part * 8 + i;
+        const bool pos = (kSignMask[e >> 5] >> (e & 31)) & 1u;
+        x[i] = pos ? x[i] : -x[i];
+      }
+      wht8_inreg(x);
+      wht_xor_lanes16(x, lane);
+      const float rs = wht_scale();
+      uint32_t pk[4];
+#pragma unroll
+      for (int i = 0; i < 4; i++) pk[i] = f2h(x[2 * i] * rs) | (f2h(x[2 * i + 1] * rs) << 16);
+      // elements part*8..+7 = dims of code group `part` = 4*o + u
+      const int o = part >> 2, u = part & 3;
+      *reinterpret_cast<uint4*>(qs + (((hh * 2 + blk) * 4 + u) * 4 + o) * 8) =
+          make_uint4(pk[0], pk[1], pk[2], pk[3]);
+    }
+  }
+  __syncthreads();
+  // qa[s], slice s = 4j+u: A row = head `col`, element i = dim 128j + 8(4*row+u) + i
+  h8_t qa[8];
+  {
+    const uint16_t* qs = reinterpret_cast<const uint16_t*>(lds + kLdsV);
+#pragma unroll
+    for (int s = 0; s < 8; s++) {
+      const int j = s >> 2, u = s & 3;
+      if (col < gqa)
+        qa[s] = *reinterpret_cast<const h8_t*>(qs + (((col * 2 + j) * 4 + u) * 4 + row) * 8);
+      else
+        qa[s] = h8_t{0, 0, 0, 0, 0, 0, 0, 0};
+    }
+  }
+  {
+    uint8_t* wb = lds + kLdsW + wave * kLdsWBytes;    // W rows >= gqa stay zero
+    for (int i = lane; i < kLdsWBytes / 16; i += 64)
+      *reinterpret_cast<uint4*>(wb + 16 * i) = make_uint4(0, 0, 0, 0);
+  }
+  __syncthreads();
+
+  const float scale2 = p.scale_log2;
+  float m2[4], lsum[4];
+#pragma unroll
+  for (int r = 0; r < 4; r++) {
+    m2[r] = -INFINITY;
+    lsum[r] = 0.0f;
+  }
+  f4_t acc[16];
+#pragma unroll
+  for (int t = 0; t < 16; t++) acc[t] = f4_t{0.f, 0.f, 0.f, 0.f};
+
+  const int nkv = p.num_kv;
+  uint8_t* wl = lds + kLdsW + wave * kLdsWBytes;
+  uint32_t* vl = reinterpret_cast<uint32_t*>(lds + kLdsV + wave * kLdsVBytes);
+  const int v_dw = 1 + ((3 * col) >> 2), v_sh = (3 * col) & 3;   // value-side group col
+
+  for (int ts = lo + wave * kTile; ts < hi; ts += kWaves * kTile) {
+    if (ts != lo + wave * kTile) load_tile(rk, rv, ts, nkv, h, lane, row, col, tr);
+#pragma unroll
+    for (int i = 0; i < 6; i++) *reinterpret_cast<u4_t*>(vl + lane * kVPitchDw + 4 * i) = tr.vr[i];
+    *reinterpret_cast<u2_t*>(vl + lane * kVPitchDw + 24) = tr.vr6;
+    auto& kq = tr.kq;
+    auto& kn = tr.kn;
+
+    // ---------------- scores ----------------
+    // D layout: lane (row, col) holds key 16g+col, heads 4*row + r
+    float s[4][4];
+#pragma unroll
+    for (int g = 0; g < 4; g++) {
+      f4_t a0 = {0.f, 0.f, 0.f, 0.f}, a1 = {0.f, 0.f, 0.f, 0.f};
+      score_group<0>(lds, kq[g][0], kq[g][1], qa, group_operand<0>(lds, kq[g][0]),
+                     group_operand<0>(lds, kq[g][1]), a0, a1);
+      const int key = ts + 16 * g + col;
+      const bool vis = key < hi && rule.visible(key, active_end);   // masks padded keys too
+#pragma unroll
+      for (int r = 0; r < 4; r++)
+        s[g][r] = vis ? (kn[g][0] * a0[r] + kn[g][1] * a1[r]) * scale2 : -INFINITY;
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+
+    // ---------------- online softmax (per 16-lane row = 4 heads) ----------------
+    // value-block norms of keys 16g+col from the staged rows (dwords 0 and 13)
+    float vn0[4], vn1[4];
+#pragma unroll
+    for (int g = 0; g < 4; g++) {
+      vn0[g] = __uint_as_float(vl[(16 * g + col) * kVPitchDw]);
+      vn1[g] = __uint_as_float(vl[(16 * g + col) * kVPitchDw + 13]);
+    }
+    // W rows >= gqa receive weights of all-zero query rows; they only feed
+    // accumulator rows that are never written out.
+    float corr[4];
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+      float mt = fmaxf(fmaxf(s[0][r], s[1][r]), fmaxf(s[2][r], s[3][r]));
+      mt = row16_max(mt);
+      const float mn = fmaxf(m2[r], mt);
+      corr[r] = (mn == -INFINITY) ? 1.0f : __builtin_amdgcn_exp2f(m2[r] - mn);
+      float ps = 0.f;
+      const int head = 4 * row + r;
+#pragma unroll
+      for (int g = 0; g < 4; g++) {
+        const float pr = (s[g][r] == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(s[g][r] - mn);
+        ps += pr;
+        *reinterpret_cast<uint16_t*>(wl + ((0 * 16 + head) * kTile + 16 * g + col) * 2) =
+            (uint16_t)f2h(pr * vn0[g]);
+        *reinterpret_cast<uint16_t*>(wl + ((1 * 16 + head) * kTile + 16 * g + col) * 2) =
+            (uint16_t)f2h(pr * vn1[g]);
+      }
+      lsum[r] = lsum[r] * corr[r] + row16_sum(ps);
+      m2[r] = mn;
+    }
+#pragma unroll
+    for (int t = 0; t < 16; t++)
+#pragma unroll
+      for (int r = 0; r < 4; r++) acc[t][r] *= corr[r];
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+
+    // ---------------- values ----------------
+    // lane (row = key octet, col = dim group): keys 32*c2 + 8*row + i
+#pragma unroll
+    for (int c2 = 0; c2 < 2; c2++) {
+#pragma unroll
+      for (int j = 0; j < 2; j++) {
+        uint32_t x[8];
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+          const uint32_t* rw = vl + (32 * c2 + 8 * row + i) * kVPitchDw + 13 * j + v_dw;
+          x[i] = __builtin_amdgcn_alignbyte(rw[1], rw[0], v_sh);
+        }
+        const h8_t a = *reinterpret_cast<const h8_t*>(
+            wl + ((j * 16 + col) * kTile + 32 * c2 + 8 * row) * 2);
+        value_pipe<0>(lds, x, a, acc, 8 * j);
+      }
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  }
+
+  // ---------------- merge the 4 waves in LDS ----------------
+  __syncthreads();
+  float* mo = reinterpret_cast<float*>(lds + kLdsMergeO);    // [wave][8][256]
+  float* ml = reinterpret_cast<float*>(lds + kLdsMergeML);
+  if (row < 2) {
+    // acc tile t: rows 4*row+r, dim 128*(t>>3) + 8*col + (t&7)
+#pragma unroll
+    for (int t = 0; t < 16; t++)
+#pragma unroll
+      for (int r = 0; r < 4; r++)
+        mo[(wave * 8 + 4 * row + r) * kHD + 128 * (t >> 3) + 8 * col + (t & 7)] = acc[t][r];
+    if (col == 0) {
+#pragma unroll
+      for (int r = 0; r < 4; r++) {
+        ml[wave * 8 + 4 * row + r] = m2[r];
+        ml[32 + wave * 8 + 4 * row + r] = lsum[r];
+      }
+    }
+  }
+  __syncthreads();
+  const int rows = min(gqa, 8);
+  for (int idx = threadIdx.x; idx < rows * 64; idx += kThreads) {
+    const int r = idx >> 6, d4 = (idx & 63) * 4;
+    float M = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < kWaves; w++) M = fmaxf(M, ml[w * 8 + r]);
+    float L = 0.f, o[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int w = 0; w < kWaves; w++) {
+      const float mw = ml[w * 8 + r];
+      const float wt = (mw == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(mw - M);
+      L += wt * ml[32 + w * 8 + r];
+#pragma unroll
+      for (int i = 0; i < 4; i++) o[i] += wt * mo[(w * 8 + r) * kHD + d4 + i];
+    }
+#pragma unroll
+    for (int i = 0; i < 4; i++) mo[r * kHD + d4 + i] = o[i];   // wave-0 slot, own elements
+    if (d4 == 0) {
+      ml[kMlM + r] = M;
+      ml[kMlL + r] = L;
+    }
+  }
+  __syncthreads();
+
+  if (MODE == 1) {
+    finish_rows(lds, p, h, t_idx, rows, false, chunk, nullptr);
+    return;
+  }
+
+
+  // ---------------- fast path: records, arrival count, designated mergers ----------------
+  int* arrive = p.tickets;          // [0] records written, [1] mergers finished
+  if (has_work) {
+    store_record(lds, p, h, t_idx, rows, chunk);
+    __builtin_amdgcn_s_waitcnt(0);  // this thread's record stores are complete
+    __syncthreads();
+    if (threadIdx.x == 0) atomicAdd(&arrive[0], 1);
+  }
+  // the last n_mergers workgroups of the grid merge the (q head, query, block) units
+  const int n_units = p.num_q * p.sub_n * 2;
+  const int n_mergers = min(n_units, (int)gridDim.x);
+  const int mid = (int)blockIdx.x - ((int)gridDim.x - n_mergers);
+  if (mid < 0) return;
+  const int n_records = p.num_kv * p.sub_n * p.n_chunks;
+  int* flag = reinterpret_cast<int*>(lds + kLdsFlag);
+  if (threadIdx.x == 0) {
+    int spins = 0;
+    while (coherent_load_int(&arrive[0]) < n_records && spins < kMergeSpinLimit) {
+      __builtin_amdgcn_s_sleep(1);
+      spins++;
+    }
+    flag[0] = spins < kMergeSpinLimit;
+  }
+  __syncthreads();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+  if (flag[0]) {
+    for (int u = mid; u < n_units; u += n_mergers) {
+      const int blk = u & 1, qh = (u >> 1) % p.num_q, t = (u >> 1) / p.num_q;
+      merge_unit(lds, p, qh, t, blk, out);
+    }
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    const int done = atomicAdd(&arrive[1], 1);
+    if (done == n_mergers - 1) {    // every merger is past its wait: reset for the next call
+      atomicExch(&arrive[0], 0);
+      atomicExch(&arrive[1], 0);
+    }
+  }
+}
+
+size_t tq3_attn_lds_bytes() { return kLdsTotal; }
+
+hipError_t launch_tq3_attn(const AttnArgs& a, int mode, uint16_t* out, hipStream_t stream) {
+  const int groups = a.sub_n * a.n_chunks;
+  const int n_wg = ((groups + 7) / 8) * 8 * a.num_kv;
+  dim3 grid(n_wg), block(kThreads);
+  if (mode == 0)
+    hipLaunchKernelGGL((tq3_attn_kernel<0>), grid, block, 0, stream, a, out);
+  else
+    hipLaunchKernelGGL((tq3_attn_kernel<1>), grid, block, 0, stream, a, out);
+  return hipGetLastError();
+}
+
+}  // namespace qkv

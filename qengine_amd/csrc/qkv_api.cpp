@@ -1,0 +1,255 @@
+// qkv_api.cpp -- the extern "C" surface of libqkv.so (declared in include/qkv.h).
+//
+// Each entry point validates its arguments, then launches on the caller's
+// stream.  Nothing here allocates device memory or synchronises the host.
+#include "../../include/qkv.h"
+
+#include <hip/hip_runtime.h>
+
+#include <cstring>
+#include <mutex>
+
+#include "attn_common.h"
+#include "qkv_launch.h"
+
+namespace {
+
+constexpr int kVersion = 100;  // 0.1.0
+
+inline bool aligned(const void* p, size_t a) {
+  return (reinterpret_cast<uintptr_t>(p) % a) == 0;
+}
+
+inline int launch_status(hipError_t e) { return e == hipSuccess ? QKV_OK : QKV_ERR_LAUNCH; }
+
+std::mutex g_init_mu;
+bool g_init_ok[64];
+
+}  // namespace
+
+extern "C" {
+
+int qkv_version(void) { return kVersion; }
+
+const char* qkv_status_string(int s) {
+  switch (s) {
+    case QKV_OK: return "ok";
+    case QKV_ERR_INVALID: return "invalid argument";
+    case QKV_ERR_NULL: return "null pointer";
+    case QKV_ERR_UNSUPPORTED: return "unsupported head_dim/GQA combination";
+    case QKV_ERR_ALIGN: return "misaligned pointer";
+    case QKV_ERR_DEVICE: return "no usable gfx950 device";
+    case QKV_ERR_LAUNCH: return "kernel launch failed";
+    case QKV_ERR_WORKSPACE: return "workspace missing or too small";
+    default: return "unknown status";
+  }
+}
+
+int qkv_tq3_init(int device) {
+  if (device < 0 || device >= 64) return QKV_ERR_INVALID;
+  std::lock_guard<std::mutex> lk(g_init_mu);
+  if (g_init_ok[device]) return QKV_OK;
+  int n = 0;
+  if (hipGetDeviceCount(&n) != hipSuccess || device >= n) return QKV_ERR_DEVICE;
+  hipDeviceProp_t prop;
+  if (hipGetDeviceProperties(&prop, device) != hipSuccess) return QKV_ERR_DEVICE;
+  if (std::strncmp(prop.gcnArchName, "gfx950", 6) != 0) return QKV_ERR_DEVICE;
+  g_init_ok[device] = true;
+  return QKV_OK;
+}
+
+int qkv_tq3_append(const uint16_t* in_f16, qkv_block_tq3* out, int n_blocks, hipStream_t stream) {
+  if (n_blocks < 0) return QKV_ERR_INVALID;
+  if (n_blocks == 0) return QKV_OK;
+  if (!in_f16 || !out) return QKV_ERR_NULL;
+  if (!aligned(in_f16, 16) || !aligned(out, 4)) return QKV_ERR_ALIGN;
+  return launch_status(qkv::launch_tq3_append(in_f16, out, in_f16, out, n_blocks, 1, stream));
+}
+
+int qkv_tq3_append_kv(const uint16_t* k_f16, const uint16_t* v_f16, qkv_block_tq3* k_out,
+                      qkv_block_tq3* v_out, int n_blocks, hipStream_t stream) {
+  if (n_blocks < 0) return QKV_ERR_INVALID;
+  if (n_blocks == 0) return QKV_OK;
+  if (!k_f16 || !v_f16 || !k_out || !v_out) return QKV_ERR_NULL;
+  if (!aligned(k_f16, 16) || !aligned(v_f16, 16) || !aligned(k_out, 4) || !aligned(v_out, 4))
+    return QKV_ERR_ALIGN;
+  return launch_status(qkv::launch_tq3_append(k_f16, k_out, v_f16, v_out, n_blocks, 2, stream));
+}
+
+int qkv_tq3_dequant(const qkv_block_tq3* in, uint16_t* out_f16, int n_blocks, hipStream_t stream) {
+  if (n_blocks < 0) return QKV_ERR_INVALID;
+  if (n_blocks == 0) return QKV_OK;
+  if (!in || !out_f16) return QKV_ERR_NULL;
+  if (!aligned(in, 4) || !aligned(out_f16, 16)) return QKV_ERR_ALIGN;
+  return launch_status(qkv::launch_tq3_dequant(in, out_f16, n_blocks, stream));
+}
+
+int qkv_q8_append(const uint16_t* in_f16, qkv_block_q8* out, int n_blocks, hipStream_t stream) {
+  if (n_blocks < 0) return QKV_ERR_INVALID;
+  if (n_blocks == 0) return QKV_OK;
+  if (!in_f16 || !out) return QKV_ERR_NULL;
+  if (!aligned(in_f16, 16) || !aligned(out, 4)) return QKV_ERR_ALIGN;
+  return launch_status(qkv::launch_q8_append(in_f16, out, in_f16, out, n_blocks, 1, stream));
+}
+
+int qkv_q8_dequant(const qkv_block_q8* in, uint16_t* out_f16, int n_blocks, hipStream_t stream) {
+  if (n_blocks < 0) return QKV_ERR_INVALID;
+  if (n_blocks == 0) return QKV_OK;
+  if (!in || !out_f16) return QKV_ERR_NULL;
+  if (!aligned(in, 4) || !aligned(out_f16, 16)) return QKV_ERR_ALIGN;
+  return launch_status(qkv::launch_q8_dequant(in, out_f16, n_blocks, stream));
+}
+
+}  // extern "C"
+
+// ---------------------------------------------------------------------------
+// attention
+// ---------------------------------------------------------------------------
+namespace {
+
+constexpr int kChunkKeys = 256;
+
+int check_attn_shape(int num_q, int num_kv, int head_dim, int start_pos, int sub_n,
+                     const uint32_t* tree_mask) {
+  if (head_dim != 256) return QKV_ERR_UNSUPPORTED;
+  if (num_kv <= 0 || num_q <= 0 || num_q % num_kv != 0) return QKV_ERR_INVALID;
+  if (num_q / num_kv > 8) return QKV_ERR_UNSUPPORTED;
+  if (start_pos < 0 || sub_n < 1) return QKV_ERR_INVALID;
+  if (tree_mask && sub_n > 32) return QKV_ERR_INVALID;
+  return QKV_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int qkv_attn_split_tq3(const uint16_t* q, const qkv_block_tq3* k, const qkv_block_tq3* v,
+                       float* part_m, float* part_l, float* part_o, int num_q, int num_kv,
+                       int head_dim, int start_pos, int sub_n, int sub_n_max,
+                       int active_end_max, float scale, int k_splits, int sink_tok,
+                       int window_tok, const uint32_t* tree_mask, hipStream_t stream) {
+  int st = check_attn_shape(num_q, num_kv, head_dim, start_pos, sub_n, tree_mask);
+  if (st) return st;
+  if (sub_n > sub_n_max || k_splits < 1 || k_splits > 65536 || active_end_max < 1 ||
+      sink_tok < 0 || window_tok < 0)
+    return QKV_ERR_INVALID;
+  if (!q || !k || !v || !part_m || !part_l || !part_o) return QKV_ERR_NULL;
+  if (!aligned(q, 16) || !aligned(k, 4) || !aligned(v, 4) || !aligned(part_m, 4) ||
+      !aligned(part_l, 4) || !aligned(part_o, 4))
+    return QKV_ERR_ALIGN;
+  qkv::AttnArgs a{};
+  a.q = q;
+  a.k = reinterpret_cast<const uint32_t*>(k);
+  a.v = reinterpret_cast<const uint32_t*>(v);
+  a.num_q = num_q;
+  a.num_kv = num_kv;
+  a.start_pos = start_pos;
+  a.sub_n = sub_n;
+  a.sub_n_max = sub_n_max;
+  {
+    const uint64_t extent = (uint64_t)(start_pos + sub_n) * num_kv * 104;
+    if (extent > 0x7fffffffULL) return QKV_ERR_UNSUPPORTED;   // 32-bit buffer offsets
+    a.kv_bytes = (uint32_t)extent;
+  }
+  a.active_end_max = active_end_max;
+  a.k_splits = k_splits;
+  a.n_chunks = k_splits;
+  a.scale_log2 = scale * qkv::kLog2e;
+  a.sink_tok = sink_tok;
+  a.window_tok = window_tok;
+  a.tree_mask = tree_mask;
+  a.part_m = part_m;
+  a.part_l = part_l;
+  a.part_o = part_o;
+  return launch_status(qkv::launch_tq3_attn(a, 1, nullptr, stream));
+}
+
+int qkv_attn_split_merge(const float* part_m, const float* part_l, const float* part_o,
+                         uint16_t* out, int num_q, int num_kv, int head_dim, int sub_n,
+                         int sub_n_max, int k_splits, hipStream_t stream) {
+  if (head_dim != 256) return QKV_ERR_UNSUPPORTED;
+  if (num_q <= 0 || num_kv <= 0 || num_q % num_kv || sub_n < 1 || sub_n > sub_n_max ||
+      k_splits < 1 || k_splits > 65536)
+    return QKV_ERR_INVALID;
+  if (!part_m || !part_l || !part_o || !out) return QKV_ERR_NULL;
+  if (!aligned(part_m, 4) || !aligned(part_l, 4) || !aligned(part_o, 4) || !aligned(out, 2))
+    return QKV_ERR_ALIGN;
+  return launch_status(
+      qkv::launch_split_merge(part_m, part_l, part_o, out, num_q, sub_n, sub_n_max, k_splits, stream));
+}
+
+namespace {
+struct FastGeom {
+  int chunk_keys, n_chunks, n_slots;
+  size_t tickets_off, ml_off, o_off, total;
+};
+// Chunks of 256*tpw keys, at most 128 per (kv head, query): one record per
+// chunk and q head, merged by the designated merger workgroups.
+FastGeom fast_geom(int num_q, int num_kv, int sub_n, int n_keys) {
+  FastGeom g{};
+  const int c256 = (n_keys + kChunkKeys - 1) / kChunkKeys;
+  const int tpw = (c256 + 127) / 128;
+  g.chunk_keys = kChunkKeys * tpw;
+  g.n_chunks = (n_keys + g.chunk_keys - 1) / g.chunk_keys;
+  g.n_slots = g.n_chunks;
+  const size_t rows = (size_t)num_q * sub_n * g.n_slots;
+  g.tickets_off = 0;
+  g.ml_off = 256;                                    // two arrival counters
+  (void)num_kv;
+  g.o_off = (g.ml_off + rows * 2 * sizeof(float) + 255) & ~(size_t)255;
+  g.total = g.o_off + rows * 256 * sizeof(float);
+  return g;
+}
+}  // namespace
+
+size_t qkv_decode_attn_tq3_workspace_bytes(int num_q, int num_kv, int sub_n, int n_keys) {
+  if (num_q <= 0 || num_kv <= 0 || sub_n <= 0 || n_keys <= 0) return 0;
+  return fast_geom(num_q, num_kv, sub_n, n_keys).total;
+}
+
+int qkv_decode_attn_tq3(const uint16_t* q, const qkv_block_tq3* k, const qkv_block_tq3* v,
+                        uint16_t* out, int num_q, int num_kv, int head_dim, int start_pos,
+                        int sub_n, float scale, int sink_tok, int window_tok,
+                        const uint32_t* tree_mask, void* workspace, size_t workspace_bytes,
+                        hipStream_t stream) {
+  int st = check_attn_shape(num_q, num_kv, head_dim, start_pos, sub_n, tree_mask);
+  if (st) return st;
+  if (sink_tok < 0 || window_tok < 0) return QKV_ERR_INVALID;
+  if (!q || !k || !v || !out) return QKV_ERR_NULL;
+  if (!aligned(q, 16) || !aligned(k, 4) || !aligned(v, 4) || !aligned(out, 16))
+    return QKV_ERR_ALIGN;
+  const int n_keys = start_pos + sub_n;
+  const FastGeom g = fast_geom(num_q, num_kv, sub_n, n_keys);
+  if (!workspace || workspace_bytes < g.total) return QKV_ERR_WORKSPACE;
+  if (!aligned(workspace, 256)) return QKV_ERR_ALIGN;
+  char* ws = static_cast<char*>(workspace);
+  qkv::AttnArgs a{};
+  a.q = q;
+  a.k = reinterpret_cast<const uint32_t*>(k);
+  a.v = reinterpret_cast<const uint32_t*>(v);
+  a.num_q = num_q;
+  a.num_kv = num_kv;
+  a.start_pos = start_pos;
+  a.sub_n = sub_n;
+  a.sub_n_max = sub_n;
+  {
+    const uint64_t extent = (uint64_t)n_keys * num_kv * 104;
+    if (extent > 0x7fffffffULL) return QKV_ERR_UNSUPPORTED;   // 32-bit buffer offsets
+    a.kv_bytes = (uint32_t)extent;
+  }
+  a.active_end_max = n_keys;
+  a.k_splits = 1;
+  a.n_chunks = g.n_chunks;
+  a.chunk_keys = g.chunk_keys;
+  a.n_slots = g.n_slots;
+  a.scale_log2 = scale * qkv::kLog2e;
+  a.sink_tok = sink_tok;
+  a.window_tok = window_tok;
+  a.tree_mask = tree_mask;
+  a.tickets = reinterpret_cast<int*>(ws + g.tickets_off);
+  a.ws_ml = reinterpret_cast<float*>(ws + g.ml_off);
+  a.ws_o = reinterpret_cast<float*>(ws + g.o_off);
+  return launch_status(qkv::launch_tq3_attn(a, 0, out, stream));
+}
+
+}  // extern "C"

@@ -1,0 +1,70 @@
+// qkv_device.h -- device-side constants and helpers shared by the gfx950 kernels.
+//
+// Codec data follows the reference exactly:
+//   centroids / bounds           turboquant.cuh:27-37 (data, kept identical)
+//   sign vector                  turboquant.cuh:288-302 (xorshift64 from 0xCAFEF00D),
+//                                evaluated here at compile time into 4 bit masks
+//   WHT scale rsqrtf(128)        turboquant.cuh:61, correctly rounded 0x3DB504F3
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace qkv {
+
+constexpr int kTqBlock = 128;      // turboquant.cuh:16
+constexpr int kTqQsBytes = 48;     // turboquant.cuh:75
+constexpr int kTqBlockBytes = 52;  // turboquant.cuh:77
+constexpr int kTqBlockDwords = 13;
+constexpr int kQ8Block = 32;       // quant_gemv.cuh:8
+constexpr int kQ8BlockBytes = 36;  // quant_gemv.cuh:19
+constexpr int kQ8BlockDwords = 9;
+
+// ---- sign vector: bit i of kSignMask[i/32] is 1 where sign[i] = +1 --------
+constexpr uint64_t xorshift_step(uint64_t s) {
+  s ^= s << 13;
+  s ^= s >> 7;
+  s ^= s << 17;
+  return s;
+}
+constexpr uint32_t sign_word(int w) {
+  uint64_t s = 0xCAFEF00DULL;
+  uint32_t m = 0;
+  for (int i = 0; i < kTqBlock; i++) {
+    s = xorshift_step(s);
+    if (i / 32 == w && (s & 1u)) m |= 1u << (i % 32);
+  }
+  return m;
+}
+constexpr uint32_t kSignMask[4] = {sign_word(0), sign_word(1), sign_word(2), sign_word(3)};
+constexpr bool sign_pos(int i) { return (kSignMask[i >> 5] >> (i & 31)) & 1u; }
+static_assert(sign_word(0) == 0xfae78245u && sign_word(3) == 0x3849957eu,
+              "sign vector must match the reference seed");
+
+// ---- codebook ------------------------------------------------------------
+__device__ constexpr float kCentroids[8] = {-0.190303f, -0.118828f, -0.066847f, -0.021664f,
+                                            0.021664f,  0.066847f,  0.118828f,  0.190303f};
+constexpr float kBounds[7] = {-0.154566f, -0.092838f, -0.044256f, 0.000000f,
+                              0.044256f,  0.092838f,  0.154566f};
+constexpr float kCentroidsHost[8] = {-0.190303f, -0.118828f, -0.066847f, -0.021664f,
+                                     0.021664f,  0.066847f,  0.118828f,  0.190303f};
+
+__device__ __forceinline__ float wht_scale() { return __uint_as_float(0x3DB504F3u); }
+
+// turboquant.cuh:79-87: number of bounds strictly below y (NaN -> 0).
+__device__ __forceinline__ uint32_t tq3_bin(float y) {
+  uint32_t idx = 0;
+#pragma unroll
+  for (int i = 0; i < 7; i++) idx += (y > kBounds[i]) ? 1u : 0u;
+  return idx;
+}
+
+// ---- fp16 helpers (bit level) ---------------------------------------------
+__device__ __forceinline__ float h2f(uint32_t bits16) {
+  return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(bits16)));
+}
+__device__ __forceinline__ uint32_t f2h(float f) {  // round-to-nearest-even
+  return __builtin_bit_cast(uint16_t, static_cast<_Float16>(f));
+}
+
+}  // namespace qkv

@@ -1,0 +1,139 @@
+"""Host-side API over libqkv.so for torch device tensors.
+
+Mirrors the reference's append and attention launches (src/model.cuh call
+sites) with torch tensors as the device-memory container.  Every function
+calls the gfx950 HIP kernels through the C ABI; there is no CPU path.
+
+Cache tensors are uint8 tensors whose last dimension is the block size
+(52 bytes per TQ3 block, 36 bytes per Q8 block); fp16 tensors are
+torch.float16.  Calls are ordered on the current torch stream.
+"""
+from __future__ import annotations
+
+import torch
+
+from ._lib import check, lib
+
+TQ3_BLOCK_BYTES = 52
+Q8_BLOCK_BYTES = 36
+
+
+def _stream(stream=None) -> int:
+    s = stream if stream is not None else torch.cuda.current_stream()
+    return s.cuda_stream
+
+
+def _dev_ptr(t: torch.Tensor, what: str) -> int:
+    if not t.is_cuda:
+        raise ValueError(f"{what} must be a device tensor")
+    if not t.is_contiguous():
+        raise ValueError(f"{what} must be contiguous")
+    return t.data_ptr()
+
+
+def tq3_blocks(n_blocks: int, device) -> torch.Tensor:
+    """Zero-initialised TQ3 block storage [n_blocks, 52] (model.cuh:1914-1920)."""
+    return torch.zeros((n_blocks, TQ3_BLOCK_BYTES), dtype=torch.uint8, device=device)
+
+
+def q8_blocks(n_blocks: int, device) -> torch.Tensor:
+    return torch.zeros((n_blocks, Q8_BLOCK_BYTES), dtype=torch.uint8, device=device)
+
+
+def tq3_init(device: int = 0) -> None:
+    check(lib().qkv_tq3_init(device), "qkv_tq3_init")
+
+
+def tq3_append(x: torch.Tensor, out: torch.Tensor, stream=None) -> None:
+    """turboquant.cuh:112-165.  x: fp16 [..., 128*k]; out: uint8 blocks [n, 52]."""
+    assert x.dtype == torch.float16
+    n = x.numel() // 128
+    assert x.numel() == n * 128 and out.numel() >= n * TQ3_BLOCK_BYTES
+    check(lib().qkv_tq3_append(_dev_ptr(x, "x"), _dev_ptr(out, "out"), n, _stream(stream)),
+          "qkv_tq3_append")
+
+
+def tq3_append_kv(k: torch.Tensor, v: torch.Tensor, k_out: torch.Tensor, v_out: torch.Tensor,
+                  stream=None) -> None:
+    assert k.dtype == torch.float16 and v.dtype == torch.float16 and k.numel() == v.numel()
+    n = k.numel() // 128
+    check(lib().qkv_tq3_append_kv(_dev_ptr(k, "k"), _dev_ptr(v, "v"), _dev_ptr(k_out, "k_out"),
+                                  _dev_ptr(v_out, "v_out"), n, _stream(stream)),
+          "qkv_tq3_append_kv")
+
+
+def tq3_dequant(blocks: torch.Tensor, out: torch.Tensor | None = None, stream=None) -> torch.Tensor:
+    """turboquant.cuh:169-200.  Returns fp16 [n_blocks*128]."""
+    n = blocks.numel() // TQ3_BLOCK_BYTES
+    if out is None:
+        out = torch.empty(n * 128, dtype=torch.float16, device=blocks.device)
+    check(lib().qkv_tq3_dequant(_dev_ptr(blocks, "blocks"), _dev_ptr(out, "out"), n,
+                                _stream(stream)), "qkv_tq3_dequant")
+    return out
+
+
+def q8_append(x: torch.Tensor, out: torch.Tensor, stream=None) -> None:
+    """attention.cuh:2587-2609.  x: fp16 [..., 32*k]; out: uint8 blocks [n, 36]."""
+    assert x.dtype == torch.float16
+    n = x.numel() // 32
+    assert x.numel() == n * 32 and out.numel() >= n * Q8_BLOCK_BYTES
+    check(lib().qkv_q8_append(_dev_ptr(x, "x"), _dev_ptr(out, "out"), n, _stream(stream)),
+          "qkv_q8_append")
+
+
+def q8_dequant(blocks: torch.Tensor, out: torch.Tensor | None = None, stream=None) -> torch.Tensor:
+    """attention.cuh:2614-2626."""
+    n = blocks.numel() // Q8_BLOCK_BYTES
+    if out is None:
+        out = torch.empty(n * 32, dtype=torch.float16, device=blocks.device)
+    check(lib().qkv_q8_dequant(_dev_ptr(blocks, "blocks"), _dev_ptr(out, "out"), n,
+                               _stream(stream)), "qkv_q8_dequant")
+    return out
+
+
+# ---------------------------------------------------------------------------
+# attention
+# ---------------------------------------------------------------------------
+
+def _opt_ptr(t):
+    return 0 if t is None else _dev_ptr(t, "tensor")
+
+
+def attn_split_tq3(q, k, v, part_m, part_l, part_o, *, num_q, num_kv, start_pos, sub_n,
+                   sub_n_max, active_end_max, scale, k_splits, sink_tok=0, window_tok=0,
+                   tree_mask=None, head_dim=256, stream=None) -> None:
+    """attention.cuh:1905-2177: unnormalised split partials, reference layout."""
+    check(lib().qkv_attn_split_tq3(
+        _dev_ptr(q, "q"), _dev_ptr(k, "k"), _dev_ptr(v, "v"), _dev_ptr(part_m, "part_m"),
+        _dev_ptr(part_l, "part_l"), _dev_ptr(part_o, "part_o"), num_q, num_kv, head_dim,
+        start_pos, sub_n, sub_n_max, active_end_max, float(scale), k_splits, sink_tok,
+        window_tok, _opt_ptr(tree_mask), _stream(stream)), "qkv_attn_split_tq3")
+
+
+def attn_split_merge(part_m, part_l, part_o, out, *, num_q, num_kv, sub_n, sub_n_max, k_splits,
+                     head_dim=256, stream=None) -> None:
+    """attention.cuh:1837-1891."""
+    check(lib().qkv_attn_split_merge(
+        _dev_ptr(part_m, "part_m"), _dev_ptr(part_l, "part_l"), _dev_ptr(part_o, "part_o"),
+        _dev_ptr(out, "out"), num_q, num_kv, head_dim, sub_n, sub_n_max, k_splits,
+        _stream(stream)), "qkv_attn_split_merge")
+
+
+def decode_attn_tq3_workspace_bytes(num_q, num_kv, sub_n, n_keys) -> int:
+    return int(lib().qkv_decode_attn_tq3_workspace_bytes(num_q, num_kv, sub_n, n_keys))
+
+
+def decode_attn_tq3_workspace(num_q, num_kv, sub_n, n_keys, device) -> torch.Tensor:
+    """Zero-filled workspace for decode_attn_tq3 (the kernel keeps it zeroed)."""
+    n = decode_attn_tq3_workspace_bytes(num_q, num_kv, sub_n, n_keys)
+    return torch.zeros(n, dtype=torch.uint8, device=device)
+
+
+def decode_attn_tq3(q, k, v, out, workspace, *, num_q, num_kv, start_pos, sub_n, scale,
+                    sink_tok=0, window_tok=0, tree_mask=None, head_dim=256, stream=None) -> None:
+    """Fast path: split-K decode with the merge inside the same launch."""
+    check(lib().qkv_decode_attn_tq3(
+        _dev_ptr(q, "q"), _dev_ptr(k, "k"), _dev_ptr(v, "v"), _dev_ptr(out, "out"), num_q,
+        num_kv, head_dim, start_pos, sub_n, float(scale), sink_tok, window_tok,
+        _opt_ptr(tree_mask), _dev_ptr(workspace, "workspace"),
+        workspace.numel() * workspace.element_size(), _stream(stream)), "qkv_decode_attn_tq3")

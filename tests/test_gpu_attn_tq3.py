@@ -1,0 +1,129 @@
+"""GPU parity of the TQ3 split-K flash decode (attention.cuh:1905-2177) and
+merge (attention.cuh:1837-1891) against the CPU oracle on identical seeded
+inputs.  Bar: merged output within 2e-3 relative error (max |diff| / max |ref|),
+fp32 accumulation; split partials within the same tolerance."""
+import numpy as np
+import pytest
+
+from oracle import oracle as O
+from tests._data import kv_f16, q_f16, rel_err
+
+pytestmark = pytest.mark.gpu
+TOL = 2e-3
+
+
+def _torch():
+    import torch
+    return torch
+
+
+def _dev(a, dev):
+    return _torch().from_numpy(np.ascontiguousarray(a)).to(dev)
+
+
+def _cache(seed, n, num_kv=4, hd=256):
+    rng = np.random.default_rng(seed)
+    k16 = kv_f16(rng, n, num_kv, hd)
+    v16 = kv_f16(rng, n, num_kv, hd)
+    return rng, O.tq3_encode(k16), O.tq3_encode(v16)
+
+
+def _run_split(dev, q, kb, vb, **kw):
+    from qengine_amd import kvcache
+    torch = _torch()
+    nq, smax, ks = kw["num_q"], kw["sub_n_max"], kw["k_splits"]
+    pm = torch.full((nq, smax, ks), float("nan"), device=dev)
+    pl = torch.full((nq, smax, ks), float("nan"), device=dev)
+    po = torch.full((nq, smax, ks, 256), float("nan"), device=dev)
+    tm = kw.pop("tree_mask", None)
+    kvcache.attn_split_tq3(_dev(q.view(np.uint16), dev), _dev(kb.view(np.uint8), dev),
+                           _dev(vb.view(np.uint8), dev), pm, pl, po,
+                           tree_mask=None if tm is None else _dev(tm.astype(np.int32), dev), **kw)
+    out = torch.zeros((kw["sub_n"], nq, 256), dtype=torch.float16, device=dev)
+    kvcache.attn_split_merge(pm, pl, po, out, num_q=nq, num_kv=kw["num_kv"], sub_n=kw["sub_n"],
+                             sub_n_max=smax, k_splits=ks)
+    torch.cuda.synchronize()
+    return pm.cpu().numpy(), pl.cpu().numpy(), po.cpu().numpy(), out.cpu().numpy()
+
+
+def _check_partials(pm, pl, po, em, el, eo, sub_n):
+    pm, pl, po = pm[:, :sub_n], pl[:, :sub_n], po[:, :sub_n]
+    em, el, eo = em[:, :sub_n], el[:, :sub_n], eo[:, :sub_n]
+    empty = ~np.isfinite(em)
+    assert np.array_equal(empty, ~np.isfinite(pm)), "empty-split pattern differs"
+    assert np.all(pl[empty] == 0) and np.all(po[empty] == 0)
+    live = ~empty
+    assert np.max(np.abs(pm[live] - em[live])) < 1e-2
+    # compare l and o after bringing both to the reference max
+    w = np.exp(pm[live] - em[live])
+    assert np.max(np.abs(pl[live] * w - el[live]) / el[live]) < TOL
+    assert rel_err(po[live] * w[:, None], eo[live]) < TOL
+
+
+@pytest.mark.parametrize("n,k_splits,num_q", [(4097, 8, 16), (1000, 8, 16), (33, 8, 16),
+                                              (1, 1, 16), (777, 5, 24), (2500, 32, 16)])
+def test_split_decode_vs_oracle(dev, n, k_splits, num_q):
+    rng, kb, vb = _cache(n, n)
+    q = q_f16(rng, 1, num_q, 256)
+    kw = dict(num_q=num_q, num_kv=4, start_pos=n - 1, sub_n=1, sub_n_max=16,
+              active_end_max=n, scale=1 / 16, k_splits=k_splits)
+    pm, pl, po, out = _run_split(dev, q, kb, vb, **kw)
+    em, el, eo = O.attn_split(O.KV_TQ3, q, kb, vb, hd=256, **kw)
+    exp = O.attn_split_merge(em, el, eo, num_q=num_q, num_kv=4, hd=256, sub_n=1, sub_n_max=16,
+                             k_splits=k_splits)
+    _check_partials(pm, pl, po, em, el, eo, 1)
+    assert rel_err(out, exp.view(np.float16)) < TOL
+
+
+@pytest.mark.parametrize("sink,window,tree", [(0, 0, False), (0, 0, True), (64, 256, False),
+                                              (32, 100, True)])
+def test_split_verify_masks(dev, sink, window, tree):
+    n, sub_n = 3000, 16
+    rng, kb, vb = _cache(7 + sink, n)
+    q = q_f16(rng, sub_n, 16, 256)
+    tm = None
+    if tree:
+        tm = np.array([(1 << t) | (int(rng.integers(0, 1 << max(t, 1))) & ((1 << t) - 1))
+                       for t in range(sub_n)], np.uint32)
+    kw = dict(num_q=16, num_kv=4, start_pos=n - sub_n, sub_n=sub_n, sub_n_max=16,
+              active_end_max=n, scale=1 / 16, k_splits=8, sink_tok=sink, window_tok=window)
+    pm, pl, po, out = _run_split(dev, q, kb, vb, tree_mask=tm, **kw)
+    em, el, eo = O.attn_split(O.KV_TQ3, q, kb, vb, hd=256, tree_mask=tm, **kw)
+    exp = O.attn_split_merge(em, el, eo, num_q=16, num_kv=4, hd=256, sub_n=sub_n, sub_n_max=16,
+                             k_splits=8)
+    _check_partials(pm, pl, po, em, el, eo, sub_n)
+    assert rel_err(out, exp.view(np.float16)) < TOL
+
+
+@pytest.mark.parametrize("n,num_q,sub_n", [(4097, 16, 1), (32768, 16, 1), (1, 16, 1),
+                                           (300, 24, 1), (2064, 16, 16)])
+def test_fast_decode_vs_oracle(dev, n, num_q, sub_n):
+    from qengine_amd import kvcache
+    torch = _torch()
+    rng, kb, vb = _cache(100 + n, n)
+    q = q_f16(rng, sub_n, num_q, 256)
+    start = n - sub_n
+    ws = kvcache.decode_attn_tq3_workspace(num_q, 4, sub_n, n, dev)
+    out = torch.zeros((sub_n, num_q, 256), dtype=torch.float16, device=dev)
+    kvcache.decode_attn_tq3(_dev(q.view(np.uint16), dev), _dev(kb.view(np.uint8), dev),
+                            _dev(vb.view(np.uint8), dev), out, ws, num_q=num_q, num_kv=4,
+                            start_pos=start, sub_n=sub_n, scale=1 / 16)
+    torch.cuda.synchronize()
+    em, el, eo = O.attn_split(O.KV_TQ3, q, kb, vb, num_q=num_q, num_kv=4, hd=256,
+                              start_pos=start, sub_n=sub_n, sub_n_max=sub_n, active_end_max=n,
+                              scale=1 / 16, k_splits=8)
+    exp = O.attn_split_merge(em, el, eo, num_q=num_q, num_kv=4, hd=256, sub_n=sub_n,
+                             sub_n_max=sub_n, k_splits=8)
+    assert rel_err(out.cpu().numpy(), exp.view(np.float16)) < TOL
+
+
+def test_fast_decode_rejects_small_workspace(dev):
+    from qengine_amd import QKVError, kvcache
+    torch = _torch()
+    q = torch.zeros((1, 16, 256), dtype=torch.float16, device=dev)
+    kv = torch.zeros((100 * 8, 52), dtype=torch.uint8, device=dev)
+    out = torch.zeros_like(q)
+    ws = torch.zeros(16, dtype=torch.uint8, device=dev)
+    with pytest.raises(QKVError):
+        kvcache.decode_attn_tq3(q, kv, kv, out, ws, num_q=16, num_kv=4, start_pos=99, sub_n=1,
+                                scale=1 / 16)
