@@ -32,6 +32,7 @@ struct AttnArgs {
   float* ws_ml;             // [num_q][sub_n][n_slots][2] (m in log2 units, l)
   float* ws_o;              // [num_q][sub_n][n_slots][256] rotated coordinates
   int* tickets;             // [2]: records written, mergers finished (zero between calls)
+  uint32_t ws_ml_bytes, ws_o_bytes;
 };
 
 // ---- DPP wave reductions (result broadcast through lane 63) -------------

@@ -41,6 +41,8 @@ typedef float f4_t __attribute__((ext_vector_type(4)));
 typedef uint32_t u4_t __attribute__((ext_vector_type(4)));
 typedef uint32_t u3_t __attribute__((ext_vector_type(3)));
 typedef uint32_t u2_t __attribute__((ext_vector_type(2)));
+typedef uint32_t u32_a1 __attribute__((aligned(1)));
+typedef float f2_t __attribute__((ext_vector_type(2)));
 
 // word 3 of a raw buffer resource on gfx9-family GPUs (32-bit data format)
 constexpr int kBufferRsrcWord3 = 0x00020000;
@@ -71,6 +73,15 @@ constexpr int kMlM = 64, kMlL = 72, kMlC = 80, kMlW = 96;
 
 __device__ __forceinline__ uint32_t lut_read(const uint8_t* lds, uint32_t addr) {
   return *reinterpret_cast<const uint32_t*>(lds + addr);
+}
+
+// Lloyd-Max centroid i (turboquant.cuh:27-30) selected from immediates.
+__device__ __forceinline__ float centroid_imm(uint32_t i) {
+  // i >= 4: +m[i-4]; i < 4: -m[3-i]  (symmetric table)
+  const float mpos = (i & 2) ? ((i & 1) ? 0.190303f : 0.118828f) : ((i & 1) ? 0.066847f : 0.021664f);
+  const uint32_t j = 3u - (i & 3u);
+  const float mneg = (j & 2) ? ((j & 1) ? 0.190303f : 0.118828f) : ((j & 1) ? 0.066847f : 0.021664f);
+  return (i & 4) ? mpos : -mneg;
 }
 
 // Centroid-pair table address of the 6-bit field at bit BIT of a 3-dword
@@ -161,10 +172,8 @@ struct TileRegs {
 __device__ __forceinline__ void load_tile(__amdgpu_buffer_rsrc_t rk, __amdgpu_buffer_rsrc_t rv,
                                           int ts, int nkv, int h, int lane, int row, int col,
                                           TileRegs& tr) {
-  const uint32_t vrow = (uint32_t)((ts + lane) * nkv + h) * 104u;
-#pragma unroll
-  for (int i = 0; i < 6; i++) tr.vr[i] = __builtin_amdgcn_raw_buffer_load_b128(rv, vrow + 16 * i, 0, 0);
-  tr.vr6 = __builtin_amdgcn_raw_buffer_load_b64(rv, vrow + 96, 0, 0);
+  // keys first (group by group): the score MFMAs of group g only wait for
+  // group g, and values arrive while the scores are computed
 #pragma unroll
   for (int g = 0; g < 4; g++) {
     const uint32_t krow = (uint32_t)((ts + 16 * g + col) * nkv + h) * 104u;
@@ -177,6 +186,10 @@ __device__ __forceinline__ void load_tile(__amdgpu_buffer_rsrc_t rk, __amdgpu_bu
       tr.kn[g][j] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rk, krow + 52 * j, 0, 0));
     }
   }
+  const uint32_t vrow = (uint32_t)((ts + lane) * nkv + h) * 104u;
+#pragma unroll
+  for (int i = 0; i < 6; i++) tr.vr[i] = __builtin_amdgcn_raw_buffer_load_b128(rv, vrow + 16 * i, 0, 0);
+  tr.vr6 = __builtin_amdgcn_raw_buffer_load_b64(rv, vrow + 96, 0, 0);
 }
 
 struct KeyRule {
@@ -210,16 +223,14 @@ __device__ __forceinline__ float row16_sum(float v) {
 }
 
 // Records move between workgroups (possibly on different XCDs, whose L2s are
-// not coherent with each other).  Writers store them with agent-scope atomic
-// stores, which gfx950 performs at the device coherence point (sc1), and wait
-// for completion (s_waitcnt vmcnt(0)) before counting themselves in; a merger
-// observes the full count, invalidates its caches once (agent-scope acquire)
-// and then reads the records with ordinary 16-byte loads.  Only the few merging
-// workgroups pay a cache invalidation, instead of an L2 write-back and
-// invalidate in every workgroup.
-__device__ __forceinline__ void coherent_store(float* p, float v) {
-  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
+// not coherent with each other) with 16-byte buffer accesses carrying the
+// sc0|sc1 cache policy: stores write through to the device coherence point
+// and loads read from it.  A writer waits for its stores to complete
+// (s_waitcnt vmcnt(0)) before counting itself in; a merger reads records only
+// after it has seen the full count.  No workgroup pays an L2 write-back or
+// invalidate (what agent-scope fences cost on this GPU).
+constexpr int kCoherent = 1 | 16;   // sc0 | sc1
+
 __device__ __forceinline__ int coherent_load_int(int* p) {
   return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
@@ -233,67 +244,56 @@ __device__ __forceinline__ long rec_index(const AttnArgs& p, int qh, int t, int 
 // sleeps ~64 cycles; the limit is seconds, far beyond any legitimate wait).
 constexpr int kMergeSpinLimit = 1 << 24;
 
-// Merge all chunk records of one unit (q head qh, query t, 128-block blk) and
-// write its fp16 output: o = rs*D*H*(sum_c w_c o_c / sum_c w_c l_c).
-// Thread = (record slice sl = tid/32 of 8, dim quad dq = tid%32): records
-// sl, sl+8, ...; one round of 16-byte loads.
-__device__ void merge_unit(uint8_t* lds, const AttnArgs& p, int qh, int t, int blk,
-                           uint16_t* out) {
-  float* red = reinterpret_cast<float*>(lds + kLdsMergeO);   // [8 slices][128] + scalars
+// Merge all chunk records (n_chunks <= 128) of one unit (q head qh, query t,
+// 128-block blk) and write its fp16 output o = rs*D*H*(sum w_c o_c / sum w_c l_c).
+// Thread = (record slice sl = tid/32 of 8, dim quad dq = tid%32) with records
+// sl, sl+8, ...: all loads are issued in one round.
+__device__ void merge_unit(uint8_t* lds, const AttnArgs& p, __amdgpu_buffer_rsrc_t rml,
+                           __amdgpu_buffer_rsrc_t ro, int qh, int t, int blk, uint16_t* out) {
+  float* red = reinterpret_cast<float*>(lds + kLdsMergeO);   // [8][128] sums, then scalars
   const int tid = threadIdx.x;
   const int sl = tid >> 5, dq = tid & 31;
   const int n = p.n_chunks;
   const long base = rec_index(p, qh, t, 0);
-  constexpr int kMaxPer = 16;                                 // records per thread per pass
-  float M = -INFINITY;
-  // pass 1: global max of m over all records
-  for (int c = tid; c < n; c += kThreads) {
-    const float m = p.ws_ml[2 * (base + c)];
-    const float l = p.ws_ml[2 * (base + c) + 1];
-    if (l > 0.f) M = fmaxf(M, m);
+  f2_t ml[16];
+  f4_t v[16];
+#pragma unroll
+  for (int i = 0; i < 16; i++) {
+    const int c = sl + 8 * i;
+    if (c < n) {
+      ml[i] = __builtin_amdgcn_raw_buffer_load_b64(rml, (uint32_t)((base + c) * 8), 0, kCoherent);
+      v[i] = __builtin_amdgcn_raw_buffer_load_b128(
+          ro, (uint32_t)(((base + c) * kHD + blk * 128 + 4 * dq) * 4), 0, kCoherent);
+    } else {
+      ml[i] = f2_t{-INFINITY, 0.f};
+      v[i] = f4_t{0.f, 0.f, 0.f, 0.f};
+    }
   }
-  M = fmaxf(M, __shfl_xor(M, 1));
-  M = fmaxf(M, __shfl_xor(M, 2));
-  M = fmaxf(M, __shfl_xor(M, 4));
-  M = fmaxf(M, __shfl_xor(M, 8));
-  M = fmaxf(M, __shfl_xor(M, 16));
-  M = fmaxf(M, __shfl_xor(M, 32));
-  if ((tid & 63) == 0) red[1024 + (tid >> 6)] = M;
+  float mloc = -INFINITY;
+#pragma unroll
+  for (int i = 0; i < 16; i++)
+    if (ml[i][1] > 0.f) mloc = fmaxf(mloc, ml[i][0]);
+  if (dq == 0) red[1024 + sl] = mloc;
   __syncthreads();
-  M = fmaxf(fmaxf(red[1024], red[1025]), fmaxf(red[1026], red[1027]));
-  // pass 2: weighted sums (records sl, sl+8, ...), 16 loads in flight per batch
-  float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+  float M = red[1024];
+#pragma unroll
+  for (int k = 1; k < 8; k++) M = fmaxf(M, red[1024 + k]);
+  f4_t acc = {0.f, 0.f, 0.f, 0.f};
   float L = 0.f;
-  for (int c0 = sl; c0 < n; c0 += 8 * kMaxPer) {
-    float4 v[kMaxPer];
-    float w[kMaxPer];
 #pragma unroll
-    for (int i = 0; i < kMaxPer; i++) {
-      const int c = c0 + 8 * i;
-      if (c < n) {
-        const float m = p.ws_ml[2 * (base + c)];
-        const float l = p.ws_ml[2 * (base + c) + 1];
-        w[i] = (l > 0.f) ? __builtin_amdgcn_exp2f(m - M) : 0.f;
-        L += (dq == 0) ? w[i] * l : 0.f;
-        v[i] = *reinterpret_cast<const float4*>(&p.ws_o[(base + c) * kHD + blk * 128 + 4 * dq]);
-      } else {
-        w[i] = 0.f;
-        v[i] = make_float4(0.f, 0.f, 0.f, 0.f);
-      }
-    }
-#pragma unroll
-    for (int i = 0; i < kMaxPer; i++) {
-      acc.x += w[i] * v[i].x; acc.y += w[i] * v[i].y; acc.z += w[i] * v[i].z; acc.w += w[i] * v[i].w;
-    }
+  for (int i = 0; i < 16; i++) {
+    const float w = (ml[i][1] > 0.f) ? __builtin_amdgcn_exp2f(ml[i][0] - M) : 0.f;
+    L += w * ml[i][1];
+    acc += w * v[i];
   }
-  *reinterpret_cast<float4*>(&red[sl * 128 + 4 * dq]) = acc;
+  *reinterpret_cast<f4_t*>(&red[sl * 128 + 4 * dq]) = acc;
   if (dq == 0) red[1032 + sl] = L;
   __syncthreads();
   // rotate back: 16 lanes x 8 elements (threads 0..15)
   if (tid < 16) {
     float Lt = 0.f;
 #pragma unroll
-    for (int i = 0; i < 8; i++) Lt += red[1032 + i];
+    for (int k = 0; k < 8; k++) Lt += red[1032 + k];
     const float inv = Lt > 0.f ? 1.0f / Lt : 0.f;
     float x[8];
 #pragma unroll
@@ -314,8 +314,8 @@ __device__ void merge_unit(uint8_t* lds, const AttnArgs& p, int qh, int t, int b
       for (int e2 = 0; e2 < 2; e2++) {
         const int e = tid * 8 + 2 * i + e2;
         const bool pos = (kSignMask[e >> 5] >> (e & 31)) & 1u;
-        const float v = x[2 * i + e2] * rs;
-        y[e2] = pos ? v : -v;
+        const float vv = x[2 * i + e2] * rs;
+        y[e2] = pos ? vv : -vv;
       }
       pk[i] = f2h(y[0]) | (f2h(y[1]) << 16);
     }
@@ -326,20 +326,19 @@ __device__ void merge_unit(uint8_t* lds, const AttnArgs& p, int qh, int t, int b
 }
 
 // Store the merged rows in LDS as this workgroup's records (rotated).
-__device__ void store_record(const uint8_t* lds, const AttnArgs& p, int h, int t, int rows,
-                             int chunk) {
+__device__ void store_record(const uint8_t* lds, const AttnArgs& p, __amdgpu_buffer_rsrc_t rml,
+                             __amdgpu_buffer_rsrc_t ro, int h, int t, int rows, int chunk) {
   const float* mo = reinterpret_cast<const float*>(lds + kLdsMergeO);
-  const float* ml = reinterpret_cast<const float*>(lds + kLdsMergeML);
+  const float* mlv = reinterpret_cast<const float*>(lds + kLdsMergeML);
   const int gqa = p.num_q / p.num_kv;
   for (int idx = threadIdx.x; idx < rows * 64; idx += kThreads) {
     const int r = idx >> 6, d4 = (idx & 63) * 4;
     const long rec = rec_index(p, h * gqa + r, t, chunk);
-#pragma unroll
-    for (int i = 0; i < 4; i++) coherent_store(&p.ws_o[rec * kHD + d4 + i], mo[r * kHD + d4 + i]);
-    if (d4 == 0) {
-      coherent_store(&p.ws_ml[2 * rec], ml[kMlM + r]);
-      coherent_store(&p.ws_ml[2 * rec + 1], ml[kMlL + r]);
-    }
+    __builtin_amdgcn_raw_buffer_store_b128(*reinterpret_cast<const f4_t*>(&mo[r * kHD + d4]), ro,
+                                           (uint32_t)((rec * kHD + d4) * 4), 0, kCoherent);
+    if (d4 == 0)
+      __builtin_amdgcn_raw_buffer_store_b64(f2_t{mlv[kMlM + r], mlv[kMlL + r]}, rml,
+                                            (uint32_t)(rec * 8), 0, kCoherent);
   }
 }
 
@@ -439,15 +438,16 @@ __global__ __launch_bounds__(kThreads, 2) void tq3_attn_kernel(AttnArgs p, uint1
       __builtin_amdgcn_make_buffer_rsrc(const_cast<uint32_t*>(p.k), 0, p.kv_bytes, kBufferRsrcWord3);
   const __amdgpu_buffer_rsrc_t rv =
       __builtin_amdgcn_make_buffer_rsrc(const_cast<uint32_t*>(p.v), 0, p.kv_bytes, kBufferRsrcWord3);
-  TileRegs tr;
-  if (lo + wave * kTile < hi) load_tile(rk, rv, lo + wave * kTile, p.num_kv, h, lane, row, col, tr);
 
   // ---- setup: centroid-pair table; rotated query ---------------------------
   if (threadIdx.x < 64) {
+    // entry e = (centroid[e & 7], centroid[e >> 3]) as fp16, from immediates
+    // (a table load here would wait behind the tile loads already in flight)
     const uint32_t e = threadIdx.x;
     *reinterpret_cast<uint32_t*>(lds + kLdsLut + 4 * e) =
-        f2h(kCentroids[e & 7]) | (f2h(kCentroids[e >> 3]) << 16);
+        f2h(centroid_imm(e & 7)) | (f2h(centroid_imm(e >> 3)) << 16);
   }
+  TileRegs tr;
   {
     // 16 WHTs of 128 (8 heads x 2 blocks), 16 lanes each; fp16 result in LDS
     // scratch laid out [head][block][group u][octet o][8] so each lane's A
@@ -456,11 +456,15 @@ __global__ __launch_bounds__(kThreads, 2) void tq3_attn_kernel(AttnArgs p, uint1
     const int wht = threadIdx.x >> 4;
     const int part = threadIdx.x & 15;
     const int hh = wht >> 1, blk = wht & 1;
+    // the query piece is requested before the tile, so its wait does not
+    // include the tile's loads (the vector memory counter is in order)
+    uint4 raw = make_uint4(0, 0, 0, 0);
+    if (hh < gqa)
+      raw = *reinterpret_cast<const uint4*>(
+          p.q + ((long)t_idx * p.num_q + h * gqa + hh) * kHD + blk * 128 + part * 8);
+    if (lo + wave * kTile < hi) load_tile(rk, rv, lo + wave * kTile, p.num_kv, h, lane, row, col, tr);
     if (hh < gqa) {
       float x[8];
-      const uint16_t* qsrc =
-          p.q + ((long)t_idx * p.num_q + h * gqa + hh) * kHD + blk * 128 + part * 8;
-      const uint4 raw = *reinterpret_cast<const uint4*>(qsrc);
       const uint32_t wv[4] = {raw.x, raw.y, raw.z, raw.w};
 #pragma unroll
       for (int i = 0; i < 4; i++) {
@@ -520,13 +524,9 @@ __global__ __launch_bounds__(kThreads, 2) void tq3_attn_kernel(AttnArgs p, uint1
   const int nkv = p.num_kv;
   uint8_t* wl = lds + kLdsW + wave * kLdsWBytes;
   uint32_t* vl = reinterpret_cast<uint32_t*>(lds + kLdsV + wave * kLdsVBytes);
-  const int v_dw = 1 + ((3 * col) >> 2), v_sh = (3 * col) & 3;   // value-side group col
 
   for (int ts = lo + wave * kTile; ts < hi; ts += kWaves * kTile) {
     if (ts != lo + wave * kTile) load_tile(rk, rv, ts, nkv, h, lane, row, col, tr);
-#pragma unroll
-    for (int i = 0; i < 6; i++) *reinterpret_cast<u4_t*>(vl + lane * kVPitchDw + 4 * i) = tr.vr[i];
-    *reinterpret_cast<u2_t*>(vl + lane * kVPitchDw + 24) = tr.vr6;
     auto& kq = tr.kq;
     auto& kn = tr.kn;
 
@@ -544,6 +544,10 @@ __global__ __launch_bounds__(kThreads, 2) void tq3_attn_kernel(AttnArgs p, uint1
       for (int r = 0; r < 4; r++)
         s[g][r] = vis ? (kn[g][0] * a0[r] + kn[g][1] * a1[r]) * scale2 : -INFINITY;
     }
+    // stage the value rows (loaded last) once the scores are done
+#pragma unroll
+    for (int i = 0; i < 6; i++) *reinterpret_cast<u4_t*>(vl + lane * kVPitchDw + 4 * i) = tr.vr[i];
+    *reinterpret_cast<u2_t*>(vl + lane * kVPitchDw + 24) = tr.vr6;
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
@@ -579,10 +583,12 @@ __global__ __launch_bounds__(kThreads, 2) void tq3_attn_kernel(AttnArgs p, uint1
       lsum[r] = lsum[r] * corr[r] + row16_sum(ps);
       m2[r] = mn;
     }
+    if (ts != lo + wave * kTile) {   // accumulators are still zero on the first tile
 #pragma unroll
-    for (int t = 0; t < 16; t++)
+      for (int t = 0; t < 16; t++)
 #pragma unroll
-      for (int r = 0; r < 4; r++) acc[t][r] *= corr[r];
+        for (int r = 0; r < 4; r++) acc[t][r] *= corr[r];
+    }
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
@@ -593,12 +599,14 @@ __global__ __launch_bounds__(kThreads, 2) void tq3_attn_kernel(AttnArgs p, uint1
     for (int c2 = 0; c2 < 2; c2++) {
 #pragma unroll
       for (int j = 0; j < 2; j++) {
+        // 3-byte code group `col` of block j of keys 32*c2+8*row+i: one
+        // unaligned LDS read each (gfx950 LDS reads at any byte address; the
+        // top byte is the next group's and is masked by the table addressing)
         uint32_t x[8];
+        const uint8_t* vb = reinterpret_cast<const uint8_t*>(vl) + 52 * j + 4 + 3 * col;
 #pragma unroll
-        for (int i = 0; i < 8; i++) {
-          const uint32_t* rw = vl + (32 * c2 + 8 * row + i) * kVPitchDw + 13 * j + v_dw;
-          x[i] = __builtin_amdgcn_alignbyte(rw[1], rw[0], v_sh);
-        }
+        for (int i = 0; i < 8; i++)
+          x[i] = *reinterpret_cast<const u32_a1*>(vb + (32 * c2 + 8 * row + i) * kVPitchDw * 4);
         const h8_t a = *reinterpret_cast<const h8_t*>(
             wl + ((j * 16 + col) * kTile + 32 * c2 + 8 * row) * 2);
         value_pipe<0>(lds, x, a, acc, 8 * j);
@@ -661,8 +669,12 @@ __global__ __launch_bounds__(kThreads, 2) void tq3_attn_kernel(AttnArgs p, uint1
 
   // ---------------- fast path: records, arrival count, designated mergers ----------------
   int* arrive = p.tickets;          // [0] records written, [1] mergers finished
+  const __amdgpu_buffer_rsrc_t rml =
+      __builtin_amdgcn_make_buffer_rsrc(p.ws_ml, 0, p.ws_ml_bytes, kBufferRsrcWord3);
+  const __amdgpu_buffer_rsrc_t ro =
+      __builtin_amdgcn_make_buffer_rsrc(p.ws_o, 0, p.ws_o_bytes, kBufferRsrcWord3);
   if (has_work) {
-    store_record(lds, p, h, t_idx, rows, chunk);
+    store_record(lds, p, rml, ro, h, t_idx, rows, chunk);
     __builtin_amdgcn_s_waitcnt(0);  // this thread's record stores are complete
     __syncthreads();
     if (threadIdx.x == 0) atomicAdd(&arrive[0], 1);
@@ -683,11 +695,10 @@ __global__ __launch_bounds__(kThreads, 2) void tq3_attn_kernel(AttnArgs p, uint1
     flag[0] = spins < kMergeSpinLimit;
   }
   __syncthreads();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
   if (flag[0]) {
     for (int u = mid; u < n_units; u += n_mergers) {
       const int blk = u & 1, qh = (u >> 1) % p.num_q, t = (u >> 1) / p.num_q;
-      merge_unit(lds, p, qh, t, blk, out);
+      merge_unit(lds, p, rml, ro, qh, t, blk, out);
     }
   }
   __syncthreads();

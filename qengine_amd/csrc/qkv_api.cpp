@@ -249,6 +249,9 @@ int qkv_decode_attn_tq3(const uint16_t* q, const qkv_block_tq3* k, const qkv_blo
   a.tickets = reinterpret_cast<int*>(ws + g.tickets_off);
   a.ws_ml = reinterpret_cast<float*>(ws + g.ml_off);
   a.ws_o = reinterpret_cast<float*>(ws + g.o_off);
+  if (g.total > 0xffffffffULL) return QKV_ERR_UNSUPPORTED;   // 32-bit buffer offsets
+  a.ws_ml_bytes = (uint32_t)(g.o_off - g.ml_off);
+  a.ws_o_bytes = (uint32_t)(g.total - g.o_off);
   return launch_status(qkv::launch_tq3_attn(a, 0, out, stream));
 }
 
