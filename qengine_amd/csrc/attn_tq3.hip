@@ -192,16 +192,22 @@ __device__ __forceinline__ void load_tile(__amdgpu_buffer_rsrc_t rk, __amdgpu_bu
   tr.vr6 = __builtin_amdgcn_raw_buffer_load_b64(rv, vrow + 96, 0, 0);
 }
 
+// Key visibility of one query (attention.cuh:1923-1929, 2101-2105): the
+// sink/window rule on 32-key tiles, then the tree bits for keys of the block.
 struct KeyRule {
-  int start_pos, t_idx, sink, window;
-  const uint32_t* tree;
+  int start_pos, sink, window;
+  bool has_tree;
+  uint32_t tree_bits;   // bit j: key start_pos + j is visible
+  __device__ KeyRule(int start_pos_, int t_idx, int sink_, int window_, const uint32_t* tree)
+      : start_pos(start_pos_), sink(sink_), window(window_), has_tree(tree != nullptr),
+        tree_bits(tree ? tree[t_idx] : 0u) {}
   __device__ __forceinline__ bool visible(int key, int active_end) const {
     if (sink > 0 || window > 0) {
       const int ts = key & ~31;
       const int te = min(ts + 32, active_end);
       if (!(ts < sink) && !(te > active_end - window)) return false;
     }
-    if (tree && key >= start_pos) return (tree[t_idx] >> (key - start_pos)) & 1u;
+    if (has_tree && key >= start_pos) return (tree_bits >> (key - start_pos)) & 1u;
     return true;
   }
 };
@@ -307,13 +313,13 @@ __device__ void merge_unit(uint8_t* lds, const AttnArgs& p, __amdgpu_buffer_rsrc
     wht_xor_lanes16(x, tid);
     const float rs = wht_scale();
     uint32_t pk[4];
+    const uint32_t sbits = sign_word_sel(tid >> 2) >> (8 * (tid & 3));   // signs of elements tid*8..+7
 #pragma unroll
     for (int i = 0; i < 4; i++) {
       float y[2];
 #pragma unroll
       for (int e2 = 0; e2 < 2; e2++) {
-        const int e = tid * 8 + 2 * i + e2;
-        const bool pos = (kSignMask[e >> 5] >> (e & 31)) & 1u;
+        const bool pos = (sbits >> (2 * i + e2)) & 1u;
         const float vv = x[2 * i + e2] * rs;
         y[e2] = pos ? vv : -vv;
       }
@@ -367,10 +373,10 @@ __device__ void finish_rows(const uint8_t* lds, const AttnArgs& p, int h, int t,
     const float rs = wht_scale();
     const int qh = h * gqa + r;
     float y[8];
+    const uint32_t sbits = sign_word_sel(part >> 2) >> (8 * (part & 3));  // elements part*8..+7
 #pragma unroll
     for (int i = 0; i < 8; i++) {
-      const int e = part * 8 + i;
-      const bool pos = (kSignMask[e >> 5] >> (e & 31)) & 1u;
+      const bool pos = (sbits >> i) & 1u;
       const float v = x[i] * rs;
       y[i] = pos ? v : -v;
     }
@@ -429,7 +435,7 @@ __global__ __launch_bounds__(kThreads, 2) void tq3_attn_kernel(AttnArgs p, uint1
     lo = chunk * tps * 32;
     hi = min((chunk + 1) * tps * 32, active_end);
   }
-  const KeyRule rule{p.start_pos, t_idx, p.sink_tok, p.window_tok, p.tree_mask};
+  const KeyRule rule(p.start_pos, t_idx, p.sink_tok, p.window_tok, p.tree_mask);
   const int row = lane >> 4;        // 16-lane row of the MFMA D layout
   const int col = lane & 15;
 
@@ -456,25 +462,30 @@ __global__ __launch_bounds__(kThreads, 2) void tq3_attn_kernel(AttnArgs p, uint1
     const int wht = threadIdx.x >> 4;
     const int part = threadIdx.x & 15;
     const int hh = wht >> 1, blk = wht & 1;
-    // the query piece is requested before the tile, so its wait does not
-    // include the tile's loads (the vector memory counter is in order)
-    uint4 raw = make_uint4(0, 0, 0, 0);
-    if (hh < gqa)
-      raw = *reinterpret_cast<const uint4*>(
-          p.q + ((long)t_idx * p.num_q + h * gqa + hh) * kHD + blk * 128 + part * 8);
-    if (lo + wave * kTile < hi) load_tile(rk, rv, lo + wave * kTile, p.num_kv, h, lane, row, col, tr);
-    if (hh < gqa) {
+    // The query piece is requested before the tile, so its wait does not
+    // include the tile's loads (the vector memory counter is in order).  Both
+    // loads are unconditional (rows past a buffer's extent read as zero):
+    // a load under a branch makes the compiler wait for every load at the join.
+    const uint32_t q_extent = (uint32_t)(p.sub_n * p.num_q * kHD * 2);
+    const __amdgpu_buffer_rsrc_t rq =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(p.q), 0, q_extent, kBufferRsrcWord3);
+    const uint32_t qoff =
+        hh < gqa ? (uint32_t)(((t_idx * p.num_q + h * gqa + hh) * kHD + blk * 128 + part * 8) * 2)
+                 : q_extent;
+    const u4_t raw = __builtin_amdgcn_raw_buffer_load_b128(rq, qoff, 0, 0);
+    load_tile(rk, rv, lo + wave * kTile, p.num_kv, h, lane, row, col, tr);
+    {
       float x[8];
-      const uint32_t wv[4] = {raw.x, raw.y, raw.z, raw.w};
+      const uint32_t wv[4] = {raw[0], raw[1], raw[2], raw[3]};
 #pragma unroll
       for (int i = 0; i < 4; i++) {
         x[2 * i] = h2f(wv[i] & 0xffffu);
         x[2 * i + 1] = h2f(wv[i] >> 16);
       }
+      const uint32_t sbits = sign_word_sel(part >> 2) >> (8 * (part & 3));   // elements part*8..+7
 #pragma unroll
       for (int i = 0; i < 8; i++) {
-        const int e = part * 8 + i;
-        const bool pos = (kSignMask[e >> 5] >> (e & 31)) & 1u;
+        const bool pos = (sbits >> i) & 1u;
         x[i] = pos ? x[i] : -x[i];
       }
       wht8_inreg(x);
@@ -497,10 +508,9 @@ __global__ __launch_bounds__(kThreads, 2) void tq3_attn_kernel(AttnArgs p, uint1
 #pragma unroll
     for (int s = 0; s < 8; s++) {
       const int j = s >> 2, u = s & 3;
-      if (col < gqa)
-        qa[s] = *reinterpret_cast<const h8_t*>(qs + (((col * 2 + j) * 4 + u) * 4 + row) * 8);
-      else
-        qa[s] = h8_t{0, 0, 0, 0, 0, 0, 0, 0};
+      // rows 8..15 are never written and must read as zero
+      qa[s] = col < 8 ? *reinterpret_cast<const h8_t*>(qs + (((col * 2 + j) * 4 + u) * 4 + row) * 8)
+                      : h8_t{0, 0, 0, 0, 0, 0, 0, 0};
     }
   }
   {

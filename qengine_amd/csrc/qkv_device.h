@@ -38,6 +38,13 @@ constexpr uint32_t sign_word(int w) {
 }
 constexpr uint32_t kSignMask[4] = {sign_word(0), sign_word(1), sign_word(2), sign_word(3)};
 constexpr bool sign_pos(int i) { return (kSignMask[i >> 5] >> (i & 31)) & 1u; }
+// Sign word w (0..3) for a runtime w, selected from immediates: indexing the
+// constexpr array with a runtime value would turn it into a memory load.
+__device__ __forceinline__ uint32_t sign_word_sel(int w) {
+  const uint32_t lo = (w & 1) ? kSignMask[1] : kSignMask[0];
+  const uint32_t hi = (w & 1) ? kSignMask[3] : kSignMask[2];
+  return (w & 2) ? hi : lo;
+}
 static_assert(sign_word(0) == 0xfae78245u && sign_word(3) == 0x3849957eu,
               "sign vector must match the reference seed");
 
