@@ -9,6 +9,13 @@ namespace qkv {
 constexpr float kLn2 = 0.69314718055994531f;
 constexpr float kLog2e = 1.44269504088896341f;
 
+// Fast-path arrival counters: workgroup b counts itself in slot b % kArriveSlots
+// (one 128-byte line each, so arrivals do not queue on a single address); the
+// mergers-finished counter follows the slots.
+constexpr int kArriveSlots = 32;
+constexpr int kArriveStride = 32;   // ints
+constexpr int kTicketBytes = ((kArriveSlots + 1) * kArriveStride * 4 + 255) & ~255;
+
 struct AttnArgs {
   const uint16_t* q;        // [sub_n][num_q][256] fp16
   const uint32_t* k;        // slot-base key cache (blocks viewed as dwords)
@@ -31,7 +38,7 @@ struct AttnArgs {
   // fast-path workspace
   float* ws_ml;             // [num_q][sub_n][n_slots][2] (m in log2 units, l)
   float* ws_o;              // [num_q][sub_n][n_slots][256] rotated coordinates
-  int* tickets;             // [2]: records written, mergers finished (zero between calls)
+  int* tickets;             // arrival counters, then the mergers-finished counter (zero between calls)
   uint32_t ws_ml_bytes, ws_o_bytes;
 };
 

@@ -52,20 +52,27 @@ constexpr int kWaves = 4;
 constexpr int kThreads = 64 * kWaves;
 constexpr int kHD = 256;
 constexpr int kRowDw = 26;        // one kv head of one key: 2 blocks x 13 dwords
-constexpr int kVPitchDw = 28;     // LDS pitch of a staged value row (conflict-free b128 writes)
 
-// LDS layout (bytes).  The merge area aliases the tile buffers (used after the loop).
+// Per-wave staging of one 64-key tile, in dwords; every row holds 64 keys
+// (key = position in the tile) at a pitch of 68, so 16 lanes reading 16-byte
+// pieces of 16 different rows hit 16 disjoint bank quads.
+constexpr int kKeyPitch = 68;
+constexpr int kStCodes = 0;                  // [block j][group g] rows: value code group g (3 bytes, dword-expanded)
+constexpr int kStVn = 32 * kKeyPitch;        // [block j] rows: value block norms
+constexpr int kStKn = 34 * kKeyPitch;        // [block j] rows: key block norms
+constexpr int kStCorr = 36 * kKeyPitch;      // 16 floats: per-head rescale of the accumulators
+constexpr int kStageBytes = (36 * kKeyPitch + 16) * 4;   // 9856
+
+// LDS layout (bytes).  The merge area aliases the staging areas (used after the loop).
 constexpr int kLdsLut = 0;                                   // 64 x u32 centroid pairs
-constexpr int kLdsW = 256;                                   // per wave [2][16][64] fp16
-constexpr int kLdsWBytes = 2 * 16 * kTile * 2;               // 4096
-constexpr int kLdsV = kLdsW + kWaves * kLdsWBytes;           // per wave [64][28] dwords
-constexpr int kLdsVBytes = kTile * kVPitchDw * 4;            // 7168
-constexpr int kLdsTileEnd = kLdsV + kWaves * kLdsVBytes;     // 45056
-constexpr int kLdsMergeO = kLdsW;                            // [4 waves][8 rows][256] f32
+constexpr int kLdsStage = 256;                               // per wave, kStageBytes
+constexpr int kLdsQ = kLdsStage + kWaves * kStageBytes;      // rotated query, [8][2][4][4][8] fp16
+constexpr int kLdsTileEnd = kLdsQ + 16 * 128 * 2;            // 43776
+constexpr int kLdsMergeO = kLdsStage;                        // [4 waves][8 rows][256] f32
 constexpr int kLdsMergeML = kLdsMergeO + kWaves * 8 * kHD * 4;
 constexpr int kLdsFlag = kLdsMergeML + 256 * 4;
 constexpr int kLdsTotal = (kLdsFlag + 16 > kLdsTileEnd ? kLdsFlag + 16 : kLdsTileEnd);
-static_assert(kLdsV + 16 * 128 * 4 <= kLdsTileEnd, "query scratch must fit the value area");
+static_assert(kLdsFlag + 16 <= kLdsQ, "merge area must not reach the query scratch");
 
 // merge-area float offsets (ML): m[w][8] 0, l[w][8] 32, M[8] 64, L[8] 72,
 // rescale[8] 80, weights[8][16] 96
@@ -124,8 +131,8 @@ __device__ __forceinline__ void score_group(const uint8_t* lds, const uint32_t (
       n0 = group_operand<U + 1>(lds, k0);
       n1 = group_operand<U + 1>(lds, k1);
     }
-    a0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(qa[U], b0, a0, 0, 0, 0);
-    a1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(qa[4 + U], b1, a1, 0, 0, 0);
+    a0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(b0, qa[U], a0, 0, 0, 0);
+    a1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(b1, qa[4 + U], a1, 0, 0, 0);
     __builtin_amdgcn_sched_barrier(0);
     if constexpr (U < 3) score_group<U + 1>(lds, k0, k1, qa, n0, n1, a0, a1);
   }
@@ -194,21 +201,25 @@ __device__ __forceinline__ void load_tile(__amdgpu_buffer_rsrc_t rk, __amdgpu_bu
 
 // Key visibility of one query (attention.cuh:1923-1929, 2101-2105): the
 // sink/window rule on 32-key tiles, then the tree bits for keys of the block.
+// Branch-free: every key of a tile is tested with the same instructions.
 struct KeyRule {
   int start_pos, sink, window;
-  bool has_tree;
+  bool sw, has_tree;
   uint32_t tree_bits;   // bit j: key start_pos + j is visible
   __device__ KeyRule(int start_pos_, int t_idx, int sink_, int window_, const uint32_t* tree)
-      : start_pos(start_pos_), sink(sink_), window(window_), has_tree(tree != nullptr),
-        tree_bits(tree ? tree[t_idx] : 0u) {}
+      : start_pos(start_pos_), sink(sink_), window(window_), sw(sink_ > 0 || window_ > 0),
+        has_tree(tree != nullptr), tree_bits(tree ? tree[t_idx] : 0u) {}
+  // every key of [a, b) is visible (no rule applies there)
+  __device__ __forceinline__ bool all_visible(int b) const {
+    return !sw && (!has_tree || b <= start_pos);
+  }
   __device__ __forceinline__ bool visible(int key, int active_end) const {
-    if (sink > 0 || window > 0) {
-      const int ts = key & ~31;
-      const int te = min(ts + 32, active_end);
-      if (!(ts < sink) && !(te > active_end - window)) return false;
-    }
-    if (has_tree && key >= start_pos) return (tree_bits >> (key - start_pos)) & 1u;
-    return true;
+    const int ts = key & ~31;
+    const int te = min(ts + 32, active_end);
+    const bool sw_ok = !sw | (ts < sink) | (te > active_end - window);
+    const bool tree_ok = !has_tree | (key < start_pos) |
+                         (((tree_bits >> ((key - start_pos) & 31)) & 1u) != 0u);
+    return sw_ok & tree_ok;
   }
 };
 
@@ -226,6 +237,22 @@ __device__ __forceinline__ float row16_sum(float v) {
   v += dpp_f<0x124>(v);
   v += dpp_f<0x128>(v);
   return v;
+}
+
+// Max / sum over the 4 rows of the wave (lanes l, l^16, l^32, l^48); every
+// lane receives the result.  Each gfx950 row swap leaves a lane holding its
+// own value and its partner row's value in the two registers.
+__device__ __forceinline__ float xrow_max(float v) {
+  const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  v = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+  const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
+}
+__device__ __forceinline__ float xrow_sum(float v) {
+  const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  v = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+  const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(b[0]) + __uint_as_float(b[1]);
 }
 
 // Records move between workgroups (possibly on different XCDs, whose L2s are
@@ -458,7 +485,7 @@ __global__ __launch_bounds__(kThreads, 2) void tq3_attn_kernel(AttnArgs p, uint1
     // 16 WHTs of 128 (8 heads x 2 blocks), 16 lanes each; fp16 result in LDS
     // scratch laid out [head][block][group u][octet o][8] so each lane's A
     // operand slice is one 16-byte read.
-    uint16_t* qs = reinterpret_cast<uint16_t*>(lds + kLdsV);
+    uint16_t* qs = reinterpret_cast<uint16_t*>(lds + kLdsQ);
     const int wht = threadIdx.x >> 4;
     const int part = threadIdx.x & 15;
     const int hh = wht >> 1, blk = wht & 1;
@@ -504,7 +531,7 @@ __global__ __launch_bounds__(kThreads, 2) void tq3_attn_kernel(AttnArgs p, uint1
   // qa[s], slice s = 4j+u: A row = head `col`, element i = dim 128j + 8(4*row+u) + i
   h8_t qa[8];
   {
-    const uint16_t* qs = reinterpret_cast<const uint16_t*>(lds + kLdsV);
+    const uint16_t* qs = reinterpret_cast<const uint16_t*>(lds + kLdsQ);
 #pragma unroll
     for (int s = 0; s < 8; s++) {
       const int j = s >> 2, u = s & 3;
@@ -513,112 +540,133 @@ __global__ __launch_bounds__(kThreads, 2) void tq3_attn_kernel(AttnArgs p, uint1
                       : h8_t{0, 0, 0, 0, 0, 0, 0, 0};
     }
   }
-  {
-    uint8_t* wb = lds + kLdsW + wave * kLdsWBytes;    // W rows >= gqa stay zero
-    for (int i = lane; i < kLdsWBytes / 16; i += 64)
-      *reinterpret_cast<uint4*>(wb + 16 * i) = make_uint4(0, 0, 0, 0);
-  }
-  __syncthreads();
 
   const float scale2 = p.scale_log2;
-  float m2[4], lsum[4];
-#pragma unroll
-  for (int r = 0; r < 4; r++) {
-    m2[r] = -INFINITY;
-    lsum[r] = 0.0f;
-  }
+  float m2 = -INFINITY;   // running max of head `col` (base-2 units)
+  float lsum = 0.0f;      // this lane's part of the running sum of head `col`
   f4_t acc[16];
 #pragma unroll
   for (int t = 0; t < 16; t++) acc[t] = f4_t{0.f, 0.f, 0.f, 0.f};
 
-  const int nkv = p.num_kv;
-  uint8_t* wl = lds + kLdsW + wave * kLdsWBytes;
-  uint32_t* vl = reinterpret_cast<uint32_t*>(lds + kLdsV + wave * kLdsVBytes);
+  float* st = reinterpret_cast<float*>(lds + kLdsStage + wave * kStageBytes);
+  uint32_t* stu = reinterpret_cast<uint32_t*>(st);
 
   for (int ts = lo + wave * kTile; ts < hi; ts += kWaves * kTile) {
-    if (ts != lo + wave * kTile) load_tile(rk, rv, ts, nkv, h, lane, row, col, tr);
+    const bool first = ts == lo + wave * kTile;
+    if (!first) load_tile(rk, rv, ts, p.num_kv, h, lane, row, col, tr);
     auto& kq = tr.kq;
     auto& kn = tr.kn;
 
-    // ---------------- scores ----------------
-    // D layout: lane (row, col) holds key 16g+col, heads 4*row + r
+    // ---------------- scores: D rows = keys 16g + 4*row + r, D col = head `col` ----------------
+    f4_t sa[4][2];
+#pragma unroll
+    for (int g = 0; g < 4; g++) {
+      sa[g][0] = f4_t{0.f, 0.f, 0.f, 0.f};
+      sa[g][1] = f4_t{0.f, 0.f, 0.f, 0.f};
+      score_group<0>(lds, kq[g][0], kq[g][1], qa, group_operand<0>(lds, kq[g][0]),
+                     group_operand<0>(lds, kq[g][1]), sa[g][0], sa[g][1]);
+    }
+
+    // ---------------- staging: key norms, value rows (lane = key ts + lane) ----------------
+    if (row == 0) {
+#pragma unroll
+      for (int g = 0; g < 4; g++) {
+        st[kStKn + 16 * g + col] = kn[g][0];
+        st[kStKn + kKeyPitch + 16 * g + col] = kn[g][1];
+      }
+    }
+    {
+      uint32_t d[27];
+#pragma unroll
+      for (int i = 0; i < 6; i++)
+#pragma unroll
+        for (int e = 0; e < 4; e++) d[4 * i + e] = tr.vr[i][e];
+      d[24] = tr.vr6[0];
+      d[25] = tr.vr6[1];
+      d[26] = 0u;
+#pragma unroll
+      for (int j = 0; j < 2; j++) {
+        stu[kStVn + j * kKeyPitch + lane] = d[13 * j];
+#pragma unroll
+        for (int g = 0; g < 16; g++) {
+          // code group g of block j: bytes 3g..3g+2 of the codes (dword 13j+1 on)
+          const int w = 13 * j + 1 + ((3 * g) >> 2), sh = (3 * g) & 3;
+          stu[kStCodes + (16 * j + g) * kKeyPitch + lane] =
+              sh ? __builtin_amdgcn_alignbyte(d[w + 1], d[w], sh) : d[w];
+        }
+      }
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+
+    const bool dense = ts + kTile <= hi && rule.all_visible(ts + kTile);
     float s[4][4];
 #pragma unroll
     for (int g = 0; g < 4; g++) {
-      f4_t a0 = {0.f, 0.f, 0.f, 0.f}, a1 = {0.f, 0.f, 0.f, 0.f};
-      score_group<0>(lds, kq[g][0], kq[g][1], qa, group_operand<0>(lds, kq[g][0]),
-                     group_operand<0>(lds, kq[g][1]), a0, a1);
-      const int key = ts + 16 * g + col;
-      const bool vis = key < hi && rule.visible(key, active_end);   // masks padded keys too
+      const f4_t k0 = *reinterpret_cast<const f4_t*>(st + kStKn + 16 * g + 4 * row);
+      const f4_t k1 = *reinterpret_cast<const f4_t*>(st + kStKn + kKeyPitch + 16 * g + 4 * row);
 #pragma unroll
-      for (int r = 0; r < 4; r++)
-        s[g][r] = vis ? (kn[g][0] * a0[r] + kn[g][1] * a1[r]) * scale2 : -INFINITY;
-    }
-    // stage the value rows (loaded last) once the scores are done
-#pragma unroll
-    for (int i = 0; i < 6; i++) *reinterpret_cast<u4_t*>(vl + lane * kVPitchDw + 4 * i) = tr.vr[i];
-    *reinterpret_cast<u2_t*>(vl + lane * kVPitchDw + 24) = tr.vr6;
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-
-    // ---------------- online softmax (per 16-lane row = 4 heads) ----------------
-    // value-block norms of keys 16g+col from the staged rows (dwords 0 and 13)
-    float vn0[4], vn1[4];
-#pragma unroll
-    for (int g = 0; g < 4; g++) {
-      vn0[g] = __uint_as_float(vl[(16 * g + col) * kVPitchDw]);
-      vn1[g] = __uint_as_float(vl[(16 * g + col) * kVPitchDw + 13]);
-    }
-    // W rows >= gqa receive weights of all-zero query rows; they only feed
-    // accumulator rows that are never written out.
-    float corr[4];
-#pragma unroll
-    for (int r = 0; r < 4; r++) {
-      float mt = fmaxf(fmaxf(s[0][r], s[1][r]), fmaxf(s[2][r], s[3][r]));
-      mt = row16_max(mt);
-      const float mn = fmaxf(m2[r], mt);
-      corr[r] = (mn == -INFINITY) ? 1.0f : __builtin_amdgcn_exp2f(m2[r] - mn);
-      float ps = 0.f;
-      const int head = 4 * row + r;
-#pragma unroll
-      for (int g = 0; g < 4; g++) {
-        const float pr = (s[g][r] == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(s[g][r] - mn);
-        ps += pr;
-        *reinterpret_cast<uint16_t*>(wl + ((0 * 16 + head) * kTile + 16 * g + col) * 2) =
-            (uint16_t)f2h(pr * vn0[g]);
-        *reinterpret_cast<uint16_t*>(wl + ((1 * 16 + head) * kTile + 16 * g + col) * 2) =
-            (uint16_t)f2h(pr * vn1[g]);
+      for (int r = 0; r < 4; r++) {
+        const int key = ts + 16 * g + 4 * row + r;
+        const bool vis = dense || ((key < hi) & rule.visible(key, active_end));   // masks padded keys too
+        s[g][r] = vis ? (k0[r] * sa[g][0][r] + k1[r] * sa[g][1][r]) * scale2 : -INFINITY;
       }
-      lsum[r] = lsum[r] * corr[r] + row16_sum(ps);
-      m2[r] = mn;
     }
-    if (ts != lo + wave * kTile) {   // accumulators are still zero on the first tile
+
+    // ---------------- online softmax of head `col` (its 64 keys sit in 4 rows) ----------------
+    float mt = s[0][0];
+#pragma unroll
+    for (int g = 0; g < 4; g++)
+#pragma unroll
+      for (int r = 0; r < 4; r++) mt = fmaxf(mt, s[g][r]);
+    mt = xrow_max(mt);
+    const float mn = fmaxf(m2, mt);
+    const float msafe = (mn == -INFINITY) ? 0.0f : mn;   // all keys so far masked: p = 0
+    const float corr = __builtin_amdgcn_exp2f(m2 - msafe);
+    float ps = 0.0f;
+#pragma unroll
+    for (int g = 0; g < 4; g++)
+#pragma unroll
+      for (int r = 0; r < 4; r++) {
+        s[g][r] = __builtin_amdgcn_exp2f(s[g][r] - msafe);
+        ps += s[g][r];
+      }
+    lsum = lsum * corr + ps;
+    m2 = mn;
+    if (!first) {   // accumulators are still zero on the first tile
+      // accumulator rows are heads 4*row + r: their factors come from lanes 4*row + r
+      if (row == 0) st[kStCorr + col] = corr;
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+      const f4_t cr = *reinterpret_cast<const f4_t*>(st + kStCorr + 4 * row);
 #pragma unroll
       for (int t = 0; t < 16; t++)
 #pragma unroll
-        for (int r = 0; r < 4; r++) acc[t][r] *= corr[r];
+        for (int r = 0; r < 4; r++) acc[t][r] *= cr[r];
     }
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 
     // ---------------- values ----------------
-    // lane (row = key octet, col = dim group): keys 32*c2 + 8*row + i
+    // 32-key chunk c2: MFMA k index i <-> key 32*c2 + 4*row + i (i < 4) and
+    // 32*c2 + 16 + 4*row + (i - 4) (i >= 4), in both operands.  A = p * value
+    // norm (head `col`, this lane's own probabilities), B = codes of 8 keys
+    // in dim group `col`.
 #pragma unroll
     for (int c2 = 0; c2 < 2; c2++) {
 #pragma unroll
       for (int j = 0; j < 2; j++) {
-        // 3-byte code group `col` of block j of keys 32*c2+8*row+i: one
-        // unaligned LDS read each (gfx950 LDS reads at any byte address; the
-        // top byte is the next group's and is masked by the table addressing)
-        uint32_t x[8];
-        const uint8_t* vb = reinterpret_cast<const uint8_t*>(vl) + 52 * j + 4 + 3 * col;
+        const f4_t va = *reinterpret_cast<const f4_t*>(st + kStVn + j * kKeyPitch + 32 * c2 + 4 * row);
+        const f4_t vb = *reinterpret_cast<const f4_t*>(st + kStVn + j * kKeyPitch + 32 * c2 + 16 + 4 * row);
+        const u4_t xa = *reinterpret_cast<const u4_t*>(stu + kStCodes + (16 * j + col) * kKeyPitch + 32 * c2 + 4 * row);
+        const u4_t xb = *reinterpret_cast<const u4_t*>(stu + kStCodes + (16 * j + col) * kKeyPitch + 32 * c2 + 16 + 4 * row);
+        h8_t a;
 #pragma unroll
-        for (int i = 0; i < 8; i++)
-          x[i] = *reinterpret_cast<const u32_a1*>(vb + (32 * c2 + 8 * row + i) * kVPitchDw * 4);
-        const h8_t a = *reinterpret_cast<const h8_t*>(
-            wl + ((j * 16 + col) * kTile + 32 * c2 + 8 * row) * 2);
+        for (int r = 0; r < 4; r++) {
+          a[r] = (_Float16)(s[2 * c2][r] * va[r]);
+          a[4 + r] = (_Float16)(s[2 * c2 + 1][r] * vb[r]);
+        }
+        const uint32_t x[8] = {xa[0], xa[1], xa[2], xa[3], xb[0], xb[1], xb[2], xb[3]};
         value_pipe<0>(lds, x, a, acc, 8 * j);
       }
     }
@@ -626,6 +674,7 @@ __global__ __launch_bounds__(kThreads, 2) void tq3_attn_kernel(AttnArgs p, uint1
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
   }
+  lsum = xrow_sum(lsum);
 
   // ---------------- merge the 4 waves in LDS ----------------
   __syncthreads();
@@ -638,13 +687,10 @@ __global__ __launch_bounds__(kThreads, 2) void tq3_attn_kernel(AttnArgs p, uint1
 #pragma unroll
       for (int r = 0; r < 4; r++)
         mo[(wave * 8 + 4 * row + r) * kHD + 128 * (t >> 3) + 8 * col + (t & 7)] = acc[t][r];
-    if (col == 0) {
-#pragma unroll
-      for (int r = 0; r < 4; r++) {
-        ml[wave * 8 + 4 * row + r] = m2[r];
-        ml[32 + wave * 8 + 4 * row + r] = lsum[r];
-      }
-    }
+  }
+  if (row == 0 && col < 8) {
+    ml[wave * 8 + col] = m2;
+    ml[32 + wave * 8 + col] = lsum;
   }
   __syncthreads();
   const int rows = min(gqa, 8);
@@ -687,7 +733,7 @@ __global__ __launch_bounds__(kThreads, 2) void tq3_attn_kernel(AttnArgs p, uint1
     store_record(lds, p, rml, ro, h, t_idx, rows, chunk);
     __builtin_amdgcn_s_waitcnt(0);  // this thread's record stores are complete
     __syncthreads();
-    if (threadIdx.x == 0) atomicAdd(&arrive[0], 1);
+    if (threadIdx.x == 0) atomicAdd(&arrive[(blockIdx.x % kArriveSlots) * kArriveStride], 1);
   }
   // the last n_mergers workgroups of the grid merge the (q head, query, block) units
   const int n_units = p.num_q * p.sub_n * 2;
@@ -696,13 +742,21 @@ __global__ __launch_bounds__(kThreads, 2) void tq3_attn_kernel(AttnArgs p, uint1
   if (mid < 0) return;
   const int n_records = p.num_kv * p.sub_n * p.n_chunks;
   int* flag = reinterpret_cast<int*>(lds + kLdsFlag);
-  if (threadIdx.x == 0) {
+  if (wave == 0) {
     int spins = 0;
-    while (coherent_load_int(&arrive[0]) < n_records && spins < kMergeSpinLimit) {
+    bool complete = false;
+    while (spins < kMergeSpinLimit) {
+      int c = lane < kArriveSlots ? coherent_load_int(&arrive[lane * kArriveStride]) : 0;
+#pragma unroll
+      for (int o = 32; o > 0; o >>= 1) c += __shfl_xor(c, o);
+      if (c >= n_records) {
+        complete = true;
+        break;
+      }
       __builtin_amdgcn_s_sleep(1);
       spins++;
     }
-    flag[0] = spins < kMergeSpinLimit;
+    if (lane == 0) flag[0] = complete;
   }
   __syncthreads();
   if (flag[0]) {
@@ -712,13 +766,13 @@ __global__ __launch_bounds__(kThreads, 2) void tq3_attn_kernel(AttnArgs p, uint1
     }
   }
   __syncthreads();
-  if (threadIdx.x == 0) {
-    const int done = atomicAdd(&arrive[1], 1);
-    if (done == n_mergers - 1) {    // every merger is past its wait: reset for the next call
-      atomicExch(&arrive[0], 0);
-      atomicExch(&arrive[1], 0);
-    }
-  }
+  int* finished = &arrive[kArriveSlots * kArriveStride];
+  if (threadIdx.x == 0) flag[1] = atomicAdd(finished, 1) == n_mergers - 1;
+  __syncthreads();
+  // every merger is past its wait: the last one resets the counters for the next call
+  if (flag[1] && threadIdx.x <= kArriveSlots)
+    __hip_atomic_store(&arrive[threadIdx.x * kArriveStride], 0, __ATOMIC_RELAXED,
+                       __HIP_MEMORY_SCOPE_AGENT);
 }
 
 size_t tq3_attn_lds_bytes() { return kLdsTotal; }

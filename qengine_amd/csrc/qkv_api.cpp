@@ -194,7 +194,7 @@ FastGeom fast_geom(int num_q, int num_kv, int sub_n, int n_keys) {
   g.n_slots = g.n_chunks;
   const size_t rows = (size_t)num_q * sub_n * g.n_slots;
   g.tickets_off = 0;
-  g.ml_off = 256;                                    // two arrival counters
+  g.ml_off = qkv::kTicketBytes;                      // arrival counters
   (void)num_kv;
   g.o_off = (g.ml_off + rows * 2 * sizeof(float) + 255) & ~(size_t)255;
   g.total = g.o_off + rows * 256 * sizeof(float);
