@@ -10,8 +10,10 @@ them.  A step = one decode token: decode attention over all 8 layers.
 
 Prints one JSON line (value = microseconds per token, lower is better) with:
   roofline      HBM roofline of the attention kernel: algorithmic bytes per
-                launch / its average duration (HIP events around each launch,
-                on the launch stream), against 8 TB/s
+                launch / its average duration (HIP events on the launch stream
+                around the timed region, which holds only these launches),
+                against 8 TB/s; traffic = HBM bytes per launch from rocprofv3
+                counters (profiles/traffic.json)
   append        TQ3 append (K+V) throughput of the cache build
   cpu_baseline  the CPU oracle (C port of the reference arithmetic, OpenMP)
                 on a bounded sample: one decode token over the 8 layers
@@ -33,6 +35,7 @@ BLOCKS_PER_TOKEN = NUM_KV * HD // 128              # 8 TQ3 blocks per token for 
 # algorithmic bytes per layer and query token: K+V blocks + Q + O
 ATTN_BYTES = CTX * 2 * BLOCKS_PER_TOKEN * 52 + NUM_Q * HD * 2 * 2
 APPEND_BYTES_PER_TOKEN = 2 * NUM_KV * HD * 2 + 2 * BLOCKS_PER_TOKEN * 52   # 4928
+CPU_REPS = 5
 
 
 def parse():
@@ -80,25 +83,24 @@ def main():
     gen = torch.Generator(device=dev).manual_seed(3)
     stream = torch.cuda.current_stream()
 
-    # ---- cache build with the append kernel (timed: append throughput) ----
+    # ---- cache build with the append kernel (timed: append throughput of the
+    # 8 back-to-back K+V appends of each set) ----
     caches, append_ms = [], 0.0
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     for s in range(SETS):
-        layers = []
-        for l in range(LAYERS):
-            k16 = outlier_kv(torch, gen, CTX, dev)
-            v16 = outlier_kv(torch, gen, CTX, dev)
-            kb = kvcache.tq3_blocks(CTX * BLOCKS_PER_TOKEN, dev)
-            vb = kvcache.tq3_blocks(CTX * BLOCKS_PER_TOKEN, dev)
-            torch.cuda.synchronize()
-            e0.record(stream)
+        src = [(outlier_kv(torch, gen, CTX, dev), outlier_kv(torch, gen, CTX, dev))
+               for _ in range(LAYERS)]
+        layers = [(kvcache.tq3_blocks(CTX * BLOCKS_PER_TOKEN, dev),
+                   kvcache.tq3_blocks(CTX * BLOCKS_PER_TOKEN, dev)) for _ in range(LAYERS)]
+        torch.cuda.synchronize()
+        e0.record(stream)
+        for (k16, v16), (kb, vb) in zip(src, layers):
             kvcache.tq3_append_kv(k16, v16, kb, vb)
-            e1.record(stream)
-            torch.cuda.synchronize()
-            append_ms += e0.elapsed_time(e1)
-            layers.append((kb, vb))
-            del k16, v16
+        e1.record(stream)
+        torch.cuda.synchronize()
+        append_ms += e0.elapsed_time(e1)
         caches.append(layers)
+        del src
     append_tok_layers = SETS * LAYERS * CTX
     append_s = append_ms * 1e-3
     q = [torch.randn(1, NUM_Q, HD, generator=gen, device=dev).to(torch.float16)
@@ -133,7 +135,12 @@ def main():
     ms_per_step = t0.elapsed_time(t1) / args.steps
     us_per_token = ms_per_step * 1e3
 
-    # ---- per-launch durations of the attention kernel (events on its stream) ----
+    # ---- roofline: the timed region holds only attention launches (LAYERS per
+    # step, back to back on `stream`), so its events give the kernel's average
+    # launch duration directly ----
+    launch_ms = ms_per_step / LAYERS
+    achieved = ATTN_BYTES / (launch_ms * 1e-3) / 1e9
+    # isolated launches (an event pair around each), for reference
     n_launch = min(args.steps, 40) * LAYERS
     evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
            for _ in range(n_launch)]
@@ -144,8 +151,6 @@ def main():
         b.record(stream)
     torch.cuda.synchronize()
     durs = sorted(a.elapsed_time(b) for a, b in evs)
-    launch_ms = sum(durs) / len(durs)
-    achieved = ATTN_BYTES / (launch_ms * 1e-3) / 1e9
 
     traffic = None
     tpath = os.path.join(ROOT, "profiles", "traffic.json")
@@ -164,7 +169,7 @@ def main():
                  caches[0][l][1].cpu().numpy().view(O.BLOCK_TQ3).reshape(-1),
                  q[l].cpu().numpy().view(np.uint16)) for l in range(LAYERS)]
         times = []
-        for rep in range(2):
+        for rep in range(CPU_REPS):
             t = time.perf_counter()
             for kb, vb, qh in host:
                 pm, pl, po = O.attn_split(O.KV_TQ3, qh, kb, vb, num_q=NUM_Q, num_kv=NUM_KV,
@@ -176,7 +181,7 @@ def main():
             times.append(time.perf_counter() - t)
         cpu_us = min(times) * 1e6
         cpu = {"value": round(cpu_us, 1), "unit": "us/token", "cores": cores, "kind": "port",
-               "sample": "1 decode token x 8 layers at 32768 ctx (2 reps, best), oracle C "
+               "sample": f"1 decode token x 8 layers at 32768 ctx ({CPU_REPS} reps, best), oracle C "
                          "port of the reference split-K decode, OpenMP over (kv head, split)",
                "gbps": round(ATTN_BYTES * LAYERS / (cpu_us * 1e-6) / 1e9, 3)}
 
@@ -203,7 +208,7 @@ def main():
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
                      "traffic": traffic, "kernel": "tq3_attn_kernel<0>",
                      "avg_launch_us": round(launch_ms * 1e3, 3),
-                     "median_launch_us": round(durs[len(durs) // 2] * 1e3, 3)},
+                     "isolated_launch_median_us": round(durs[len(durs) // 2] * 1e3, 3)},
         "append": {"mtok_layers_per_s": round(append_tok_layers / append_s / 1e6, 1),
                    "gbps": round(append_tok_layers * APPEND_BYTES_PER_TOKEN / append_s / 1e9, 1),
                    "frac": round(append_tok_layers * APPEND_BYTES_PER_TOKEN / append_s / 1e9
