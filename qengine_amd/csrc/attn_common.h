@@ -9,12 +9,13 @@ namespace qkv {
 constexpr float kLn2 = 0.69314718055994531f;
 constexpr float kLog2e = 1.44269504088896341f;
 
-// Fast-path arrival counters: workgroup b counts itself in slot b % kArriveSlots
-// (one 128-byte line each, so arrivals do not queue on a single address); the
-// mergers-finished counter follows the slots.
-constexpr int kArriveSlots = 32;
-constexpr int kArriveStride = 32;   // ints
-constexpr int kTicketBytes = ((kArriveSlots + 1) * kArriveStride * 4 + 255) & ~255;
+// Fast-path workspace header: the launch epoch (records of the current call
+// carry tag epoch + 1) and, one 128-byte line further, the count of merger
+// workgroups that finished (the last one advances the epoch and resets it).
+constexpr int kWsEpoch = 0;          // ints
+constexpr int kWsFinished = 32;      // ints
+constexpr int kWsHeaderBytes = 256;
+constexpr int kRecMlBytes = 16;      // {m, l, tag, 0} per record
 
 struct AttnArgs {
   const uint16_t* q;        // [sub_n][num_q][256] fp16
@@ -36,9 +37,9 @@ struct AttnArgs {
   float* part_l;
   float* part_o;
   // fast-path workspace
-  float* ws_ml;             // [num_q][sub_n][n_slots][2] (m in log2 units, l)
+  float* ws_ml;             // [num_q][sub_n][n_slots] x {m (log2 units), l, tag, 0}
   float* ws_o;              // [num_q][sub_n][n_slots][256] rotated coordinates
-  int* tickets;             // arrival counters, then the mergers-finished counter (zero between calls)
+  int* ws_header;           // epoch, finished-merger count (kWsHeaderBytes)
   uint32_t ws_ml_bytes, ws_o_bytes;
 };
 
@@ -86,16 +87,39 @@ __device__ __forceinline__ void wht8_inreg(float (&x)[8]) {
       }
 }
 
-__device__ __forceinline__ void wht_xor_lanes16(float (&x)[8], int lane) {
-#pragma unroll
-  for (int m = 1; m < 16; m <<= 1) {
-    const bool upper = (lane & m) != 0;
-#pragma unroll
-    for (int i = 0; i < 8; i++) {
-      const float o = __shfl_xor(x[i], m);
-      x[i] = upper ? (o - x[i]) : (x[i] + o);
-    }
+// Value of lane (lane ^ M) inside each 16-lane row, through DPP (no LDS):
+// quad_perm for M = 1, 2; row_ror:8 for M = 8; for M = 4 lanes with bit 2 set
+// take row_ror:4 (lane - 4), the others row_ror:12 (lane + 4).
+template <int M>
+__device__ __forceinline__ float xor16_partner(float v, int lane) {
+  if constexpr (M == 1) return dpp_f<0xB1>(v);
+  else if constexpr (M == 2) return dpp_f<0x4E>(v);
+  else if constexpr (M == 8) return dpp_f<0x128>(v);
+  else {
+    // both moves run on every lane (a DPP move reading a lane that is
+    // inactive at that point returns the lane's own value)
+    const float from_lower = dpp_f<0x124>(v), from_upper = dpp_f<0x12C>(v);
+    return (lane & 4) ? from_lower : from_upper;
   }
+}
+
+template <int M>
+__device__ __forceinline__ void wht_xor_stage(float (&x)[8], int lane) {
+  const bool upper = (lane & M) != 0;
+#pragma unroll
+  for (int i = 0; i < 8; i++) {
+    const float o = xor16_partner<M>(x[i], lane);
+    x[i] = upper ? (o - x[i]) : (x[i] + o);
+  }
+}
+
+// Butterfly stages 8..64 of a 128-point WHT spread over 16 lanes x 8 elements
+// (lane = element octet): stage 8*M pairs lane with lane ^ M.
+__device__ __forceinline__ void wht_xor_lanes16(float (&x)[8], int lane) {
+  wht_xor_stage<1>(x, lane);
+  wht_xor_stage<2>(x, lane);
+  wht_xor_stage<4>(x, lane);
+  wht_xor_stage<8>(x, lane);
 }
 
 hipError_t launch_tq3_attn(const AttnArgs& a, int mode, uint16_t* out, hipStream_t stream);

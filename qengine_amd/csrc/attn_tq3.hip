@@ -48,10 +48,9 @@ typedef float f2_t __attribute__((ext_vector_type(2)));
 constexpr int kBufferRsrcWord3 = 0x00020000;
 
 constexpr int kTile = 64;
-constexpr int kWaves = 4;
+constexpr int kWaves = 8;
 constexpr int kThreads = 64 * kWaves;
 constexpr int kHD = 256;
-constexpr int kRowDw = 26;        // one kv head of one key: 2 blocks x 13 dwords
 
 // Per-wave staging of one 64-key tile, in dwords; every row holds 64 keys
 // (key = position in the tile) at a pitch of 68, so 16 lanes reading 16-byte
@@ -70,13 +69,13 @@ constexpr int kLdsQ = kLdsStage + kWaves * kStageBytes;      // rotated query, [
 constexpr int kLdsTileEnd = kLdsQ + 16 * 128 * 2;            // 43776
 constexpr int kLdsMergeO = kLdsStage;                        // [4 waves][8 rows][256] f32
 constexpr int kLdsMergeML = kLdsMergeO + kWaves * 8 * kHD * 4;
-constexpr int kLdsFlag = kLdsMergeML + 256 * 4;
-constexpr int kLdsTotal = (kLdsFlag + 16 > kLdsTileEnd ? kLdsFlag + 16 : kLdsTileEnd);
-static_assert(kLdsFlag + 16 <= kLdsQ, "merge area must not reach the query scratch");
+constexpr int kLdsMergeEnd = kLdsMergeML + 256 * 4;
+constexpr int kLdsTotal = kLdsTileEnd;
+static_assert(kLdsMergeEnd <= kLdsQ, "merge area must not reach the query scratch");
 
-// merge-area float offsets (ML): m[w][8] 0, l[w][8] 32, M[8] 64, L[8] 72,
-// rescale[8] 80, weights[8][16] 96
-constexpr int kMlM = 64, kMlL = 72, kMlC = 80, kMlW = 96;
+// merge-area float offsets (ML): m[w][8], l[w][8], M[8], L[8]
+constexpr int kMlW0 = 0, kMlLw0 = 8 * kWaves, kMlM = 16 * kWaves, kMlL = 16 * kWaves + 8;
+static_assert(kMlL + 8 <= 256, "merge scalars must fit the ML area");
 
 __device__ __forceinline__ uint32_t lut_read(const uint8_t* lds, uint32_t addr) {
   return *reinterpret_cast<const uint32_t*>(lds + addr);
@@ -256,86 +255,121 @@ __device__ __forceinline__ float xrow_sum(float v) {
 }
 
 // Records move between workgroups (possibly on different XCDs, whose L2s are
-// not coherent with each other) with 16-byte buffer accesses carrying the
-// sc0|sc1 cache policy: stores write through to the device coherence point
-// and loads read from it.  A writer waits for its stores to complete
-// (s_waitcnt vmcnt(0)) before counting itself in; a merger reads records only
-// after it has seen the full count.  No workgroup pays an L2 write-back or
-// invalidate (what agent-scope fences cost on this GPU).
+// not coherent with each other) with buffer accesses carrying the sc0|sc1
+// cache policy: stores write through to the device coherence point and loads
+// read from it.  A writer stores a record's data, waits for those stores to
+// complete (s_waitcnt vmcnt(0)) and only then stores the record's tag; a
+// merger loads a record's data only after it has read the tag.  No workgroup
+// pays an L2 write-back or invalidate (what agent-scope fences cost on this
+// GPU), and no arrival counter is contended.
 constexpr int kCoherent = 1 | 16;   // sc0 | sc1
 
-__device__ __forceinline__ int coherent_load_int(int* p) {
-  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
 
 // Record index of (q head, query t, chunk) in the fast-path workspace.
 __device__ __forceinline__ long rec_index(const AttnArgs& p, int qh, int t, int chunk) {
   return (long)(qh * p.sub_n + t) * p.n_slots + chunk;
 }
 
-// Spin limit of a merger waiting for the records of one launch (each poll
-// sleeps ~64 cycles; the limit is seconds, far beyond any legitimate wait).
-constexpr int kMergeSpinLimit = 1 << 24;
+// Merger thread layout: kSlices record slices of 32 threads (one dim quad of
+// a 128-block each), kRecPerThread records per thread (n_chunks <= 128); the
+// LDS reduction area holds [kSlices][128] sums, then maxima, sums of l and
+// the 128 merged dims.
+constexpr int kSlices = kThreads / 32;
+constexpr int kRecPerThread = 128 / kSlices;
+constexpr int kRedM = kSlices * 128, kRedL = kRedM + kSlices, kRedSum = kRedL + kSlices;
+static_assert(kLdsMergeO + (kRedSum + 128) * 4 <= kLdsMergeML, "merge reduction must fit");
+
+// Poll limit of a merger waiting for the records of one launch (each poll
+// sleeps ~64 cycles after two memory round trips; the limit is seconds, far
+// beyond any legitimate wait).
+constexpr int kMergeSpinLimit = 1 << 22;
 
 // Merge all chunk records (n_chunks <= 128) of one unit (q head qh, query t,
 // 128-block blk) and write its fp16 output o = rs*D*H*(sum w_c o_c / sum w_c l_c).
-// Thread = (record slice sl = tid/32 of 8, dim quad dq = tid%32) with records
-// sl, sl+8, ...: all loads are issued in one round.
-__device__ void merge_unit(uint8_t* lds, const AttnArgs& p, __amdgpu_buffer_rsrc_t rml,
-                           __amdgpu_buffer_rsrc_t ro, int qh, int t, int blk, uint16_t* out) {
-  float* red = reinterpret_cast<float*>(lds + kLdsMergeO);   // [8][128] sums, then scalars
+// 1. Threads 0..n-1 poll one record each ({m, l, tag} in one 16-byte load)
+//    until every tag is current; m and l go to LDS.
+// 2. Thread (record slice sl = tid/32, dim quad dq = tid%32) loads the
+//    rotated rows of records sl, sl+kSlices, ... in one round and merges them.
+// Returns false (and writes nothing) if the records did not all appear within
+// the poll limit.
+__device__ bool merge_unit(uint8_t* lds, const AttnArgs& p, __amdgpu_buffer_rsrc_t rml,
+                           __amdgpu_buffer_rsrc_t ro, int qh, int t, int blk, uint32_t tag,
+                           uint16_t* out) {
+  float* red = reinterpret_cast<float*>(lds + kLdsMergeO);   // [kSlices][128] sums, scalars after
+  f2_t* mls = reinterpret_cast<f2_t*>(lds + kLdsMergeML);     // [128] {m, l} of the records
   const int tid = threadIdx.x;
   const int sl = tid >> 5, dq = tid & 31;
   const int n = p.n_chunks;
   const long base = rec_index(p, qh, t, 0);
-  f2_t ml[16];
-  f4_t v[16];
-#pragma unroll
-  for (int i = 0; i < 16; i++) {
-    const int c = sl + 8 * i;
-    if (c < n) {
-      ml[i] = __builtin_amdgcn_raw_buffer_load_b64(rml, (uint32_t)((base + c) * 8), 0, kCoherent);
-      v[i] = __builtin_amdgcn_raw_buffer_load_b128(
-          ro, (uint32_t)(((base + c) * kHD + blk * 128 + 4 * dq) * 4), 0, kCoherent);
-    } else {
-      ml[i] = f2_t{-INFINITY, 0.f};
-      v[i] = f4_t{0.f, 0.f, 0.f, 0.f};
+  bool seen = tid >= n;
+  bool complete = false;
+  for (int spins = 0; spins < kMergeSpinLimit; spins++) {
+    if (!seen) {
+      const f4_t r = __builtin_amdgcn_raw_buffer_load_b128(
+          rml, (uint32_t)((base + tid) * kRecMlBytes), 0, kCoherent);
+      if (__float_as_uint(r[2]) == tag) {
+        seen = true;
+        mls[tid] = f2_t{r[0], r[1]};
+      }
     }
+    if (__syncthreads_and(seen)) {
+      complete = true;
+      break;
+    }
+    __builtin_amdgcn_s_sleep(1);
   }
-  float mloc = -INFINITY;
+  if (!complete) return false;
+  f4_t v[kRecPerThread];
 #pragma unroll
-  for (int i = 0; i < 16; i++)
-    if (ml[i][1] > 0.f) mloc = fmaxf(mloc, ml[i][0]);
-  if (dq == 0) red[1024 + sl] = mloc;
+  for (int i = 0; i < kRecPerThread; i++) {
+    const int c = sl + kSlices * i;
+    v[i] = c < n ? __builtin_amdgcn_raw_buffer_load_b128(
+                       ro, (uint32_t)(((base + c) * kHD + blk * 128 + 4 * dq) * 4), 0, kCoherent)
+                 : f4_t{0.f, 0.f, 0.f, 0.f};
+  }
+  // common max over all records (empty chunks, l = 0, carry no weight)
+  float M = -INFINITY;
+#pragma unroll
+  for (int i = 0; i < kRecPerThread; i++) {
+    const int c = sl + kSlices * i;
+    if (c < n && mls[c][1] > 0.f) M = fmaxf(M, mls[c][0]);
+  }
+  if (dq == 0) red[kRedM + sl] = M;
   __syncthreads();
-  float M = red[1024];
+  M = red[kRedM];
 #pragma unroll
-  for (int k = 1; k < 8; k++) M = fmaxf(M, red[1024 + k]);
+  for (int k = 1; k < kSlices; k++) M = fmaxf(M, red[kRedM + k]);
   f4_t acc = {0.f, 0.f, 0.f, 0.f};
   float L = 0.f;
 #pragma unroll
-  for (int i = 0; i < 16; i++) {
-    const float w = (ml[i][1] > 0.f) ? __builtin_amdgcn_exp2f(ml[i][0] - M) : 0.f;
-    L += w * ml[i][1];
-    acc += w * v[i];
+  for (int i = 0; i < kRecPerThread; i++) {
+    const int c = sl + kSlices * i;
+    if (c < n && mls[c][1] > 0.f) {
+      const float w = __builtin_amdgcn_exp2f(mls[c][0] - M);
+      L += w * mls[c][1];
+      acc += w * v[i];
+    }
   }
   *reinterpret_cast<f4_t*>(&red[sl * 128 + 4 * dq]) = acc;
-  if (dq == 0) red[1032 + sl] = L;
+  if (dq == 0) red[kRedL + sl] = L;
+  __syncthreads();
+  // sum the slices: thread d < 128 owns dim d
+  if (tid < 128) {
+    float sum = 0.f;
+#pragma unroll
+    for (int k = 0; k < kSlices; k++) sum += red[k * 128 + tid];
+    red[kRedSum + tid] = sum;
+  }
   __syncthreads();
   // rotate back: 16 lanes x 8 elements (threads 0..15)
   if (tid < 16) {
     float Lt = 0.f;
 #pragma unroll
-    for (int k = 0; k < 8; k++) Lt += red[1032 + k];
+    for (int k = 0; k < kSlices; k++) Lt += red[kRedL + k];
     const float inv = Lt > 0.f ? 1.0f / Lt : 0.f;
     float x[8];
 #pragma unroll
-    for (int i = 0; i < 8; i++) {
-      float sum = 0.f;
-#pragma unroll
-      for (int k = 0; k < 8; k++) sum += red[k * 128 + tid * 8 + i];
-      x[i] = sum * inv;
-    }
+    for (int i = 0; i < 8; i++) x[i] = red[kRedSum + tid * 8 + i] * inv;
     wht8_inreg(x);
     wht_xor_lanes16(x, tid);
     const float rs = wht_scale();
@@ -356,11 +390,14 @@ __device__ void merge_unit(uint8_t* lds, const AttnArgs& p, __amdgpu_buffer_rsrc
         make_uint4(pk[0], pk[1], pk[2], pk[3]);
   }
   __syncthreads();
+  return true;
 }
 
-// Store the merged rows in LDS as this workgroup's records (rotated).
+// Store the merged rows in LDS as this workgroup's records (rotated): data
+// first, then (once every thread's data stores are complete) the tags.
 __device__ void store_record(const uint8_t* lds, const AttnArgs& p, __amdgpu_buffer_rsrc_t rml,
-                             __amdgpu_buffer_rsrc_t ro, int h, int t, int rows, int chunk) {
+                             __amdgpu_buffer_rsrc_t ro, int h, int t, int rows, int chunk,
+                             uint32_t tag) {
   const float* mo = reinterpret_cast<const float*>(lds + kLdsMergeO);
   const float* mlv = reinterpret_cast<const float*>(lds + kLdsMergeML);
   const int gqa = p.num_q / p.num_kv;
@@ -371,8 +408,14 @@ __device__ void store_record(const uint8_t* lds, const AttnArgs& p, __amdgpu_buf
                                            (uint32_t)((rec * kHD + d4) * 4), 0, kCoherent);
     if (d4 == 0)
       __builtin_amdgcn_raw_buffer_store_b64(f2_t{mlv[kMlM + r], mlv[kMlL + r]}, rml,
-                                            (uint32_t)(rec * 8), 0, kCoherent);
+                                            (uint32_t)(rec * kRecMlBytes), 0, kCoherent);
   }
+  __builtin_amdgcn_s_waitcnt(0);  // this thread's data stores are complete
+  __syncthreads();
+  if ((int)threadIdx.x < rows)
+    __builtin_amdgcn_raw_buffer_store_b32(
+        tag, rml, (uint32_t)(rec_index(p, h * gqa + threadIdx.x, t, chunk) * kRecMlBytes + 8), 0,
+        kCoherent);
 }
 
 // Rotate the merged rows back (o = rs*D*H*o_rot per 128-block).  final: divide
@@ -428,7 +471,7 @@ __device__ void finish_rows(const uint8_t* lds, const AttnArgs& p, int h, int t,
 
 // MODE 0: fast path (final fp16 rows).  MODE 1: reference split partials.
 template <int MODE>
-__global__ __launch_bounds__(kThreads, 2) void tq3_attn_kernel(AttnArgs p, uint16_t* out) {
+__global__ __launch_bounds__(kThreads, 1) void tq3_attn_kernel(AttnArgs p, uint16_t* out) {
   // static LDS: table and tile offsets fold into the instructions' offset field
   __shared__ __attribute__((aligned(16))) uint8_t lds[kLdsTotal];
   const int lane = threadIdx.x & 63;
@@ -463,6 +506,11 @@ __global__ __launch_bounds__(kThreads, 2) void tq3_attn_kernel(AttnArgs p, uint1
     hi = min((chunk + 1) * tps * 32, active_end);
   }
   const KeyRule rule(p.start_pos, t_idx, p.sink_tok, p.window_tok, p.tree_mask);
+  // launch epoch of the fast-path workspace (records of this call carry epoch + 1)
+  const uint32_t epoch =
+      MODE == 0 ? (uint32_t)__hip_atomic_load(&p.ws_header[kWsEpoch], __ATOMIC_RELAXED,
+                                              __HIP_MEMORY_SCOPE_AGENT)
+                : 0u;
   const int row = lane >> 4;        // 16-lane row of the MFMA D layout
   const int col = lane & 15;
 
@@ -482,7 +530,7 @@ __global__ __launch_bounds__(kThreads, 2) void tq3_attn_kernel(AttnArgs p, uint1
   }
   TileRegs tr;
   {
-    // 16 WHTs of 128 (8 heads x 2 blocks), 16 lanes each; fp16 result in LDS
+    // 16 WHTs of 128 (8 heads x 2 blocks), 16 lanes each (threads 0..255); fp16 result in LDS
     // scratch laid out [head][block][group u][octet o][8] so each lane's A
     // operand slice is one 16-byte read.
     uint16_t* qs = reinterpret_cast<uint16_t*>(lds + kLdsQ);
@@ -523,8 +571,9 @@ __global__ __launch_bounds__(kThreads, 2) void tq3_attn_kernel(AttnArgs p, uint1
       for (int i = 0; i < 4; i++) pk[i] = f2h(x[2 * i] * rs) | (f2h(x[2 * i + 1] * rs) << 16);
       // elements part*8..+7 = dims of code group `part` = 4*o + u
       const int o = part >> 2, u = part & 3;
-      *reinterpret_cast<uint4*>(qs + (((hh * 2 + blk) * 4 + u) * 4 + o) * 8) =
-          make_uint4(pk[0], pk[1], pk[2], pk[3]);
+      if (wht < 16)   // threads past the 8 heads x 2 blocks have no piece
+        *reinterpret_cast<uint4*>(qs + (((hh * 2 + blk) * 4 + u) * 4 + o) * 8) =
+            make_uint4(pk[0], pk[1], pk[2], pk[3]);
     }
   }
   __syncthreads();
@@ -680,7 +729,7 @@ __global__ __launch_bounds__(kThreads, 2) void tq3_attn_kernel(AttnArgs p, uint1
   __syncthreads();
   float* mo = reinterpret_cast<float*>(lds + kLdsMergeO);    // [wave][8][256]
   float* ml = reinterpret_cast<float*>(lds + kLdsMergeML);
-  if (row < 2) {
+  if (4 * row < gqa) {   // accumulator rows 4*row + r hold heads; rows >= gqa are unused
     // acc tile t: rows 4*row+r, dim 128*(t>>3) + 8*col + (t&7)
 #pragma unroll
     for (int t = 0; t < 16; t++)
@@ -689,8 +738,8 @@ __global__ __launch_bounds__(kThreads, 2) void tq3_attn_kernel(AttnArgs p, uint1
         mo[(wave * 8 + 4 * row + r) * kHD + 128 * (t >> 3) + 8 * col + (t & 7)] = acc[t][r];
   }
   if (row == 0 && col < 8) {
-    ml[wave * 8 + col] = m2;
-    ml[32 + wave * 8 + col] = lsum;
+    ml[kMlW0 + wave * 8 + col] = m2;
+    ml[kMlLw0 + wave * 8 + col] = lsum;
   }
   __syncthreads();
   const int rows = min(gqa, 8);
@@ -698,13 +747,13 @@ __global__ __launch_bounds__(kThreads, 2) void tq3_attn_kernel(AttnArgs p, uint1
     const int r = idx >> 6, d4 = (idx & 63) * 4;
     float M = -INFINITY;
 #pragma unroll
-    for (int w = 0; w < kWaves; w++) M = fmaxf(M, ml[w * 8 + r]);
+    for (int w = 0; w < kWaves; w++) M = fmaxf(M, ml[kMlW0 + w * 8 + r]);
     float L = 0.f, o[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int w = 0; w < kWaves; w++) {
-      const float mw = ml[w * 8 + r];
+      const float mw = ml[kMlW0 + w * 8 + r];
       const float wt = (mw == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(mw - M);
-      L += wt * ml[32 + w * 8 + r];
+      L += wt * ml[kMlLw0 + w * 8 + r];
 #pragma unroll
       for (int i = 0; i < 4; i++) o[i] += wt * mo[(w * 8 + r) * kHD + d4 + i];
     }
@@ -723,56 +772,31 @@ __global__ __launch_bounds__(kThreads, 2) void tq3_attn_kernel(AttnArgs p, uint1
   }
 
 
-  // ---------------- fast path: records, arrival count, designated mergers ----------------
-  int* arrive = p.tickets;          // [0] records written, [1] mergers finished
+  // ---------------- fast path: tagged records, designated mergers ----------------
   const __amdgpu_buffer_rsrc_t rml =
       __builtin_amdgcn_make_buffer_rsrc(p.ws_ml, 0, p.ws_ml_bytes, kBufferRsrcWord3);
   const __amdgpu_buffer_rsrc_t ro =
       __builtin_amdgcn_make_buffer_rsrc(p.ws_o, 0, p.ws_o_bytes, kBufferRsrcWord3);
-  if (has_work) {
-    store_record(lds, p, rml, ro, h, t_idx, rows, chunk);
-    __builtin_amdgcn_s_waitcnt(0);  // this thread's record stores are complete
-    __syncthreads();
-    if (threadIdx.x == 0) atomicAdd(&arrive[(blockIdx.x % kArriveSlots) * kArriveStride], 1);
-  }
+  const uint32_t tag = epoch + 1u;
+  if (has_work) store_record(lds, p, rml, ro, h, t_idx, rows, chunk, tag);
   // the last n_mergers workgroups of the grid merge the (q head, query, block) units
   const int n_units = p.num_q * p.sub_n * 2;
   const int n_mergers = min(n_units, (int)gridDim.x);
   const int mid = (int)blockIdx.x - ((int)gridDim.x - n_mergers);
   if (mid < 0) return;
-  const int n_records = p.num_kv * p.sub_n * p.n_chunks;
-  int* flag = reinterpret_cast<int*>(lds + kLdsFlag);
-  if (wave == 0) {
-    int spins = 0;
-    bool complete = false;
-    while (spins < kMergeSpinLimit) {
-      int c = lane < kArriveSlots ? coherent_load_int(&arrive[lane * kArriveStride]) : 0;
-#pragma unroll
-      for (int o = 32; o > 0; o >>= 1) c += __shfl_xor(c, o);
-      if (c >= n_records) {
-        complete = true;
-        break;
-      }
-      __builtin_amdgcn_s_sleep(1);
-      spins++;
-    }
-    if (lane == 0) flag[0] = complete;
+  for (int u = mid; u < n_units; u += n_mergers) {
+    const int blk = u & 1, qh = (u >> 1) % p.num_q, t = (u >> 1) / p.num_q;
+    if (!merge_unit(lds, p, rml, ro, qh, t, blk, tag, out)) break;
   }
-  __syncthreads();
-  if (flag[0]) {
-    for (int u = mid; u < n_units; u += n_mergers) {
-      const int blk = u & 1, qh = (u >> 1) % p.num_q, t = (u >> 1) / p.num_q;
-      merge_unit(lds, p, rml, ro, qh, t, blk, out);
+  // every merger is past its records: the last one advances the epoch (all
+  // workgroups of this launch have read it) and resets the count
+  if (threadIdx.x == 0) {
+    const int done = atomicAdd(&p.ws_header[kWsFinished], 1);
+    if (done == n_mergers - 1) {
+      __hip_atomic_store(&p.ws_header[kWsFinished], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(&p.ws_header[kWsEpoch], (int)tag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
   }
-  __syncthreads();
-  int* finished = &arrive[kArriveSlots * kArriveStride];
-  if (threadIdx.x == 0) flag[1] = atomicAdd(finished, 1) == n_mergers - 1;
-  __syncthreads();
-  // every merger is past its wait: the last one resets the counters for the next call
-  if (flag[1] && threadIdx.x <= kArriveSlots)
-    __hip_atomic_store(&arrive[threadIdx.x * kArriveStride], 0, __ATOMIC_RELAXED,
-                       __HIP_MEMORY_SCOPE_AGENT);
 }
 
 size_t tq3_attn_lds_bytes() { return kLdsTotal; }

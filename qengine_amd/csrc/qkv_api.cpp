@@ -107,7 +107,7 @@ int qkv_q8_dequant(const qkv_block_q8* in, uint16_t* out_f16, int n_blocks, hipS
 // ---------------------------------------------------------------------------
 namespace {
 
-constexpr int kChunkKeys = 256;
+constexpr int kChunkKeys = 512;   // 8 waves x 64-key tiles
 
 int check_attn_shape(int num_q, int num_kv, int head_dim, int start_pos, int sub_n,
                      const uint32_t* tree_mask) {
@@ -181,22 +181,22 @@ int qkv_attn_split_merge(const float* part_m, const float* part_l, const float* 
 namespace {
 struct FastGeom {
   int chunk_keys, n_chunks, n_slots;
-  size_t tickets_off, ml_off, o_off, total;
+  size_t header_off, ml_off, o_off, total;
 };
-// Chunks of 256*tpw keys, at most 128 per (kv head, query): one record per
+// Chunks of 512*tpw keys, at most 128 per (kv head, query): one record per
 // chunk and q head, merged by the designated merger workgroups.
 FastGeom fast_geom(int num_q, int num_kv, int sub_n, int n_keys) {
   FastGeom g{};
-  const int c256 = (n_keys + kChunkKeys - 1) / kChunkKeys;
-  const int tpw = (c256 + 127) / 128;
+  const int c512 = (n_keys + kChunkKeys - 1) / kChunkKeys;
+  const int tpw = (c512 + 127) / 128;
   g.chunk_keys = kChunkKeys * tpw;
   g.n_chunks = (n_keys + g.chunk_keys - 1) / g.chunk_keys;
   g.n_slots = g.n_chunks;
   const size_t rows = (size_t)num_q * sub_n * g.n_slots;
-  g.tickets_off = 0;
-  g.ml_off = qkv::kTicketBytes;                      // arrival counters
+  g.header_off = 0;
+  g.ml_off = qkv::kWsHeaderBytes;
   (void)num_kv;
-  g.o_off = (g.ml_off + rows * 2 * sizeof(float) + 255) & ~(size_t)255;
+  g.o_off = (g.ml_off + rows * qkv::kRecMlBytes + 255) & ~(size_t)255;
   g.total = g.o_off + rows * 256 * sizeof(float);
   return g;
 }
@@ -246,7 +246,7 @@ int qkv_decode_attn_tq3(const uint16_t* q, const qkv_block_tq3* k, const qkv_blo
   a.sink_tok = sink_tok;
   a.window_tok = window_tok;
   a.tree_mask = tree_mask;
-  a.tickets = reinterpret_cast<int*>(ws + g.tickets_off);
+  a.ws_header = reinterpret_cast<int*>(ws + g.header_off);
   a.ws_ml = reinterpret_cast<float*>(ws + g.ml_off);
   a.ws_o = reinterpret_cast<float*>(ws + g.o_off);
   if (g.total > 0xffffffffULL) return QKV_ERR_UNSUPPORTED;   // 32-bit buffer offsets

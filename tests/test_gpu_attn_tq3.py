@@ -127,3 +127,44 @@ def test_fast_decode_rejects_small_workspace(dev):
     with pytest.raises(QKVError):
         kvcache.decode_attn_tq3(q, kv, kv, out, ws, num_q=16, num_kv=4, start_pos=99, sub_n=1,
                                 scale=1 / 16)
+
+
+def _fast_expected(q, kb, vb, n, num_q, sub_n):
+    em, el, eo = O.attn_split(O.KV_TQ3, q, kb, vb, num_q=num_q, num_kv=4, hd=256,
+                              start_pos=n - sub_n, sub_n=sub_n, sub_n_max=sub_n,
+                              active_end_max=n, scale=1 / 16, k_splits=8)
+    return O.attn_split_merge(em, el, eo, num_q=num_q, num_kv=4, hd=256, sub_n=sub_n,
+                              sub_n_max=sub_n, k_splits=8).view(np.float16)
+
+
+def test_fast_decode_workspace_reuse(dev):
+    """One workspace across calls of different lengths and query counts: each
+    call's records are told apart from earlier calls' by the launch epoch."""
+    from qengine_amd import kvcache
+    torch = _torch()
+    ws = kvcache.decode_attn_tq3_workspace(16, 4, 4, 32768, dev)
+    for i, (n, sub_n) in enumerate([(32768, 1), (4097, 1), (32768, 1), (1000, 4), (4097, 1),
+                                    (32768, 4)]):
+        rng, kb, vb = _cache(500 + i, n)
+        q = q_f16(rng, sub_n, 16, 256)
+        out = torch.zeros((sub_n, 16, 256), dtype=torch.float16, device=dev)
+        kvcache.decode_attn_tq3(_dev(q.view(np.uint16), dev), _dev(kb.view(np.uint8), dev),
+                                _dev(vb.view(np.uint8), dev), out, ws, num_q=16, num_kv=4,
+                                start_pos=n - sub_n, sub_n=sub_n, scale=1 / 16)
+        torch.cuda.synchronize()
+        assert rel_err(out.cpu().numpy(), _fast_expected(q, kb, vb, n, 16, sub_n)) < TOL, (n, sub_n)
+
+
+def test_fast_decode_output_may_alias_query(dev):
+    """The output may overwrite the query in place (model.cuh:2479-2482 merges into q_buf)."""
+    from qengine_amd import kvcache
+    torch = _torch()
+    n = 4097
+    rng, kb, vb = _cache(777, n)
+    q = q_f16(rng, 1, 16, 256)
+    qt = _dev(q.view(np.uint16), dev).view(torch.float16)
+    ws = kvcache.decode_attn_tq3_workspace(16, 4, 1, n, dev)
+    kvcache.decode_attn_tq3(qt, _dev(kb.view(np.uint8), dev), _dev(vb.view(np.uint8), dev), qt, ws,
+                            num_q=16, num_kv=4, start_pos=n - 1, sub_n=1, scale=1 / 16)
+    torch.cuda.synchronize()
+    assert rel_err(qt.cpu().numpy(), _fast_expected(q, kb, vb, n, 16, 1)) < TOL
