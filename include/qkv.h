@@ -128,6 +128,17 @@ int qkv_attn_split_tq3(const uint16_t* q, const qkv_block_tq3* k, const qkv_bloc
                        int active_end_max, float scale, int k_splits, int sink_tok,
                        int window_tok, const uint32_t* tree_mask, hipStream_t stream);
 
+/* Replaces flash_attn_chunk_fused_split_q8<256, GQA, 32, 256, K_SPLITS>
+ * <<<(num_kv, sub_n, K_SPLITS), 256>>> (attention.cuh:2633-2801; launched at
+ * model.cuh:2438-2457).  Same split rule and partial layout as
+ * qkv_attn_split_tq3; K/V elements decode to half(q*d) (no masks: the
+ * reference's Q8 kernel has none).  k, v: slot-base Q8_0 caches
+ * [pos][num_kv][8] blocks.  Merge with qkv_attn_split_merge. */
+int qkv_attn_split_q8(const uint16_t* q, const qkv_block_q8* k, const qkv_block_q8* v,
+                      float* part_m, float* part_l, float* part_o, int num_q, int num_kv,
+                      int head_dim, int start_pos, int sub_n, int sub_n_max, int active_end_max,
+                      float scale, int k_splits, hipStream_t stream);
+
 /* Replaces flash_attn_split_merge<256, GQA, 256, K_SPLITS><<<(num_kv, sub_n), 256>>>
  * (attention.cuh:1837-1891).  out [sub_n][num_q][256] fp16; may alias q of the
  * preceding split call (model.cuh:2479-2482 merges in place). */

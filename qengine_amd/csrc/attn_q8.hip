@@ -1,0 +1,321 @@
+// attn_q8.hip -- split-K flash decode over the Q8_0 KV cache (gfx950).
+//
+// Reference semantics: flash_attn_chunk_fused_split_q8 (attention.cuh:2633-2801).
+// Query t (absolute position start_pos + t) attends keys [0, start_pos + t] of
+// split z's range [z*tps*32, min((z+1)*tps*32, start_pos + t + 1)),
+// tps = ceil(ceil(active_end_max/32)/k_splits).  K and V elements decode to
+// half(q*d); scores are fp32 sums of fp16 products times `scale`; online
+// softmax; the split writes its unnormalised partials (m in natural-log
+// units, l, o[256]) in the reference layout.  Merged by attn_merge.hip.
+//
+// Design (not the reference's): one workgroup of 4 waves per (kv head,
+// query, split); each wave takes 32-key tiles.
+//   scores  v_mfma_f32_16x16x32_f16 with A = keys (16 per MFMA) decoded in
+//           registers from 72 contiguous bytes per lane (two whole Q8 blocks:
+//           lane k-group g owns blocks 2g and 2g+1, so the reduction order
+//           over dims is permuted identically in both operands) and B = the
+//           fp16 query.  D rows = keys, D cols = heads.
+//   softmax online per head, base 2, the head's max over the 4 rows through
+//           gfx950 row swaps.
+//   values  A = the lane's own probabilities (fp16), B = 8 keys x 1 dim.
+//           Value rows are staged in LDS as [dim quad][key] dwords plus
+//           [block][key] scales; a lane reads one dim quad of 8 keys and
+//           decodes it into the B operands of 4 MFMA tiles (tile 4a+e,
+//           column n = dim 64a + 4n + e).
+#include "qkv_device.h"
+#include "attn_common.h"
+
+namespace qkv {
+namespace {
+
+typedef _Float16 h8_t __attribute__((ext_vector_type(8)));
+typedef float f4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t u4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t u2_t __attribute__((ext_vector_type(2)));
+
+constexpr int kBufferRsrcWord3 = 0x00020000;   // raw buffer, 32-bit data format
+constexpr int kWaves = 4;
+constexpr int kThreads = 64 * kWaves;
+constexpr int kTile = 32;                      // keys per wave tile
+constexpr int kHD = 256;
+constexpr int kRowBytes = 288;                 // one kv head of one token: 8 blocks x 36 B
+constexpr int kPitch = kTile + 4;              // dwords per staged row of 32 keys
+
+// per-wave staging (dwords): value code quads [64][kPitch], value scales
+// [8][kPitch], per-head rescale [16]
+constexpr int kStCodes = 0;
+constexpr int kStScale = 64 * kPitch;
+constexpr int kStCorr = 72 * kPitch;
+constexpr int kStageBytes = (72 * kPitch + 16) * 4;
+constexpr int kLdsStage = 0;
+constexpr int kLdsTotalTile = kLdsStage + kWaves * kStageBytes;
+// merge area (aliases the staging): [wave][8 rows][256] f32, then scalars
+constexpr int kLdsMergeO = 0;
+constexpr int kLdsMergeML = kLdsMergeO + kWaves * 8 * kHD * 4;
+constexpr int kLdsMergeEnd = kLdsMergeML + 256 * 4;
+constexpr int kLdsTotal = kLdsMergeEnd > kLdsTotalTile ? kLdsMergeEnd : kLdsTotalTile;
+constexpr int kMlW0 = 0, kMlLw0 = 8 * kWaves;   // merge scalars: m[w][8], l[w][8]
+
+struct TileQ8 {
+  uint32_t k[2][18];   // key 16g+col: blocks 2*row and 2*row+1 (qs, pad|d, qs, pad|d)
+  u4_t v[9];           // key ts + (lane & 31): blocks 4*(lane>>5) .. +3 (36 dwords)
+};
+
+__device__ __forceinline__ void load_tile_q8(__amdgpu_buffer_rsrc_t rk, __amdgpu_buffer_rsrc_t rv,
+                                             int ts, int nkv, int h, int lane, int row, int col,
+                                             TileQ8& t) {
+#pragma unroll
+  for (int g = 0; g < 2; g++) {
+    const uint32_t off = (uint32_t)((ts + 16 * g + col) * nkv + h) * kRowBytes + 72u * row;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      const u4_t c = __builtin_amdgcn_raw_buffer_load_b128(rk, off + 16 * i, 0, 0);
+#pragma unroll
+      for (int e = 0; e < 4; e++) t.k[g][4 * i + e] = c[e];
+    }
+    const u2_t c = __builtin_amdgcn_raw_buffer_load_b64(rk, off + 64, 0, 0);
+    t.k[g][16] = c[0];
+    t.k[g][17] = c[1];
+  }
+  const uint32_t voff =
+      (uint32_t)((ts + (lane & 31)) * nkv + h) * kRowBytes + 144u * (uint32_t)(lane >> 5);
+#pragma unroll
+  for (int i = 0; i < 9; i++) t.v[i] = __builtin_amdgcn_raw_buffer_load_b128(rv, voff + 16 * i, 0, 0);
+}
+
+__device__ __forceinline__ float scale_of(uint32_t pad_d) { return h2f(pad_d >> 16); }
+
+// half(q * d) for the signed byte B of w (the fp32 product is exact)
+template <int B>
+__device__ __forceinline__ _Float16 dec(uint32_t w, float d) {
+  return (_Float16)((float)(int8_t)(w >> (8 * B)) * d);
+}
+
+// A operand of score slice s: block s>>2 of the lane's two, elements 8(s&3)..+7
+template <int S>
+__device__ __forceinline__ h8_t key_operand(const uint32_t (&k)[18]) {
+  constexpr int base = 9 * (S >> 2) + 2 * (S & 3);
+  const float d = scale_of(k[9 * (S >> 2) + 8]);
+  const uint32_t w0 = k[base], w1 = k[base + 1];
+  return h8_t{dec<0>(w0, d), dec<1>(w0, d), dec<2>(w0, d), dec<3>(w0, d),
+              dec<0>(w1, d), dec<1>(w1, d), dec<2>(w1, d), dec<3>(w1, d)};
+}
+
+__device__ __forceinline__ float xrow_max(float v) {
+  const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  v = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+  const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
+}
+__device__ __forceinline__ float xrow_sum(float v) {
+  const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  v = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+  const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(b[0]) + __uint_as_float(b[1]);
+}
+
+__device__ __forceinline__ void wave_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+__global__ __launch_bounds__(kThreads, 2) void q8_attn_split_kernel(AttnArgs p) {
+  __shared__ __attribute__((aligned(16))) uint8_t lds[kLdsTotal];
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int row = lane >> 4, col = lane & 15;
+  const int gqa = p.num_q / p.num_kv;
+
+  // work id: (kv head, query, split)
+  const int L = blockIdx.x;
+  const int h = L % p.num_kv;
+  const int t_idx = (L / p.num_kv) % p.sub_n;
+  const int split = L / (p.num_kv * p.sub_n);
+  const int active_end = p.start_pos + t_idx + 1;
+  const int total_tiles = (p.active_end_max + 31) / 32;   // attention.cuh:2660-2663
+  const int tps = (total_tiles + p.k_splits - 1) / p.k_splits;
+  const int lo = split * tps * 32;
+  const int hi = min((split + 1) * tps * 32, active_end);
+
+  const __amdgpu_buffer_rsrc_t rk =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<uint32_t*>(p.k), 0, p.kv_bytes, kBufferRsrcWord3);
+  const __amdgpu_buffer_rsrc_t rv =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<uint32_t*>(p.v), 0, p.kv_bytes, kBufferRsrcWord3);
+
+  // query operand, slice s: head `col`, dims (2*row + (s>>2))*32 + 8*(s&3) + i
+  h8_t qa[8];
+#pragma unroll
+  for (int s = 0; s < 8; s++) {
+    const int dim = (2 * row + (s >> 2)) * 32 + 8 * (s & 3);
+    qa[s] = col < gqa ? *reinterpret_cast<const h8_t*>(
+                            p.q + ((long)t_idx * p.num_q + h * gqa + col) * kHD + dim)
+                      : h8_t{0, 0, 0, 0, 0, 0, 0, 0};
+  }
+
+  const float scale2 = p.scale_log2;
+  float m2 = -INFINITY, lsum = 0.0f;
+  f4_t acc[16];
+#pragma unroll
+  for (int t = 0; t < 16; t++) acc[t] = f4_t{0.f, 0.f, 0.f, 0.f};
+  float* st = reinterpret_cast<float*>(lds + kLdsStage + wave * kStageBytes);
+  uint32_t* stu = reinterpret_cast<uint32_t*>(st);
+
+  bool first = true;
+  for (int ts = lo + wave * kTile; ts < hi; ts += kWaves * kTile) {
+    TileQ8 tr;
+    load_tile_q8(rk, rv, ts, p.num_kv, h, lane, row, col, tr);
+
+    // ---- scores: D rows = keys 16g + 4*row + r, D col = head `col`
+    f4_t sa[2];
+#pragma unroll
+    for (int g = 0; g < 2; g++) {
+      f4_t a = {0.f, 0.f, 0.f, 0.f};
+      a = __builtin_amdgcn_mfma_f32_16x16x32_f16(key_operand<0>(tr.k[g]), qa[0], a, 0, 0, 0);
+      a = __builtin_amdgcn_mfma_f32_16x16x32_f16(key_operand<1>(tr.k[g]), qa[1], a, 0, 0, 0);
+      a = __builtin_amdgcn_mfma_f32_16x16x32_f16(key_operand<2>(tr.k[g]), qa[2], a, 0, 0, 0);
+      a = __builtin_amdgcn_mfma_f32_16x16x32_f16(key_operand<3>(tr.k[g]), qa[3], a, 0, 0, 0);
+      a = __builtin_amdgcn_mfma_f32_16x16x32_f16(key_operand<4>(tr.k[g]), qa[4], a, 0, 0, 0);
+      a = __builtin_amdgcn_mfma_f32_16x16x32_f16(key_operand<5>(tr.k[g]), qa[5], a, 0, 0, 0);
+      a = __builtin_amdgcn_mfma_f32_16x16x32_f16(key_operand<6>(tr.k[g]), qa[6], a, 0, 0, 0);
+      a = __builtin_amdgcn_mfma_f32_16x16x32_f16(key_operand<7>(tr.k[g]), qa[7], a, 0, 0, 0);
+      sa[g] = a;
+    }
+
+    // ---- value rows to LDS (keys past the range stage as zeros)
+    {
+      const int kl = lane & 31, hf = lane >> 5;
+      const bool live = ts + kl < hi;
+#pragma unroll
+      for (int b = 0; b < 4; b++) {
+        const int blk = 4 * hf + b;
+        uint32_t w[9];
+#pragma unroll
+        for (int i = 0; i < 9; i++) w[i] = live ? tr.v[(9 * b + i) >> 2][(9 * b + i) & 3] : 0u;
+#pragma unroll
+        for (int q = 0; q < 8; q++) stu[kStCodes + (8 * blk + q) * kPitch + kl] = w[q];
+        st[kStScale + blk * kPitch + kl] = scale_of(w[8]);
+      }
+    }
+    wave_sync();
+
+    float s[2][4];
+#pragma unroll
+    for (int g = 0; g < 2; g++)
+#pragma unroll
+      for (int r = 0; r < 4; r++) {
+        const int key = ts + 16 * g + 4 * row + r;
+        s[g][r] = key < hi ? sa[g][r] * scale2 : -INFINITY;
+      }
+
+    // ---- online softmax of head `col`
+    float mt = fmaxf(fmaxf(fmaxf(s[0][0], s[0][1]), fmaxf(s[0][2], s[0][3])),
+                     fmaxf(fmaxf(s[1][0], s[1][1]), fmaxf(s[1][2], s[1][3])));
+    mt = xrow_max(mt);
+    const float mn = fmaxf(m2, mt);
+    const float msafe = (mn == -INFINITY) ? 0.0f : mn;
+    const float corr = __builtin_amdgcn_exp2f(m2 - msafe);
+    float ps = 0.0f;
+#pragma unroll
+    for (int g = 0; g < 2; g++)
+#pragma unroll
+      for (int r = 0; r < 4; r++) {
+        s[g][r] = __builtin_amdgcn_exp2f(s[g][r] - msafe);
+        ps += s[g][r];
+      }
+    lsum = lsum * corr + ps;
+    m2 = mn;
+    if (!first) {
+      if (row == 0) st[kStCorr + col] = corr;
+      wave_sync();
+      const f4_t cr = *reinterpret_cast<const f4_t*>(st + kStCorr + 4 * row);
+#pragma unroll
+      for (int t = 0; t < 16; t++)
+#pragma unroll
+        for (int r = 0; r < 4; r++) acc[t][r] *= cr[r];
+    }
+    first = false;
+
+    // ---- values: k index i <-> key 4*row + i (i < 4), 16 + 4*row + (i - 4)
+    h8_t pa;
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+      pa[r] = (_Float16)s[0][r];
+      pa[4 + r] = (_Float16)s[1][r];
+    }
+#pragma unroll
+    for (int a = 0; a < 4; a++) {
+      const int dq = 16 * a + col;          // dims 4*dq .. 4*dq+3
+      const int blk = dq >> 3;
+      const u4_t xa = *reinterpret_cast<const u4_t*>(stu + kStCodes + dq * kPitch + 4 * row);
+      const u4_t xb = *reinterpret_cast<const u4_t*>(stu + kStCodes + dq * kPitch + 16 + 4 * row);
+      const f4_t da = *reinterpret_cast<const f4_t*>(st + kStScale + blk * kPitch + 4 * row);
+      const f4_t db = *reinterpret_cast<const f4_t*>(st + kStScale + blk * kPitch + 16 + 4 * row);
+      const uint32_t x[8] = {xa[0], xa[1], xa[2], xa[3], xb[0], xb[1], xb[2], xb[3]};
+      const float d[8] = {da[0], da[1], da[2], da[3], db[0], db[1], db[2], db[3]};
+#pragma unroll
+      for (int e = 0; e < 4; e++) {
+        h8_t b;
+#pragma unroll
+        for (int i = 0; i < 8; i++) b[i] = (_Float16)((float)(int8_t)(x[i] >> (8 * e)) * d[i]);
+        acc[4 * a + e] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pa, b, acc[4 * a + e], 0, 0, 0);
+      }
+    }
+    wave_sync();
+  }
+  lsum = xrow_sum(lsum);
+
+  // ---- merge the waves in LDS, then write the split's partials
+  __syncthreads();
+  float* mo = reinterpret_cast<float*>(lds + kLdsMergeO);
+  float* ml = reinterpret_cast<float*>(lds + kLdsMergeML);
+  if (4 * row < gqa) {
+    // tile 4a+e, row 4*row+r (head), column col: dim 64a + 4*col + e
+#pragma unroll
+    for (int a = 0; a < 4; a++)
+#pragma unroll
+      for (int r = 0; r < 4; r++) {
+        f4_t v4 = {acc[4 * a][r], acc[4 * a + 1][r], acc[4 * a + 2][r], acc[4 * a + 3][r]};
+        *reinterpret_cast<f4_t*>(&mo[(wave * 8 + 4 * row + r) * kHD + 64 * a + 4 * col]) = v4;
+      }
+  }
+  if (row == 0 && col < 8) {
+    ml[kMlW0 + wave * 8 + col] = m2;
+    ml[kMlLw0 + wave * 8 + col] = lsum;
+  }
+  __syncthreads();
+  const int rows = min(gqa, 8);
+  for (int idx = threadIdx.x; idx < rows * 64; idx += kThreads) {
+    const int r = idx >> 6, d4 = (idx & 63) * 4;
+    float M = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < kWaves; w++) M = fmaxf(M, ml[kMlW0 + w * 8 + r]);
+    float Ls = 0.f;
+    f4_t o = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int w = 0; w < kWaves; w++) {
+      const float mw = ml[kMlW0 + w * 8 + r];
+      const float wt = (mw == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(mw - M);
+      Ls += wt * ml[kMlLw0 + w * 8 + r];
+      o += wt * *reinterpret_cast<const f4_t*>(&mo[(w * 8 + r) * kHD + d4]);
+    }
+    const int qh = h * gqa + r;
+    const long mlx = ((long)qh * p.sub_n_max + t_idx) * p.k_splits + split;
+#pragma unroll
+    for (int i = 0; i < 4; i++) p.part_o[mlx * kHD + d4 + i] = o[i];
+    if (d4 == 0) {
+      p.part_m[mlx] = (M == -INFINITY) ? -INFINITY : M * kLn2;
+      p.part_l[mlx] = Ls;
+    }
+  }
+}
+
+}  // namespace
+
+hipError_t launch_q8_attn_split(const AttnArgs& a, hipStream_t stream) {
+  const int n_wg = a.num_kv * a.sub_n * a.k_splits;
+  hipLaunchKernelGGL(q8_attn_split_kernel, dim3(n_wg), dim3(kThreads), 0, stream, a);
+  return hipGetLastError();
+}
+
+}  // namespace qkv

@@ -164,6 +164,43 @@ int qkv_attn_split_tq3(const uint16_t* q, const qkv_block_tq3* k, const qkv_bloc
   return launch_status(qkv::launch_tq3_attn(a, 1, nullptr, stream));
 }
 
+int qkv_attn_split_q8(const uint16_t* q, const qkv_block_q8* k, const qkv_block_q8* v,
+                      float* part_m, float* part_l, float* part_o, int num_q, int num_kv,
+                      int head_dim, int start_pos, int sub_n, int sub_n_max, int active_end_max,
+                      float scale, int k_splits, hipStream_t stream) {
+  int st = check_attn_shape(num_q, num_kv, head_dim, start_pos, sub_n, nullptr);
+  if (st) return st;
+  if (sub_n > sub_n_max || k_splits < 1 || k_splits > 65536 || active_end_max < 1)
+    return QKV_ERR_INVALID;
+  if ((int64_t)num_kv * sub_n * k_splits > 0x7fffffff) return QKV_ERR_INVALID;
+  if (!q || !k || !v || !part_m || !part_l || !part_o) return QKV_ERR_NULL;
+  if (!aligned(q, 16) || !aligned(k, 4) || !aligned(v, 4) || !aligned(part_m, 4) ||
+      !aligned(part_l, 4) || !aligned(part_o, 4))
+    return QKV_ERR_ALIGN;
+  qkv::AttnArgs a{};
+  a.q = q;
+  a.k = reinterpret_cast<const uint32_t*>(k);
+  a.v = reinterpret_cast<const uint32_t*>(v);
+  a.num_q = num_q;
+  a.num_kv = num_kv;
+  a.start_pos = start_pos;
+  a.sub_n = sub_n;
+  a.sub_n_max = sub_n_max;
+  {
+    const uint64_t extent = (uint64_t)(start_pos + sub_n) * num_kv * 8 * sizeof(qkv_block_q8);
+    if (extent > 0x7fffffffULL) return QKV_ERR_UNSUPPORTED;   // 32-bit buffer offsets
+    a.kv_bytes = (uint32_t)extent;
+  }
+  a.active_end_max = active_end_max;
+  a.k_splits = k_splits;
+  a.n_chunks = k_splits;
+  a.scale_log2 = scale * qkv::kLog2e;
+  a.part_m = part_m;
+  a.part_l = part_l;
+  a.part_o = part_o;
+  return launch_status(qkv::launch_q8_attn_split(a, stream));
+}
+
 int qkv_attn_split_merge(const float* part_m, const float* part_l, const float* part_o,
                          uint16_t* out, int num_q, int num_kv, int head_dim, int sub_n,
                          int sub_n_max, int k_splits, hipStream_t stream) {

@@ -110,6 +110,16 @@ def attn_split_tq3(q, k, v, part_m, part_l, part_o, *, num_q, num_kv, start_pos,
         window_tok, _opt_ptr(tree_mask), _stream(stream)), "qkv_attn_split_tq3")
 
 
+def attn_split_q8(q, k, v, part_m, part_l, part_o, *, num_q, num_kv, start_pos, sub_n,
+                  sub_n_max, active_end_max, scale, k_splits, head_dim=256, stream=None) -> None:
+    """attention.cuh:2633-2801: unnormalised split partials over the Q8_0 cache."""
+    check(lib().qkv_attn_split_q8(
+        _dev_ptr(q, "q"), _dev_ptr(k, "k"), _dev_ptr(v, "v"), _dev_ptr(part_m, "part_m"),
+        _dev_ptr(part_l, "part_l"), _dev_ptr(part_o, "part_o"), num_q, num_kv, head_dim,
+        start_pos, sub_n, sub_n_max, active_end_max, float(scale), k_splits, _stream(stream)),
+        "qkv_attn_split_q8")
+
+
 def attn_split_merge(part_m, part_l, part_o, out, *, num_q, num_kv, sub_n, sub_n_max, k_splits,
                      head_dim=256, stream=None) -> None:
     """attention.cuh:1837-1891."""

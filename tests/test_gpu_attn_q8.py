@@ -1,0 +1,90 @@
+"""GPU parity of the Q8_0 split-K flash decode (attention.cuh:2633-2801) and its
+merge (attention.cuh:1837-1891) against the CPU oracle on identical seeded
+inputs.  Bar: merged output within 2e-3 relative error (max |diff| / max |ref|),
+fp32 accumulation; split partials within the same tolerance."""
+import numpy as np
+import pytest
+
+from oracle import oracle as O
+from tests._data import kv_f16, q_f16, rel_err
+
+pytestmark = pytest.mark.gpu
+TOL = 2e-3
+
+
+def _torch():
+    import torch
+    return torch
+
+
+def _dev(a, dev):
+    return _torch().from_numpy(np.ascontiguousarray(a)).to(dev)
+
+
+def _cache(seed, n, num_kv=4, hd=256):
+    rng = np.random.default_rng(seed)
+    k16 = kv_f16(rng, n, num_kv, hd)
+    v16 = kv_f16(rng, n, num_kv, hd)
+    return rng, O.q8_encode(k16), O.q8_encode(v16)
+
+
+def _run(dev, q, kb, vb, **kw):
+    from qengine_amd import kvcache
+    torch = _torch()
+    nq, smax, ks = kw["num_q"], kw["sub_n_max"], kw["k_splits"]
+    pm = torch.full((nq, smax, ks), float("nan"), device=dev)
+    pl = torch.full((nq, smax, ks), float("nan"), device=dev)
+    po = torch.full((nq, smax, ks, 256), float("nan"), device=dev)
+    kvcache.attn_split_q8(_dev(q.view(np.uint16), dev), _dev(kb.view(np.uint8), dev),
+                          _dev(vb.view(np.uint8), dev), pm, pl, po, **kw)
+    out = torch.zeros((kw["sub_n"], nq, 256), dtype=torch.float16, device=dev)
+    kvcache.attn_split_merge(pm, pl, po, out, num_q=nq, num_kv=kw["num_kv"], sub_n=kw["sub_n"],
+                             sub_n_max=smax, k_splits=ks)
+    torch.cuda.synchronize()
+    return pm.cpu().numpy(), pl.cpu().numpy(), po.cpu().numpy(), out.cpu().numpy()
+
+
+@pytest.mark.parametrize("n,k_splits,num_q,sub_n", [
+    (4097, 8, 16, 1),      # config 2: one token appended to a 4096-token Q8 cache
+    (4097, 16, 16, 1),
+    (1000, 8, 16, 1),
+    (33, 8, 16, 1),
+    (1, 4, 16, 1),
+    (700, 8, 24, 1),       # GQA 6
+    (530, 4, 16, 16),      # 16 causal queries (verify-style)
+])
+def test_q8_split_decode_vs_oracle(dev, n, k_splits, num_q, sub_n):
+    rng, kb, vb = _cache(300 + n + k_splits, n)
+    q = q_f16(rng, sub_n, num_q, 256)
+    kw = dict(num_q=num_q, num_kv=4, start_pos=n - sub_n, sub_n=sub_n, sub_n_max=sub_n,
+              active_end_max=n, scale=1 / 16, k_splits=k_splits)
+    pm, pl, po, out = _run(dev, q, kb, vb, **kw)
+    em, el, eo = O.attn_split(O.KV_Q8, q, kb, vb, hd=256, **kw)
+    exp = O.attn_split_merge(em, el, eo, num_q=num_q, num_kv=4, hd=256, sub_n=sub_n,
+                             sub_n_max=sub_n, k_splits=k_splits)
+    # partials: same empty-split pattern, m/l/o within tolerance after a common rescale
+    empty = ~np.isfinite(em)
+    assert np.array_equal(empty, ~np.isfinite(pm)), "empty-split pattern differs"
+    assert np.all(pl[empty] == 0) and np.all(po[empty] == 0)
+    live = ~empty
+    assert np.max(np.abs(pm[live] - em[live])) < 1e-2
+    w = np.exp(pm[live] - em[live])
+    assert np.max(np.abs(pl[live] * w - el[live]) / el[live]) < TOL
+    assert rel_err(po[live] * w[:, None], eo[live]) < TOL
+    assert rel_err(out, exp.view(np.float16)) < TOL
+
+
+def test_q8_split_rejects_bad_shapes(dev):
+    from qengine_amd import QKVError, kvcache
+    torch = _torch()
+    q = torch.zeros((1, 16, 256), dtype=torch.float16, device=dev)
+    kv = torch.zeros((10 * 32, 36), dtype=torch.uint8, device=dev)
+    pm = torch.zeros((16, 1, 8), device=dev)
+    po = torch.zeros((16, 1, 8, 256), device=dev)
+    with pytest.raises(QKVError):   # head_dim 128 is not compiled
+        kvcache.attn_split_q8(q, kv, kv, pm, pm, po, num_q=16, num_kv=4, start_pos=9, sub_n=1,
+                              sub_n_max=1, active_end_max=10, scale=1 / 16, k_splits=8,
+                              head_dim=128)
+    with pytest.raises(QKVError):   # sub_n > sub_n_max
+        kvcache.attn_split_q8(q, kv, kv, pm, pm, po, num_q=16, num_kv=4, start_pos=9, sub_n=2,
+                              sub_n_max=1, active_end_max=10, scale=1 / 16, k_splits=8)
