@@ -63,8 +63,16 @@ constexpr int kStCorr = 36 * kKeyPitch;      // 16 floats: per-head rescale of t
 constexpr int kStageBytes = (36 * kKeyPitch + 16) * 4;   // 9856
 
 // LDS layout (bytes).  The merge area aliases the staging areas (used after the loop).
-constexpr int kLdsLut = 0;                                   // 64 x u32 centroid pairs
-constexpr int kLdsStage = 256;                               // per wave, kStageBytes
+// Centroid-pair table, one copy per lane: entry E of lane L at byte
+// E * 256 + 4 * L, so every lane reads its own bank and a wave's 64 lookups
+// never conflict.  An address is 4 * L in byte 0 and an 8-bit index in byte 1,
+// written by one SDWA shift (sdwa_index): the low 6 bits of the index are two
+// 3-bit codes, the top 2 bits are whatever follows them in the code stream,
+// so entry E holds the pair of E & 63.  The table sits at LDS offset 0 so
+// that no base has to be added (256 x 64 x 4 B = 64 KiB).
+constexpr int kLdsLut = 0;
+constexpr int kLdsLutBytes = 256 * 64 * 4;
+constexpr int kLdsStage = kLdsLut + kLdsLutBytes;            // per wave, kStageBytes
 constexpr int kLdsQ = kLdsStage + kWaves * kStageBytes;      // rotated query, [8][2][4][4][8] fp16
 constexpr int kLdsTileEnd = kLdsQ + 16 * 128 * 2;            // 43776
 constexpr int kLdsMergeO = kLdsStage;                        // [4 waves][8 rows][256] f32
@@ -77,8 +85,20 @@ static_assert(kLdsMergeEnd <= kLdsQ, "merge area must not reach the query scratc
 constexpr int kMlW0 = 0, kMlLw0 = 8 * kWaves, kMlM = 16 * kWaves, kMlL = 16 * kWaves + 8;
 static_assert(kMlL + 8 <= 256, "merge scalars must fit the ML area");
 
+// Table address: byte 1 of `addr` := bits SHIFT..SHIFT+7 of w, bytes 0, 2, 3
+// (4 * lane, 0, 0) kept -- one v_lshrrev_b32 with SDWA dst_sel:BYTE_1 and
+// dst_unused:UNUSED_PRESERVE.  Each address register is reused by the next
+// lookup of its chain, so no copy of 4 * lane is needed per lookup.
+template <int SHIFT>
+__device__ __forceinline__ uint32_t sdwa_index(uint32_t addr, uint32_t w) {
+  asm("v_lshrrev_b32_sdwa %0, %2, %1 dst_sel:BYTE_1 dst_unused:UNUSED_PRESERVE src0_sel:DWORD "
+      "src1_sel:DWORD"
+      : "+v"(addr)
+      : "v"(w), "i"(SHIFT));
+  return addr;
+}
 __device__ __forceinline__ uint32_t lut_read(const uint8_t* lds, uint32_t addr) {
-  return *reinterpret_cast<const uint32_t*>(lds + addr);
+  return *reinterpret_cast<const uint32_t*>(lds + kLdsLut + addr);
 }
 
 // Lloyd-Max centroid i (turboquant.cuh:27-30) selected from immediates.
@@ -90,65 +110,61 @@ __device__ __forceinline__ float centroid_imm(uint32_t i) {
   return (i & 4) ? mpos : -mneg;
 }
 
-// Centroid-pair table address of the 6-bit field at bit BIT of a 3-dword
-// code stream (the field lands at bits 2..7: byte offset of a 4-byte entry).
+// Table address of the 6-bit field at bit BIT of a 3-dword code stream
+// (a field that crosses a dword boundary is first funnel-shifted to bit 0).
 template <int BIT>
-__device__ __forceinline__ uint32_t pair_addr3(const uint32_t (&q)[3]) {
-  if constexpr (BIT == 0) {
-    return (q[0] << 2) & 0xFCu;
-  } else {
-    constexpr int b = BIT - 2;
-    constexpr int w = b >> 5, sh = b & 31;
-    if constexpr (sh + 8 <= 32) {
-      return (q[w] >> sh) & 0xFCu;
-    } else {
-      return __builtin_amdgcn_alignbit(q[w + 1], q[w], sh) & 0xFCu;
-    }
-  }
+__device__ __forceinline__ uint32_t pair_addr3(uint32_t& chain, const uint32_t (&q)[3]) {
+  constexpr int w = BIT >> 5, sh = BIT & 31;
+  if constexpr (sh + 6 <= 32)
+    chain = sdwa_index<sh>(chain, q[w]);
+  else
+    chain = sdwa_index<0>(chain, __builtin_amdgcn_alignbit(q[w + 1], q[w], sh));
+  return chain;
 }
 
 // B operand for code group U (8 codes, bits 24U..24U+23) of a 3-dword stream.
 template <int U>
-__device__ __forceinline__ h8_t group_operand(const uint8_t* lds, const uint32_t (&q)[3]) {
+__device__ __forceinline__ h8_t group_operand(const uint8_t* lds, uint32_t (&ac)[4],
+                                              const uint32_t (&q)[3]) {
   u4_t v;
-  v[0] = lut_read(lds, kLdsLut + pair_addr3<24 * U + 0>(q));
-  v[1] = lut_read(lds, kLdsLut + pair_addr3<24 * U + 6>(q));
-  v[2] = lut_read(lds, kLdsLut + pair_addr3<24 * U + 12>(q));
-  v[3] = lut_read(lds, kLdsLut + pair_addr3<24 * U + 18>(q));
+  v[0] = lut_read(lds, pair_addr3<24 * U + 0>(ac[0], q));
+  v[1] = lut_read(lds, pair_addr3<24 * U + 6>(ac[1], q));
+  v[2] = lut_read(lds, pair_addr3<24 * U + 12>(ac[2], q));
+  v[3] = lut_read(lds, pair_addr3<24 * U + 18>(ac[3], q));
   return __builtin_bit_cast(h8_t, v);
 }
 
 // Score MFMAs for one 16-key group: 4 slices per block, one accumulator per
 // block.  Slice U+1's table reads are issued before slice U's MFMAs.
 template <int U>
-__device__ __forceinline__ void score_group(const uint8_t* lds, const uint32_t (&k0)[3],
+__device__ __forceinline__ void score_group(const uint8_t* lds, uint32_t (&ac)[4], const uint32_t (&k0)[3],
                                             const uint32_t (&k1)[3], const h8_t (&qa)[8],
                                             const h8_t& b0, const h8_t& b1, f4_t& a0, f4_t& a1) {
   if constexpr (U < 4) {
     h8_t n0, n1;
     if constexpr (U < 3) {
-      n0 = group_operand<U + 1>(lds, k0);
-      n1 = group_operand<U + 1>(lds, k1);
+      n0 = group_operand<U + 1>(lds, ac, k0);
+      n1 = group_operand<U + 1>(lds, ac, k1);
     }
     a0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(b0, qa[U], a0, 0, 0, 0);
     a1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(b1, qa[4 + U], a1, 0, 0, 0);
     __builtin_amdgcn_sched_barrier(0);
-    if constexpr (U < 3) score_group<U + 1>(lds, k0, k1, qa, n0, n1, a0, a1);
+    if constexpr (U < 3) score_group<U + 1>(lds, ac, k0, k1, qa, n0, n1, a0, a1);
   }
 }
 
 // Values for one (32-key chunk, 128-block): centroid pair PP of the lane's
 // dim group gives tiles t0+2PP (low dim) and t0+2PP+1 (high dim).
 template <int PP>
-__device__ __forceinline__ void value_pipe(const uint8_t* lds, const uint32_t (&x)[8],
+__device__ __forceinline__ void value_pipe(const uint8_t* lds, uint32_t (&ac)[4], const uint32_t (&x)[8],
                                            const h8_t& a, f4_t (&acc)[16], int t0) {
   if constexpr (PP < 4) {
     uint32_t cp[8];
 #pragma unroll
     for (int i = 0; i < 8; i++) {
       const uint32_t xi = x[i];
-      const uint32_t addr = (PP == 0) ? ((xi << 2) & 0xFCu) : ((xi >> (6 * PP - 2)) & 0xFCu);
-      cp[i] = lut_read(lds, kLdsLut + addr);
+      ac[i & 3] = sdwa_index<6 * PP>(ac[i & 3], xi);
+      cp[i] = lut_read(lds, ac[i & 3]);
     }
 #pragma unroll
     for (int e = 0; e < 2; e++) {
@@ -161,7 +177,7 @@ __device__ __forceinline__ void value_pipe(const uint8_t* lds, const uint32_t (&
                                                          acc[tile], 0, 0, 0);
     }
     __builtin_amdgcn_sched_barrier(0);
-    value_pipe<PP + 1>(lds, x, a, acc, t0);
+    value_pipe<PP + 1>(lds, ac, x, a, acc, t0);
   }
 }
 
@@ -506,11 +522,6 @@ __global__ __launch_bounds__(kThreads, 1) void tq3_attn_kernel(AttnArgs p, uint1
     hi = min((chunk + 1) * tps * 32, active_end);
   }
   const KeyRule rule(p.start_pos, t_idx, p.sink_tok, p.window_tok, p.tree_mask);
-  // launch epoch of the fast-path workspace (records of this call carry epoch + 1)
-  const uint32_t epoch =
-      MODE == 0 ? (uint32_t)__hip_atomic_load(&p.ws_header[kWsEpoch], __ATOMIC_RELAXED,
-                                              __HIP_MEMORY_SCOPE_AGENT)
-                : 0u;
   const int row = lane >> 4;        // 16-lane row of the MFMA D layout
   const int col = lane & 15;
 
@@ -521,13 +532,24 @@ __global__ __launch_bounds__(kThreads, 1) void tq3_attn_kernel(AttnArgs p, uint1
       __builtin_amdgcn_make_buffer_rsrc(const_cast<uint32_t*>(p.v), 0, p.kv_bytes, kBufferRsrcWord3);
 
   // ---- setup: centroid-pair table; rotated query ---------------------------
-  if (threadIdx.x < 64) {
-    // entry e = (centroid[e & 7], centroid[e >> 3]) as fp16, from immediates
-    // (a table load here would wait behind the tile loads already in flight)
-    const uint32_t e = threadIdx.x;
-    *reinterpret_cast<uint32_t*>(lds + kLdsLut + 4 * e) =
-        f2h(centroid_imm(e & 7)) | (f2h(centroid_imm(e >> 3)) << 16);
+  // entry e = (centroid[e & 7], centroid[e >> 3]) as fp16, from immediates
+  // (wave-uniform values); wave w writes every lane's copy of entries 8w..8w+7
+  // wave w writes every lane's copy of entries 32w .. 32w+31 (entry E holds
+  // the pair of E & 63: low code E & 7, high code (E >> 3) & 7)
+  static_assert(kWaves == 8, "8 waves x 32 entries");
+  const uint32_t lane4 = 4u * (uint32_t)lane;
+  {
+    const uint32_t w = (uint32_t)__builtin_amdgcn_readfirstlane(wave);
+#pragma unroll
+    for (int hk = 0; hk < 4; hk++) {
+      const uint32_t hi = f2h(centroid_imm((4u * w + hk) & 7u)) << 16;
+#pragma unroll
+      for (int k = 0; k < 8; k++)
+        *reinterpret_cast<uint32_t*>(lds + kLdsLut + (w * 32 + hk * 8 + k) * 256 + lane4) =
+            f2h(centroid_imm(k)) | hi;
+    }
   }
+  uint32_t ac[4] = {lane4, lane4, lane4, lane4};   // table address chains
   TileRegs tr;
   {
     // 16 WHTs of 128 (8 heads x 2 blocks), 16 lanes each (threads 0..255); fp16 result in LDS
@@ -537,10 +559,11 @@ __global__ __launch_bounds__(kThreads, 1) void tq3_attn_kernel(AttnArgs p, uint1
     const int wht = threadIdx.x >> 4;
     const int part = threadIdx.x & 15;
     const int hh = wht >> 1, blk = wht & 1;
-    // The query piece is requested before the tile, so its wait does not
-    // include the tile's loads (the vector memory counter is in order).  Both
-    // loads are unconditional (rows past a buffer's extent read as zero):
-    // a load under a branch makes the compiler wait for every load at the join.
+    // The query is loaded and rotated before any tile load is issued: a
+    // query load issued after the tile loads of the whole chip would wait
+    // behind them in the memory queues.  The load is unconditional (rows
+    // past the buffer's extent read as zero): a load under a branch makes the
+    // compiler wait for every load at the join.
     const uint32_t q_extent = (uint32_t)(p.sub_n * p.num_q * kHD * 2);
     const __amdgpu_buffer_rsrc_t rq =
         __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(p.q), 0, q_extent, kBufferRsrcWord3);
@@ -548,7 +571,6 @@ __global__ __launch_bounds__(kThreads, 1) void tq3_attn_kernel(AttnArgs p, uint1
         hh < gqa ? (uint32_t)(((t_idx * p.num_q + h * gqa + hh) * kHD + blk * 128 + part * 8) * 2)
                  : q_extent;
     const u4_t raw = __builtin_amdgcn_raw_buffer_load_b128(rq, qoff, 0, 0);
-    load_tile(rk, rv, lo + wave * kTile, p.num_kv, h, lane, row, col, tr);
     {
       float x[8];
       const uint32_t wv[4] = {raw[0], raw[1], raw[2], raw[3]};
@@ -577,6 +599,16 @@ __global__ __launch_bounds__(kThreads, 1) void tq3_attn_kernel(AttnArgs p, uint1
     }
   }
   __syncthreads();
+  load_tile(rk, rv, lo + wave * kTile, p.num_kv, h, lane, row, col, tr);
+  // launch epoch of the fast-path workspace (records of this call carry
+  // epoch + 1); requested after the first tile so that it is in flight
+  // during the tile's compute and needed only when the records are stored
+  __builtin_amdgcn_sched_barrier(0);
+  const uint32_t epoch =
+      MODE == 0 ? (uint32_t)__hip_atomic_load(&p.ws_header[kWsEpoch], __ATOMIC_RELAXED,
+                                              __HIP_MEMORY_SCOPE_AGENT)
+                : 0u;
+  __builtin_amdgcn_sched_barrier(0);
   // qa[s], slice s = 4j+u: A row = head `col`, element i = dim 128j + 8(4*row+u) + i
   h8_t qa[8];
   {
@@ -612,8 +644,8 @@ __global__ __launch_bounds__(kThreads, 1) void tq3_attn_kernel(AttnArgs p, uint1
     for (int g = 0; g < 4; g++) {
       sa[g][0] = f4_t{0.f, 0.f, 0.f, 0.f};
       sa[g][1] = f4_t{0.f, 0.f, 0.f, 0.f};
-      score_group<0>(lds, kq[g][0], kq[g][1], qa, group_operand<0>(lds, kq[g][0]),
-                     group_operand<0>(lds, kq[g][1]), sa[g][0], sa[g][1]);
+      score_group<0>(lds, ac, kq[g][0], kq[g][1], qa, group_operand<0>(lds, ac, kq[g][0]),
+                     group_operand<0>(lds, ac, kq[g][1]), sa[g][0], sa[g][1]);
     }
 
     // ---------------- staging: key norms, value rows (lane = key ts + lane) ----------------
@@ -649,6 +681,7 @@ __global__ __launch_bounds__(kThreads, 1) void tq3_attn_kernel(AttnArgs p, uint1
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 
+    // dense is wave-uniform: the common full tile skips the per-key rule
     const bool dense = ts + kTile <= hi && rule.all_visible(ts + kTile);
     float s[4][4];
 #pragma unroll
@@ -656,11 +689,17 @@ __global__ __launch_bounds__(kThreads, 1) void tq3_attn_kernel(AttnArgs p, uint1
       const f4_t k0 = *reinterpret_cast<const f4_t*>(st + kStKn + 16 * g + 4 * row);
       const f4_t k1 = *reinterpret_cast<const f4_t*>(st + kStKn + kKeyPitch + 16 * g + 4 * row);
 #pragma unroll
-      for (int r = 0; r < 4; r++) {
-        const int key = ts + 16 * g + 4 * row + r;
-        const bool vis = dense || ((key < hi) & rule.visible(key, active_end));   // masks padded keys too
-        s[g][r] = vis ? (k0[r] * sa[g][0][r] + k1[r] * sa[g][1][r]) * scale2 : -INFINITY;
-      }
+      for (int r = 0; r < 4; r++) s[g][r] = (k0[r] * sa[g][0][r] + k1[r] * sa[g][1][r]) * scale2;
+    }
+    if (!dense) {
+#pragma unroll
+      for (int g = 0; g < 4; g++)
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+          const int key = ts + 16 * g + 4 * row + r;
+          const bool vis = (key < hi) & rule.visible(key, active_end);   // masks padded keys too
+          s[g][r] = vis ? s[g][r] : -INFINITY;
+        }
     }
 
     // ---------------- online softmax of head `col` (its 64 keys sit in 4 rows) ----------------
@@ -716,7 +755,7 @@ __global__ __launch_bounds__(kThreads, 1) void tq3_attn_kernel(AttnArgs p, uint1
           a[4 + r] = (_Float16)(s[2 * c2 + 1][r] * vb[r]);
         }
         const uint32_t x[8] = {xa[0], xa[1], xa[2], xa[3], xb[0], xb[1], xb[2], xb[3]};
-        value_pipe<0>(lds, x, a, acc, 8 * j);
+        value_pipe<0>(lds, ac, x, a, acc, 8 * j);
       }
     }
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
