@@ -165,6 +165,40 @@ int qkv_decode_attn_tq3(const uint16_t* q, const qkv_block_tq3* k, const qkv_blo
                         const uint32_t* tree_mask, void* workspace, size_t workspace_bytes,
                         hipStream_t stream);
 
+/* Paged, ragged decode: one query per slot over per-slot block tables
+ * This generalises the reference, which keeps every
+ * slot contiguous and hands the attention launch a slot-base pointer
+ * (model.cuh:1708-1715 kv_slot_offset, model.cuh:2466-2468); a block table
+ * that maps block b of a slot to pool block base + b reproduces that call.
+ * q, out: [n_slots][num_q][256] fp16 (16-byte aligned).
+ * k_pool, v_pool: pool_rows token rows of num_kv*256/128 TQ3 blocks (the
+ * contiguous cache's row layout).  Key k of slot s lives in pool row
+ * block_tables[s*max_blocks + k/block_tokens]*block_tokens + k%block_tokens.
+ * ctx_lens: device int32 [n_slots]; slot s attends to its keys
+ * 0..ctx_lens[s]-1 (clamped to [0, max_ctx]; a slot without keys gets a zero
+ * row).  block_tokens: a multiple of 64; max_ctx <= max_blocks*block_tokens.
+ * Table entries pointing outside the pool read as zero keys.  Workspace: as
+ * for qkv_decode_attn_tq3 (zero-filled before first use, reused in order). */
+size_t qkv_decode_attn_tq3_paged_workspace_bytes(int num_q, int num_kv, int n_slots, int max_ctx);
+int qkv_decode_attn_tq3_paged(const uint16_t* q, const qkv_block_tq3* k_pool,
+                              const qkv_block_tq3* v_pool, uint16_t* out, int num_q, int num_kv,
+                              int head_dim, int n_slots, const int32_t* block_tables,
+                              int max_blocks, int block_tokens, int pool_rows,
+                              const int32_t* ctx_lens, int max_ctx, float scale, void* workspace,
+                              size_t workspace_bytes, hipStream_t stream);
+
+/* Paged append of K and V (tq3_quantize_kernel, turboquant.cuh:112-165, with
+ * the destination row of each token taken from the slot's block table):
+ * k_f16, v_f16: [n_slots][n_tok][num_kv][256] fp16; token t of slot s is
+ * written at position positions[s] + t of that slot (row rule as in
+ * qkv_decode_attn_tq3_paged).  Tokens whose row falls outside
+ * [0, pool_rows) or whose block index is >= max_blocks are not written. */
+int qkv_tq3_append_kv_paged(const uint16_t* k_f16, const uint16_t* v_f16, qkv_block_tq3* k_pool,
+                            qkv_block_tq3* v_pool, int n_slots, int n_tok, int num_kv,
+                            int head_dim, const int32_t* block_tables, int max_blocks,
+                            int block_tokens, int pool_rows, const int32_t* positions,
+                            hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -251,3 +251,47 @@ def attn_ref_f64(q, k_f16, v_f16, *, num_q, num_kv, hd, start_pos, sub_n, scale,
 def key_visible(key, start_pos, t_idx, sink_tok=0, window_tok=0, tree_mask=None):
     tm = None if tree_mask is None else np.ascontiguousarray(tree_mask, np.uint32)
     return bool(lib().or_key_visible(key, start_pos, t_idx, sink_tok, window_tok, _ptr(tm)))
+
+
+# ---- paged caches ------------------------------------------------------------
+# The reference keeps each slot contiguous from kv_slot_offset(slot)
+# (model.cuh:1708-1715) and hands attention a slot-base pointer
+# (model.cuh:2466-2468).  A per-slot block table generalises that offset per
+# block_tokens keys; gathering a slot's rows and running the contiguous
+# reference decode on them is the paged decode's definition.
+
+def paged_rows(block_table, n_keys, block_tokens):
+    """Cache rows of keys 0..n_keys-1 of one slot."""
+    k = np.arange(n_keys, dtype=np.int64)
+    bt = np.asarray(block_table, np.int64)
+    return bt[k // block_tokens] * block_tokens + k % block_tokens
+
+
+def gather_rows(pool_blocks, rows, blocks_per_row):
+    """Blocks of the given token rows, in row order ([len(rows)*blocks_per_row])."""
+    idx = np.asarray(rows, np.int64)[:, None] * blocks_per_row + np.arange(blocks_per_row)
+    return np.ascontiguousarray(pool_blocks[idx.reshape(-1)])
+
+
+def decode_paged(kind, q, k_pool, v_pool, block_tables, ctx_lens, *, num_q, num_kv, hd,
+                 block_tokens, scale, k_splits=8):
+    """One decode query per slot (q [n_slots][num_q][hd]) over its gathered rows:
+    the reference split decode + merge with start_pos = ctx - 1, sub_n = 1.
+    A slot without keys gives a zero row.  Returns fp16 bits."""
+    q = _u16(q)
+    bpr = num_kv * hd // 128
+    out = np.zeros((q.shape[0], num_q, hd), np.uint16)
+    for s, ctx in enumerate(ctx_lens):
+        ctx = int(ctx)
+        if ctx <= 0:
+            continue
+        rows = paged_rows(block_tables[s], ctx, block_tokens)
+        kb = gather_rows(k_pool, rows, bpr)
+        vb = gather_rows(v_pool, rows, bpr)
+        ks = min(k_splits, ctx)
+        pm, pl, po = attn_split(kind, q[s:s + 1], kb, vb, num_q=num_q, num_kv=num_kv, hd=hd,
+                                start_pos=ctx - 1, sub_n=1, sub_n_max=1, active_end_max=ctx,
+                                scale=scale, k_splits=ks)
+        out[s] = attn_split_merge(pm, pl, po, num_q=num_q, num_kv=num_kv, hd=hd, sub_n=1,
+                                  sub_n_max=1, k_splits=ks)[0]
+    return out

@@ -32,6 +32,14 @@ struct AttnArgs {
   float scale_log2;         // softmax scale * log2(e)
   int sink_tok, window_tok;
   const uint32_t* tree_mask;
+  // paged caches (fast path): when block_tables is set, key index k of query
+  // (slot) t lives in cache row block_tables[t * bt_stride + k / block_tokens]
+  // * block_tokens + k % block_tokens, and ctx_lens[t] (clamped to
+  // [0, ctx_max]) replaces start_pos + t + 1 as the query's key count
+  const int32_t* block_tables;
+  int bt_stride, block_tokens;
+  const int32_t* ctx_lens;
+  int ctx_max;
   // split API partials (reference layout)
   float* part_m;
   float* part_l;

@@ -191,14 +191,15 @@ struct TileRegs {
   float kn[4][2];        // key block norms, group g, block j
 };
 
+// prow: cache row of the tile's first key (64 consecutive rows)
 __device__ __forceinline__ void load_tile(__amdgpu_buffer_rsrc_t rk, __amdgpu_buffer_rsrc_t rv,
-                                          int ts, int nkv, int h, int lane, int row, int col,
+                                          int prow, int nkv, int h, int lane, int row, int col,
                                           TileRegs& tr) {
   // keys first (group by group): the score MFMAs of group g only wait for
   // group g, and values arrive while the scores are computed
 #pragma unroll
   for (int g = 0; g < 4; g++) {
-    const uint32_t krow = (uint32_t)((ts + 16 * g + col) * nkv + h) * 104u;
+    const uint32_t krow = (uint32_t)((prow + 16 * g + col) * nkv + h) * 104u;
 #pragma unroll
     for (int j = 0; j < 2; j++) {
       const u3_t c = __builtin_amdgcn_raw_buffer_load_b96(rk, krow + 52 * j + 4 + 12 * row, 0, 0);
@@ -208,10 +209,23 @@ __device__ __forceinline__ void load_tile(__amdgpu_buffer_rsrc_t rk, __amdgpu_bu
       tr.kn[g][j] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rk, krow + 52 * j, 0, 0));
     }
   }
-  const uint32_t vrow = (uint32_t)((ts + lane) * nkv + h) * 104u;
+  const uint32_t vrow = (uint32_t)((prow + lane) * nkv + h) * 104u;
 #pragma unroll
   for (int i = 0; i < 6; i++) tr.vr[i] = __builtin_amdgcn_raw_buffer_load_b128(rv, vrow + 16 * i, 0, 0);
   tr.vr6 = __builtin_amdgcn_raw_buffer_load_b64(rv, vrow + 96, 0, 0);
+}
+
+// Cache row of key index ts (a multiple of 64) of query t: ts itself for a
+// contiguous cache; through the query's block table for a paged one (block
+// sizes are multiples of 64, so a 64-key tile never straddles two blocks).
+// The table is read only for a tile that has keys (ts < hi <= ctx_max, so the
+// entry lies inside the query's row of the table); rows outside the cache
+// extent read as zero (buffer range checks).
+__device__ __forceinline__ int tile_row(const AttnArgs& p, int t, int ts, int hi) {
+  if (p.block_tables == nullptr) return ts;
+  if (ts >= hi) return 0;
+  const int b = ts / p.block_tokens;
+  return p.block_tables[t * p.bt_stride + b] * p.block_tokens + (ts - b * p.block_tokens);
 }
 
 // Key visibility of one query (attention.cuh:1923-1929, 2101-2105): the
@@ -507,7 +521,8 @@ __global__ __launch_bounds__(kThreads, 1) void tq3_attn_kernel(AttnArgs p, uint1
     chunk = has_work ? g - t_idx * p.n_chunks : 0;
   }
   if (MODE == 1 && !has_work) return;
-  const int active_end = p.start_pos + t_idx + 1;
+  const int active_end = p.ctx_lens ? min(max(p.ctx_lens[t_idx], 0), p.ctx_max)
+                                    : p.start_pos + t_idx + 1;
   int lo = 0, hi = 0;
   if (MODE == 0) {
     if (has_work) {
@@ -599,7 +614,7 @@ __global__ __launch_bounds__(kThreads, 1) void tq3_attn_kernel(AttnArgs p, uint1
     }
   }
   __syncthreads();
-  load_tile(rk, rv, lo + wave * kTile, p.num_kv, h, lane, row, col, tr);
+  load_tile(rk, rv, tile_row(p, t_idx, lo + wave * kTile, hi), p.num_kv, h, lane, row, col, tr);
   // launch epoch of the fast-path workspace (records of this call carry
   // epoch + 1); requested after the first tile so that it is in flight
   // during the tile's compute and needed only when the records are stored
@@ -634,7 +649,7 @@ __global__ __launch_bounds__(kThreads, 1) void tq3_attn_kernel(AttnArgs p, uint1
 
   for (int ts = lo + wave * kTile; ts < hi; ts += kWaves * kTile) {
     const bool first = ts == lo + wave * kTile;
-    if (!first) load_tile(rk, rv, ts, p.num_kv, h, lane, row, col, tr);
+    if (!first) load_tile(rk, rv, tile_row(p, t_idx, ts, hi), p.num_kv, h, lane, row, col, tr);
     auto& kq = tr.kq;
     auto& kn = tr.kn;
 

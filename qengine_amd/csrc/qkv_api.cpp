@@ -76,6 +76,35 @@ int qkv_tq3_append_kv(const uint16_t* k_f16, const uint16_t* v_f16, qkv_block_tq
   return launch_status(qkv::launch_tq3_append(k_f16, k_out, v_f16, v_out, n_blocks, 2, stream));
 }
 
+int qkv_tq3_append_kv_paged(const uint16_t* k_f16, const uint16_t* v_f16, qkv_block_tq3* k_pool,
+                            qkv_block_tq3* v_pool, int n_slots, int n_tok, int num_kv,
+                            int head_dim, const int32_t* block_tables, int max_blocks,
+                            int block_tokens, int pool_rows, const int32_t* positions,
+                            hipStream_t stream) {
+  if (head_dim != 256) return QKV_ERR_UNSUPPORTED;
+  if (n_slots < 0 || n_tok < 0 || num_kv <= 0 || max_blocks <= 0 || block_tokens <= 0 ||
+      pool_rows < 0)
+    return QKV_ERR_INVALID;
+  if (n_slots == 0 || n_tok == 0) return QKV_OK;
+  if (!k_f16 || !v_f16 || !k_pool || !v_pool || !block_tables || !positions) return QKV_ERR_NULL;
+  if (!aligned(k_f16, 16) || !aligned(v_f16, 16) || !aligned(k_pool, 4) || !aligned(v_pool, 4) ||
+      !aligned(block_tables, 4) || !aligned(positions, 4))
+    return QKV_ERR_ALIGN;
+  const int bpr = num_kv * head_dim / 128;
+  const long n_blocks = (long)n_slots * n_tok * bpr;
+  if (n_blocks > 0x7fffffffL) return QKV_ERR_UNSUPPORTED;
+  qkv::PagedRows pr{};
+  pr.block_tables = block_tables;
+  pr.positions = positions;
+  pr.max_blocks = max_blocks;
+  pr.block_tokens = block_tokens;
+  pr.blocks_per_row = bpr;
+  pr.n_tok = n_tok;
+  pr.pool_rows = pool_rows;
+  return launch_status(
+      qkv::launch_tq3_append(k_f16, k_pool, v_f16, v_pool, (int)n_blocks, 2, stream, &pr));
+}
+
 int qkv_tq3_dequant(const qkv_block_tq3* in, uint16_t* out_f16, int n_blocks, hipStream_t stream) {
   if (n_blocks < 0) return QKV_ERR_INVALID;
   if (n_blocks == 0) return QKV_OK;
@@ -283,6 +312,65 @@ int qkv_decode_attn_tq3(const uint16_t* q, const qkv_block_tq3* k, const qkv_blo
   a.sink_tok = sink_tok;
   a.window_tok = window_tok;
   a.tree_mask = tree_mask;
+  a.ws_header = reinterpret_cast<int*>(ws + g.header_off);
+  a.ws_ml = reinterpret_cast<float*>(ws + g.ml_off);
+  a.ws_o = reinterpret_cast<float*>(ws + g.o_off);
+  if (g.total > 0xffffffffULL) return QKV_ERR_UNSUPPORTED;   // 32-bit buffer offsets
+  a.ws_ml_bytes = (uint32_t)(g.o_off - g.ml_off);
+  a.ws_o_bytes = (uint32_t)(g.total - g.o_off);
+  return launch_status(qkv::launch_tq3_attn(a, 0, out, stream));
+}
+
+size_t qkv_decode_attn_tq3_paged_workspace_bytes(int num_q, int num_kv, int n_slots,
+                                                 int max_ctx) {
+  if (num_q <= 0 || num_kv <= 0 || n_slots <= 0 || max_ctx <= 0) return 0;
+  return fast_geom(num_q, num_kv, n_slots, max_ctx).total;
+}
+
+int qkv_decode_attn_tq3_paged(const uint16_t* q, const qkv_block_tq3* k_pool,
+                              const qkv_block_tq3* v_pool, uint16_t* out, int num_q, int num_kv,
+                              int head_dim, int n_slots, const int32_t* block_tables,
+                              int max_blocks, int block_tokens, int pool_rows,
+                              const int32_t* ctx_lens, int max_ctx, float scale, void* workspace,
+                              size_t workspace_bytes, hipStream_t stream) {
+  int st = check_attn_shape(num_q, num_kv, head_dim, 0, 1, nullptr);
+  if (st) return st;
+  if (n_slots < 1 || max_ctx < 1 || max_blocks < 1 || pool_rows < 1) return QKV_ERR_INVALID;
+  if (block_tokens < 64 || block_tokens % 64 != 0) return QKV_ERR_UNSUPPORTED;
+  if ((long)max_blocks * block_tokens < max_ctx) return QKV_ERR_INVALID;
+  if (!q || !k_pool || !v_pool || !out || !block_tables || !ctx_lens) return QKV_ERR_NULL;
+  if (!aligned(q, 16) || !aligned(k_pool, 4) || !aligned(v_pool, 4) || !aligned(out, 16) ||
+      !aligned(block_tables, 4) || !aligned(ctx_lens, 4))
+    return QKV_ERR_ALIGN;
+  const FastGeom g = fast_geom(num_q, num_kv, n_slots, max_ctx);
+  if (!workspace || workspace_bytes < g.total) return QKV_ERR_WORKSPACE;
+  if (!aligned(workspace, 256)) return QKV_ERR_ALIGN;
+  char* ws = static_cast<char*>(workspace);
+  qkv::AttnArgs a{};
+  a.q = q;
+  a.k = reinterpret_cast<const uint32_t*>(k_pool);
+  a.v = reinterpret_cast<const uint32_t*>(v_pool);
+  a.num_q = num_q;
+  a.num_kv = num_kv;
+  a.start_pos = 0;
+  a.sub_n = n_slots;
+  a.sub_n_max = n_slots;
+  {
+    const uint64_t extent = (uint64_t)pool_rows * num_kv * 104;
+    if (extent > 0x7fffffffULL) return QKV_ERR_UNSUPPORTED;   // 32-bit buffer offsets
+    a.kv_bytes = (uint32_t)extent;
+  }
+  a.active_end_max = max_ctx;
+  a.k_splits = 1;
+  a.n_chunks = g.n_chunks;
+  a.chunk_keys = g.chunk_keys;
+  a.n_slots = g.n_slots;
+  a.scale_log2 = scale * qkv::kLog2e;
+  a.block_tables = block_tables;
+  a.bt_stride = max_blocks;
+  a.block_tokens = block_tokens;
+  a.ctx_lens = ctx_lens;
+  a.ctx_max = max_ctx;
   a.ws_header = reinterpret_cast<int*>(ws + g.header_off);
   a.ws_ml = reinterpret_cast<float*>(ws + g.ml_off);
   a.ws_o = reinterpret_cast<float*>(ws + g.o_off);

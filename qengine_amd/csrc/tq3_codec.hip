@@ -12,6 +12,7 @@
 // single-rounding IEEE operation in the same order as the reference, so
 // codes and norms are bit-identical.
 #include "qkv_device.h"
+#include "qkv_launch.h"
 
 // Bit-exact codec: no FMA contraction across the reference's separate roundings.
 #pragma clang fp contract(off)
@@ -80,11 +81,28 @@ __device__ __forceinline__ void tq3_encode_block(const uint32_t (&hw)[64], uint3
   }
 }
 
-// in: n_blocks*128 fp16 as uint4 (16 B aligned); out: n_blocks*13 dwords.
+// Output block of input block i for a paged append (PagedRows), or -1 when
+// the row it maps to lies outside the pool (then nothing is written).
+__device__ __forceinline__ long paged_block(const PagedRows& pr, long i) {
+  const long tok = i / pr.blocks_per_row;
+  const int j = (int)(i - tok * pr.blocks_per_row);
+  const int s = (int)(tok / pr.n_tok), t = (int)(tok - (long)s * pr.n_tok);
+  const long pos = (long)pr.positions[s] + t;
+  if (pos < 0) return -1;
+  const long b = pos / pr.block_tokens;
+  if (b >= pr.max_blocks) return -1;
+  const long row = (long)pr.block_tables[(long)s * pr.max_blocks + b] * pr.block_tokens +
+                   (pos - b * pr.block_tokens);
+  if (row < 0 || row >= pr.pool_rows) return -1;
+  return row * pr.blocks_per_row + j;
+}
+
+// in: n_blocks*128 fp16 as uint4 (16 B aligned); out: n_blocks*13 dwords,
+// or, when pr.block_tables is set, each block at its paged_block position.
 // gridDim.y selects the (in, out) pair so K and V can share one launch.
 __global__ __launch_bounds__(kCodecThreads) void tq3_append_kernel(
     const uint4* __restrict__ in0, uint32_t* __restrict__ out0, const uint4* __restrict__ in1,
-    uint32_t* __restrict__ out1, int n_blocks) {
+    uint32_t* __restrict__ out1, int n_blocks, PagedRows pr) {
   __shared__ uint32_t lds[kCodecWaves * kWaveLdsDw];
   const uint4* __restrict__ in = blockIdx.y ? in1 : in0;
   uint32_t* __restrict__ out = blockIdx.y ? out1 : out0;
@@ -126,6 +144,18 @@ __global__ __launch_bounds__(kCodecThreads) void tq3_append_kernel(
   __builtin_amdgcn_wave_barrier();
   __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "workgroup");
 
+  // paged: each lane stores its block at its own row
+  if (pr.block_tables != nullptr) {
+    if (lane < nb) {
+      const long ob = paged_block(pr, b0 + lane);
+      if (ob >= 0) {
+        uint32_t* dst = out + ob * 13;
+#pragma unroll
+        for (int k = 0; k < 13; k++) dst[k] = o[k];
+      }
+    }
+    return;
+  }
   // 3. stage 13 dwords per lane (odd pitch: conflict-free), then store the
   //    wave's contiguous 64*52 bytes with dword stores.
   if (lane < nb) {
@@ -220,12 +250,14 @@ __global__ __launch_bounds__(kCodecThreads) void tq3_dequant_kernel(
 // host launchers (validated by the C ABI layer)
 // ---------------------------------------------------------------------------
 hipError_t launch_tq3_append(const void* in0, void* out0, const void* in1, void* out1,
-                             int n_blocks, int n_tensors, hipStream_t stream) {
+                             int n_blocks, int n_tensors, hipStream_t stream,
+                             const PagedRows* paged) {
   const int per_wg = 64 * kCodecWaves;
   dim3 grid((n_blocks + per_wg - 1) / per_wg, n_tensors);
+  const PagedRows pr = paged ? *paged : PagedRows{};
   hipLaunchKernelGGL(tq3_append_kernel, grid, dim3(kCodecThreads), 0, stream,
                      static_cast<const uint4*>(in0), static_cast<uint32_t*>(out0),
-                     static_cast<const uint4*>(in1), static_cast<uint32_t*>(out1), n_blocks);
+                     static_cast<const uint4*>(in1), static_cast<uint32_t*>(out1), n_blocks, pr);
   return hipGetLastError();
 }
 

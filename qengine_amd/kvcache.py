@@ -147,3 +147,46 @@ def decode_attn_tq3(q, k, v, out, workspace, *, num_q, num_kv, start_pos, sub_n,
         num_kv, head_dim, start_pos, sub_n, float(scale), sink_tok, window_tok,
         _opt_ptr(tree_mask), _dev_ptr(workspace, "workspace"),
         workspace.numel() * workspace.element_size(), _stream(stream)), "qkv_decode_attn_tq3")
+
+
+# ---------------------------------------------------------------------------
+# paged caches (per-slot int32 block tables)
+# ---------------------------------------------------------------------------
+
+def _i32(t, what):
+    if t.dtype != torch.int32:
+        raise ValueError(f"{what} must be int32")
+    return _dev_ptr(t, what)
+
+
+def tq3_append_kv_paged(k, v, k_pool, v_pool, block_tables, positions, *, block_tokens,
+                        head_dim=256, stream=None) -> None:
+    """Paged append: k, v fp16 [n_slots][n_tok][num_kv][256]; token t of slot s
+    goes to position positions[s] + t through block_tables [n_slots][max_blocks]."""
+    assert k.dtype == torch.float16 and v.dtype == torch.float16 and k.shape == v.shape
+    n_slots, n_tok, num_kv = k.shape[0], k.shape[1], k.shape[2]
+    pool_rows = k_pool.numel() // (TQ3_BLOCK_BYTES * num_kv * head_dim // 128)
+    check(lib().qkv_tq3_append_kv_paged(
+        _dev_ptr(k, "k"), _dev_ptr(v, "v"), _dev_ptr(k_pool, "k_pool"), _dev_ptr(v_pool, "v_pool"),
+        n_slots, n_tok, num_kv, head_dim, _i32(block_tables, "block_tables"),
+        block_tables.shape[1], block_tokens, pool_rows, _i32(positions, "positions"),
+        _stream(stream)), "qkv_tq3_append_kv_paged")
+
+
+def decode_attn_tq3_paged_workspace(num_q, num_kv, n_slots, max_ctx, device) -> torch.Tensor:
+    n = int(lib().qkv_decode_attn_tq3_paged_workspace_bytes(num_q, num_kv, n_slots, max_ctx))
+    return torch.zeros(n, dtype=torch.uint8, device=device)
+
+
+def decode_attn_tq3_paged(q, k_pool, v_pool, out, workspace, block_tables, ctx_lens, *, num_q,
+                          num_kv, max_ctx, block_tokens, scale, head_dim=256,
+                          stream=None) -> None:
+    """One decode query per slot over per-slot block tables (ragged contexts)."""
+    pool_rows = k_pool.numel() // (TQ3_BLOCK_BYTES * num_kv * head_dim // 128)
+    check(lib().qkv_decode_attn_tq3_paged(
+        _dev_ptr(q, "q"), _dev_ptr(k_pool, "k_pool"), _dev_ptr(v_pool, "v_pool"),
+        _dev_ptr(out, "out"), num_q, num_kv, head_dim, q.shape[0],
+        _i32(block_tables, "block_tables"), block_tables.shape[1], block_tokens, pool_rows,
+        _i32(ctx_lens, "ctx_lens"), max_ctx, float(scale), _dev_ptr(workspace, "workspace"),
+        workspace.numel() * workspace.element_size(), _stream(stream)),
+        "qkv_decode_attn_tq3_paged")

@@ -41,3 +41,47 @@ def test_argument_errors_without_gpu(L):
     assert L.qkv_q8_append(p16, p16, -5, None) == -1
     assert L.qkv_q8_dequant(None, p16, 1, None) == -2
     assert L.qkv_tq3_init(-1) == -1
+
+
+def test_paged_argument_errors_without_gpu(L):
+    buf = ctypes.create_string_buffer(1 << 16)
+    p = (ctypes.addressof(buf) + 255) & ~255
+    ws_n = L.qkv_decode_attn_tq3_paged_workspace_bytes(16, 4, 2, 1000)
+    assert ws_n > 0
+    assert L.qkv_decode_attn_tq3_paged_workspace_bytes(16, 4, 0, 1000) == 0
+
+    def dec(**kw):
+        a = dict(q=p, k=p, v=p, out=p, num_q=16, num_kv=4, hd=256, n_slots=2, bt=p, max_blocks=4,
+                 block_tokens=256, pool_rows=1024, ctx=p, max_ctx=1000, scale=0.0625, ws=p,
+                 ws_bytes=ws_n)
+        a.update(kw)
+        return L.qkv_decode_attn_tq3_paged(a["q"], a["k"], a["v"], a["out"], a["num_q"],
+                                           a["num_kv"], a["hd"], a["n_slots"], a["bt"],
+                                           a["max_blocks"], a["block_tokens"], a["pool_rows"],
+                                           a["ctx"], a["max_ctx"], a["scale"], a["ws"],
+                                           a["ws_bytes"], None)
+    assert dec(block_tokens=100) == -3          # block size must be a multiple of 64
+    assert dec(block_tokens=32) == -3
+    assert dec(max_ctx=2000) == -1              # max_ctx beyond max_blocks * block_tokens
+    assert dec(n_slots=0) == -1
+    assert dec(hd=128) == -3
+    assert dec(num_q=40) == -3                  # GQA 10 is not instantiated
+    assert dec(bt=None) == -2
+    assert dec(ctx=None) == -2
+    assert dec(ws_bytes=ws_n - 1) == -7
+    assert dec(q=p + 2) == -4
+    assert dec(ws=p + 4) == -4
+
+    def app(**kw):
+        a = dict(k=p, v=p, kp=p, vp=p, n_slots=2, n_tok=1, num_kv=4, hd=256, bt=p, max_blocks=4,
+                 block_tokens=256, pool_rows=1024, pos=p)
+        a.update(kw)
+        return L.qkv_tq3_append_kv_paged(a["k"], a["v"], a["kp"], a["vp"], a["n_slots"],
+                                         a["n_tok"], a["num_kv"], a["hd"], a["bt"],
+                                         a["max_blocks"], a["block_tokens"], a["pool_rows"],
+                                         a["pos"], None)
+    assert app(n_slots=0) == 0                  # nothing to append
+    assert app(n_tok=-1) == -1
+    assert app(hd=64) == -3
+    assert app(pos=None) == -2
+    assert app(k=p + 8) == -4
