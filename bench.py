@@ -36,6 +36,7 @@ BLOCKS_PER_TOKEN = NUM_KV * HD // 128              # 8 TQ3 blocks per token for 
 ATTN_BYTES = CTX * 2 * BLOCKS_PER_TOKEN * 52 + NUM_Q * HD * 2 * 2
 APPEND_BYTES_PER_TOKEN = 2 * NUM_KV * HD * 2 + 2 * BLOCKS_PER_TOKEN * 52   # 4928
 CPU_REPS = 5
+APPEND_REPS = 5
 
 
 def parse():
@@ -83,26 +84,34 @@ def main():
     gen = torch.Generator(device=dev).manual_seed(3)
     stream = torch.cuda.current_stream()
 
-    # ---- cache build with the append kernel (timed: append throughput of the
-    # 8 back-to-back K+V appends of each set) ----
-    caches, append_ms = [], 0.0
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    # ---- cache build with the append kernel (untimed; it also warms the GPU) ----
+    caches, keep_src = [], None
     for s in range(SETS):
         src = [(outlier_kv(torch, gen, CTX, dev), outlier_kv(torch, gen, CTX, dev))
                for _ in range(LAYERS)]
         layers = [(kvcache.tq3_blocks(CTX * BLOCKS_PER_TOKEN, dev),
                    kvcache.tq3_blocks(CTX * BLOCKS_PER_TOKEN, dev)) for _ in range(LAYERS)]
-        torch.cuda.synchronize()
-        e0.record(stream)
         for (k16, v16), (kb, vb) in zip(src, layers):
             kvcache.tq3_append_kv(k16, v16, kb, vb)
-        e1.record(stream)
-        torch.cuda.synchronize()
-        append_ms += e0.elapsed_time(e1)
         caches.append(layers)
+        if s == 0:
+            keep_src = src
         del src
-    append_tok_layers = SETS * LAYERS * CTX
-    append_s = append_ms * 1e-3
+    torch.cuda.synchronize()
+
+    # ---- append throughput: APPEND_REPS passes re-encoding set 0's 8 layers
+    # (K+V, one launch per layer) into its own caches, which leaves the bytes
+    # unchanged; events on the launch stream around the back-to-back launches ----
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for _ in range(APPEND_REPS):
+        for (k16, v16), (kb, vb) in zip(keep_src, caches[0]):
+            kvcache.tq3_append_kv(k16, v16, kb, vb)
+    e1.record(stream)
+    torch.cuda.synchronize()
+    append_s = e0.elapsed_time(e1) * 1e-3
+    append_tok_layers = APPEND_REPS * LAYERS * CTX
+    del keep_src
     q = [torch.randn(1, NUM_Q, HD, generator=gen, device=dev).to(torch.float16)
          for _ in range(LAYERS)]
     out = torch.empty(1, NUM_Q, HD, dtype=torch.float16, device=dev)

@@ -18,6 +18,9 @@
  *                                   scipy.linalg.hadamard, H*H = 128*I
  *   or_tq3_find_bin                 numpy.searchsorted(bounds, v, 'left') on
  *                                   random + all-boundary + signed-zero + NaN
+ *   or_tq3_prescale_threshold_mismatches
+ *                                   exhaustive over all 2^32 fp32 patterns; a
+ *                                   threshold moved by one ulp must fail
  *   or_pack/unpack_3bit_8           numpy bit-level packing (LE 3-bit stream)
  *   or_tq3_encode                   fp64 rotation y = H*D*x/|x|/sqrt(128):
  *                                   codes equal searchsorted(bounds, y) except
@@ -162,6 +165,31 @@ uint8_t or_tq3_find_bin(float v) {
     for (int i = 0; i < 7; i++)
         if (v > k_bounds[i]) idx = (uint8_t)(i + 1);
     return idx;
+}
+
+/* Check of a table of bin thresholds on the WHT output before the x rs
+ * scaling (the form the GPU encoder uses): for every fp32 bit pattern w in
+ * [lo, hi], or_tq3_find_bin(fl(w * rs)) must equal #{k : w > thr[k]}.  Returns
+ * the number of bit patterns where the two differ; over [0, 2^32 - 1] a zero
+ * proves the folding exact. */
+int64_t or_tq3_prescale_threshold_mismatches(const uint32_t* thr, int64_t lo, int64_t hi,
+                                             int nthreads) {
+    const float rs = or_tq3_wht_scale();
+    float t[7];
+    for (int k = 0; k < 7; k++) t[k] = bits_f32(thr[k]);
+    int64_t bad = 0;
+#ifdef _OPENMP
+    if (nthreads <= 0) nthreads = omp_get_max_threads();
+#pragma omp parallel for schedule(static) num_threads(nthreads) reduction(+ : bad)
+#endif
+    for (int64_t u = lo; u <= hi; u++) {
+        const float w = bits_f32((uint32_t)u);
+        const float y = w * rs;
+        uint8_t c = 0;
+        for (int k = 0; k < 7; k++) c = (uint8_t)(c + (w > t[k]));
+        bad += (c != or_tq3_find_bin(y));
+    }
+    return bad;
 }
 
 /* turboquant.cuh:90-100 */

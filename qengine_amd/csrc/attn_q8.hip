@@ -28,12 +28,6 @@
 namespace qkv {
 namespace {
 
-typedef _Float16 h8_t __attribute__((ext_vector_type(8)));
-typedef float f4_t __attribute__((ext_vector_type(4)));
-typedef uint32_t u4_t __attribute__((ext_vector_type(4)));
-typedef uint32_t u2_t __attribute__((ext_vector_type(2)));
-
-constexpr int kBufferRsrcWord3 = 0x00020000;   // raw buffer, 32-bit data format
 constexpr int kWaves = 4;
 constexpr int kThreads = 64 * kWaves;
 constexpr int kTile = 32;                      // keys per wave tile

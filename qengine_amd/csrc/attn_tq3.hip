@@ -36,16 +36,7 @@
 
 namespace qkv {
 
-typedef _Float16 h8_t __attribute__((ext_vector_type(8)));
-typedef float f4_t __attribute__((ext_vector_type(4)));
-typedef uint32_t u4_t __attribute__((ext_vector_type(4)));
-typedef uint32_t u3_t __attribute__((ext_vector_type(3)));
-typedef uint32_t u2_t __attribute__((ext_vector_type(2)));
 typedef uint32_t u32_a1 __attribute__((aligned(1)));
-typedef float f2_t __attribute__((ext_vector_type(2)));
-
-// word 3 of a raw buffer resource on gfx9-family GPUs (32-bit data format)
-constexpr int kBufferRsrcWord3 = 0x00020000;
 
 constexpr int kTile = 64;
 constexpr int kWaves = 8;

@@ -66,6 +66,63 @@ __device__ __forceinline__ uint32_t tq3_bin(float y) {
   return idx;
 }
 
+// ---- bin thresholds on the WHT output before the x rs scaling -------------
+// The reference bins y = fl(w * rs) (turboquant.cuh:145-150).  w -> fl(w * rs)
+// is monotone non-decreasing for rs > 0, so for every bound B there is an fp32
+// value R with  fl(w * rs) > B  <=>  w > R  for all w (NaN compares false on
+// both sides).  R is found by bisection over the bit patterns of non-negative
+// floats (ordered like the floats themselves), evaluated at compile time with
+// IEEE round-to-nearest-even products:
+//   B >= 0:  R = largest w >= 0 with fl(w * rs) <= B
+//   B <  0:  fl(w * rs) > B  <=>  fl(-w * rs) < -B  <=>  -w < Q,  Q = smallest
+//            w >= 0 with fl(w * rs) >= -B, so R = -Q.
+// Some bounds are hit exactly by fl(w * rs), so the negative thresholds are not
+// the mirror images of the positive ones; the static_assert pins the values.
+constexpr float bits_to_float(uint32_t b) { return __builtin_bit_cast(float, b); }
+constexpr uint32_t float_to_bits(float f) { return __builtin_bit_cast(uint32_t, f); }
+constexpr float kWhtScaleHost = bits_to_float(0x3DB504F3u);
+constexpr uint32_t last_bits_at_most(float bound) {   // largest w >= 0, fl(w*rs) <= bound
+  uint32_t lo = 0u, hi = 0x7f800000u;                  // f(lo) <= bound < f(hi)
+  while (hi - lo > 1u) {
+    const uint32_t mid = lo + (hi - lo) / 2u;
+    if (bits_to_float(mid) * kWhtScaleHost <= bound) lo = mid; else hi = mid;
+  }
+  return lo;
+}
+constexpr uint32_t first_bits_at_least(float bound) {  // smallest w >= 0, fl(w*rs) >= bound
+  uint32_t lo = 0u, hi = 0x7f800000u;                  // f(lo) < bound <= f(hi)
+  while (hi - lo > 1u) {
+    const uint32_t mid = lo + (hi - lo) / 2u;
+    if (bits_to_float(mid) * kWhtScaleHost >= bound) hi = mid; else lo = mid;
+  }
+  return hi;
+}
+constexpr uint32_t bin_threshold_bits(int k) {
+  return kBounds[k] >= 0.0f ? last_bits_at_most(kBounds[k])
+                            : (first_bits_at_least(-kBounds[k]) | 0x80000000u);
+}
+constexpr uint32_t kBinThrBits[7] = {bin_threshold_bits(0), bin_threshold_bits(1),
+                                     bin_threshold_bits(2), bin_threshold_bits(3),
+                                     bin_threshold_bits(4), bin_threshold_bits(5),
+                                     bin_threshold_bits(6)};
+static_assert(kBinThrBits[0] == 0xbfdfd5e2u && kBinThrBits[1] == 0xbf86719cu &&
+                  kBinThrBits[2] == 0xbf002dd8u && kBinThrBits[3] == 0x00000005u &&
+                  kBinThrBits[4] == 0x3f002dd8u && kBinThrBits[5] == 0x3f86719cu &&
+                  kBinThrBits[6] == 0x3fdfd5e3u,
+              "pre-scale bin thresholds (checked exhaustively against fl(w*rs) on the host)");
+
+// ---- vector types and raw buffer resources --------------------------------
+typedef _Float16 h8_t __attribute__((ext_vector_type(8)));
+typedef float f4_t __attribute__((ext_vector_type(4)));
+typedef float f2_t __attribute__((ext_vector_type(2)));
+typedef uint32_t u4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t u3_t __attribute__((ext_vector_type(3)));
+typedef uint32_t u2_t __attribute__((ext_vector_type(2)));
+
+// Word 3 of a raw buffer resource on gfx9-family GPUs (32-bit data format).
+// Buffer loads past num_records return zero and stores past it are dropped.
+constexpr int kBufferRsrcWord3 = 0x00020000;
+
 // ---- fp16 helpers (bit level) ---------------------------------------------
 __device__ __forceinline__ float h2f(uint32_t bits16) {
   return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(bits16)));

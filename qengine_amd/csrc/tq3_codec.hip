@@ -2,15 +2,21 @@
 //
 // Reference arithmetic: turboquant.cuh:112-165 (encode) and 169-200 (decode).
 //
-// Layout on the GPU: one lane owns one 128-element block.  A wave stages its
-// 64 input blocks (16 KiB of fp16) from HBM with coalesced 16-byte loads into
-// LDS at a 272-byte pitch (bank-conflict-free 16-byte reads per lane), each
-// lane then runs the reference's sequential norm, unit scaling, random signs,
-// 7-stage butterfly WHT and 7-bound bin search in registers, and the wave
-// writes its 64 x 52-byte output through an LDS staging area with dword
-// stores that cover whole cache lines.  Every float operation is the same
-// single-rounding IEEE operation in the same order as the reference, so
-// codes and norms are bit-identical.
+// Layout on the GPU: one lane owns one 128-element block.  Waves are
+// persistent: each takes 64-block tiles (16 KiB of fp16) in turn, with the
+// coalesced 16-byte buffer loads of its next tile in flight into registers
+// while it encodes the current one.  A tile passes through LDS at a 272-byte
+// pitch (bank-conflict-free 16-byte reads per lane); each lane then runs the
+// reference's sequential norm, unit scaling, random signs and 7-stage
+// butterfly WHT in registers, bins the result against thresholds that fold
+// the final x rs scaling in exactly, and the wave writes its 64 x 52-byte
+// output through an LDS staging area with dword stores that cover whole cache
+// lines.  Every float operation that feeds a code or a norm is the same
+// single-rounding IEEE operation in the same order as the reference, so codes
+// and norms are bit-identical.
+#include <algorithm>
+#include <atomic>
+
 #include "qkv_device.h"
 #include "qkv_launch.h"
 
@@ -43,8 +49,67 @@ __device__ __forceinline__ void wht128_butterflies(float (&x)[128]) {
   }
 }
 
+// Bin two elements xa, xb against the seven pre-scale thresholds r[] into
+// scalar lane-mask bit planes: bit b of element a's bin index is lane bit of
+// pa[b] (likewise pb for xb).
+//   t_k = [x > r_k] (ordered compare into a lane mask) is a thermometer code,
+//   so  b2 = t3,  b1 = t1 ^ t3 ^ t5,  b0 = b1 ^ t0 ^ t2 ^ t4 ^ t6.
+// The XORs run on the scalar unit, in place: b1 ends in t1, b0 in t0 and b2
+// is t3 itself.  Each scalar instruction reads masks written by compares at
+// least seven instructions earlier, and every plane is read by a vector
+// instruction only after the ten-plus instructions that end this block.
+__device__ __forceinline__ void bin_planes2(float xa, float xb, const uint32_t (&r)[7],
+                                            uint64_t (&pa)[3], uint64_t (&pb)[3]) {
+  uint64_t a2, a4, a5, a6, b2, b4, b5, b6;
+  asm("v_cmp_gt_f32_e64 %[a3], %[xa], %[r3]\n\t"
+      "v_cmp_gt_f32_e64 %[b3], %[xb], %[r3]\n\t"
+      "v_cmp_gt_f32_e64 %[a1], %[xa], %[r1]\n\t"
+      "v_cmp_gt_f32_e64 %[a5], %[xa], %[r5]\n\t"
+      "v_cmp_gt_f32_e64 %[a0], %[xa], %[r0]\n\t"
+      "v_cmp_gt_f32_e64 %[a2], %[xa], %[r2]\n\t"
+      "v_cmp_gt_f32_e64 %[a4], %[xa], %[r4]\n\t"
+      "v_cmp_gt_f32_e64 %[a6], %[xa], %[r6]\n\t"
+      "v_cmp_gt_f32_e64 %[b1], %[xb], %[r1]\n\t"
+      "v_cmp_gt_f32_e64 %[b5], %[xb], %[r5]\n\t"
+      "v_cmp_gt_f32_e64 %[b0], %[xb], %[r0]\n\t"
+      "v_cmp_gt_f32_e64 %[b2], %[xb], %[r2]\n\t"
+      "v_cmp_gt_f32_e64 %[b4], %[xb], %[r4]\n\t"
+      "v_cmp_gt_f32_e64 %[b6], %[xb], %[r6]\n\t"
+      "s_xor_b64 %[a1], %[a1], %[a5]\n\t"
+      "s_xor_b64 %[a1], %[a1], %[a3]\n\t"
+      "s_xor_b64 %[a0], %[a0], %[a2]\n\t"
+      "s_xor_b64 %[a4], %[a4], %[a6]\n\t"
+      "s_xor_b64 %[a0], %[a0], %[a4]\n\t"
+      "s_xor_b64 %[a0], %[a0], %[a1]\n\t"
+      "s_xor_b64 %[b1], %[b1], %[b5]\n\t"
+      "s_xor_b64 %[b1], %[b1], %[b3]\n\t"
+      "s_xor_b64 %[b0], %[b0], %[b2]\n\t"
+      "s_xor_b64 %[b4], %[b4], %[b6]\n\t"
+      "s_xor_b64 %[b0], %[b0], %[b4]\n\t"
+      "s_xor_b64 %[b0], %[b0], %[b1]"
+      : [a0] "=&s"(pa[0]), [a1] "=&s"(pa[1]), [a3] "=&s"(pa[2]), [a2] "=&s"(a2),
+        [a4] "=&s"(a4), [a5] "=&s"(a5), [a6] "=&s"(a6), [b0] "=&s"(pb[0]),
+        [b1] "=&s"(pb[1]), [b3] "=&s"(pb[2]), [b2] "=&s"(b2), [b4] "=&s"(b4),
+        [b5] "=&s"(b5), [b6] "=&s"(b6)
+      : [xa] "v"(xa), [xb] "v"(xb), [r0] "s"(r[0]), [r1] "s"(r[1]), [r2] "s"(r[2]),
+        [r3] "s"(r[3]), [r4] "s"(r[4]), [r5] "s"(r[5]), [r6] "s"(r[6]));
+}
+
+// acc = 2 * acc + (this lane's bit of the mask): shifts one plane bit in.
+__device__ __forceinline__ void shift_in(uint32_t& acc, uint64_t plane) {
+  uint64_t cy;
+  asm("v_addc_co_u32_e64 %[a], %[cy], %[a], %[a], %[p]"
+      : [a] "+v"(acc), [cy] "=&s"(cy) : [p] "s"(plane));
+}
+
 // Encode one block held as 64 dwords of packed fp16 (element 2k in the low
 // half of hw[k]).  Writes the 13 output dwords (norm, qs[0..47]) to o[].
+//
+// Instruction budget per element: one v_fma_mix for the norm, one for the
+// scaling (fp16 operand converted inside the instruction), seven butterfly
+// add/subs, seven compares into scalar lane masks and three shifts of a mask
+// bit into the packed words.  The bit planes of the 3-bit code are formed from
+// the compare masks on the scalar unit, which runs beside the vector ALU.
 __device__ __forceinline__ void tq3_encode_block(const uint32_t (&hw)[64], uint32_t (&o)[13]) {
   // Sequential sum of squares in reference order (x^2 of an fp16 value is
   // exact in fp32, so an FMA gives the same result as mul+add).
@@ -56,29 +121,43 @@ __device__ __forceinline__ void tq3_encode_block(const uint32_t (&hw)[64], uint3
     nsq = __builtin_fmaf(hi, hi, nsq);
   }
   const float norm = __builtin_sqrtf(nsq);
-  o[0] = __float_as_uint(norm);
-#pragma unroll
-  for (int k = 1; k < 13; k++) o[k] = 0u;
-  if (norm < 1e-10f) return;  // zero block: norm stored, codes zero
-
   const float inv = 1.0f / norm;
   float x[128];
 #pragma unroll
   for (int k = 0; k < 64; k++) {
-    // x * inv then * sign: the sign multiply is exact, so fold it into the factor.
-    x[2 * k] = h2f(hw[k] & 0xffffu) * (sign_pos(2 * k) ? inv : -inv);
-    x[2 * k + 1] = h2f(hw[k] >> 16) * (sign_pos(2 * k + 1) ? inv : -inv);
+    // x * inv then * sign: the sign multiply is exact, so it folds into the
+    // factor.  The +0 addend only changes the sign of an exact zero, which no
+    // later sum or bin comparison can observe.
+    x[2 * k] = __builtin_fmaf(h2f(hw[k] & 0xffffu), sign_pos(2 * k) ? inv : -inv, 0.0f);
+    x[2 * k + 1] = __builtin_fmaf(h2f(hw[k] >> 16), sign_pos(2 * k + 1) ? inv : -inv, 0.0f);
   }
   wht128_butterflies(x);
-  const float rs = wht_scale();
+
+  // Bins against the pre-scale thresholds (same result as binning x * rs).
+  // t_k = [x > R_k] is a thermometer code, so the bin index bits are
+  //   b2 = t3,  b1 = t1 ^ t3 ^ t5,  b0 = t0 ^ t1 ^ ... ^ t6.
+  // Bit 3e+b of the 384-bit code stream is bit b of element e; the words are
+  // filled by shifting bits in from the top, highest element first.
+  uint32_t acc[12];
 #pragma unroll
-  for (int e = 0; e < 128; e++) {
-    uint32_t c = tq3_bin(x[e] * rs);
-    const int bit = 3 * e;
-    const int w = bit >> 5, sh = bit & 31;
-    o[1 + w] |= c << sh;
-    if (sh > 29) o[2 + w] |= c >> (32 - sh);
+  for (int w = 0; w < 12; w++) acc[w] = 0u;
+  uint32_t r[7];
+#pragma unroll
+  for (int k = 0; k < 7; k++) r[k] = __builtin_amdgcn_readfirstlane(kBinThrBits[k]);
+#pragma unroll
+  for (int e = 127; e >= 1; e -= 2) {
+    uint64_t pa[3], pb[3];
+    bin_planes2(x[e], x[e - 1], r, pa, pb);
+#pragma unroll
+    for (int b = 2; b >= 0; b--) shift_in(acc[(3 * e + b) >> 5], pa[b]);
+#pragma unroll
+    for (int b = 2; b >= 0; b--) shift_in(acc[(3 * (e - 1) + b) >> 5], pb[b]);
   }
+  // zero block (turboquant.cuh:133-140): norm stored, codes zero
+  const bool zero = norm < 1e-10f;
+  o[0] = __float_as_uint(norm);
+#pragma unroll
+  for (int w = 0; w < 12; w++) o[1 + w] = zero ? 0u : acc[w];
 }
 
 // Output block of input block i for a paged append (PagedRows), or -1 when
@@ -97,79 +176,123 @@ __device__ __forceinline__ long paged_block(const PagedRows& pr, long i) {
   return row * pr.blocks_per_row + j;
 }
 
-// in: n_blocks*128 fp16 as uint4 (16 B aligned); out: n_blocks*13 dwords,
-// or, when pr.block_tables is set, each block at its paged_block position.
-// gridDim.y selects the (in, out) pair so K and V can share one launch.
-__global__ __launch_bounds__(kCodecThreads) void tq3_append_kernel(
-    const uint4* __restrict__ in0, uint32_t* __restrict__ out0, const uint4* __restrict__ in1,
-    uint32_t* __restrict__ out1, int n_blocks, PagedRows pr) {
-  __shared__ uint32_t lds[kCodecWaves * kWaveLdsDw];
-  const uint4* __restrict__ in = blockIdx.y ? in1 : in0;
-  uint32_t* __restrict__ out = blockIdx.y ? out1 : out0;
-  const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
-  uint32_t* wl = lds + wave * kWaveLdsDw;
-  const long b0 = ((long)blockIdx.x * kCodecWaves + wave) * 64;  // first block of this wave
-  if (b0 >= n_blocks) return;                                     // whole wave idle
-  const int nb = (int)min<long>(64, n_blocks - b0);
-
-  // 1. coalesced 16-byte loads of the wave's blocks into LDS
+// Issue the 16 coalesced 16-byte loads of one 64-block tile (blocks b0..b0+nb-1
+// of `in`); chunk j*64+lane is 16-byte piece (chunk & 15) of block (chunk >> 4).
+// The buffer resource spans exactly the tile's nb blocks, so chunks past the
+// last block read zero: the loads carry no branches or clamps.
+__device__ __forceinline__ void load_tile(uint32_t (&pre)[64], const uint4* __restrict__ in,
+                                          long b0, int nb, int lane) {
+  const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint4*>(in + b0 * 16), 0, nb * 256, kBufferRsrcWord3);
 #pragma unroll
   for (int j = 0; j < 16; j++) {
-    const int chunk = j * 64 + lane;  // 16-byte chunk within the wave's 16 KiB
-    const int blk = chunk >> 4, part = chunk & 15;
-    if (blk < nb) {
-      uint4 v = in[(b0 + blk) * 16 + part];
-      *reinterpret_cast<uint4*>(wl + blk * kInPitchDw + part * 4) = v;
-    }
+    const u4_t v = __builtin_amdgcn_raw_buffer_load_b128(rs, lane * 16, j * 1024, 0);
+    pre[4 * j] = v.x;
+    pre[4 * j + 1] = v.y;
+    pre[4 * j + 2] = v.z;
+    pre[4 * j + 3] = v.w;
   }
-  __builtin_amdgcn_s_waitcnt(0);
-  __builtin_amdgcn_wave_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "workgroup");
+}
 
-  // 2. one lane per block
-  uint32_t o[13];
-  if (lane < nb) {
-    uint32_t hw[64];
+// in: n_blocks*128 fp16 as uint4 (16 B aligned); out: n_blocks*13 dwords,
+// or, when pr.block_tables is set, each block at its paged_block position.
+// n_tensors (1 or 2) (in, out) pairs share one launch (K and V).
+//
+// Persistent waves: tile t (64 blocks) of the n_tensors * tiles work list is
+// taken by wave t mod (total waves).  While a wave encodes one tile, the
+// loads of its next tile are in flight into registers, so each wave overlaps
+// its own HBM latency with its vector work.
+__global__ __launch_bounds__(kCodecThreads, 2) void tq3_append_kernel(
+    const uint4* __restrict__ in0, uint32_t* __restrict__ out0, const uint4* __restrict__ in1,
+    uint32_t* __restrict__ out1, int n_blocks, int n_tensors, PagedRows pr) {
+  __shared__ uint32_t lds[kCodecWaves * kWaveLdsDw];
+  const int lane = threadIdx.x & 63;
+  // wave-uniform: keeps the tile bookkeeping on the scalar unit
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  uint32_t* wl = lds + wave * kWaveLdsDw;
+  const long tiles = ((long)n_blocks + 63) / 64;
+  const long total = tiles * n_tensors;
+  const long stride = (long)gridDim.x * kCodecWaves;
+  long t = (long)blockIdx.x * kCodecWaves + wave;
+  if (t >= total) return;  // whole wave idle
+
+  uint32_t pre[64];
+  {
+    const long b0 = (t % tiles) * 64;
+    load_tile(pre, t < tiles ? in0 : in1, b0, (int)min<long>(64, n_blocks - b0), lane);
+  }
+  for (;;) {
+    const bool second = t >= tiles;
+    uint32_t* __restrict__ out = second ? out1 : out0;
+    const long b0 = (t % tiles) * 64;
+    const int nb = (int)min<long>(64, n_blocks - b0);
+
+    // 1. the prefetched tile into LDS (272-byte pitch: conflict-free reads;
+    //    pieces of blocks past nb are zeros and are never read)
 #pragma unroll
-    for (int k = 0; k < 16; k++) {
-      uint4 v = *reinterpret_cast<const uint4*>(wl + lane * kInPitchDw + 4 * k);
-      hw[4 * k] = v.x;
-      hw[4 * k + 1] = v.y;
-      hw[4 * k + 2] = v.z;
-      hw[4 * k + 3] = v.w;
+    for (int j = 0; j < 16; j++) {
+      const int chunk = j * 64 + lane;
+      const int blk = chunk >> 4, part = chunk & 15;
+      *reinterpret_cast<uint4*>(wl + blk * kInPitchDw + part * 4) =
+          make_uint4(pre[4 * j], pre[4 * j + 1], pre[4 * j + 2], pre[4 * j + 3]);
     }
-    tq3_encode_block(hw, o);
-  }
-  __builtin_amdgcn_wave_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "workgroup");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "workgroup");
 
-  // paged: each lane stores its block at its own row
-  if (pr.block_tables != nullptr) {
+    // 2. next tile's loads go out before this tile's vector work
+    const long tn = t + stride;
+    if (tn < total) {
+      const long nb0 = (tn % tiles) * 64;
+      load_tile(pre, tn < tiles ? in0 : in1, nb0, (int)min<long>(64, n_blocks - nb0), lane);
+    }
+
+    // 3. one lane per block
+    uint32_t o[13];
     if (lane < nb) {
-      const long ob = paged_block(pr, b0 + lane);
-      if (ob >= 0) {
-        uint32_t* dst = out + ob * 13;
+      uint32_t hw[64];
 #pragma unroll
-        for (int k = 0; k < 13; k++) dst[k] = o[k];
+      for (int k = 0; k < 16; k++) {
+        uint4 v = *reinterpret_cast<const uint4*>(wl + lane * kInPitchDw + 4 * k);
+        hw[4 * k] = v.x;
+        hw[4 * k + 1] = v.y;
+        hw[4 * k + 2] = v.z;
+        hw[4 * k + 3] = v.w;
       }
+      tq3_encode_block(hw, o);
     }
-    return;
-  }
-  // 3. stage 13 dwords per lane (odd pitch: conflict-free), then store the
-  //    wave's contiguous 64*52 bytes with dword stores.
-  if (lane < nb) {
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "workgroup");
+
+    if (pr.block_tables != nullptr) {
+      // paged: each lane stores its block at its own row
+      if (lane < nb) {
+        const long ob = paged_block(pr, b0 + lane);
+        if (ob >= 0) {
+          uint32_t* dst = out + ob * 13;
 #pragma unroll
-    for (int k = 0; k < 13; k++) wl[lane * 13 + k] = o[k];
-  }
-  __builtin_amdgcn_wave_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "workgroup");
-  const int n_dw = nb * 13;
-  uint32_t* dst = out + b0 * 13;
+          for (int k = 0; k < 13; k++) dst[k] = o[k];
+        }
+      }
+    } else {
+      // 4. stage 13 dwords per lane (odd pitch: conflict-free), then store the
+      //    wave's contiguous 64*52 bytes with dword stores.
+      if (lane < nb) {
 #pragma unroll
-  for (int j = 0; j < 13; j++) {
-    const int idx = j * 64 + lane;
-    if (idx < n_dw) dst[idx] = wl[idx];
+        for (int k = 0; k < 13; k++) wl[lane * 13 + k] = o[k];
+      }
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "workgroup");
+      // the resource spans the tile's nb * 52 bytes: stores past it are dropped
+      const __amdgpu_buffer_rsrc_t rd = __builtin_amdgcn_make_buffer_rsrc(
+          out + b0 * 13, 0, nb * 52, kBufferRsrcWord3);
+#pragma unroll
+      for (int j = 0; j < 13; j++)
+        __builtin_amdgcn_raw_buffer_store_b32(wl[j * 64 + lane], rd, lane * 4, j * 256, 0);
+    }
+    if (tn >= total) break;
+    t = tn;
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "workgroup");
   }
 }
 
@@ -252,12 +375,29 @@ __global__ __launch_bounds__(kCodecThreads) void tq3_dequant_kernel(
 hipError_t launch_tq3_append(const void* in0, void* out0, const void* in1, void* out1,
                              int n_blocks, int n_tensors, hipStream_t stream,
                              const PagedRows* paged) {
-  const int per_wg = 64 * kCodecWaves;
-  dim3 grid((n_blocks + per_wg - 1) / per_wg, n_tensors);
+  // Persistent grid: two workgroups (8 waves) per CU, fewer when the work
+  // list is shorter.
+  static std::atomic<int> cus[64];
+  int dev = 0;
+  hipError_t err = hipGetDevice(&dev);
+  if (err != hipSuccess) return err;
+  if (dev < 0 || dev >= 64) return hipErrorInvalidDevice;
+  int n_cu = cus[dev].load(std::memory_order_relaxed);
+  if (n_cu == 0) {
+    err = hipDeviceGetAttribute(&n_cu, hipDeviceAttributeMultiprocessorCount, dev);
+    if (err != hipSuccess) return err;
+    n_cu = n_cu > 0 ? n_cu : 1;
+    cus[dev].store(n_cu, std::memory_order_relaxed);
+  }
+  const long tiles = ((long)n_blocks + 63) / 64 * n_tensors;
+  const long wgs_needed = (tiles + kCodecWaves - 1) / kCodecWaves;
+  const int grid = (int)std::min<long>(wgs_needed, 2L * n_cu);
+  if (grid == 0) return hipSuccess;
   const PagedRows pr = paged ? *paged : PagedRows{};
-  hipLaunchKernelGGL(tq3_append_kernel, grid, dim3(kCodecThreads), 0, stream,
+  hipLaunchKernelGGL(tq3_append_kernel, dim3(grid), dim3(kCodecThreads), 0, stream,
                      static_cast<const uint4*>(in0), static_cast<uint32_t*>(out0),
-                     static_cast<const uint4*>(in1), static_cast<uint32_t*>(out1), n_blocks, pr);
+                     static_cast<const uint4*>(in1), static_cast<uint32_t*>(out1), n_blocks,
+                     n_tensors, pr);
   return hipGetLastError();
 }
 

@@ -1,6 +1,8 @@
 """Pins the CPU oracle's codec functions with checks that do not restate its
 formulas: known answers, textbook identities, numpy/scipy routines and fp64
 mathematics.  Reference: src/turboquant.cuh, src/attention.cuh:2587-2626."""
+import os
+
 import numpy as np
 import pytest
 from scipy.linalg import hadamard
@@ -8,6 +10,8 @@ from scipy.stats import norm as normal
 
 from oracle import oracle as O
 from tests._data import kv_f16
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 
 RS64 = 1.0 / np.sqrt(128.0)
 
@@ -257,3 +261,34 @@ def test_q8_decode_vs_numpy():
     d = blk["d"].view(np.float16).astype(np.float32)
     ref = (blk["qs"].astype(np.float32) * d[:, None]).astype(np.float16).view(np.uint16)
     assert np.array_equal(O.q8_decode(blk).reshape(128, 32), ref)
+
+
+# ---------------------------------------------------------------------------
+# Pre-scale bin thresholds used by the GPU encoder: binning the WHT output w
+# against them is the same as binning fl(w * rs) against the reference bounds
+# (turboquant.cuh:145-150), for every fp32 value.
+# ---------------------------------------------------------------------------
+PRESCALE_THR = [0xbfdfd5e2, 0xbf86719c, 0xbf002dd8, 0x00000005,
+                0x3f002dd8, 0x3f86719c, 0x3fdfd5e3]
+
+
+def test_prescale_thresholds_match_device_header():
+    import re
+    hdr = open(os.path.join(ROOT, "qengine_amd", "csrc", "qkv_device.h")).read()
+    pinned = {int(k): int(v, 16) for k, v in re.findall(r"kBinThrBits\[(\d)\] == (0x[0-9a-f]+)u", hdr)}
+    assert pinned == dict(enumerate(PRESCALE_THR))
+
+
+def test_prescale_thresholds_exhaustive():
+    assert O.prescale_threshold_mismatches(PRESCALE_THR) == 0
+
+
+@pytest.mark.parametrize("k,delta", [(0, 1), (1, -1), (2, -1), (3, -5), (4, 1), (5, 1), (6, -1)])
+def test_prescale_thresholds_one_ulp_off_fails(k, delta):
+    """Moving any threshold by one ulp (the zero bound's to +0) breaks the
+    equivalence; the search window is the 2^16 patterns around it."""
+    thr = list(PRESCALE_THR)
+    thr[k] = (thr[k] + delta) & 0xffffffff
+    lo, hi = max(0, thr[k] - (1 << 15)), min(0xFFFFFFFF, thr[k] + (1 << 15))
+    assert O.prescale_threshold_mismatches(PRESCALE_THR, lo, hi) == 0
+    assert O.prescale_threshold_mismatches(thr, lo, hi) > 0
