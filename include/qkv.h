@@ -199,6 +199,31 @@ int qkv_tq3_append_kv_paged(const uint16_t* k_f16, const uint16_t* v_f16, qkv_bl
                             int block_tokens, int pool_rows, const int32_t* positions,
                             hipStream_t stream);
 
+/* Chunked prefill attention over a TQ3 cache (BASELINE config 5(i)).
+ * Replaces, for one slot, the reference's per-chunk sequence: bulk dequant of
+ * the history into an fp16 scratch plus a copy of the chunk's fp16 K/V after
+ * it (model.cuh:5189-5214), then per 16-token sub-chunk the split-K kernel
+ * flash_attn_chunk_fused_split_ntb and flash_attn_split_merge over that
+ * scratch (model.cuh:5256-5330, 5680-5721; attention.cuh:1690-1831,
+ * 1837-1891).  The history is read from the packed cache directly.
+ * q: [n_tok][num_q][256] fp16 (post-RoPE queries of chunk positions
+ *    start_pos .. start_pos + n_tok - 1);
+ * k_cache, v_cache: slot-base TQ3 caches whose rows 0 .. start_pos-1 hold
+ *    the history (rows from start_pos on are not read);
+ * k_chunk, v_chunk: [n_tok][num_kv][256] fp16, the chunk's own keys and
+ *    values, attended unquantized as in the reference;
+ * out: [n_tok][num_q][256] fp16.  Query token t attends to keys
+ * 0 .. start_pos + t.  The append of the chunk into the cache is a separate
+ * qkv_tq3_append_kv call (model.cuh:5176-5190).  GQA 4 and 6.  workspace:
+ * caller-owned device memory of qkv_prefill_attn_tq3_workspace_bytes() bytes,
+ * 256-byte aligned (no initialisation needed). */
+size_t qkv_prefill_attn_tq3_workspace_bytes(int num_q, int num_kv, int n_tok, int start_pos);
+int qkv_prefill_attn_tq3(const uint16_t* q, const qkv_block_tq3* k_cache,
+                         const qkv_block_tq3* v_cache, const uint16_t* k_chunk,
+                         const uint16_t* v_chunk, uint16_t* out, int num_q, int num_kv,
+                         int head_dim, int start_pos, int n_tok, float scale, void* workspace,
+                         size_t workspace_bytes, hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

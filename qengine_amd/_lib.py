@@ -53,6 +53,8 @@ SIGNATURES = {
     "qkv_decode_attn_tq3_paged_workspace_bytes": (_SZ, [_I, _I, _I, _I]),
     "qkv_decode_attn_tq3_paged": (_I, [_P, _P, _P, _P, _I, _I, _I, _I, _P, _I, _I, _I, _P, _I,
                                       _F, _P, _SZ, _P]),
+    "qkv_prefill_attn_tq3_workspace_bytes": (_SZ, [_I, _I, _I, _I]),
+    "qkv_prefill_attn_tq3": (_I, [_P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _F, _P, _SZ, _P]),
 }
 
 _lib = None

@@ -79,6 +79,27 @@ __device__ __forceinline__ float wave_sum(float v) {
   return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
 }
 
+// Table address: byte 1 of `addr` := bits SHIFT..SHIFT+7 of w, bytes 0, 2, 3
+// (4 * lane, 0, 0) kept -- one v_lshrrev_b32 with SDWA dst_sel:BYTE_1 and
+// dst_unused:UNUSED_PRESERVE.  Each address register is reused by the next
+// lookup of its chain, so no copy of 4 * lane is needed per lookup.
+template <int SHIFT>
+__device__ __forceinline__ uint32_t sdwa_index(uint32_t addr, uint32_t w) {
+  asm("v_lshrrev_b32_sdwa %0, %2, %1 dst_sel:BYTE_1 dst_unused:UNUSED_PRESERVE src0_sel:DWORD "
+      "src1_sel:DWORD"
+      : "+v"(addr)
+      : "v"(w), "i"(SHIFT));
+  return addr;
+}
+// Lloyd-Max centroid i (turboquant.cuh:27-30) selected from immediates.
+__device__ __forceinline__ float centroid_imm(uint32_t i) {
+  // i >= 4: +m[i-4]; i < 4: -m[3-i]  (symmetric table)
+  const float mpos = (i & 2) ? ((i & 1) ? 0.190303f : 0.118828f) : ((i & 1) ? 0.066847f : 0.021664f);
+  const uint32_t j = 3u - (i & 3u);
+  const float mneg = (j & 2) ? ((j & 1) ? 0.190303f : 0.118828f) : ((j & 1) ? 0.066847f : 0.021664f);
+  return (i & 4) ? mpos : -mneg;
+}
+
 // ---- 128-point Walsh-Hadamard pieces (butterflies (a,b) -> (a+b, a-b)) ----
 // Element e = part*8 + i of a 128-block lives in register i of lane `part`
 // (16 consecutive lanes per block).

@@ -76,29 +76,8 @@ static_assert(kLdsMergeEnd <= kLdsQ, "merge area must not reach the query scratc
 constexpr int kMlW0 = 0, kMlLw0 = 8 * kWaves, kMlM = 16 * kWaves, kMlL = 16 * kWaves + 8;
 static_assert(kMlL + 8 <= 256, "merge scalars must fit the ML area");
 
-// Table address: byte 1 of `addr` := bits SHIFT..SHIFT+7 of w, bytes 0, 2, 3
-// (4 * lane, 0, 0) kept -- one v_lshrrev_b32 with SDWA dst_sel:BYTE_1 and
-// dst_unused:UNUSED_PRESERVE.  Each address register is reused by the next
-// lookup of its chain, so no copy of 4 * lane is needed per lookup.
-template <int SHIFT>
-__device__ __forceinline__ uint32_t sdwa_index(uint32_t addr, uint32_t w) {
-  asm("v_lshrrev_b32_sdwa %0, %2, %1 dst_sel:BYTE_1 dst_unused:UNUSED_PRESERVE src0_sel:DWORD "
-      "src1_sel:DWORD"
-      : "+v"(addr)
-      : "v"(w), "i"(SHIFT));
-  return addr;
-}
 __device__ __forceinline__ uint32_t lut_read(const uint8_t* lds, uint32_t addr) {
   return *reinterpret_cast<const uint32_t*>(lds + kLdsLut + addr);
-}
-
-// Lloyd-Max centroid i (turboquant.cuh:27-30) selected from immediates.
-__device__ __forceinline__ float centroid_imm(uint32_t i) {
-  // i >= 4: +m[i-4]; i < 4: -m[3-i]  (symmetric table)
-  const float mpos = (i & 2) ? ((i & 1) ? 0.190303f : 0.118828f) : ((i & 1) ? 0.066847f : 0.021664f);
-  const uint32_t j = 3u - (i & 3u);
-  const float mneg = (j & 2) ? ((j & 1) ? 0.190303f : 0.118828f) : ((j & 1) ? 0.066847f : 0.021664f);
-  return (i & 4) ? mpos : -mneg;
 }
 
 // Table address of the 6-bit field at bit BIT of a 3-dword code stream

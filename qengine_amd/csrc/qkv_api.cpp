@@ -380,4 +380,50 @@ int qkv_decode_attn_tq3_paged(const uint16_t* q, const qkv_block_tq3* k_pool,
   return launch_status(qkv::launch_tq3_attn(a, 0, out, stream));
 }
 
+size_t qkv_prefill_attn_tq3_workspace_bytes(int num_q, int num_kv, int n_tok, int start_pos) {
+  if (num_q <= 0 || num_kv <= 0 || n_tok <= 0 || start_pos < 0) return 0;
+  return qkv::prefill_geom(num_q, num_kv, n_tok, start_pos).total;
+}
+
+int qkv_prefill_attn_tq3(const uint16_t* q, const qkv_block_tq3* k_cache,
+                         const qkv_block_tq3* v_cache, const uint16_t* k_chunk,
+                         const uint16_t* v_chunk, uint16_t* out, int num_q, int num_kv,
+                         int head_dim, int start_pos, int n_tok, float scale, void* workspace,
+                         size_t workspace_bytes, hipStream_t stream) {
+  if (head_dim != 256) return QKV_ERR_UNSUPPORTED;
+  if (num_kv <= 0 || num_q <= 0 || num_q % num_kv != 0 || n_tok < 1 || start_pos < 0)
+    return QKV_ERR_INVALID;
+  const int gqa = num_q / num_kv;
+  if (gqa != 4 && gqa != 6) return QKV_ERR_UNSUPPORTED;
+  if (!q || !k_chunk || !v_chunk || !out) return QKV_ERR_NULL;
+  if (start_pos > 0 && (!k_cache || !v_cache)) return QKV_ERR_NULL;
+  if (!aligned(q, 16) || !aligned(k_chunk, 16) || !aligned(v_chunk, 16) || !aligned(out, 16) ||
+      !aligned(k_cache, 8) || !aligned(v_cache, 8))
+    return QKV_ERR_ALIGN;
+  const qkv::PrefillGeom g = qkv::prefill_geom(num_q, num_kv, n_tok, start_pos);
+  if (!workspace || workspace_bytes < g.total) return QKV_ERR_WORKSPACE;
+  if (!aligned(workspace, 256)) return QKV_ERR_ALIGN;
+  const uint64_t hist = (uint64_t)start_pos * num_kv * 104;
+  const uint64_t qbytes = (uint64_t)n_tok * num_q * 256 * 2;
+  if (hist > 0x7fffffffULL || qbytes > 0x7fffffffULL) return QKV_ERR_UNSUPPORTED;   // 32-bit offsets
+  char* ws = static_cast<char*>(workspace);
+  qkv::PrefillArgs a{};
+  a.k_cache = reinterpret_cast<const uint32_t*>(k_cache);
+  a.v_cache = reinterpret_cast<const uint32_t*>(v_cache);
+  a.kv_bytes = (uint32_t)hist;
+  a.qr = reinterpret_cast<uint16_t*>(ws + g.qr_off);
+  a.kr = reinterpret_cast<uint16_t*>(ws + g.kr_off);
+  a.vt = reinterpret_cast<uint16_t*>(ws + g.vt_off);
+  a.part_ml = reinterpret_cast<float*>(ws + g.ml_off);
+  a.part_o = reinterpret_cast<float*>(ws + g.o_off);
+  a.num_q = num_q;
+  a.num_kv = num_kv;
+  a.start_pos = start_pos;
+  a.n_tok = n_tok;
+  a.n_pad = g.n_pad;
+  a.n_split = g.n_split;
+  a.scale_log2 = scale * qkv::kLog2e;
+  return launch_status(qkv::launch_prefill_tq3(a, gqa, q, k_chunk, v_chunk, out, stream));
+}
+
 }  // extern "C"

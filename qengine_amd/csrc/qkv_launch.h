@@ -25,4 +25,30 @@ hipError_t launch_q8_append(const void* in0, void* out0, const void* in1, void* 
                             int n_blocks, int n_tensors, hipStream_t stream);
 hipError_t launch_q8_dequant(const void* in, void* out, int n_blocks, hipStream_t stream);
 
+// Chunked prefill over a TQ3 cache (prefill_tq3.hip).  Workspace pieces:
+// qr  rotated queries [n_tok][num_q][256] fp16
+// kr  rotated chunk keys [num_kv][n_pad][256] fp16
+// vt  rotated chunk values, 64-key tiles [num_kv][n_pad/64][256 dims][64] fp16
+// part_ml / part_o  key-split partials {m (log2 units), l} and rotated o
+//                   [n_split][n_tok][num_q] (x 256 for o)
+struct PrefillArgs {
+  const uint32_t* k_cache;   // slot-base TQ3 caches (history rows 0 .. start_pos-1)
+  const uint32_t* v_cache;
+  uint32_t kv_bytes;         // readable history bytes from the slot base
+  uint16_t* qr;
+  uint16_t* kr;
+  uint16_t* vt;
+  float* part_ml;
+  float* part_o;
+  int num_q, num_kv, start_pos, n_tok, n_pad, n_split;
+  float scale_log2;
+};
+struct PrefillGeom {
+  int n_pad, n_split;
+  size_t qr_off, kr_off, vt_off, ml_off, o_off, total;
+};
+PrefillGeom prefill_geom(int num_q, int num_kv, int n_tok, int start_pos);
+hipError_t launch_prefill_tq3(const PrefillArgs& a, int gqa, const uint16_t* q, const uint16_t* k,
+                              const uint16_t* v, uint16_t* out, hipStream_t stream);
+
 }  // namespace qkv

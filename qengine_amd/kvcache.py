@@ -190,3 +190,26 @@ def decode_attn_tq3_paged(q, k_pool, v_pool, out, workspace, block_tables, ctx_l
         _i32(ctx_lens, "ctx_lens"), max_ctx, float(scale), _dev_ptr(workspace, "workspace"),
         workspace.numel() * workspace.element_size(), _stream(stream)),
         "qkv_decode_attn_tq3_paged")
+
+
+# ---------------------------------------------------------------------------
+# chunked prefill over the TQ3 cache
+# ---------------------------------------------------------------------------
+
+def prefill_attn_tq3_workspace(num_q, num_kv, n_tok, start_pos, device) -> torch.Tensor:
+    n = int(lib().qkv_prefill_attn_tq3_workspace_bytes(num_q, num_kv, n_tok, start_pos))
+    return torch.empty(n, dtype=torch.uint8, device=device)
+
+
+def prefill_attn_tq3(q, k_cache, v_cache, k_chunk, v_chunk, out, workspace, *, num_q, num_kv,
+                     start_pos, scale, head_dim=256, stream=None) -> None:
+    """Causal attention of a chunk (q [n_tok][num_q][256]) over the cache
+    history rows 0..start_pos-1 (TQ3) and the chunk's own fp16 k/v."""
+    n_tok = q.shape[0]
+    kc = _dev_ptr(k_cache, "k_cache") if start_pos > 0 else 0
+    vc = _dev_ptr(v_cache, "v_cache") if start_pos > 0 else 0
+    check(lib().qkv_prefill_attn_tq3(
+        _dev_ptr(q, "q"), kc, vc, _dev_ptr(k_chunk, "k_chunk"), _dev_ptr(v_chunk, "v_chunk"),
+        _dev_ptr(out, "out"), num_q, num_kv, head_dim, start_pos, n_tok, float(scale),
+        _dev_ptr(workspace, "workspace"), workspace.numel() * workspace.element_size(),
+        _stream(stream)), "qkv_prefill_attn_tq3")
