@@ -45,6 +45,8 @@ def parse():
     ap.add_argument("--steps", type=int, default=100)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-secondary", action="store_true",
+                    help="skip the configs 2, 4 and 5 measurements")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a 256 MiB device copy (reference for HBM byte counters)")
     return ap.parse_args()
@@ -59,6 +61,164 @@ def outlier_kv(torch, gen, n_tok, dev):
         ch = torch.randperm(HD, generator=gen, device=dev)[:n_out]
         x[:, h, ch] *= 8.0
     return x.to(torch.float16)
+
+
+def _time(torch, stream, fn, reps):
+    """Mean ms of fn() over reps calls, events on the launch stream."""
+    fn()
+    torch.cuda.synchronize()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record(stream)
+    for i in range(reps):
+        fn(i)
+    b.record(stream)
+    torch.cuda.synchronize()
+    return a.elapsed_time(b) / reps
+
+
+def secondary(torch, kvcache, dev, stream):
+    """BASELINE configs 2, 4 and 5 on synthetic inputs of their stated shapes
+    (seeded N(0,1) fp16, encoded on the GPU).  Rates use algorithmic bytes
+    (packed cache read + q/o) or FLOPs as stated per entry."""
+    import numpy as np
+    out = {}
+    gen = torch.Generator(device=dev).manual_seed(7)
+    rnd = lambda *shape: torch.randn(*shape, generator=gen, device=dev).to(torch.float16)
+    scale = 1.0 / 16
+
+    # ---- config 2: Q8_0 cache of 4096 tokens, append 1 token, split decode +
+    # merge (reference K_SPLITS 8, sub_n_max 16); 8 layers x 4 sets rotated ----
+    ctx, layers, sets = 4096, 8, 4
+    blocks_tok = NUM_KV * HD // 32
+    caches = []
+    for _ in range(sets * layers):
+        kb = kvcache.q8_blocks((ctx + 1) * blocks_tok, dev)
+        vb = kvcache.q8_blocks((ctx + 1) * blocks_tok, dev)
+        kvcache.q8_append(rnd(ctx, NUM_KV, HD), kb[: ctx * blocks_tok])
+        kvcache.q8_append(rnd(ctx, NUM_KV, HD), vb[: ctx * blocks_tok])
+        caches.append((kb, vb))
+    knew, vnew, q = rnd(1, NUM_KV, HD), rnd(1, NUM_KV, HD), rnd(1, NUM_Q, HD)
+    pm = torch.empty(NUM_Q, 16, 8, device=dev)
+    pl = torch.empty(NUM_Q, 16, 8, device=dev)
+    po = torch.empty(NUM_Q, 16, 8, HD, device=dev)
+    o = torch.empty(1, NUM_Q, HD, dtype=torch.float16, device=dev)
+
+    def q8_layer(i=0):
+        kb, vb = caches[i % len(caches)]
+        kvcache.q8_append(knew, kb[ctx * blocks_tok:])
+        kvcache.q8_append(vnew, vb[ctx * blocks_tok:])
+        kvcache.attn_split_q8(q, kb, vb, pm, pl, po, num_q=NUM_Q, num_kv=NUM_KV, start_pos=ctx,
+                              sub_n=1, sub_n_max=16, active_end_max=ctx + 1, scale=scale,
+                              k_splits=8)
+        kvcache.attn_split_merge(pm, pl, po, o, num_q=NUM_Q, num_kv=NUM_KV, sub_n=1,
+                                 sub_n_max=16, k_splits=8)
+    ms = _time(torch, stream, q8_layer, 200)
+    q8_bytes = 2 * (ctx + 1) * blocks_tok * 36 + NUM_Q * HD * 2 * 2
+    out["config2_q8_decode"] = {
+        "us_per_layer": round(ms * 1e3, 3),
+        "bytes_per_layer": q8_bytes, "gbps": round(q8_bytes / (ms * 1e-3) / 1e9, 1),
+        "frac": round(q8_bytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+        "note": "per layer: Q8 append of the new token's K and V, split-K decode over 4097 "
+                "keys, merge (4 launches); 8 layers x 4 cache sets rotated"}
+    del caches
+
+    # ---- config 4: 8 slots, 24 q / 4 kv heads, 256-token blocks, ctx ~ U[1K, 64K],
+    # slots 0-3 share a 4096-token prefix; a step appends 1 token per slot
+    # (paged) and decodes all 8 slots; two pools rotated ----
+    rng = np.random.default_rng(4)
+    n_slots, nq4, bt_tok = 8, 24, 256
+    ctx_s = rng.integers(1024, 65537, size=n_slots)
+    ctx_s[:4] = np.maximum(ctx_s[:4], 4096 + 1)
+    new_s = ctx_s + 1
+    max_ctx = int(new_s.max())
+    max_blocks = (max_ctx + bt_tok - 1) // bt_tok
+    shared = 4096 // bt_tok
+    tables = np.zeros((n_slots, max_blocks), np.int32)
+    nxt = shared
+    for s_ in range(n_slots):
+        nb = (int(new_s[s_]) + bt_tok - 1) // bt_tok
+        for b in range(nb):
+            if s_ < 4 and b < shared:
+                tables[s_, b] = b
+            else:
+                tables[s_, b] = nxt
+                nxt += 1
+    pool_rows = nxt * bt_tok
+    pools = []
+    for _ in range(2):
+        kp = kvcache.tq3_blocks(pool_rows * 8, dev)
+        vp = kvcache.tq3_blocks(pool_rows * 8, dev)
+        for r0 in range(0, pool_rows, 65536):
+            n = min(65536, pool_rows - r0)
+            kvcache.tq3_append_kv(rnd(n, NUM_KV, HD), rnd(n, NUM_KV, HD),
+                                  kp[r0 * 8:(r0 + n) * 8], vp[r0 * 8:(r0 + n) * 8])
+        pools.append((kp, vp))
+    bt_d = torch.from_numpy(tables).to(dev)
+    pos_d = torch.from_numpy(ctx_s.astype(np.int32)).to(dev)
+    len_d = torch.from_numpy(new_s.astype(np.int32)).to(dev)
+    k4, v4, q4 = rnd(n_slots, 1, NUM_KV, HD), rnd(n_slots, 1, NUM_KV, HD), rnd(n_slots, nq4, HD)
+    o4 = torch.empty(n_slots, nq4, HD, dtype=torch.float16, device=dev)
+    ws4 = kvcache.decode_attn_tq3_paged_workspace(nq4, NUM_KV, n_slots, max_ctx, dev)
+
+    def step4(i=0):
+        kp, vp = pools[i % 2]
+        kvcache.tq3_append_kv_paged(k4, v4, kp, vp, bt_d, pos_d, block_tokens=bt_tok)
+        kvcache.decode_attn_tq3_paged(q4, kp, vp, o4, ws4, bt_d, len_d, num_q=nq4, num_kv=NUM_KV,
+                                      max_ctx=max_ctx, block_tokens=bt_tok, scale=scale)
+    ms = _time(torch, stream, step4, 100)
+    logical = int(new_s.sum()) * 2 * BLOCKS_PER_TOKEN * 52 + n_slots * nq4 * HD * 2 * 2
+    physical = logical - 3 * 4096 * 2 * BLOCKS_PER_TOKEN * 52
+    out["config4_paged_step"] = {
+        "us_per_step": round(ms * 1e3, 3), "ctx": [int(c) for c in new_s],
+        "bytes_logical": logical, "bytes_physical": physical,
+        "gbps_logical": round(logical / (ms * 1e-3) / 1e9, 1),
+        "frac_logical": round(logical / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+        "note": "one layer: paged append of 1 token per slot + paged decode of 8 slots "
+                "(2 launches); physical bytes count the shared prefix once"}
+    del pools
+
+    # ---- config 5: one slot, 16 q / 4 kv, 131072-token history ----
+    hist, chunk = 131072, 2048
+    kb = kvcache.tq3_blocks((hist + chunk) * 8, dev)
+    vb = kvcache.tq3_blocks((hist + chunk) * 8, dev)
+    for r0 in range(0, hist, 65536):
+        kvcache.tq3_append_kv(rnd(65536, NUM_KV, HD), rnd(65536, NUM_KV, HD),
+                              kb[r0 * 8:(r0 + 65536) * 8], vb[r0 * 8:(r0 + 65536) * 8])
+    qc, kc, vc = rnd(chunk, NUM_Q, HD), rnd(chunk, NUM_KV, HD), rnd(chunk, NUM_KV, HD)
+    oc = torch.empty(chunk, NUM_Q, HD, dtype=torch.float16, device=dev)
+    wsp = kvcache.prefill_attn_tq3_workspace(NUM_Q, NUM_KV, chunk, hist, dev)
+
+    def prefill(i=0):
+        kvcache.tq3_append_kv(kc, vc, kb[hist * 8:], vb[hist * 8:])
+        kvcache.prefill_attn_tq3(qc, kb, vb, kc, vc, oc, wsp, num_q=NUM_Q, num_kv=NUM_KV,
+                                 start_pos=hist, scale=scale)
+    ms = _time(torch, stream, prefill, 5)
+    flop = sum(4 * NUM_Q * HD * (hist + t + 1) for t in range(chunk))
+    out["config5_prefill_chunk"] = {
+        "ms_per_chunk": round(ms, 3), "tflops": round(flop / (ms * 1e-3) / 1e12, 1),
+        "frac_mfma_fp16": round(flop / (ms * 1e-3) / 1e12 / 2500.0, 4),
+        "note": "append of the 2048-token chunk + causal attention of the chunk over 131072 "
+                "history keys (TQ3) and its own 2048 fp16 keys; FLOPs 4*num_q*hd per "
+                "(query, visible key)"}
+
+    nv = 16
+    qv, kv_, vv = rnd(nv, NUM_Q, HD), rnd(nv, NUM_KV, HD), rnd(nv, NUM_KV, HD)
+    ov = torch.empty(nv, NUM_Q, HD, dtype=torch.float16, device=dev)
+    wsv = kvcache.prefill_attn_tq3_workspace(NUM_Q, NUM_KV, nv, hist, dev)
+
+    def verify(i=0):
+        kvcache.tq3_append_kv(kv_, vv, kb[hist * 8:(hist + nv) * 8], vb[hist * 8:(hist + nv) * 8])
+        kvcache.prefill_attn_tq3(qv, kb, vb, None, None, ov, wsv, num_q=NUM_Q, num_kv=NUM_KV,
+                                 start_pos=hist, scale=scale)
+    ms = _time(torch, stream, verify, 50)
+    vbytes = (hist + nv) * 2 * BLOCKS_PER_TOKEN * 52 + nv * NUM_Q * HD * 2 * 2
+    out["config5_verify16"] = {
+        "us": round(ms * 1e3, 3), "bytes": vbytes,
+        "gbps": round(vbytes / (ms * 1e-3) / 1e9, 1),
+        "frac": round(vbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+        "note": "append of the 16 verify tokens, then causal attention of the 16 queries over "
+                "the TQ3 cache (131088 keys, the block's own keys read back quantized)"}
+    return out
 
 
 def main():
@@ -194,6 +354,8 @@ def main():
                          "port of the reference split-K decode, OpenMP over (kv head, split)",
                "gbps": round(ATTN_BYTES * LAYERS / (cpu_us * 1e-6) / 1e9, 3)}
 
+    sec = None if args.no_secondary else secondary(torch, kvcache, dev, stream)
+
     line = {
         "metric": METRIC,
         "value": round(us_per_token, 3),
@@ -223,6 +385,7 @@ def main():
                    "frac": round(append_tok_layers * APPEND_BYTES_PER_TOKEN / append_s / 1e9
                                  / HBM_PEAK_GBS, 4)},
         "cpu_baseline": cpu,
+        "secondary": sec,
     }
     print(json.dumps(line))
     return 0

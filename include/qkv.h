@@ -214,7 +214,12 @@ int qkv_tq3_append_kv_paged(const uint16_t* k_f16, const uint16_t* v_f16, qkv_bl
  *    values, attended unquantized as in the reference;
  * out: [n_tok][num_q][256] fp16.  Query token t attends to keys
  * 0 .. start_pos + t.  The append of the chunk into the cache is a separate
- * qkv_tq3_append_kv call (model.cuh:5176-5190).  GQA 4 and 6.  workspace:
+ * qkv_tq3_append_kv call (model.cuh:5176-5190).
+ * Multi-token verify (model.cuh:4566-4571, 4663-4687: the verify block is
+ * quantized first and attended from the cache): pass k_chunk = v_chunk =
+ * NULL; every key, the block's own included, is then read from cache rows
+ * 0 .. start_pos + n_tok - 1 (causal within the block; no tree mask -- tree,
+ * sink and window rules stay with qkv_decode_attn_tq3).  GQA 4 and 6.  workspace:
  * caller-owned device memory of qkv_prefill_attn_tq3_workspace_bytes() bytes,
  * 256-byte aligned (no initialisation needed). */
 size_t qkv_prefill_attn_tq3_workspace_bytes(int num_q, int num_kv, int n_tok, int start_pos);

@@ -217,7 +217,7 @@ __global__ __launch_bounds__(256) void prefill_rotate_kernel(PrefillArgs p, cons
 // attention: grid (num_kv * gqa / WAVES, ceil(n_tok / 32), n_split); WAVES
 // query heads of one kv head per workgroup, one wave per head
 // ---------------------------------------------------------------------------
-template <int WAVES>
+template <int WAVES, bool FROM_CACHE>
 __global__ __launch_bounds__(64 * WAVES, 1) void prefill_attn_kernel(PrefillArgs p) {
   __shared__ __attribute__((aligned(16))) uint8_t lds[kLdsBytes];
   constexpr int NT = 64 * WAVES;
@@ -234,9 +234,11 @@ __global__ __launch_bounds__(64 * WAVES, 1) void prefill_attn_kernel(PrefillArgs
   const int n_q = min(kToks, p.n_tok - t0);
   const int qh = h * gqa + hg * WAVES + wave;
 
-  // tiles: history [0, start_pos) then chunk keys [0, t0 + n_q)
-  const int th = (p.start_pos + kKeys - 1) / kKeys;
-  const int tc = (t0 + n_q + kKeys - 1) / kKeys;
+  // tiles: cache rows [0, hist) then (unless every key comes from the cache)
+  // the chunk's own keys [0, t0 + n_q)
+  const int hist = FROM_CACHE ? p.start_pos + t0 + n_q : p.start_pos;
+  const int th = (hist + kKeys - 1) / kKeys;
+  const int tc = FROM_CACHE ? 0 : (t0 + n_q + kKeys - 1) / kKeys;
   const int total = th + tc;
   const int tps = (total + p.n_split - 1) / p.n_split;
   const int tlo = min(total, z * tps), thi = min(total, tlo + tps);
@@ -282,11 +284,11 @@ __global__ __launch_bounds__(64 * WAVES, 1) void prefill_attn_kernel(PrefillArgs
   if (tlo < min(thi, th)) load_raw(raw, rk, rv, tlo * kKeys, p.num_kv, h, tid);
 
   for (int ti = tlo; ti < thi; ti++) {
-    const bool hist = ti < th;
-    const int k0 = hist ? ti * kKeys : (ti - th) * kKeys;
-    const int nkeys = hist ? min(kKeys, p.start_pos - k0) : kKeys;
+    const bool cached = ti < th;
+    const int k0 = cached ? ti * kKeys : (ti - th) * kKeys;
+    const int nkeys = cached ? min(kKeys, hist - k0) : kKeys;
     __syncthreads();   // the previous tile's MFMAs are done with the tile buffers
-    if (hist) {
+    if (cached) {
       // raw rows of kv head h (104 B per key: 2 blocks of 52 B), loaded during
       // the previous tile; rows past start_pos read as zero (buffer range)
       store_raw(raw, lds, tid);
@@ -310,6 +312,7 @@ __global__ __launch_bounds__(64 * WAVES, 1) void prefill_attn_kernel(PrefillArgs
           *reinterpret_cast<uint4*>(dst + 16 * w) =
               make_uint4(pr[4 * w], pr[4 * w + 1], pr[4 * w + 2], pr[4 * w + 3]);
       }
+      __builtin_amdgcn_sched_barrier(0);   // keep the key and value decode apart (registers)
       // values: item (block, code group g, half kt, pair A, row group r): keys
       // kt*32 + 16A + 8(i>>2) + 4r + (i&3), i = 0..7, at value positions
       // kt*32 + 16A + 8r + i; dims b*128 + 8g .. +7
@@ -340,6 +343,7 @@ __global__ __launch_bounds__(64 * WAVES, 1) void prefill_attn_kernel(PrefillArgs
                            __builtin_amdgcn_perm(cp[7][m], cp[6][m], sel));
           }
       }
+      __builtin_amdgcn_sched_barrier(0);
       for (int it = tid; it < 4 * kKeys; it += NT) {
         const int key = it & 63, b = (it >> 6) & 1, tv = it >> 7;
         const float nrm = *reinterpret_cast<const float*>(lds + (tv ? kRawV : kRawK) + key * 104 + b * 52);
@@ -362,12 +366,15 @@ __global__ __launch_bounds__(64 * WAVES, 1) void prefill_attn_kernel(PrefillArgs
         *reinterpret_cast<float*>(lds + kNk + it * 4) = 1.0f;   // kNk and kNv are adjacent
     }
     __syncthreads();
+    __builtin_amdgcn_sched_barrier(0);
 
     // The two 32-key halves kt of the tile run one after the other: scores,
     // an online-softmax step, values.
-    const bool dense = hist && nkeys == kKeys;
+    // every key of the tile visible to every token of the workgroup
+    const bool dense = cached && nkeys == kKeys && (!FROM_CACHE || k0 + kKeys - 1 <= p.start_pos + t0);
 #pragma unroll
     for (int kt = 0; kt < 2; kt++) {
+      __builtin_amdgcn_sched_barrier(0);
       // ---- scores S^T = K~ Q~^T: D[b], row = key kt*32 + 8(v/4) + 4hh + v%4, col = token
       f16x_t sd[2];
 #pragma unroll
@@ -391,7 +398,9 @@ __global__ __launch_bounds__(64 * WAVES, 1) void prefill_attn_kernel(PrefillArgs
           float sv = (n0[c] * sd[0][4 * a + c] + n1[c] * sd[1][4 * a + c]) * p.scale_log2;
           if (!dense) {
             const int key = kb + c;
-            const bool vis = hist ? (key < nkeys) : (k0 + key <= t_abs);
+            // history keys (k0 + key < start_pos) are visible to every token
+            const bool vis = cached ? (key < nkeys) & (!FROM_CACHE || k0 + key <= p.start_pos + t_abs)
+                                    : (k0 + key <= t_abs);
             sv = vis ? sv : -INFINITY;
           }
           sc[4 * a + c] = sv;
@@ -548,12 +557,15 @@ hipError_t launch_prefill_tq3(const PrefillArgs& a, int gqa, const uint16_t* q, 
                        stream, a, q, k, v);
   }
   const int qtiles = (a.n_tok + kToks - 1) / kToks;
-  if (gqa == 4)
-    hipLaunchKernelGGL(prefill_attn_kernel<4>, dim3(a.num_kv, qtiles, a.n_split), dim3(256), 0,
-                       stream, a);
-  else if (gqa == 6)   // two workgroups of three heads per kv head
-    hipLaunchKernelGGL(prefill_attn_kernel<3>, dim3(a.num_kv * 2, qtiles, a.n_split), dim3(192),
-                       0, stream, a);
+  const dim3 g4(a.num_kv, qtiles, a.n_split), g6(a.num_kv * 2, qtiles, a.n_split);
+  if (gqa == 4 && !a.from_cache)
+    hipLaunchKernelGGL((prefill_attn_kernel<4, false>), g4, dim3(256), 0, stream, a);
+  else if (gqa == 4)
+    hipLaunchKernelGGL((prefill_attn_kernel<4, true>), g4, dim3(256), 0, stream, a);
+  else if (gqa == 6 && !a.from_cache)   // two workgroups of three heads per kv head
+    hipLaunchKernelGGL((prefill_attn_kernel<3, false>), g6, dim3(192), 0, stream, a);
+  else if (gqa == 6)
+    hipLaunchKernelGGL((prefill_attn_kernel<3, true>), g6, dim3(192), 0, stream, a);
   else
     return hipErrorInvalidValue;
   const long rows = (long)a.n_tok * a.num_q;

@@ -395,15 +395,17 @@ int qkv_prefill_attn_tq3(const uint16_t* q, const qkv_block_tq3* k_cache,
     return QKV_ERR_INVALID;
   const int gqa = num_q / num_kv;
   if (gqa != 4 && gqa != 6) return QKV_ERR_UNSUPPORTED;
-  if (!q || !k_chunk || !v_chunk || !out) return QKV_ERR_NULL;
-  if (start_pos > 0 && (!k_cache || !v_cache)) return QKV_ERR_NULL;
+  if (!q || !out) return QKV_ERR_NULL;
+  if ((k_chunk == nullptr) != (v_chunk == nullptr)) return QKV_ERR_NULL;
+  const bool from_cache = k_chunk == nullptr;   // verify: the chunk's rows are in the cache
+  if ((start_pos > 0 || from_cache) && (!k_cache || !v_cache)) return QKV_ERR_NULL;
   if (!aligned(q, 16) || !aligned(k_chunk, 16) || !aligned(v_chunk, 16) || !aligned(out, 16) ||
       !aligned(k_cache, 8) || !aligned(v_cache, 8))
     return QKV_ERR_ALIGN;
   const qkv::PrefillGeom g = qkv::prefill_geom(num_q, num_kv, n_tok, start_pos);
   if (!workspace || workspace_bytes < g.total) return QKV_ERR_WORKSPACE;
   if (!aligned(workspace, 256)) return QKV_ERR_ALIGN;
-  const uint64_t hist = (uint64_t)start_pos * num_kv * 104;
+  const uint64_t hist = (uint64_t)(start_pos + (from_cache ? n_tok : 0)) * num_kv * 104;
   const uint64_t qbytes = (uint64_t)n_tok * num_q * 256 * 2;
   if (hist > 0x7fffffffULL || qbytes > 0x7fffffffULL) return QKV_ERR_UNSUPPORTED;   // 32-bit offsets
   char* ws = static_cast<char*>(workspace);
@@ -420,8 +422,9 @@ int qkv_prefill_attn_tq3(const uint16_t* q, const qkv_block_tq3* k_cache,
   a.num_kv = num_kv;
   a.start_pos = start_pos;
   a.n_tok = n_tok;
-  a.n_pad = g.n_pad;
+  a.n_pad = from_cache ? 0 : g.n_pad;   // no chunk keys to rotate or tile
   a.n_split = g.n_split;
+  a.from_cache = from_cache ? 1 : 0;
   a.scale_log2 = scale * qkv::kLog2e;
   return launch_status(qkv::launch_prefill_tq3(a, gqa, q, k_chunk, v_chunk, out, stream));
 }

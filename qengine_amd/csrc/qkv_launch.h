@@ -32,7 +32,8 @@ hipError_t launch_q8_dequant(const void* in, void* out, int n_blocks, hipStream_
 // part_ml / part_o  key-split partials {m (log2 units), l} and rotated o
 //                   [n_split][n_tok][num_q] (x 256 for o)
 struct PrefillArgs {
-  const uint32_t* k_cache;   // slot-base TQ3 caches (history rows 0 .. start_pos-1)
+  const uint32_t* k_cache;   // slot-base TQ3 caches (rows 0 .. start_pos-1, or
+                             // 0 .. start_pos+n_tok-1 when from_cache)
   const uint32_t* v_cache;
   uint32_t kv_bytes;         // readable history bytes from the slot base
   uint16_t* qr;
@@ -41,6 +42,7 @@ struct PrefillArgs {
   float* part_ml;
   float* part_o;
   int num_q, num_kv, start_pos, n_tok, n_pad, n_split;
+  int from_cache;            // 1: the chunk's keys are cache rows too (verify)
   float scale_log2;
 };
 struct PrefillGeom {

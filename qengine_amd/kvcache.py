@@ -204,12 +204,15 @@ def prefill_attn_tq3_workspace(num_q, num_kv, n_tok, start_pos, device) -> torch
 def prefill_attn_tq3(q, k_cache, v_cache, k_chunk, v_chunk, out, workspace, *, num_q, num_kv,
                      start_pos, scale, head_dim=256, stream=None) -> None:
     """Causal attention of a chunk (q [n_tok][num_q][256]) over the cache
-    history rows 0..start_pos-1 (TQ3) and the chunk's own fp16 k/v."""
+    history rows 0..start_pos-1 (TQ3) and the chunk's own fp16 k/v; with
+    k_chunk = v_chunk = None (verify) every key comes from the cache rows
+    0..start_pos+n_tok-1."""
     n_tok = q.shape[0]
-    kc = _dev_ptr(k_cache, "k_cache") if start_pos > 0 else 0
-    vc = _dev_ptr(v_cache, "v_cache") if start_pos > 0 else 0
+    from_cache = k_chunk is None
+    kc = _dev_ptr(k_cache, "k_cache") if (start_pos > 0 or from_cache) else 0
+    vc = _dev_ptr(v_cache, "v_cache") if (start_pos > 0 or from_cache) else 0
     check(lib().qkv_prefill_attn_tq3(
-        _dev_ptr(q, "q"), kc, vc, _dev_ptr(k_chunk, "k_chunk"), _dev_ptr(v_chunk, "v_chunk"),
+        _dev_ptr(q, "q"), kc, vc, _opt_ptr(k_chunk), _opt_ptr(v_chunk),
         _dev_ptr(out, "out"), num_q, num_kv, head_dim, start_pos, n_tok, float(scale),
         _dev_ptr(workspace, "workspace"), workspace.numel() * workspace.element_size(),
         _stream(stream)), "qkv_prefill_attn_tq3")

@@ -184,3 +184,66 @@ def test_prefill_config5_sampled_rows(dev):
                       k_splits=32)[0]
         assert rel_err(got[t], exact[t]) < TOL, t
         assert rel_err(got[t], ref) < TOL + rel_err(ref, exact[t]), t
+
+
+# ---------------------------------------------------------------------------
+# Multi-token verify (model.cuh:4566-4571, 4663-4687): the verify block is
+# appended to the cache first and every key, its own included, is read from
+# the cache; causal within the block.  Oracle: the reference split decode over
+# the TQ3 cache with sub_n = n_tok.
+# ---------------------------------------------------------------------------
+def _verify_gpu(dev, q, kb, vb, *, num_q, num_kv, start_pos, scale):
+    from qengine_amd import kvcache
+    torch = _torch()
+    n_tok = q.shape[0]
+    out = torch.zeros((n_tok, num_q, 256), dtype=torch.float16, device=dev)
+    ws = kvcache.prefill_attn_tq3_workspace(num_q, num_kv, n_tok, start_pos, dev)
+    kvcache.prefill_attn_tq3(_t(q, dev), _t(kb.view(np.uint8), dev), _t(vb.view(np.uint8), dev),
+                             None, None, out, ws, num_q=num_q, num_kv=num_kv,
+                             start_pos=start_pos, scale=scale)
+    torch.cuda.synchronize()
+    return out.cpu().numpy()
+
+
+@pytest.mark.parametrize("start_pos,n_tok,num_q", [(1000, 16, 16), (5000, 7, 16), (0, 16, 16),
+                                                   (777, 16, 24), (63, 40, 16)])
+def test_verify_from_cache_vs_oracle(dev, start_pos, n_tok, num_q):
+    num_kv, scale = 4, 1 / 16
+    rng = np.random.default_rng(start_pos + 3 * n_tok)
+    n = start_pos + n_tok
+    kb = O.tq3_encode(kv_f16(rng, n, num_kv, 256))
+    vb = O.tq3_encode(kv_f16(rng, n, num_kv, 256))
+    q = q_f16(rng, n_tok, num_q, 256)
+    got = _verify_gpu(dev, q, kb, vb, num_q=num_q, num_kv=num_kv, start_pos=start_pos, scale=scale)
+    pm, pl, po = O.attn_split(O.KV_TQ3, q, kb, vb, num_q=num_q, num_kv=num_kv, hd=256,
+                              start_pos=start_pos, sub_n=n_tok, sub_n_max=n_tok,
+                              active_end_max=n, scale=scale, k_splits=8)
+    ref = O.attn_split_merge(pm, pl, po, num_q=num_q, num_kv=num_kv, hd=256, sub_n=n_tok,
+                             sub_n_max=n_tok, k_splits=8).view(np.float16)
+    assert np.all(np.isfinite(got))
+    assert rel_err(got, ref) < TOL
+
+
+def test_verify_matches_decode_path(dev):
+    """The MFMA verify and the split-K decode kernel (sub_n = 16) compute the
+    same rows over a 32768-token cache."""
+    from qengine_amd import kvcache
+    torch = _torch()
+    num_q, num_kv, start_pos, n_tok, scale = 16, 4, 32768, 16, 1 / 16
+    rng = np.random.default_rng(9)
+    n = start_pos + n_tok
+    kbt, vbt = kvcache.tq3_blocks(n * 8, dev), kvcache.tq3_blocks(n * 8, dev)
+    kvcache.tq3_append_kv(_t(kv_f16(rng, n, num_kv, 256), dev), _t(kv_f16(rng, n, num_kv, 256), dev),
+                          kbt, vbt)
+    q = q_f16(rng, n_tok, num_q, 256)
+    qt = _t(q, dev)
+    a = torch.zeros((n_tok, num_q, 256), dtype=torch.float16, device=dev)
+    ws = kvcache.prefill_attn_tq3_workspace(num_q, num_kv, n_tok, start_pos, dev)
+    kvcache.prefill_attn_tq3(qt, kbt, vbt, None, None, a, ws, num_q=num_q, num_kv=num_kv,
+                             start_pos=start_pos, scale=scale)
+    b = torch.zeros_like(a)
+    wsd = kvcache.decode_attn_tq3_workspace(num_q, num_kv, n_tok, n, dev)
+    kvcache.decode_attn_tq3(qt, kbt, vbt, b, wsd, num_q=num_q, num_kv=num_kv, start_pos=start_pos,
+                            sub_n=n_tok, scale=scale)
+    torch.cuda.synchronize()
+    assert rel_err(a.cpu().numpy(), b.cpu().numpy()) < TOL
