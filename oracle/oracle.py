@@ -64,7 +64,7 @@ def _declare(L):
     L.or_tq3_find_bin.restype = ctypes.c_uint8
     L.or_tq3_find_bin.argtypes = [_F]
     L.or_tq3_prescale_threshold_mismatches.restype = _I64
-    L.or_tq3_prescale_threshold_mismatches.argtypes = [_P, _I64, _I64, _I]
+    L.or_tq3_prescale_threshold_mismatches.argtypes = [_P, _I64, _I64, _I, _I]
     L.or_pack_3bit_8.argtypes = [_P, _P]
     L.or_unpack_3bit_8.argtypes = [_P, _P]
     L.or_tq3_encode.argtypes = [_P, _P, _I64, _I]
@@ -145,13 +145,15 @@ def find_bin(v: np.ndarray) -> np.ndarray:
 
 
 def prescale_threshold_mismatches(thr_bits, lo: int = 0, hi: int = 0xFFFFFFFF,
-                                  nthreads: int = 0) -> int:
+                                  negated: bool = False, nthreads: int = 0) -> int:
     """Number of fp32 bit patterns w in [lo, hi] (default: all 2^32) where
     binning fl(w * rs) per the reference differs from counting the thresholds
-    below w."""
+    below w; with `negated` the pattern holds -w and the bin is 7 minus the
+    count (NaN patterns skipped)."""
     t = np.ascontiguousarray(thr_bits, np.uint32)
     assert t.size == 7 and 0 <= lo <= hi <= 0xFFFFFFFF
-    return int(lib().or_tq3_prescale_threshold_mismatches(_ptr(t), lo, hi, nthreads))
+    return int(lib().or_tq3_prescale_threshold_mismatches(_ptr(t), lo, hi, int(negated),
+                                                          nthreads))
 
 
 def pack_3bit_8(idx8: np.ndarray) -> np.ndarray:

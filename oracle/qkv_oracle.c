@@ -169,11 +169,13 @@ uint8_t or_tq3_find_bin(float v) {
 
 /* Check of a table of bin thresholds on the WHT output before the x rs
  * scaling (the form the GPU encoder uses): for every fp32 bit pattern w in
- * [lo, hi], or_tq3_find_bin(fl(w * rs)) must equal #{k : w > thr[k]}.  Returns
- * the number of bit patterns where the two differ; over [0, 2^32 - 1] a zero
- * proves the folding exact. */
+ * [lo, hi], or_tq3_find_bin(fl(w * rs)) must equal #{k : w > thr[k]}.  With
+ * `negated`, the pattern holds v = -w (a lane that carries its butterfly
+ * output negated) and the bin of w must equal 7 - #{k : v > thr[k]} (NaN
+ * patterns skipped).  Returns the number of bit patterns where the two
+ * differ; over [0, 2^32 - 1] a zero proves the folding exact. */
 int64_t or_tq3_prescale_threshold_mismatches(const uint32_t* thr, int64_t lo, int64_t hi,
-                                             int nthreads) {
+                                             int negated, int nthreads) {
     const float rs = or_tq3_wht_scale();
     float t[7];
     for (int k = 0; k < 7; k++) t[k] = bits_f32(thr[k]);
@@ -183,11 +185,18 @@ int64_t or_tq3_prescale_threshold_mismatches(const uint32_t* thr, int64_t lo, in
 #pragma omp parallel for schedule(static) num_threads(nthreads) reduction(+ : bad)
 #endif
     for (int64_t u = lo; u <= hi; u++) {
-        const float w = bits_f32((uint32_t)u);
-        const float y = w * rs;
+        const float v = bits_f32((uint32_t)u);
         uint8_t c = 0;
-        for (int k = 0; k < 7; k++) c = (uint8_t)(c + (w > t[k]));
-        bad += (c != or_tq3_find_bin(y));
+        for (int k = 0; k < 7; k++) c = (uint8_t)(c + (v > t[k]));
+        if (!negated) {
+            bad += (c != or_tq3_find_bin(v * rs));
+        } else if (v == v) {
+            /* v holds -w: the bin of w is 7 minus the count (NaN is excluded:
+             * a NaN element only occurs in a block with a non-finite norm,
+             * whose codes are zero by rule) */
+            const float w = -v;
+            bad += ((uint8_t)(7 - c) != or_tq3_find_bin(w * rs));
+        }
     }
     return bad;
 }

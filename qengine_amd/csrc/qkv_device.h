@@ -105,6 +105,24 @@ constexpr uint32_t kBinThrBits[7] = {bin_threshold_bits(0), bin_threshold_bits(1
                                      bin_threshold_bits(2), bin_threshold_bits(3),
                                      bin_threshold_bits(4), bin_threshold_bits(5),
                                      bin_threshold_bits(6)};
+// A lane holding its butterfly output negated (v = -w) bins w as
+// 7 - #{m : v > T_m} with T_m = prev(-R_{6-m}) (the next float towards -inf):
+// v > prev(-R) <=> v >= -R <=> w <= R <=> NOT fl(w*rs) > B.
+constexpr uint32_t prev_float_bits(uint32_t b) {   // next float towards -inf (b finite, != +-0 handled)
+  return (b & 0x80000000u) ? b + 1u : (b == 0u ? 0x80000001u : b - 1u);
+}
+constexpr uint32_t bin_threshold_neg_bits(int m) {
+  return prev_float_bits(bin_threshold_bits(6 - m) ^ 0x80000000u);
+}
+constexpr uint32_t kBinThrNegBits[7] = {bin_threshold_neg_bits(0), bin_threshold_neg_bits(1),
+                                        bin_threshold_neg_bits(2), bin_threshold_neg_bits(3),
+                                        bin_threshold_neg_bits(4), bin_threshold_neg_bits(5),
+                                        bin_threshold_neg_bits(6)};
+static_assert(kBinThrNegBits[0] == 0xbfdfd5e4u && kBinThrNegBits[1] == 0xbf86719du &&
+                  kBinThrNegBits[2] == 0xbf002dd9u && kBinThrNegBits[3] == 0x80000006u &&
+                  kBinThrNegBits[4] == 0x3f002dd7u && kBinThrNegBits[5] == 0x3f86719bu &&
+                  kBinThrNegBits[6] == 0x3fdfd5e1u,
+              "negated-lane bin thresholds (checked exhaustively on the host)");
 static_assert(kBinThrBits[0] == 0xbfdfd5e2u && kBinThrBits[1] == 0xbf86719cu &&
                   kBinThrBits[2] == 0xbf002dd8u && kBinThrBits[3] == 0x00000005u &&
                   kBinThrBits[4] == 0x3f002dd8u && kBinThrBits[5] == 0x3f86719cu &&

@@ -270,6 +270,10 @@ def test_q8_decode_vs_numpy():
 # ---------------------------------------------------------------------------
 PRESCALE_THR = [0xbfdfd5e2, 0xbf86719c, 0xbf002dd8, 0x00000005,
                 0x3f002dd8, 0x3f86719c, 0x3fdfd5e3]
+# for a lane that carries its butterfly output negated (v = -w):
+# bin(w) = 7 - #{m : v > T_m},  T_m = prev(-R_{6-m})
+PRESCALE_THR_NEG = [0xbfdfd5e4, 0xbf86719d, 0xbf002dd9, 0x80000006,
+                    0x3f002dd7, 0x3f86719b, 0x3fdfd5e1]
 
 
 def test_prescale_thresholds_match_device_header():
@@ -277,10 +281,25 @@ def test_prescale_thresholds_match_device_header():
     hdr = open(os.path.join(ROOT, "qengine_amd", "csrc", "qkv_device.h")).read()
     pinned = {int(k): int(v, 16) for k, v in re.findall(r"kBinThrBits\[(\d)\] == (0x[0-9a-f]+)u", hdr)}
     assert pinned == dict(enumerate(PRESCALE_THR))
+    neg = {int(k): int(v, 16) for k, v in re.findall(r"kBinThrNegBits\[(\d)\] == (0x[0-9a-f]+)u", hdr)}
+    assert neg == dict(enumerate(PRESCALE_THR_NEG))
 
 
 def test_prescale_thresholds_exhaustive():
     assert O.prescale_threshold_mismatches(PRESCALE_THR) == 0
+
+
+def test_prescale_thresholds_negated_exhaustive():
+    assert O.prescale_threshold_mismatches(PRESCALE_THR_NEG, negated=True) == 0
+
+
+@pytest.mark.parametrize("k,delta", [(0, -1), (3, 1), (4, 1), (6, 1)])
+def test_prescale_thresholds_negated_one_ulp_off_fails(k, delta):
+    thr = list(PRESCALE_THR_NEG)
+    thr[k] = (thr[k] + delta) & 0xffffffff
+    lo, hi = max(0, thr[k] - (1 << 15)), min(0xFFFFFFFF, thr[k] + (1 << 15))
+    assert O.prescale_threshold_mismatches(PRESCALE_THR_NEG, lo, hi, negated=True) == 0
+    assert O.prescale_threshold_mismatches(thr, lo, hi, negated=True) > 0
 
 
 @pytest.mark.parametrize("k,delta", [(0, 1), (1, -1), (2, -1), (3, -5), (4, 1), (5, 1), (6, -1)])
