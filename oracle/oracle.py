@@ -65,6 +65,8 @@ def _declare(L):
     L.or_tq3_find_bin.argtypes = [_F]
     L.or_tq3_prescale_threshold_mismatches.restype = _I64
     L.or_tq3_prescale_threshold_mismatches.argtypes = [_P, _I64, _I64, _I, _I]
+    L.or_tq3_fold_mismatches.restype = _I64
+    L.or_tq3_fold_mismatches.argtypes = [ctypes.c_uint32, _P, _I64, _I64, _I, _I]
     L.or_pack_3bit_8.argtypes = [_P, _P]
     L.or_unpack_3bit_8.argtypes = [_P, _P]
     L.or_tq3_encode.argtypes = [_P, _P, _I64, _I]
@@ -142,6 +144,17 @@ def wht128(x: np.ndarray) -> np.ndarray:
 def find_bin(v: np.ndarray) -> np.ndarray:
     v = np.asarray(v, np.float32).ravel()
     return np.array([lib().or_tq3_find_bin(float(x)) for x in v], np.uint8)
+
+
+def fold_mismatches(a_bits: int, q_bits, lo: int = 0, hi: int = 0xFFFFFFFF,
+                    negated: bool = False, nthreads: int = 0) -> int:
+    """Number of reachable fp32 patterns w in [lo, hi] (w = +-0 or
+    2^-67 <= |w| < 2^100) where the sign-folded binning (y = fl(-A w + |w|),
+    bin = 4 + m or 3 - m by the sign of y, m = #{j: |y| > q_j}) differs from
+    binning fl(w * rs); `negated` checks a lane holding -w."""
+    q = np.ascontiguousarray(q_bits, np.uint32)
+    assert q.size == 3 and 0 <= lo <= hi <= 0xFFFFFFFF
+    return int(lib().or_tq3_fold_mismatches(a_bits, _ptr(q), lo, hi, int(negated), nthreads))
 
 
 def prescale_threshold_mismatches(thr_bits, lo: int = 0, hi: int = 0xFFFFFFFF,

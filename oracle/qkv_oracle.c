@@ -21,6 +21,10 @@
  *   or_tq3_prescale_threshold_mismatches
  *                                   exhaustive over all 2^32 fp32 patterns; a
  *                                   threshold moved by one ulp must fail
+ *   or_tq3_fold_mismatches          exhaustive over the reachable fp32
+ *                                   patterns (both signs of the lane); a
+ *                                   threshold moved by one ulp, or A = 2^24,
+ *                                   must fail
  *   or_pack/unpack_3bit_8           numpy bit-level packing (LE 3-bit stream)
  *   or_tq3_encode                   fp64 rotation y = H*D*x/|x|/sqrt(128):
  *                                   codes equal searchsorted(bounds, y) except
@@ -197,6 +201,41 @@ int64_t or_tq3_prescale_threshold_mismatches(const uint32_t* thr, int64_t lo, in
             const float w = -v;
             bad += ((uint8_t)(7 - c) != or_tq3_find_bin(w * rs));
         }
+    }
+    return bad;
+}
+
+/* Check of the sign-folded binning (the GPU encoder's form): with
+ * y = fl(-A w + |w|) (one rounding; exact in double before the float cast),
+ * bin(w) must equal 4 + m for signbit(y) = 1 and 3 - m otherwise, with
+ * m = #{j : |y| > q[j]}.  With `negated` the pattern holds v = -w and
+ * y = fl(A v + |v|).  Checked patterns: w = +-0 and 2^-67 <= |w| < 2^100 (the
+ * reachable WHT outputs: every nonzero one is a multiple of 2^-67).  Returns
+ * the number of mismatching bit patterns in [lo, hi]. */
+int64_t or_tq3_fold_mismatches(uint32_t a_bits, const uint32_t* q, int64_t lo, int64_t hi,
+                               int negated, int nthreads) {
+    const float rs = or_tq3_wht_scale();
+    const double A = (double)bits_f32(a_bits);
+    float t[3];
+    for (int k = 0; k < 3; k++) t[k] = bits_f32(q[k]);
+    int64_t bad = 0;
+#ifdef _OPENMP
+    if (nthreads <= 0) nthreads = omp_get_max_threads();
+#pragma omp parallel for schedule(static) num_threads(nthreads) reduction(+ : bad)
+#endif
+    for (int64_t u = lo; u <= hi; u++) {
+        const uint32_t e = ((uint32_t)u >> 23) & 0xffu;
+        if ((((uint32_t)u & 0x7fffffffu) != 0u) && (e < 127u - 67u || e >= 127u + 100u)) continue;
+        const float v = bits_f32((uint32_t)u);
+        const double dv = (double)v;
+        const float y = (float)((negated ? A : -A) * dv + fabs(dv));
+        uint32_t ybits;
+        memcpy(&ybits, &y, 4);
+        const float ay = fabsf(y);
+        const int m = (ay > t[0]) + (ay > t[1]) + (ay > t[2]);
+        const int idx = (ybits >> 31) ? 4 + m : 3 - m;
+        const float w = negated ? -v : v;
+        bad += ((uint8_t)idx != or_tq3_find_bin(w * rs));
     }
     return bad;
 }

@@ -54,6 +54,8 @@ void or_wht128(float* x);                                 /* turboquant.cuh:48-6
 uint8_t or_tq3_find_bin(float v);                         /* turboquant.cuh:79-87   */
 int64_t or_tq3_prescale_threshold_mismatches(const uint32_t* thr, int64_t lo, int64_t hi,
                                              int negated, int nthreads);
+int64_t or_tq3_fold_mismatches(uint32_t a_bits, const uint32_t* q, int64_t lo, int64_t hi,
+                               int negated, int nthreads);
 void or_pack_3bit_8(uint8_t* dst, const uint8_t* idx8);   /* turboquant.cuh:90-100  */
 void or_unpack_3bit_8(const uint8_t* src, uint8_t* idx8); /* turboquant.cuh:103-108 */
 

@@ -129,6 +129,44 @@ static_assert(kBinThrBits[0] == 0xbfdfd5e2u && kBinThrBits[1] == 0xbf86719cu &&
                   kBinThrBits[6] == 0x3fdfd5e3u,
               "pre-scale bin thresholds (checked exhaustively against fl(w*rs) on the host)");
 
+// ---- sign-folded binning: one FMA and three compares per element ----------
+// y = fma(w, -A, |w|) = -w (A - 1) for w > 0 and |w| (A + 1) for w < 0 (one
+// rounding; +0 for w = +-0).  Its sign bit is [w > 0], which is bit 2 of the
+// bin (bins 4..7 are w > R_3 = 5 denormal ulps, and no reachable nonzero w is
+// that small).  |y| carries |w| scaled by A - 1 on the positive side and by
+// A + 1 on the negative side, and that difference absorbs the asymmetry of the
+// thresholds (the negative bounds are met with >=, the positive with >), so
+// three thresholds Q_j on |y| serve both sides:
+//   w > 0:  bin = 4 + m,  w <= 0:  bin = 3 - m,   m = #{j : |y| > Q_j}.
+// Q_j lies in [fl(P_j (A-1)), fl(next(P_j)(A-1))) (positive side, P_j = R_{4+j})
+// and in [fl(prev(N_j)(A+1)), fl(N_j (A+1))) (negative side, N_j = -R_{2-j});
+// A = 2^24 + 2 makes the two intervals overlap for j = 0, 1, 2.  The
+// products are exact in double, so the double -> float conversion is the one
+// rounding.  Reachable inputs: nonzero WHT outputs of a block with a finite
+// norm >= 1e-10 are multiples of 2^-67 (every scaled element is an fp16 value
+// over a norm below 2^20), so |w| >= 2^-67; the table is checked exhaustively
+// on that domain on the host.
+constexpr float kFoldA = 16777218.0f;
+constexpr uint32_t fold_product_bits(uint32_t wbits, double c) {
+  return float_to_bits((float)((double)bits_to_float(wbits) * c));
+}
+constexpr uint32_t fold_lo(int j) {
+  const uint32_t p = fold_product_bits(kBinThrBits[4 + j], (double)kFoldA - 1.0);
+  const uint32_t n = fold_product_bits((kBinThrBits[2 - j] & 0x7fffffffu) - 1u, (double)kFoldA + 1.0);
+  return p > n ? p : n;
+}
+constexpr uint32_t fold_hi(int j) {
+  const uint32_t p = fold_product_bits(kBinThrBits[4 + j] + 1u, (double)kFoldA - 1.0);
+  const uint32_t n = fold_product_bits(kBinThrBits[2 - j] & 0x7fffffffu, (double)kFoldA + 1.0);
+  return p < n ? p : n;
+}
+static_assert(fold_lo(0) < fold_hi(0) && fold_lo(1) < fold_hi(1) && fold_lo(2) < fold_hi(2),
+              "fold constant A separates both sides of every threshold");
+constexpr uint32_t kFoldQBits[3] = {fold_lo(0), fold_lo(1), fold_lo(2)};
+static_assert(kFoldQBits[0] == 0x4b002dd9u && kFoldQBits[1] == 0x4b86719du &&
+                  kFoldQBits[2] == 0x4bdfd5e4u,
+              "sign-folded thresholds (checked exhaustively on the host)");
+
 // ---- vector types and raw buffer resources --------------------------------
 typedef _Float16 h8_t __attribute__((ext_vector_type(8)));
 typedef float f4_t __attribute__((ext_vector_type(4)));

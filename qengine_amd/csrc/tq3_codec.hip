@@ -49,50 +49,57 @@ __device__ __forceinline__ void wht128_butterflies(float (&x)[128]) {
   }
 }
 
-// Bin two elements xa, xb against the seven pre-scale thresholds r[] into
-// scalar lane-mask bit planes: bit b of element a's bin index is lane bit of
-// pa[b] (likewise pb for xb).
-//   t_k = [x > r_k] (ordered compare into a lane mask) is a thermometer code,
-//   so  b2 = t3,  b1 = t1 ^ t3 ^ t5,  b0 = b1 ^ t0 ^ t2 ^ t4 ^ t6.
-// The XORs run on the scalar unit, in place: b1 ends in t1, b0 in t0 and b2
-// is t3 itself.  Each scalar instruction reads masks written by compares at
-// least seven instructions earlier, and every plane is read by a vector
-// instruction only after the ten-plus instructions that end this block.
-__device__ __forceinline__ void bin_planes2(float xa, float xb, const uint32_t (&r)[7],
-                                            uint64_t (&pa)[3], uint64_t (&pb)[3]) {
-  uint64_t a2, a4, a5, a6, b2, b4, b5, b6;
-  asm("v_cmp_gt_f32_e64 %[a3], %[xa], %[r3]\n\t"
-      "v_cmp_gt_f32_e64 %[b3], %[xb], %[r3]\n\t"
-      "v_cmp_gt_f32_e64 %[a1], %[xa], %[r1]\n\t"
-      "v_cmp_gt_f32_e64 %[a5], %[xa], %[r5]\n\t"
-      "v_cmp_gt_f32_e64 %[a0], %[xa], %[r0]\n\t"
-      "v_cmp_gt_f32_e64 %[a2], %[xa], %[r2]\n\t"
-      "v_cmp_gt_f32_e64 %[a4], %[xa], %[r4]\n\t"
-      "v_cmp_gt_f32_e64 %[a6], %[xa], %[r6]\n\t"
-      "v_cmp_gt_f32_e64 %[b1], %[xb], %[r1]\n\t"
-      "v_cmp_gt_f32_e64 %[b5], %[xb], %[r5]\n\t"
-      "v_cmp_gt_f32_e64 %[b0], %[xb], %[r0]\n\t"
-      "v_cmp_gt_f32_e64 %[b2], %[xb], %[r2]\n\t"
-      "v_cmp_gt_f32_e64 %[b4], %[xb], %[r4]\n\t"
-      "v_cmp_gt_f32_e64 %[b6], %[xb], %[r6]\n\t"
-      "s_xor_b64 %[a1], %[a1], %[a5]\n\t"
-      "s_xor_b64 %[a1], %[a1], %[a3]\n\t"
+// Bit planes of two elements from their sign-folded values ya, yb (see
+// kFoldQBits): c_j = [|y| > Q_j] is a thermometer code of m, so bit 1 of m is
+// c_1 and bit 0 is c_0 ^ c_1 ^ c_2.  pa[0] = bit 1, pa[1] = bit 0 of element
+// a's m (likewise pb); the XORs run on the scalar unit.  The sign fix (bits
+// 0 and 1 of the bin are those of m, or inverted for w <= 0) is applied to
+// the packed words afterwards.
+__device__ __forceinline__ void fold_planes2(float ya, float yb, const uint32_t (&q)[3],
+                                             uint64_t (&pa)[2], uint64_t (&pb)[2]) {
+  uint64_t a2, b2;
+  asm("v_cmp_gt_f32_e64 %[a1], |%[ya]|, %[q1]\n\t"
+      "v_cmp_gt_f32_e64 %[b1], |%[yb]|, %[q1]\n\t"
+      "v_cmp_gt_f32_e64 %[a0], |%[ya]|, %[q0]\n\t"
+      "v_cmp_gt_f32_e64 %[a2], |%[ya]|, %[q2]\n\t"
+      "v_cmp_gt_f32_e64 %[b0], |%[yb]|, %[q0]\n\t"
+      "v_cmp_gt_f32_e64 %[b2], |%[yb]|, %[q2]\n\t"
       "s_xor_b64 %[a0], %[a0], %[a2]\n\t"
-      "s_xor_b64 %[a4], %[a4], %[a6]\n\t"
-      "s_xor_b64 %[a0], %[a0], %[a4]\n\t"
-      "s_xor_b64 %[a0], %[a0], %[a1]\n\t"
-      "s_xor_b64 %[b1], %[b1], %[b5]\n\t"
-      "s_xor_b64 %[b1], %[b1], %[b3]\n\t"
       "s_xor_b64 %[b0], %[b0], %[b2]\n\t"
-      "s_xor_b64 %[b4], %[b4], %[b6]\n\t"
-      "s_xor_b64 %[b0], %[b0], %[b4]\n\t"
+      "s_xor_b64 %[a0], %[a0], %[a1]\n\t"
       "s_xor_b64 %[b0], %[b0], %[b1]"
-      : [a0] "=&s"(pa[0]), [a1] "=&s"(pa[1]), [a3] "=&s"(pa[2]), [a2] "=&s"(a2),
-        [a4] "=&s"(a4), [a5] "=&s"(a5), [a6] "=&s"(a6), [b0] "=&s"(pb[0]),
-        [b1] "=&s"(pb[1]), [b3] "=&s"(pb[2]), [b2] "=&s"(b2), [b4] "=&s"(b4),
-        [b5] "=&s"(b5), [b6] "=&s"(b6)
-      : [xa] "v"(xa), [xb] "v"(xb), [r0] "s"(r[0]), [r1] "s"(r[1]), [r2] "s"(r[2]),
-        [r3] "s"(r[3]), [r4] "s"(r[4]), [r5] "s"(r[5]), [r6] "s"(r[6]));
+      : [a1] "=&s"(pa[0]), [a0] "=&s"(pa[1]), [a2] "=&s"(a2), [b1] "=&s"(pb[0]),
+        [b0] "=&s"(pb[1]), [b2] "=&s"(b2)
+      : [ya] "v"(ya), [yb] "v"(yb), [q0] "s"(q[0]), [q1] "s"(q[1]), [q2] "s"(q[2]));
+}
+
+// acc = 2 * acc + (sign bit of y): shifts bit 2 of a bin in.
+__device__ __forceinline__ void shift_in_sign(uint32_t& acc, float y) {
+  acc = __builtin_amdgcn_alignbit(acc, __float_as_uint(y), 31);
+}
+
+// Mask of the bit-2 positions (bit 3e+2 of the code stream) in word w.
+constexpr uint32_t bit2_mask(int w) {
+  uint32_t m = 0u;
+  for (int p = 0; p < 32; p++)
+    if ((32 * w + p) % 3 == 2) m |= 1u << p;
+  return m;
+}
+
+// Sign fix of packed words (w0 .. w0+n-1 of the stream, whose last element
+// ends inside them): for every element with bit 2 clear (w <= 0), invert bits
+// 1 and 0.  nb = the bit-2 positions that are clear, moved down by one and by
+// two bits (across word boundaries with a funnel shift).
+template <int W0, int N>
+__device__ __forceinline__ void sign_fix(uint32_t* acc) {
+  uint32_t nb[N + 1];
+#pragma unroll
+  for (int i = 0; i < N; i++) nb[i] = ~acc[i] & bit2_mask(W0 + i);
+  nb[N] = 0u;
+#pragma unroll
+  for (int i = 0; i < N; i++)
+    acc[i] ^= __builtin_amdgcn_alignbit(nb[i + 1], nb[i], 1) ^
+              __builtin_amdgcn_alignbit(nb[i + 1], nb[i], 2);
 }
 
 // acc = 2 * acc + (this lane's bit of the mask): shifts one plane bit in.
@@ -107,9 +114,11 @@ __device__ __forceinline__ void shift_in(uint32_t& acc, uint64_t plane) {
 //
 // Instruction budget per element: one v_fma_mix for the norm, one for the
 // scaling (fp16 operand converted inside the instruction), seven butterfly
-// add/subs, seven compares into scalar lane masks and three shifts of a mask
-// bit into the packed words.  The bit planes of the 3-bit code are formed from
-// the compare masks on the scalar unit, which runs beside the vector ALU.
+// add/subs, one FMA that folds the sign, three compares into scalar lane
+// masks and three shifts into the packed words (the sign bit directly, two
+// mask bits), plus about 0.4 for the sign fix of the packed words.  Bit 0 of
+// the code is formed from the compare masks on the scalar unit, which runs
+// beside the vector ALU.
 __device__ __forceinline__ void tq3_encode_block(const uint32_t (&hw)[64], uint32_t (&o)[13]) {
   // Sequential sum of squares in reference order (x^2 of an fp16 value is
   // exact in fp32, so an FMA gives the same result as mul+add).
@@ -133,31 +142,43 @@ __device__ __forceinline__ void tq3_encode_block(const uint32_t (&hw)[64], uint3
   }
   wht128_butterflies(x);
 
-  // Bins against the pre-scale thresholds (same result as binning x * rs).
-  // t_k = [x > R_k] is a thermometer code, so the bin index bits are
-  //   b2 = t3,  b1 = t1 ^ t3 ^ t5,  b0 = t0 ^ t1 ^ ... ^ t6.
-  // Bit 3e+b of the 384-bit code stream is bit b of element e; the words are
-  // filled by shifting bits in from the top, highest element first.
+  // Bins (sign-folded form, kFoldQBits): y = fma(w, -A, |w|), bit 2 = sign
+  // bit of y, bits 1..0 from three compares of |y|.  Bit 3e+b of the 384-bit
+  // code stream is bit b of element e; the words are filled by shifting bits
+  // in from the top, highest element first, in two independent chains
+  // (elements 127..64 fill words 11..6, elements 63..0 words 5..0) so that no
+  // shift waits on the one before it.
   uint32_t acc[12];
 #pragma unroll
   for (int w = 0; w < 12; w++) acc[w] = 0u;
-  uint32_t r[7];
+  uint32_t q[3];
 #pragma unroll
-  for (int k = 0; k < 7; k++) r[k] = __builtin_amdgcn_readfirstlane(kBinThrBits[k]);
+  for (int k = 0; k < 3; k++) q[k] = __builtin_amdgcn_readfirstlane(kFoldQBits[k]);
+  const float neg_a = __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(
+                                                    __builtin_bit_cast(uint32_t, -kFoldA)));
 #pragma unroll
-  for (int e = 127; e >= 1; e -= 2) {
-    uint64_t pa[3], pb[3];
-    bin_planes2(x[e], x[e - 1], r, pa, pb);
-#pragma unroll
-    for (int b = 2; b >= 0; b--) shift_in(acc[(3 * e + b) >> 5], pa[b]);
-#pragma unroll
-    for (int b = 2; b >= 0; b--) shift_in(acc[(3 * (e - 1) + b) >> 5], pb[b]);
+  for (int i = 0; i < 64; i++) {
+    const int ea = 127 - i, eb = 63 - i;
+    const float ya = __builtin_fmaf(x[ea], neg_a, __builtin_fabsf(x[ea]));
+    const float yb = __builtin_fmaf(x[eb], neg_a, __builtin_fabsf(x[eb]));
+    uint64_t pa[2], pb[2];
+    fold_planes2(ya, yb, q, pa, pb);
+    shift_in_sign(acc[(3 * ea + 2) >> 5], ya);
+    shift_in_sign(acc[(3 * eb + 2) >> 5], yb);
+    shift_in(acc[(3 * ea + 1) >> 5], pa[0]);
+    shift_in(acc[(3 * eb + 1) >> 5], pb[0]);
+    shift_in(acc[(3 * ea) >> 5], pa[1]);
+    shift_in(acc[(3 * eb) >> 5], pb[1]);
   }
-  // zero block (turboquant.cuh:133-140): norm stored, codes zero
-  const bool zero = norm < 1e-10f;
+  sign_fix<0, 6>(acc);
+  sign_fix<6, 6>(acc + 6);
+  // zero block (turboquant.cuh:133-140): norm stored, codes zero.  A block
+  // with a non-finite norm (an inf or NaN element) has NaN WHT outputs, which
+  // the reference bins to 0: its codes are zero as well.
+  const bool keep = norm >= 1e-10f && norm < __builtin_inff();
   o[0] = __float_as_uint(norm);
 #pragma unroll
-  for (int w = 0; w < 12; w++) o[1 + w] = zero ? 0u : acc[w];
+  for (int w = 0; w < 12; w++) o[1 + w] = keep ? acc[w] : 0u;
 }
 
 // Output block of input block i for a paged append (PagedRows), or -1 when

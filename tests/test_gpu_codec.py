@@ -70,6 +70,36 @@ def test_tq3_append_config1_and_specials(dev):
     assert bad.size == 0, f"{bad.size} of {len(exp)} blocks differ, first {bad[:5]}"
 
 
+def test_tq3_append_nonfinite_and_extreme_blocks(dev):
+    """Blocks with inf / NaN elements: the reference bins the NaN WHT outputs
+    to 0, so the codes are zero and the norm is inf or NaN.  Blocks mixing
+    the largest and the smallest fp16 magnitudes reach the smallest nonzero
+    WHT outputs."""
+    rng = np.random.default_rng(5)
+    x = kv_f16(rng, 16, 1, 128).reshape(16, 128)
+    x[0, 3] = np.inf
+    x[1, 100] = -np.inf
+    x[2, 0] = np.nan
+    x[3, :] = np.nan
+    x[4, 5] = np.inf
+    x[4, 6] = -np.inf
+    x[8, :] = np.float16(6e-8)
+    x[8, 17] = np.float16(65504.0)
+    x[9, :] = -np.float16(6e-8)
+    x[9, 90] = np.float16(-65504.0)
+    x[10, ::2] = np.float16(6e-8)
+    x[10, 1::2] = np.float16(-6e-8)
+    x[10, 64] = np.float16(65504.0)
+    got = _tq3_gpu(x, dev)
+    exp = O.tq3_encode(x)
+    gn, en = got["norm"], exp["norm"]
+    assert np.array_equal(np.isnan(gn), np.isnan(en))
+    ok = ~np.isnan(en)
+    assert np.array_equal(gn[ok].view(np.uint32), en[ok].view(np.uint32))
+    assert np.array_equal(got["qs"], exp["qs"])
+    assert not exp["qs"][:5].any()
+
+
 def test_tq3_append_large_bitexact(dev):
     """Config-3 layer build size: 32768 tokens x 8 blocks (262144 blocks)."""
     torch = _torch()

@@ -285,6 +285,46 @@ def test_prescale_thresholds_match_device_header():
     assert neg == dict(enumerate(PRESCALE_THR_NEG))
 
 
+FOLD_A = 0x4b800001          # 2^24 + 2
+FOLD_Q = [0x4b002dd9, 0x4b86719d, 0x4bdfd5e4]
+
+
+def test_fold_thresholds_match_device_header():
+    import re
+    hdr = open(os.path.join(ROOT, "qengine_amd", "csrc", "qkv_device.h")).read()
+    pinned = {int(k): int(v, 16) for k, v in re.findall(r"kFoldQBits\[(\d)\] == (0x[0-9a-f]+)u", hdr)}
+    assert pinned == dict(enumerate(FOLD_Q))
+    a = re.search(r"kFoldA = ([0-9.]+)f;", hdr).group(1)
+    assert np.float32(float(a)).view(np.uint32) == FOLD_A
+
+
+@pytest.mark.parametrize("negated", [False, True])
+def test_fold_binning_exhaustive(negated):
+    assert O.fold_mismatches(FOLD_A, FOLD_Q, negated=negated) == 0
+
+
+@pytest.mark.parametrize("k,delta", [(0, 1), (0, -1), (1, 1), (1, -1), (2, 1), (2, -1)])
+def test_fold_binning_one_ulp_off_fails(k, delta):
+    q = list(FOLD_Q)
+    q[k] += delta
+    # the patterns near the pre-scale threshold pair this Q separates
+    for neg in (False, True):
+        assert O.fold_mismatches(FOLD_A, FOLD_Q, 0x3f000000, 0x40000000, negated=neg) == 0
+    bad = sum(O.fold_mismatches(FOLD_A, q, lo, hi, negated=neg)
+              for lo, hi in ((0x3f000000, 0x40000000), (0xbf000000, 0xc0000000))
+              for neg in (False, True))
+    assert bad > 0
+
+
+def test_fold_binning_needs_the_offset():
+    # A = 2^24 (no asymmetry between the sides) cannot serve both signs
+    q = [int(np.float32(np.float64(np.uint32(b).view(np.float32)) * 2.0**24).view(np.uint32))
+         for b in PRESCALE_THR[4:]]
+    bad = sum(O.fold_mismatches(0x4b800000, q, lo, hi, negated=False)
+              for lo, hi in ((0x3f000000, 0x40000000), (0xbf000000, 0xc0000000)))
+    assert bad > 0
+
+
 def test_prescale_thresholds_exhaustive():
     assert O.prescale_threshold_mismatches(PRESCALE_THR) == 0
 
