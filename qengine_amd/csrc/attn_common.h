@@ -24,9 +24,10 @@ struct AttnArgs {
   uint32_t kv_bytes;        // readable bytes of each cache from its base (buffer range)
   int num_q, num_kv;
   int start_pos, sub_n, sub_n_max;
+  int qpw;                  // queries per workgroup (MFMA columns = qpw * gqa <= 16)
   int active_end_max;       // reference split sizing (split API)
   int k_splits;             // reference split count (split API)
-  int n_chunks;             // workgroups per (kv head, query): k_splits or key chunks
+  int n_chunks;             // workgroups per (kv head, query group): k_splits or key chunks
   int chunk_keys;           // keys per fast-path chunk (multiple of 256)
   int n_slots;              // fast-path records per (q head, query): n_chunks
   float scale_log2;         // softmax scale * log2(e)

@@ -64,17 +64,19 @@ constexpr int kStageBytes = (36 * kKeyPitch + 16) * 4;   // 9856
 constexpr int kLdsLut = 0;
 constexpr int kLdsLutBytes = 256 * 64 * 4;
 constexpr int kLdsStage = kLdsLut + kLdsLutBytes;            // per wave, kStageBytes
-constexpr int kLdsQ = kLdsStage + kWaves * kStageBytes;      // rotated query, [8][2][4][4][8] fp16
-constexpr int kLdsTileEnd = kLdsQ + 16 * 128 * 2;            // 43776
-constexpr int kLdsMergeO = kLdsStage;                        // [4 waves][8 rows][256] f32
-constexpr int kLdsMergeML = kLdsMergeO + kWaves * 8 * kHD * 4;
-constexpr int kLdsMergeEnd = kLdsMergeML + 256 * 4;
+constexpr int kLdsQ = kLdsStage + kWaves * kStageBytes;      // rotated query, [16][2][4][4][8] fp16
+constexpr int kLdsTileEnd = kLdsQ + 16 * 256 * 2;
+// After the tile loop the table and the staging areas are free: the merge
+// area starts at 0.
+constexpr int kLdsMergeO = 0;                                // [waves][16 rows][256] f32
+constexpr int kLdsMergeML = kLdsMergeO + kWaves * 16 * kHD * 4;
+constexpr int kLdsMergeEnd = kLdsMergeML + 512 * 4;
 constexpr int kLdsTotal = kLdsTileEnd;
 static_assert(kLdsMergeEnd <= kLdsQ, "merge area must not reach the query scratch");
 
 // merge-area float offsets (ML): m[w][8], l[w][8], M[8], L[8]
-constexpr int kMlW0 = 0, kMlLw0 = 8 * kWaves, kMlM = 16 * kWaves, kMlL = 16 * kWaves + 8;
-static_assert(kMlL + 8 <= 256, "merge scalars must fit the ML area");
+constexpr int kMlW0 = 0, kMlLw0 = 16 * kWaves, kMlM = 32 * kWaves, kMlL = 32 * kWaves + 16;
+static_assert(kMlL + 16 <= 512, "merge scalars must fit the ML area");
 
 __device__ __forceinline__ uint32_t lut_read(const uint8_t* lds, uint32_t addr) {
   return *reinterpret_cast<const uint32_t*>(lds + kLdsLut + addr);
@@ -401,9 +403,10 @@ __device__ void store_record(const uint8_t* lds, const AttnArgs& p, __amdgpu_buf
   const float* mo = reinterpret_cast<const float*>(lds + kLdsMergeO);
   const float* mlv = reinterpret_cast<const float*>(lds + kLdsMergeML);
   const int gqa = p.num_q / p.num_kv;
+  // row r = qi * gqa + hh: q head h*gqa + hh of query t + qi
   for (int idx = threadIdx.x; idx < rows * 64; idx += kThreads) {
     const int r = idx >> 6, d4 = (idx & 63) * 4;
-    const long rec = rec_index(p, h * gqa + r, t, chunk);
+    const long rec = rec_index(p, h * gqa + r % gqa, t + r / gqa, chunk);
     __builtin_amdgcn_raw_buffer_store_b128(*reinterpret_cast<const f4_t*>(&mo[r * kHD + d4]), ro,
                                            (uint32_t)((rec * kHD + d4) * 4), 0, kCoherent);
     if (d4 == 0)
@@ -412,10 +415,12 @@ __device__ void store_record(const uint8_t* lds, const AttnArgs& p, __amdgpu_buf
   }
   __builtin_amdgcn_s_waitcnt(0);  // this thread's data stores are complete
   __syncthreads();
-  if ((int)threadIdx.x < rows)
+  if ((int)threadIdx.x < rows) {
+    const int r = threadIdx.x;
     __builtin_amdgcn_raw_buffer_store_b32(
-        tag, rml, (uint32_t)(rec_index(p, h * gqa + threadIdx.x, t, chunk) * kRecMlBytes + 8), 0,
-        kCoherent);
+        tag, rml, (uint32_t)(rec_index(p, h * gqa + r % gqa, t + r / gqa, chunk) * kRecMlBytes + 8),
+        0, kCoherent);
+  }
 }
 
 // Rotate the merged rows back (o = rs*D*H*o_rot per 128-block).  final: divide
@@ -441,7 +446,7 @@ __device__ void finish_rows(const uint8_t* lds, const AttnArgs& p, int h, int t,
     wht_xor_lanes16(x, lane);
     if (!live) continue;
     const float rs = wht_scale();
-    const int qh = h * gqa + r;
+    const int qh = h * gqa + r % gqa, tq = t + r / gqa;
     float y[8];
     const uint32_t sbits = sign_word_sel(part >> 2) >> (8 * (part & 3));  // elements part*8..+7
 #pragma unroll
@@ -454,10 +459,10 @@ __device__ void finish_rows(const uint8_t* lds, const AttnArgs& p, int h, int t,
       uint32_t pk[4];
 #pragma unroll
       for (int i = 0; i < 4; i++) pk[i] = f2h(y[2 * i]) | (f2h(y[2 * i + 1]) << 16);
-      *reinterpret_cast<uint4*>(out + ((long)t * p.num_q + qh) * kHD + blk * 128 + part * 8) =
+      *reinterpret_cast<uint4*>(out + ((long)tq * p.num_q + qh) * kHD + blk * 128 + part * 8) =
           make_uint4(pk[0], pk[1], pk[2], pk[3]);
     } else {
-      const long mlx = ((long)qh * p.sub_n_max + t) * p.k_splits + split;
+      const long mlx = ((long)qh * p.sub_n_max + tq) * p.k_splits + split;
 #pragma unroll
       for (int i = 0; i < 8; i++) p.part_o[mlx * kHD + blk * 128 + part * 8 + i] = y[i];
       if (blk == 0 && part == 0) {
@@ -478,37 +483,55 @@ __global__ __launch_bounds__(kThreads, 1) void tq3_attn_kernel(AttnArgs p, uint1
   const int wave = threadIdx.x >> 6;
   const int gqa = p.num_q / p.num_kv;
 
-  // ---- work id (XCD-aware: the num_kv workgroups of one (t, chunk) share an XCD)
-  int h, t_idx, chunk;
+  // ---- work id (XCD-aware: the num_kv workgroups of one (query group, chunk)
+  // share an XCD).  A workgroup serves queries t0 .. t0+nq-1 (nq <= qpw) of
+  // one kv head: MFMA column c = qi * gqa + hh is q head h*gqa + hh of query
+  // t0 + qi (columns past nq * gqa carry nothing).
+  int h, t0, chunk;
   bool has_work;
   {
     const int L = blockIdx.x;
     const int xcd = L & 7, r = L >> 3;
     h = r % p.num_kv;
     const int g = (r / p.num_kv) * 8 + xcd;
-    has_work = g < p.sub_n * p.n_chunks;
-    t_idx = has_work ? g / p.n_chunks : 0;
-    chunk = has_work ? g - t_idx * p.n_chunks : 0;
+    const int groups = (p.sub_n + p.qpw - 1) / p.qpw;
+    has_work = g < groups * p.n_chunks;
+    const int tq = has_work ? g / p.n_chunks : 0;
+    chunk = has_work ? g - tq * p.n_chunks : 0;
+    t0 = tq * p.qpw;
   }
   if (MODE == 1 && !has_work) return;
-  const int active_end = p.ctx_lens ? min(max(p.ctx_lens[t_idx], 0), p.ctx_max)
-                                    : p.start_pos + t_idx + 1;
-  int lo = 0, hi = 0;
+  const int nq = min(p.qpw, p.sub_n - t0);
+  const int rows_used = nq * gqa;   // accumulator rows (columns) that hold heads
+  const int row = lane >> 4;        // 16-lane row of the MFMA D layout
+  const int col = lane & 15;
+  const int t_col = t0 + min(col / gqa, nq - 1);   // this lane's query (clamped for dead columns)
+  // key counts: the lane's own query, and the first / last query of the group
+  // (a paged group has one query)
+  const int active_end = p.ctx_lens ? min(max(p.ctx_lens[t_col], 0), p.ctx_max)
+                                    : p.start_pos + t_col + 1;
+  const int active_first = p.ctx_lens ? active_end : p.start_pos + t0 + 1;
+  const int active_last = p.ctx_lens ? active_end : p.start_pos + t0 + nq;
+  int lo = 0, hi = 0, hi_col = 0, hi_first = 0;
   if (MODE == 0) {
     if (has_work) {
       lo = chunk * p.chunk_keys;
-      hi = min(lo + p.chunk_keys, active_end);
+      hi = min(lo + p.chunk_keys, active_last);
+      hi_col = min(lo + p.chunk_keys, active_end);
+      hi_first = min(lo + p.chunk_keys, active_first);
     }
   } else {
     // reference split range (attention.cuh:1944-1951)
     const int total_tiles = (p.active_end_max + 31) / 32;
     const int tps = (total_tiles + p.k_splits - 1) / p.k_splits;
     lo = chunk * tps * 32;
-    hi = min((chunk + 1) * tps * 32, active_end);
+    hi = min((chunk + 1) * tps * 32, active_last);
+    hi_col = min((chunk + 1) * tps * 32, active_end);
+    hi_first = min((chunk + 1) * tps * 32, active_first);
   }
-  const KeyRule rule(p.start_pos, t_idx, p.sink_tok, p.window_tok, p.tree_mask);
-  const int row = lane >> 4;        // 16-lane row of the MFMA D layout
-  const int col = lane & 15;
+  // A dead column has a zero query: its scores are 0 and its accumulator rows
+  // are never stored, so it needs no mask of its own.
+  const KeyRule rule(p.start_pos, t_col, p.sink_tok, p.window_tok, p.tree_mask);
 
   // ---- first tile's loads go out before the setup work ----------------------
   const __amdgpu_buffer_rsrc_t rk =
@@ -537,13 +560,13 @@ __global__ __launch_bounds__(kThreads, 1) void tq3_attn_kernel(AttnArgs p, uint1
   uint32_t ac[4] = {lane4, lane4, lane4, lane4};   // table address chains
   TileRegs tr;
   {
-    // 16 WHTs of 128 (8 heads x 2 blocks), 16 lanes each (threads 0..255); fp16 result in LDS
+    // 32 WHTs of 128 (16 columns x 2 blocks), 16 lanes each; fp16 result in LDS
     // scratch laid out [head][block][group u][octet o][8] so each lane's A
     // operand slice is one 16-byte read.
     uint16_t* qs = reinterpret_cast<uint16_t*>(lds + kLdsQ);
     const int wht = threadIdx.x >> 4;
     const int part = threadIdx.x & 15;
-    const int hh = wht >> 1, blk = wht & 1;
+    const int cq = wht >> 1, blk = wht & 1;   // column, 128-block
     // The query is loaded and rotated before any tile load is issued: a
     // query load issued after the tile loads of the whole chip would wait
     // behind them in the memory queues.  The load is unconditional (rows
@@ -553,10 +576,15 @@ __global__ __launch_bounds__(kThreads, 1) void tq3_attn_kernel(AttnArgs p, uint1
     const __amdgpu_buffer_rsrc_t rq =
         __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(p.q), 0, q_extent, kBufferRsrcWord3);
     const uint32_t qoff =
-        hh < gqa ? (uint32_t)(((t_idx * p.num_q + h * gqa + hh) * kHD + blk * 128 + part * 8) * 2)
-                 : q_extent;
+        cq < rows_used ? (uint32_t)((((t0 + cq / gqa) * p.num_q + h * gqa + cq % gqa) * kHD +
+                                     blk * 128 + part * 8) * 2)
+                       : q_extent;
     const u4_t raw = __builtin_amdgcn_raw_buffer_load_b128(rq, qoff, 0, 0);
-    {
+    const int o = part >> 2, u = part & 3;   // elements part*8..+7 = code group 4*o + u
+    if (2 * wave >= rows_used) {
+      // a wave whose two columns are both dead writes zeros
+      *reinterpret_cast<uint4*>(qs + (((cq * 2 + blk) * 4 + u) * 4 + o) * 8) = make_uint4(0, 0, 0, 0);
+    } else {
       float x[8];
       const uint32_t wv[4] = {raw[0], raw[1], raw[2], raw[3]};
 #pragma unroll
@@ -576,15 +604,12 @@ __global__ __launch_bounds__(kThreads, 1) void tq3_attn_kernel(AttnArgs p, uint1
       uint32_t pk[4];
 #pragma unroll
       for (int i = 0; i < 4; i++) pk[i] = f2h(x[2 * i] * rs) | (f2h(x[2 * i + 1] * rs) << 16);
-      // elements part*8..+7 = dims of code group `part` = 4*o + u
-      const int o = part >> 2, u = part & 3;
-      if (wht < 16)   // threads past the 8 heads x 2 blocks have no piece
-        *reinterpret_cast<uint4*>(qs + (((hh * 2 + blk) * 4 + u) * 4 + o) * 8) =
-            make_uint4(pk[0], pk[1], pk[2], pk[3]);
+      *reinterpret_cast<uint4*>(qs + (((cq * 2 + blk) * 4 + u) * 4 + o) * 8) =
+          make_uint4(pk[0], pk[1], pk[2], pk[3]);
     }
   }
   __syncthreads();
-  load_tile(rk, rv, tile_row(p, t_idx, lo + wave * kTile, hi), p.num_kv, h, lane, row, col, tr);
+  load_tile(rk, rv, tile_row(p, t0, lo + wave * kTile, hi), p.num_kv, h, lane, row, col, tr);
   // launch epoch of the fast-path workspace (records of this call carry
   // epoch + 1); requested after the first tile so that it is in flight
   // during the tile's compute and needed only when the records are stored
@@ -594,16 +619,15 @@ __global__ __launch_bounds__(kThreads, 1) void tq3_attn_kernel(AttnArgs p, uint1
                                               __HIP_MEMORY_SCOPE_AGENT)
                 : 0u;
   __builtin_amdgcn_sched_barrier(0);
-  // qa[s], slice s = 4j+u: A row = head `col`, element i = dim 128j + 8(4*row+u) + i
+  // qa[s], slice s = 4j+u: column `col`, element i = dim 128j + 8(4*row+u) + i
   h8_t qa[8];
   {
     const uint16_t* qs = reinterpret_cast<const uint16_t*>(lds + kLdsQ);
 #pragma unroll
     for (int s = 0; s < 8; s++) {
       const int j = s >> 2, u = s & 3;
-      // rows 8..15 are never written and must read as zero
-      qa[s] = col < 8 ? *reinterpret_cast<const h8_t*>(qs + (((col * 2 + j) * 4 + u) * 4 + row) * 8)
-                      : h8_t{0, 0, 0, 0, 0, 0, 0, 0};
+      // dead columns were written as zeros
+      qa[s] = *reinterpret_cast<const h8_t*>(qs + (((col * 2 + j) * 4 + u) * 4 + row) * 8);
     }
   }
 
@@ -619,7 +643,7 @@ __global__ __launch_bounds__(kThreads, 1) void tq3_attn_kernel(AttnArgs p, uint1
 
   for (int ts = lo + wave * kTile; ts < hi; ts += kWaves * kTile) {
     const bool first = ts == lo + wave * kTile;
-    if (!first) load_tile(rk, rv, tile_row(p, t_idx, ts, hi), p.num_kv, h, lane, row, col, tr);
+    if (!first) load_tile(rk, rv, tile_row(p, t0, ts, hi), p.num_kv, h, lane, row, col, tr);
     auto& kq = tr.kq;
     auto& kn = tr.kn;
 
@@ -666,8 +690,9 @@ __global__ __launch_bounds__(kThreads, 1) void tq3_attn_kernel(AttnArgs p, uint1
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 
-    // dense is wave-uniform: the common full tile skips the per-key rule
-    const bool dense = ts + kTile <= hi && rule.all_visible(ts + kTile);
+    // dense is wave-uniform: the common full tile (every key visible to every
+    // query of the group) skips the per-key rule
+    const bool dense = ts + kTile <= hi_first && rule.all_visible(ts + kTile);
     float s[4][4];
 #pragma unroll
     for (int g = 0; g < 4; g++) {
@@ -682,7 +707,7 @@ __global__ __launch_bounds__(kThreads, 1) void tq3_attn_kernel(AttnArgs p, uint1
 #pragma unroll
         for (int r = 0; r < 4; r++) {
           const int key = ts + 16 * g + 4 * row + r;
-          const bool vis = (key < hi) & rule.visible(key, active_end);   // masks padded keys too
+          const bool vis = (key < hi_col) & rule.visible(key, active_end);   // padded keys too
           s[g][r] = vis ? s[g][r] : -INFINITY;
         }
     }
@@ -753,33 +778,33 @@ __global__ __launch_bounds__(kThreads, 1) void tq3_attn_kernel(AttnArgs p, uint1
   __syncthreads();
   float* mo = reinterpret_cast<float*>(lds + kLdsMergeO);    // [wave][8][256]
   float* ml = reinterpret_cast<float*>(lds + kLdsMergeML);
-  if (4 * row < gqa) {   // accumulator rows 4*row + r hold heads; rows >= gqa are unused
+  if (4 * row < rows_used) {   // accumulator rows 4*row + r; rows >= rows_used are unused
     // acc tile t: rows 4*row+r, dim 128*(t>>3) + 8*col + (t&7)
 #pragma unroll
     for (int t = 0; t < 16; t++)
 #pragma unroll
       for (int r = 0; r < 4; r++)
-        mo[(wave * 8 + 4 * row + r) * kHD + 128 * (t >> 3) + 8 * col + (t & 7)] = acc[t][r];
+        mo[(wave * 16 + 4 * row + r) * kHD + 128 * (t >> 3) + 8 * col + (t & 7)] = acc[t][r];
   }
-  if (row == 0 && col < 8) {
-    ml[kMlW0 + wave * 8 + col] = m2;
-    ml[kMlLw0 + wave * 8 + col] = lsum;
+  if (row == 0) {
+    ml[kMlW0 + wave * 16 + col] = m2;
+    ml[kMlLw0 + wave * 16 + col] = lsum;
   }
   __syncthreads();
-  const int rows = min(gqa, 8);
+  const int rows = rows_used;
   for (int idx = threadIdx.x; idx < rows * 64; idx += kThreads) {
     const int r = idx >> 6, d4 = (idx & 63) * 4;
     float M = -INFINITY;
 #pragma unroll
-    for (int w = 0; w < kWaves; w++) M = fmaxf(M, ml[kMlW0 + w * 8 + r]);
+    for (int w = 0; w < kWaves; w++) M = fmaxf(M, ml[kMlW0 + w * 16 + r]);
     float L = 0.f, o[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int w = 0; w < kWaves; w++) {
-      const float mw = ml[kMlW0 + w * 8 + r];
+      const float mw = ml[kMlW0 + w * 16 + r];
       const float wt = (mw == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(mw - M);
-      L += wt * ml[kMlLw0 + w * 8 + r];
+      L += wt * ml[kMlLw0 + w * 16 + r];
 #pragma unroll
-      for (int i = 0; i < 4; i++) o[i] += wt * mo[(w * 8 + r) * kHD + d4 + i];
+      for (int i = 0; i < 4; i++) o[i] += wt * mo[(w * 16 + r) * kHD + d4 + i];
     }
 #pragma unroll
     for (int i = 0; i < 4; i++) mo[r * kHD + d4 + i] = o[i];   // wave-0 slot, own elements
@@ -791,7 +816,7 @@ __global__ __launch_bounds__(kThreads, 1) void tq3_attn_kernel(AttnArgs p, uint1
   __syncthreads();
 
   if (MODE == 1) {
-    finish_rows(lds, p, h, t_idx, rows, false, chunk, nullptr);
+    finish_rows(lds, p, h, t0, rows, false, chunk, nullptr);
     return;
   }
 
@@ -802,7 +827,7 @@ __global__ __launch_bounds__(kThreads, 1) void tq3_attn_kernel(AttnArgs p, uint1
   const __amdgpu_buffer_rsrc_t ro =
       __builtin_amdgcn_make_buffer_rsrc(p.ws_o, 0, p.ws_o_bytes, kBufferRsrcWord3);
   const uint32_t tag = epoch + 1u;
-  if (has_work) store_record(lds, p, rml, ro, h, t_idx, rows, chunk, tag);
+  if (has_work) store_record(lds, p, rml, ro, h, t0, rows, chunk, tag);
   // the last n_mergers workgroups of the grid merge the (q head, query, block) units
   const int n_units = p.num_q * p.sub_n * 2;
   const int n_mergers = min(n_units, (int)gridDim.x);
@@ -826,7 +851,7 @@ __global__ __launch_bounds__(kThreads, 1) void tq3_attn_kernel(AttnArgs p, uint1
 size_t tq3_attn_lds_bytes() { return kLdsTotal; }
 
 hipError_t launch_tq3_attn(const AttnArgs& a, int mode, uint16_t* out, hipStream_t stream) {
-  const int groups = a.sub_n * a.n_chunks;
+  const int groups = (a.sub_n + a.qpw - 1) / a.qpw * a.n_chunks;
   const int n_wg = ((groups + 7) / 8) * 8 * a.num_kv;
   dim3 grid(n_wg), block(kThreads);
   if (mode == 0)

@@ -175,6 +175,7 @@ int qkv_attn_split_tq3(const uint16_t* q, const qkv_block_tq3* k, const qkv_bloc
   a.start_pos = start_pos;
   a.sub_n = sub_n;
   a.sub_n_max = sub_n_max;
+  a.qpw = 16 / (num_q / num_kv);   // queries share the MFMA columns
   {
     const uint64_t extent = (uint64_t)(start_pos + sub_n) * num_kv * 104;
     if (extent > 0x7fffffffULL) return QKV_ERR_UNSUPPORTED;   // 32-bit buffer offsets
@@ -298,6 +299,7 @@ int qkv_decode_attn_tq3(const uint16_t* q, const qkv_block_tq3* k, const qkv_blo
   a.start_pos = start_pos;
   a.sub_n = sub_n;
   a.sub_n_max = sub_n;
+  a.qpw = 16 / (num_q / num_kv);   // queries share the MFMA columns
   {
     const uint64_t extent = (uint64_t)n_keys * num_kv * 104;
     if (extent > 0x7fffffffULL) return QKV_ERR_UNSUPPORTED;   // 32-bit buffer offsets
@@ -355,6 +357,7 @@ int qkv_decode_attn_tq3_paged(const uint16_t* q, const qkv_block_tq3* k_pool,
   a.start_pos = 0;
   a.sub_n = n_slots;
   a.sub_n_max = n_slots;
+  a.qpw = 1;   // slots read different caches
   {
     const uint64_t extent = (uint64_t)pool_rows * num_kv * 104;
     if (extent > 0x7fffffffULL) return QKV_ERR_UNSUPPORTED;   // 32-bit buffer offsets

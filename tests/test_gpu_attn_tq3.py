@@ -117,6 +117,40 @@ def test_fast_decode_vs_oracle(dev, n, num_q, sub_n):
     assert rel_err(out.cpu().numpy(), exp.view(np.float16)) < TOL
 
 
+@pytest.mark.parametrize("n,num_q,sub_n,sink,window,tree", [
+    (3000, 16, 16, 0, 0, True), (3000, 16, 16, 64, 256, False), (3000, 16, 16, 32, 100, True),
+    (2000, 16, 5, 0, 0, False), (1500, 16, 7, 0, 0, True), (1200, 24, 3, 0, 0, False),
+    (900, 8, 11, 0, 0, True), (700, 4, 17, 0, 0, False), (20016, 16, 16, 0, 0, False)])
+def test_fast_decode_multi_query(dev, n, num_q, sub_n, sink, window, tree):
+    """Several queries per workgroup (they share the MFMA columns): partial
+    last groups, GQA 1, 2, 4, 6, causal, tree and sink/window masks."""
+    from qengine_amd import kvcache
+    torch = _torch()
+    num_kv = 4
+    rng, kb, vb = _cache(900 + n + sub_n, n, num_kv)
+    q = q_f16(rng, sub_n, num_q, 256)
+    tm = None
+    if tree:
+        tm = np.array([(1 << t) | (int(rng.integers(0, 1 << max(t, 1))) & ((1 << t) - 1))
+                       for t in range(sub_n)], np.uint32)
+    start = n - sub_n
+    ws = kvcache.decode_attn_tq3_workspace(num_q, num_kv, sub_n, n, dev)
+    out = torch.zeros((sub_n, num_q, 256), dtype=torch.float16, device=dev)
+    tmd = None if tm is None else _dev(tm, dev)
+    kvcache.decode_attn_tq3(_dev(q.view(np.uint16), dev), _dev(kb.view(np.uint8), dev),
+                            _dev(vb.view(np.uint8), dev), out, ws, num_q=num_q, num_kv=num_kv,
+                            start_pos=start, sub_n=sub_n, scale=1 / 16, sink_tok=sink,
+                            window_tok=window, tree_mask=tmd)
+    torch.cuda.synchronize()
+    em, el, eo = O.attn_split(O.KV_TQ3, q, kb, vb, num_q=num_q, num_kv=num_kv, hd=256,
+                              start_pos=start, sub_n=sub_n, sub_n_max=sub_n, active_end_max=n,
+                              scale=1 / 16, k_splits=8, sink_tok=sink, window_tok=window,
+                              tree_mask=tm)
+    exp = O.attn_split_merge(em, el, eo, num_q=num_q, num_kv=num_kv, hd=256, sub_n=sub_n,
+                             sub_n_max=sub_n, k_splits=8)
+    assert rel_err(out.cpu().numpy(), exp.view(np.float16)) < TOL
+
+
 def test_fast_decode_rejects_small_workspace(dev):
     from qengine_amd import QKVError, kvcache
     torch = _torch()
