@@ -103,7 +103,7 @@ def secondary(torch, kvcache, dev, stream):
     po = torch.empty(NUM_Q, 16, 8, HD, device=dev)
     o = torch.empty(1, NUM_Q, HD, dtype=torch.float16, device=dev)
 
-    def q8_layer(i=0):
+    def q8_layer_split(i=0):
         kb, vb = caches[i % len(caches)]
         kvcache.q8_append(knew, kb[ctx * blocks_tok:])
         kvcache.q8_append(vnew, vb[ctx * blocks_tok:])
@@ -112,14 +112,25 @@ def secondary(torch, kvcache, dev, stream):
                               k_splits=8)
         kvcache.attn_split_merge(pm, pl, po, o, num_q=NUM_Q, num_kv=NUM_KV, sub_n=1,
                                  sub_n_max=16, k_splits=8)
+    ws8 = kvcache.decode_attn_q8_workspace(NUM_Q, NUM_KV, 1, ctx + 1, dev)
+
+    def q8_layer(i=0):
+        kb, vb = caches[i % len(caches)]
+        kvcache.q8_append_kv(knew, vnew, kb[ctx * blocks_tok:], vb[ctx * blocks_tok:])
+        kvcache.decode_attn_q8(q, kb, vb, o, ws8, num_q=NUM_Q, num_kv=NUM_KV, start_pos=ctx,
+                               sub_n=1, scale=scale)
+    ms_split = _time(torch, stream, q8_layer_split, 200)
     ms = _time(torch, stream, q8_layer, 200)
     q8_bytes = 2 * (ctx + 1) * blocks_tok * 36 + NUM_Q * HD * 2 * 2
     out["config2_q8_decode"] = {
         "us_per_layer": round(ms * 1e3, 3),
         "bytes_per_layer": q8_bytes, "gbps": round(q8_bytes / (ms * 1e-3) / 1e9, 1),
         "frac": round(q8_bytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
-        "note": "per layer: Q8 append of the new token's K and V, split-K decode over 4097 "
-                "keys, merge (4 launches); 8 layers x 4 cache sets rotated"}
+        "split_api_us_per_layer": round(ms_split * 1e3, 3),
+        "note": "per layer: Q8 append of the new token's K and V and single-launch decode over "
+                "4097 keys (2 launches); split_api_us_per_layer: the same through the reference "
+                "split layout (2 appends, split-K decode K_SPLITS 8, merge: 4 launches); 8 layers "
+                "x 4 cache sets rotated"}
     del caches
 
     # ---- config 4: 8 slots, 24 q / 4 kv heads, 256-token blocks, ctx ~ U[1K, 64K],
@@ -204,20 +215,33 @@ def secondary(torch, kvcache, dev, stream):
     nv = 16
     qv, kv_, vv = rnd(nv, NUM_Q, HD), rnd(nv, NUM_KV, HD), rnd(nv, NUM_KV, HD)
     ov = torch.empty(nv, NUM_Q, HD, dtype=torch.float16, device=dev)
-    wsv = kvcache.prefill_attn_tq3_workspace(NUM_Q, NUM_KV, nv, hist, dev)
+    wsv = kvcache.decode_attn_tq3_workspace(NUM_Q, NUM_KV, nv, hist + nv, dev)
+    wsp16 = kvcache.prefill_attn_tq3_workspace(NUM_Q, NUM_KV, nv, hist, dev)
+
+    def append16():
+        kvcache.tq3_append_kv(kv_, vv, kb[hist * 8:(hist + nv) * 8], vb[hist * 8:(hist + nv) * 8])
 
     def verify(i=0):
-        kvcache.tq3_append_kv(kv_, vv, kb[hist * 8:(hist + nv) * 8], vb[hist * 8:(hist + nv) * 8])
-        kvcache.prefill_attn_tq3(qv, kb, vb, None, None, ov, wsv, num_q=NUM_Q, num_kv=NUM_KV,
+        append16()
+        kvcache.decode_attn_tq3(qv, kb, vb, ov, wsv, num_q=NUM_Q, num_kv=NUM_KV, start_pos=hist,
+                                sub_n=nv, scale=scale)
+
+    def verify_prefill_path(i=0):
+        append16()
+        kvcache.prefill_attn_tq3(qv, kb, vb, None, None, ov, wsp16, num_q=NUM_Q, num_kv=NUM_KV,
                                  start_pos=hist, scale=scale)
     ms = _time(torch, stream, verify, 50)
+    ms_pf = _time(torch, stream, verify_prefill_path, 50)
     vbytes = (hist + nv) * 2 * BLOCKS_PER_TOKEN * 52 + nv * NUM_Q * HD * 2 * 2
     out["config5_verify16"] = {
         "us": round(ms * 1e3, 3), "bytes": vbytes,
         "gbps": round(vbytes / (ms * 1e-3) / 1e9, 1),
         "frac": round(vbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+        "prefill_path_us": round(ms_pf * 1e3, 3),
         "note": "append of the 16 verify tokens, then causal attention of the 16 queries over "
-                "the TQ3 cache (131088 keys, the block's own keys read back quantized)"}
+                "the TQ3 cache (131088 keys, the block's own keys read back quantized) through "
+                "qkv_decode_attn_tq3 with sub_n 16 (4 queries per workgroup pass); "
+                "prefill_path_us: the same through qkv_prefill_attn_tq3 in verify mode"}
     return out
 
 

@@ -97,6 +97,11 @@ int qkv_tq3_dequant(const qkv_block_tq3* in, uint16_t* out_f16, int n_blocks,
 int qkv_q8_append(const uint16_t* in_f16, qkv_block_q8* out, int n_blocks,
                   hipStream_t stream);
 
+/* K and V in one launch: the two quantize_kv_q8_0_kern launches of
+ * model.cuh:2316-2333 (same blocks as two qkv_q8_append calls). */
+int qkv_q8_append_kv(const uint16_t* k_f16, const uint16_t* v_f16, qkv_block_q8* k_out,
+                     qkv_block_q8* v_out, int n_blocks, hipStream_t stream);
+
 /* Replaces dequantize_kv_q8_0_kern (attention.cuh:2614-2626). */
 int qkv_q8_dequant(const qkv_block_q8* in, uint16_t* out_f16, int n_blocks,
                    hipStream_t stream);
@@ -152,9 +157,11 @@ size_t qkv_decode_attn_tq3_workspace_bytes(int num_q, int num_kv, int sub_n, int
 
 /* Fast path for the same computation as qkv_attn_split_tq3 + qkv_attn_split_merge
  * (model.cuh:2472-2491) in ONE launch: the key range is cut into chunks of
- * 256*k keys, partials stay in rotated coordinates and are merged inside the
- * kernel (the last-arriving workgroups do the merge), and each output row is
- * rotated back once.  out [sub_n][num_q][256] fp16 (16-byte aligned).
+ * 512*k keys, partials stay in rotated coordinates and are merged inside the
+ * kernel (the last workgroups of the grid do the merge), and each output row
+ * is rotated back once.  Up to 16/GQA queries of a multi-token call (verify,
+ * sub_n > 1) share one pass over the cache.  out [sub_n][num_q][256] fp16
+ * (16-byte aligned).
  * workspace: caller-owned device memory of at least
  * qkv_decode_attn_tq3_workspace_bytes() bytes, 256-byte aligned, ZERO-FILLED
  * before its first use; every completed call leaves it ready for the next
@@ -164,6 +171,19 @@ int qkv_decode_attn_tq3(const uint16_t* q, const qkv_block_tq3* k, const qkv_blo
                         int sub_n, float scale, int sink_tok, int window_tok,
                         const uint32_t* tree_mask, void* workspace, size_t workspace_bytes,
                         hipStream_t stream);
+
+/* Fast path for qkv_attn_split_q8 + qkv_attn_split_merge over the Q8_0 cache
+ * (model.cuh:5655-5665; attention.cuh:2633-2801 and 1837-1891) in ONE launch:
+ * chunks of 128*k keys, records merged inside the kernel as for
+ * qkv_decode_attn_tq3 (values are not rotated).  Same argument meaning as
+ * qkv_attn_split_q8 (no sink/window/tree rules, as in the reference) with the
+ * merged fp16 output and a workspace of qkv_decode_attn_q8_workspace_bytes()
+ * bytes (256-byte aligned, zero-filled before first use, reused in order). */
+size_t qkv_decode_attn_q8_workspace_bytes(int num_q, int num_kv, int sub_n, int n_keys);
+int qkv_decode_attn_q8(const uint16_t* q, const qkv_block_q8* k, const qkv_block_q8* v,
+                       uint16_t* out, int num_q, int num_kv, int head_dim, int start_pos,
+                       int sub_n, float scale, void* workspace, size_t workspace_bytes,
+                       hipStream_t stream);
 
 /* Paged, ragged decode: one query per slot over per-slot block tables
  * This generalises the reference, which keeps every

@@ -41,6 +41,7 @@ SIGNATURES = {
     "qkv_tq3_append_kv": (_I, [_P, _P, _P, _P, _I, _P]),
     "qkv_tq3_dequant": (_I, [_P, _P, _I, _P]),
     "qkv_q8_append": (_I, [_P, _P, _I, _P]),
+    "qkv_q8_append_kv": (_I, [_P, _P, _P, _P, _I, _P]),
     "qkv_q8_dequant": (_I, [_P, _P, _I, _P]),
     "qkv_attn_split_tq3": (_I, [_P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _F, _I, _I,
                                _I, _P, _P]),
@@ -49,6 +50,8 @@ SIGNATURES = {
     "qkv_decode_attn_tq3_workspace_bytes": (_SZ, [_I, _I, _I, _I]),
     "qkv_decode_attn_tq3": (_I, [_P, _P, _P, _P, _I, _I, _I, _I, _I, _F, _I, _I, _P, _P, _SZ,
                                 _P]),
+    "qkv_decode_attn_q8_workspace_bytes": (_SZ, [_I, _I, _I, _I]),
+    "qkv_decode_attn_q8": (_I, [_P, _P, _P, _P, _I, _I, _I, _I, _I, _F, _P, _SZ, _P]),
     "qkv_tq3_append_kv_paged": (_I, [_P, _P, _P, _P, _I, _I, _I, _I, _P, _I, _I, _I, _P, _P]),
     "qkv_decode_attn_tq3_paged_workspace_bytes": (_SZ, [_I, _I, _I, _I]),
     "qkv_decode_attn_tq3_paged": (_I, [_P, _P, _P, _P, _I, _I, _I, _I, _P, _I, _I, _I, _P, _I,

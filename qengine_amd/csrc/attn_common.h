@@ -154,6 +154,7 @@ __device__ __forceinline__ void wht_xor_lanes16(float (&x)[8], int lane) {
 
 hipError_t launch_tq3_attn(const AttnArgs& a, int mode, uint16_t* out, hipStream_t stream);
 hipError_t launch_q8_attn_split(const AttnArgs& a, hipStream_t stream);
+hipError_t launch_q8_attn_fast(const AttnArgs& a, uint16_t* out, hipStream_t stream);
 hipError_t launch_split_merge(const float* m, const float* l, const float* o, uint16_t* out,
                               int num_q, int sub_n, int sub_n_max, int k_splits,
                               hipStream_t stream);

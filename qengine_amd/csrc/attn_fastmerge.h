@@ -1,0 +1,220 @@
+// attn_fastmerge.h -- the cross-workgroup merge of the single-launch decode
+// fast paths (TQ3 and Q8_0 caches).  Every workgroup of a launch writes one
+// record per (q head, query, key chunk) {m, l, o[256]}; the last workgroups of
+// the grid are designated mergers, one per (q head, query, 128-dim block)
+// unit, and turn the unit's records into the fp16 output.
+//
+// Records move between workgroups (possibly on different XCDs, whose L2s are
+// not coherent with each other) with buffer accesses carrying the sc0|sc1
+// cache policy: stores write through to the device coherence point and loads
+// read from it.  A writer stores a record's data, waits for those stores to
+// complete (s_waitcnt vmcnt(0)) and only then stores the record's tag; a
+// merger loads a record's data only after it has read the tag.  No workgroup
+// pays an L2 write-back or invalidate (what agent-scope fences cost on this
+// GPU), and no arrival counter is contended.  Only mergers wait, and they are
+// dispatched after every other workgroup, so progress does not depend on
+// workgroup co-residency.
+#pragma once
+#include "attn_common.h"
+#include "qkv_device.h"
+
+namespace qkv {
+
+constexpr int kCoherent = 1 | 16;   // sc0 | sc1
+
+// Record index of (q head, query t, chunk) in the fast-path workspace.
+__device__ __forceinline__ long rec_index(const AttnArgs& p, int qh, int t, int chunk) {
+  return (long)(qh * p.sub_n + t) * p.n_slots + chunk;
+}
+
+// Poll limit of a merger waiting for the records of one launch (each poll
+// sleeps ~64 cycles after two memory round trips; the limit is seconds, far
+// beyond any legitimate wait).
+constexpr int kMergeSpinLimit = 1 << 22;
+
+// Merger thread layout for a THREADS-thread workgroup: slices of 32 threads
+// (one dim quad of a 128-block each), 128/slices records per thread
+// (n_chunks <= 128).  The reduction area holds [slices][128] sums, then
+// maxima, sums of l and the 128 merged dims.
+template <int THREADS>
+struct MergeLayout {
+  static constexpr int kSlices = THREADS / 32;
+  static constexpr int kRecPerThread = 128 / kSlices;
+  static constexpr int kRedM = kSlices * 128, kRedL = kRedM + kSlices, kRedSum = kRedL + kSlices;
+  static constexpr int kRedFloats = kRedSum + 128;
+};
+
+// Merge all chunk records (n_chunks <= 128) of one unit (q head qh, query t,
+// 128-block blk) and write its fp16 output  o = sum w_c o_c / sum w_c l_c,
+// rotated back (o = rs*D*H*o per 128-block) when ROTATE.
+// 1. Threads 0..n-1 poll one record each ({m, l, tag} in one 16-byte load)
+//    until every tag is current; m and l go to LDS (mls, 128 entries).
+// 2. Thread (record slice sl = tid/32, dim quad dq = tid%32) loads the rows
+//    of records sl, sl+slices, ... in one round and merges them through the
+//    LDS reduction area red.
+// Returns false (and writes nothing) if the records did not all appear within
+// the poll limit.
+template <int THREADS, bool ROTATE>
+__device__ bool merge_unit(float* red, f2_t* mls, const AttnArgs& p, __amdgpu_buffer_rsrc_t rml,
+                           __amdgpu_buffer_rsrc_t ro, int qh, int t, int blk, uint32_t tag,
+                           uint16_t* out) {
+  using ML = MergeLayout<THREADS>;
+  constexpr int kSlices = ML::kSlices, kRecPerThread = ML::kRecPerThread;
+  constexpr int kRedM = ML::kRedM, kRedL = ML::kRedL, kRedSum = ML::kRedSum;
+  constexpr int kHD = 256;
+  const int tid = threadIdx.x;
+  const int sl = tid >> 5, dq = tid & 31;
+  const int n = p.n_chunks;
+  const long base = rec_index(p, qh, t, 0);
+  bool seen = tid >= n;
+  bool complete = false;
+  for (int spins = 0; spins < kMergeSpinLimit; spins++) {
+    if (!seen) {
+      const f4_t r = __builtin_amdgcn_raw_buffer_load_b128(
+          rml, (uint32_t)((base + tid) * kRecMlBytes), 0, kCoherent);
+      if (__float_as_uint(r[2]) == tag) {
+        seen = true;
+        mls[tid] = f2_t{r[0], r[1]};
+      }
+    }
+    if (__syncthreads_and(seen)) {
+      complete = true;
+      break;
+    }
+    __builtin_amdgcn_s_sleep(1);
+  }
+  if (!complete) return false;
+  f4_t v[kRecPerThread];
+#pragma unroll
+  for (int i = 0; i < kRecPerThread; i++) {
+    const int c = sl + kSlices * i;
+    v[i] = c < n ? __builtin_amdgcn_raw_buffer_load_b128(
+                       ro, (uint32_t)(((base + c) * kHD + blk * 128 + 4 * dq) * 4), 0, kCoherent)
+                 : f4_t{0.f, 0.f, 0.f, 0.f};
+  }
+  // common max over all records (empty chunks, l = 0, carry no weight)
+  float M = -INFINITY;
+#pragma unroll
+  for (int i = 0; i < kRecPerThread; i++) {
+    const int c = sl + kSlices * i;
+    if (c < n && mls[c][1] > 0.f) M = fmaxf(M, mls[c][0]);
+  }
+  if (dq == 0) red[kRedM + sl] = M;
+  __syncthreads();
+  M = red[kRedM];
+#pragma unroll
+  for (int k = 1; k < kSlices; k++) M = fmaxf(M, red[kRedM + k]);
+  f4_t acc = {0.f, 0.f, 0.f, 0.f};
+  float L = 0.f;
+#pragma unroll
+  for (int i = 0; i < kRecPerThread; i++) {
+    const int c = sl + kSlices * i;
+    if (c < n && mls[c][1] > 0.f) {
+      const float w = __builtin_amdgcn_exp2f(mls[c][0] - M);
+      L += w * mls[c][1];
+      acc += w * v[i];
+    }
+  }
+  *reinterpret_cast<f4_t*>(&red[sl * 128 + 4 * dq]) = acc;
+  if (dq == 0) red[kRedL + sl] = L;
+  __syncthreads();
+  // sum the slices: thread d < 128 owns dim d
+  if (tid < 128) {
+    float sum = 0.f;
+#pragma unroll
+    for (int k = 0; k < kSlices; k++) sum += red[k * 128 + tid];
+    red[kRedSum + tid] = sum;
+  }
+  __syncthreads();
+  // 16 lanes x 8 elements (threads 0..15): normalise, rotate back, store fp16
+  if (tid < 16) {
+    float Lt = 0.f;
+#pragma unroll
+    for (int k = 0; k < kSlices; k++) Lt += red[kRedL + k];
+    const float inv = Lt > 0.f ? 1.0f / Lt : 0.f;
+    float x[8];
+#pragma unroll
+    for (int i = 0; i < 8; i++) x[i] = red[kRedSum + tid * 8 + i] * inv;
+    uint32_t pk[4];
+    if constexpr (ROTATE) {
+      wht8_inreg(x);
+      wht_xor_lanes16(x, tid);
+      const float rs = wht_scale();
+      const uint32_t sbits = sign_word_sel(tid >> 2) >> (8 * (tid & 3));   // signs of elements tid*8..+7
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        float y[2];
+#pragma unroll
+        for (int e2 = 0; e2 < 2; e2++) {
+          const bool pos = (sbits >> (2 * i + e2)) & 1u;
+          const float vv = x[2 * i + e2] * rs;
+          y[e2] = pos ? vv : -vv;
+        }
+        pk[i] = f2h(y[0]) | (f2h(y[1]) << 16);
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < 4; i++) pk[i] = f2h(x[2 * i]) | (f2h(x[2 * i + 1]) << 16);
+    }
+    *reinterpret_cast<uint4*>(out + ((long)t * p.num_q + qh) * kHD + blk * 128 + tid * 8) =
+        make_uint4(pk[0], pk[1], pk[2], pk[3]);
+  }
+  __syncthreads();
+  return true;
+}
+
+// Store this workgroup's merged rows as records: row r = qi * gqa + hh (q head
+// h*gqa + hh of query t0 + qi) with data mo[r][256], maxima Mv[r] (log2
+// units) and sums Lv[r]; data first, then (once every thread's data stores
+// are complete) the tags.
+template <int THREADS>
+__device__ void store_records(const float* mo, const float* Mv, const float* Lv,
+                              const AttnArgs& p, __amdgpu_buffer_rsrc_t rml,
+                              __amdgpu_buffer_rsrc_t ro, int h, int t0, int rows, int chunk,
+                              uint32_t tag) {
+  constexpr int kHD = 256;
+  const int gqa = p.num_q / p.num_kv;
+  for (int idx = threadIdx.x; idx < rows * 64; idx += THREADS) {
+    const int r = idx >> 6, d4 = (idx & 63) * 4;
+    const long rec = rec_index(p, h * gqa + r % gqa, t0 + r / gqa, chunk);
+    __builtin_amdgcn_raw_buffer_store_b128(*reinterpret_cast<const f4_t*>(&mo[r * kHD + d4]), ro,
+                                           (uint32_t)((rec * kHD + d4) * 4), 0, kCoherent);
+    if (d4 == 0)
+      __builtin_amdgcn_raw_buffer_store_b64(f2_t{Mv[r], Lv[r]}, rml,
+                                            (uint32_t)(rec * kRecMlBytes), 0, kCoherent);
+  }
+  __builtin_amdgcn_s_waitcnt(0);  // this thread's data stores are complete
+  __syncthreads();
+  if ((int)threadIdx.x < rows) {
+    const int r = threadIdx.x;
+    __builtin_amdgcn_raw_buffer_store_b32(
+        tag, rml, (uint32_t)(rec_index(p, h * gqa + r % gqa, t0 + r / gqa, chunk) * kRecMlBytes + 8),
+        0, kCoherent);
+  }
+}
+
+// The designated mergers: the last min(units, grid) workgroups merge the
+// (q head, query, block) units; the last merger to finish advances the
+// workspace epoch (every workgroup of this launch has read it by then) and
+// resets the count.
+template <int THREADS, bool ROTATE>
+__device__ void merge_phase(float* red, f2_t* mls, const AttnArgs& p, __amdgpu_buffer_rsrc_t rml,
+                            __amdgpu_buffer_rsrc_t ro, uint32_t tag, uint16_t* out) {
+  const int n_units = p.num_q * p.sub_n * 2;
+  const int n_mergers = min(n_units, (int)gridDim.x);
+  const int mid = (int)blockIdx.x - ((int)gridDim.x - n_mergers);
+  if (mid < 0) return;
+  for (int u = mid; u < n_units; u += n_mergers) {
+    const int blk = u & 1, qh = (u >> 1) % p.num_q, t = (u >> 1) / p.num_q;
+    if (!merge_unit<THREADS, ROTATE>(red, mls, p, rml, ro, qh, t, blk, tag, out)) break;
+  }
+  if (threadIdx.x == 0) {
+    const int done = atomicAdd(&p.ws_header[kWsFinished], 1);
+    if (done == n_mergers - 1) {
+      __hip_atomic_store(&p.ws_header[kWsFinished], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(&p.ws_header[kWsEpoch], (int)tag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+  }
+}
+
+}  // namespace qkv

@@ -22,8 +22,14 @@
 //           [block][key] scales; a lane reads one dim quad of 8 keys and
 //           decodes it into the B operands of 4 MFMA tiles (tile 4a+e,
 //           column n = dim 64a + 4n + e).
+// Split API (MODE 1): one workgroup per reference split, partials in the
+// reference layout.  Fast path (MODE 0): 128-key chunks (one 32-key tile per
+// wave, or a multiple), tagged records and designated mergers in the same
+// launch (attn_fastmerge.h); values are not rotated, so the merge ends with a
+// plain fp16 store.
 #include "qkv_device.h"
 #include "attn_common.h"
+#include "attn_fastmerge.h"
 
 namespace qkv {
 namespace {
@@ -48,7 +54,11 @@ constexpr int kLdsMergeO = 0;
 constexpr int kLdsMergeML = kLdsMergeO + kWaves * 8 * kHD * 4;
 constexpr int kLdsMergeEnd = kLdsMergeML + 256 * 4;
 constexpr int kLdsTotal = kLdsMergeEnd > kLdsTotalTile ? kLdsMergeEnd : kLdsTotalTile;
-constexpr int kMlW0 = 0, kMlLw0 = 8 * kWaves;   // merge scalars: m[w][8], l[w][8]
+constexpr int kMlW0 = 0, kMlLw0 = 8 * kWaves;   // merge scalars: m[w][8], l[w][8], M[8], L[8]
+constexpr int kMlM = 16 * kWaves, kMlL = 16 * kWaves + 8;
+static_assert(kMlL + 8 <= 256, "merge scalars must fit the ML area");
+static_assert(kLdsMergeO + MergeLayout<kThreads>::kRedFloats * 4 <= kLdsMergeML,
+              "merger reduction must fit the merge area");
 
 struct TileQ8 {
   uint32_t k[2][18];   // key 16g+col: blocks 2*row and 2*row+1 (qs, pad|d, qs, pad|d)
@@ -114,23 +124,45 @@ __device__ __forceinline__ void wave_sync() {
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
-__global__ __launch_bounds__(kThreads, 2) void q8_attn_split_kernel(AttnArgs p) {
+template <int MODE>
+__global__ __launch_bounds__(kThreads, 2) void q8_attn_kernel(AttnArgs p, uint16_t* out) {
   __shared__ __attribute__((aligned(16))) uint8_t lds[kLdsTotal];
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int row = lane >> 4, col = lane & 15;
   const int gqa = p.num_q / p.num_kv;
 
-  // work id: (kv head, query, split)
-  const int L = blockIdx.x;
-  const int h = L % p.num_kv;
-  const int t_idx = (L / p.num_kv) % p.sub_n;
-  const int split = L / (p.num_kv * p.sub_n);
-  const int active_end = p.start_pos + t_idx + 1;
-  const int total_tiles = (p.active_end_max + 31) / 32;   // attention.cuh:2660-2663
-  const int tps = (total_tiles + p.k_splits - 1) / p.k_splits;
-  const int lo = split * tps * 32;
-  const int hi = min((split + 1) * tps * 32, active_end);
+  int h, t_idx, split, lo, hi;
+  bool has_work = true;
+  if (MODE == 1) {
+    // work id: (kv head, query, split)
+    const int L = blockIdx.x;
+    h = L % p.num_kv;
+    t_idx = (L / p.num_kv) % p.sub_n;
+    split = L / (p.num_kv * p.sub_n);
+    const int active_end = p.start_pos + t_idx + 1;
+    const int total_tiles = (p.active_end_max + 31) / 32;   // attention.cuh:2660-2663
+    const int tps = (total_tiles + p.k_splits - 1) / p.k_splits;
+    lo = split * tps * 32;
+    hi = min((split + 1) * tps * 32, active_end);
+  } else {
+    // work id (XCD-aware: the num_kv workgroups of one (query, chunk) share an XCD)
+    const int L = blockIdx.x;
+    const int xcd = L & 7, r = L >> 3;
+    h = r % p.num_kv;
+    const int g = (r / p.num_kv) * 8 + xcd;
+    has_work = g < p.sub_n * p.n_chunks;
+    t_idx = has_work ? g / p.n_chunks : 0;
+    split = has_work ? g - t_idx * p.n_chunks : 0;
+    const int active_end = p.start_pos + t_idx + 1;
+    lo = split * p.chunk_keys;
+    hi = has_work ? min(lo + p.chunk_keys, active_end) : lo;
+  }
+  // launch epoch of the fast-path workspace (records of this call carry epoch + 1)
+  const uint32_t epoch =
+      MODE == 0 ? (uint32_t)__hip_atomic_load(&p.ws_header[kWsEpoch], __ATOMIC_RELAXED,
+                                              __HIP_MEMORY_SCOPE_AGENT)
+                : 0u;
 
   const __amdgpu_buffer_rsrc_t rk =
       __builtin_amdgcn_make_buffer_rsrc(const_cast<uint32_t*>(p.k), 0, p.kv_bytes, kBufferRsrcWord3);
@@ -293,22 +325,52 @@ __global__ __launch_bounds__(kThreads, 2) void q8_attn_split_kernel(AttnArgs p) 
       Ls += wt * ml[kMlLw0 + w * 8 + r];
       o += wt * *reinterpret_cast<const f4_t*>(&mo[(w * 8 + r) * kHD + d4]);
     }
-    const int qh = h * gqa + r;
-    const long mlx = ((long)qh * p.sub_n_max + t_idx) * p.k_splits + split;
+    if (MODE == 1) {
+      const int qh = h * gqa + r;
+      const long mlx = ((long)qh * p.sub_n_max + t_idx) * p.k_splits + split;
 #pragma unroll
-    for (int i = 0; i < 4; i++) p.part_o[mlx * kHD + d4 + i] = o[i];
-    if (d4 == 0) {
-      p.part_m[mlx] = (M == -INFINITY) ? -INFINITY : M * kLn2;
-      p.part_l[mlx] = Ls;
+      for (int i = 0; i < 4; i++) p.part_o[mlx * kHD + d4 + i] = o[i];
+      if (d4 == 0) {
+        p.part_m[mlx] = (M == -INFINITY) ? -INFINITY : M * kLn2;
+        p.part_l[mlx] = Ls;
+      }
+    } else {
+      // merged row into the wave-0 slot (this thread's own elements), M and L
+      // beside it, for the records
+      *reinterpret_cast<f4_t*>(&mo[r * kHD + d4]) = o;
+      if (d4 == 0) {
+        ml[kMlM + r] = M;
+        ml[kMlL + r] = Ls;
+      }
     }
   }
+  if (MODE == 1) return;
+
+  // ---- fast path: tagged records, designated mergers
+  __syncthreads();
+  const __amdgpu_buffer_rsrc_t rml =
+      __builtin_amdgcn_make_buffer_rsrc(p.ws_ml, 0, p.ws_ml_bytes, kBufferRsrcWord3);
+  const __amdgpu_buffer_rsrc_t ro =
+      __builtin_amdgcn_make_buffer_rsrc(p.ws_o, 0, p.ws_o_bytes, kBufferRsrcWord3);
+  const uint32_t tag = epoch + 1u;
+  if (has_work)
+    store_records<kThreads>(mo, ml + kMlM, ml + kMlL, p, rml, ro, h, t_idx, rows, split, tag);
+  merge_phase<kThreads, false>(reinterpret_cast<float*>(lds + kLdsMergeO),
+                               reinterpret_cast<f2_t*>(lds + kLdsMergeML), p, rml, ro, tag, out);
 }
 
 }  // namespace
 
 hipError_t launch_q8_attn_split(const AttnArgs& a, hipStream_t stream) {
   const int n_wg = a.num_kv * a.sub_n * a.k_splits;
-  hipLaunchKernelGGL(q8_attn_split_kernel, dim3(n_wg), dim3(kThreads), 0, stream, a);
+  hipLaunchKernelGGL((q8_attn_kernel<1>), dim3(n_wg), dim3(kThreads), 0, stream, a, nullptr);
+  return hipGetLastError();
+}
+
+hipError_t launch_q8_attn_fast(const AttnArgs& a, uint16_t* out, hipStream_t stream) {
+  const int groups = a.sub_n * a.n_chunks;
+  const int n_wg = ((groups + 7) / 8) * 8 * a.num_kv;
+  hipLaunchKernelGGL((q8_attn_kernel<0>), dim3(n_wg), dim3(kThreads), 0, stream, a, out);
   return hipGetLastError();
 }
 

@@ -33,6 +33,7 @@
 // reference partial layout.
 #include "qkv_device.h"
 #include "attn_common.h"
+#include "attn_fastmerge.h"
 
 namespace qkv {
 
@@ -254,173 +255,6 @@ __device__ __forceinline__ float xrow_sum(float v) {
   v = __uint_as_float(a[0]) + __uint_as_float(a[1]);
   const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
   return __uint_as_float(b[0]) + __uint_as_float(b[1]);
-}
-
-// Records move between workgroups (possibly on different XCDs, whose L2s are
-// not coherent with each other) with buffer accesses carrying the sc0|sc1
-// cache policy: stores write through to the device coherence point and loads
-// read from it.  A writer stores a record's data, waits for those stores to
-// complete (s_waitcnt vmcnt(0)) and only then stores the record's tag; a
-// merger loads a record's data only after it has read the tag.  No workgroup
-// pays an L2 write-back or invalidate (what agent-scope fences cost on this
-// GPU), and no arrival counter is contended.
-constexpr int kCoherent = 1 | 16;   // sc0 | sc1
-
-
-// Record index of (q head, query t, chunk) in the fast-path workspace.
-__device__ __forceinline__ long rec_index(const AttnArgs& p, int qh, int t, int chunk) {
-  return (long)(qh * p.sub_n + t) * p.n_slots + chunk;
-}
-
-// Merger thread layout: kSlices record slices of 32 threads (one dim quad of
-// a 128-block each), kRecPerThread records per thread (n_chunks <= 128); the
-// LDS reduction area holds [kSlices][128] sums, then maxima, sums of l and
-// the 128 merged dims.
-constexpr int kSlices = kThreads / 32;
-constexpr int kRecPerThread = 128 / kSlices;
-constexpr int kRedM = kSlices * 128, kRedL = kRedM + kSlices, kRedSum = kRedL + kSlices;
-static_assert(kLdsMergeO + (kRedSum + 128) * 4 <= kLdsMergeML, "merge reduction must fit");
-
-// Poll limit of a merger waiting for the records of one launch (each poll
-// sleeps ~64 cycles after two memory round trips; the limit is seconds, far
-// beyond any legitimate wait).
-constexpr int kMergeSpinLimit = 1 << 22;
-
-// Merge all chunk records (n_chunks <= 128) of one unit (q head qh, query t,
-// 128-block blk) and write its fp16 output o = rs*D*H*(sum w_c o_c / sum w_c l_c).
-// 1. Threads 0..n-1 poll one record each ({m, l, tag} in one 16-byte load)
-//    until every tag is current; m and l go to LDS.
-// 2. Thread (record slice sl = tid/32, dim quad dq = tid%32) loads the
-//    rotated rows of records sl, sl+kSlices, ... in one round and merges them.
-// Returns false (and writes nothing) if the records did not all appear within
-// the poll limit.
-__device__ bool merge_unit(uint8_t* lds, const AttnArgs& p, __amdgpu_buffer_rsrc_t rml,
-                           __amdgpu_buffer_rsrc_t ro, int qh, int t, int blk, uint32_t tag,
-                           uint16_t* out) {
-  float* red = reinterpret_cast<float*>(lds + kLdsMergeO);   // [kSlices][128] sums, scalars after
-  f2_t* mls = reinterpret_cast<f2_t*>(lds + kLdsMergeML);     // [128] {m, l} of the records
-  const int tid = threadIdx.x;
-  const int sl = tid >> 5, dq = tid & 31;
-  const int n = p.n_chunks;
-  const long base = rec_index(p, qh, t, 0);
-  bool seen = tid >= n;
-  bool complete = false;
-  for (int spins = 0; spins < kMergeSpinLimit; spins++) {
-    if (!seen) {
-      const f4_t r = __builtin_amdgcn_raw_buffer_load_b128(
-          rml, (uint32_t)((base + tid) * kRecMlBytes), 0, kCoherent);
-      if (__float_as_uint(r[2]) == tag) {
-        seen = true;
-        mls[tid] = f2_t{r[0], r[1]};
-      }
-    }
-    if (__syncthreads_and(seen)) {
-      complete = true;
-      break;
-    }
-    __builtin_amdgcn_s_sleep(1);
-  }
-  if (!complete) return false;
-  f4_t v[kRecPerThread];
-#pragma unroll
-  for (int i = 0; i < kRecPerThread; i++) {
-    const int c = sl + kSlices * i;
-    v[i] = c < n ? __builtin_amdgcn_raw_buffer_load_b128(
-                       ro, (uint32_t)(((base + c) * kHD + blk * 128 + 4 * dq) * 4), 0, kCoherent)
-                 : f4_t{0.f, 0.f, 0.f, 0.f};
-  }
-  // common max over all records (empty chunks, l = 0, carry no weight)
-  float M = -INFINITY;
-#pragma unroll
-  for (int i = 0; i < kRecPerThread; i++) {
-    const int c = sl + kSlices * i;
-    if (c < n && mls[c][1] > 0.f) M = fmaxf(M, mls[c][0]);
-  }
-  if (dq == 0) red[kRedM + sl] = M;
-  __syncthreads();
-  M = red[kRedM];
-#pragma unroll
-  for (int k = 1; k < kSlices; k++) M = fmaxf(M, red[kRedM + k]);
-  f4_t acc = {0.f, 0.f, 0.f, 0.f};
-  float L = 0.f;
-#pragma unroll
-  for (int i = 0; i < kRecPerThread; i++) {
-    const int c = sl + kSlices * i;
-    if (c < n && mls[c][1] > 0.f) {
-      const float w = __builtin_amdgcn_exp2f(mls[c][0] - M);
-      L += w * mls[c][1];
-      acc += w * v[i];
-    }
-  }
-  *reinterpret_cast<f4_t*>(&red[sl * 128 + 4 * dq]) = acc;
-  if (dq == 0) red[kRedL + sl] = L;
-  __syncthreads();
-  // sum the slices: thread d < 128 owns dim d
-  if (tid < 128) {
-    float sum = 0.f;
-#pragma unroll
-    for (int k = 0; k < kSlices; k++) sum += red[k * 128 + tid];
-    red[kRedSum + tid] = sum;
-  }
-  __syncthreads();
-  // rotate back: 16 lanes x 8 elements (threads 0..15)
-  if (tid < 16) {
-    float Lt = 0.f;
-#pragma unroll
-    for (int k = 0; k < kSlices; k++) Lt += red[kRedL + k];
-    const float inv = Lt > 0.f ? 1.0f / Lt : 0.f;
-    float x[8];
-#pragma unroll
-    for (int i = 0; i < 8; i++) x[i] = red[kRedSum + tid * 8 + i] * inv;
-    wht8_inreg(x);
-    wht_xor_lanes16(x, tid);
-    const float rs = wht_scale();
-    uint32_t pk[4];
-    const uint32_t sbits = sign_word_sel(tid >> 2) >> (8 * (tid & 3));   // signs of elements tid*8..+7
-#pragma unroll
-    for (int i = 0; i < 4; i++) {
-      float y[2];
-#pragma unroll
-      for (int e2 = 0; e2 < 2; e2++) {
-        const bool pos = (sbits >> (2 * i + e2)) & 1u;
-        const float vv = x[2 * i + e2] * rs;
-        y[e2] = pos ? vv : -vv;
-      }
-      pk[i] = f2h(y[0]) | (f2h(y[1]) << 16);
-    }
-    *reinterpret_cast<uint4*>(out + ((long)t * p.num_q + qh) * kHD + blk * 128 + tid * 8) =
-        make_uint4(pk[0], pk[1], pk[2], pk[3]);
-  }
-  __syncthreads();
-  return true;
-}
-
-// Store the merged rows in LDS as this workgroup's records (rotated): data
-// first, then (once every thread's data stores are complete) the tags.
-__device__ void store_record(const uint8_t* lds, const AttnArgs& p, __amdgpu_buffer_rsrc_t rml,
-                             __amdgpu_buffer_rsrc_t ro, int h, int t, int rows, int chunk,
-                             uint32_t tag) {
-  const float* mo = reinterpret_cast<const float*>(lds + kLdsMergeO);
-  const float* mlv = reinterpret_cast<const float*>(lds + kLdsMergeML);
-  const int gqa = p.num_q / p.num_kv;
-  // row r = qi * gqa + hh: q head h*gqa + hh of query t + qi
-  for (int idx = threadIdx.x; idx < rows * 64; idx += kThreads) {
-    const int r = idx >> 6, d4 = (idx & 63) * 4;
-    const long rec = rec_index(p, h * gqa + r % gqa, t + r / gqa, chunk);
-    __builtin_amdgcn_raw_buffer_store_b128(*reinterpret_cast<const f4_t*>(&mo[r * kHD + d4]), ro,
-                                           (uint32_t)((rec * kHD + d4) * 4), 0, kCoherent);
-    if (d4 == 0)
-      __builtin_amdgcn_raw_buffer_store_b64(f2_t{mlv[kMlM + r], mlv[kMlL + r]}, rml,
-                                            (uint32_t)(rec * kRecMlBytes), 0, kCoherent);
-  }
-  __builtin_amdgcn_s_waitcnt(0);  // this thread's data stores are complete
-  __syncthreads();
-  if ((int)threadIdx.x < rows) {
-    const int r = threadIdx.x;
-    __builtin_amdgcn_raw_buffer_store_b32(
-        tag, rml, (uint32_t)(rec_index(p, h * gqa + r % gqa, t + r / gqa, chunk) * kRecMlBytes + 8),
-        0, kCoherent);
-  }
 }
 
 // Rotate the merged rows back (o = rs*D*H*o_rot per 128-block).  final: divide
@@ -827,25 +661,15 @@ __global__ __launch_bounds__(kThreads, 1) void tq3_attn_kernel(AttnArgs p, uint1
   const __amdgpu_buffer_rsrc_t ro =
       __builtin_amdgcn_make_buffer_rsrc(p.ws_o, 0, p.ws_o_bytes, kBufferRsrcWord3);
   const uint32_t tag = epoch + 1u;
-  if (has_work) store_record(lds, p, rml, ro, h, t0, rows, chunk, tag);
-  // the last n_mergers workgroups of the grid merge the (q head, query, block) units
-  const int n_units = p.num_q * p.sub_n * 2;
-  const int n_mergers = min(n_units, (int)gridDim.x);
-  const int mid = (int)blockIdx.x - ((int)gridDim.x - n_mergers);
-  if (mid < 0) return;
-  for (int u = mid; u < n_units; u += n_mergers) {
-    const int blk = u & 1, qh = (u >> 1) % p.num_q, t = (u >> 1) / p.num_q;
-    if (!merge_unit(lds, p, rml, ro, qh, t, blk, tag, out)) break;
+  if (has_work) {
+    const float* mlv = reinterpret_cast<const float*>(lds + kLdsMergeML);
+    store_records<kThreads>(reinterpret_cast<const float*>(lds + kLdsMergeO), mlv + kMlM,
+                            mlv + kMlL, p, rml, ro, h, t0, rows, chunk, tag);
   }
-  // every merger is past its records: the last one advances the epoch (all
-  // workgroups of this launch have read it) and resets the count
-  if (threadIdx.x == 0) {
-    const int done = atomicAdd(&p.ws_header[kWsFinished], 1);
-    if (done == n_mergers - 1) {
-      __hip_atomic_store(&p.ws_header[kWsFinished], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      __hip_atomic_store(&p.ws_header[kWsEpoch], (int)tag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
-  }
+  using ML = MergeLayout<kThreads>;
+  static_assert(kLdsMergeO + ML::kRedFloats * 4 <= kLdsMergeML, "merge reduction must fit");
+  merge_phase<kThreads, true>(reinterpret_cast<float*>(lds + kLdsMergeO),
+                              reinterpret_cast<f2_t*>(lds + kLdsMergeML), p, rml, ro, tag, out);
 }
 
 size_t tq3_attn_lds_bytes() { return kLdsTotal; }

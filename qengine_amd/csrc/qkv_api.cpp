@@ -121,6 +121,15 @@ int qkv_q8_append(const uint16_t* in_f16, qkv_block_q8* out, int n_blocks, hipSt
   return launch_status(qkv::launch_q8_append(in_f16, out, in_f16, out, n_blocks, 1, stream));
 }
 
+int qkv_q8_append_kv(const uint16_t* k_f16, const uint16_t* v_f16, qkv_block_q8* k_out,
+                     qkv_block_q8* v_out, int n_blocks, hipStream_t stream) {
+  if (n_blocks < 0) return QKV_ERR_INVALID;
+  if (n_blocks == 0) return QKV_OK;
+  if (!k_f16 || !v_f16 || !k_out || !v_out) return QKV_ERR_NULL;
+  if (!aligned(k_f16, 16) || !aligned(v_f16, 16) || !aligned(k_out, 4) || !aligned(v_out, 4))
+    return QKV_ERR_ALIGN;
+  return launch_status(qkv::launch_q8_append(k_f16, k_out, v_f16, v_out, n_blocks, 2, stream));
+}
 int qkv_q8_dequant(const qkv_block_q8* in, uint16_t* out_f16, int n_blocks, hipStream_t stream) {
   if (n_blocks < 0) return QKV_ERR_INVALID;
   if (n_blocks == 0) return QKV_OK;
@@ -136,7 +145,8 @@ int qkv_q8_dequant(const qkv_block_q8* in, uint16_t* out_f16, int n_blocks, hipS
 // ---------------------------------------------------------------------------
 namespace {
 
-constexpr int kChunkKeys = 512;   // 8 waves x 64-key tiles
+constexpr int kChunkKeys = 512;     // TQ3 fast path: 8 waves x 64-key tiles
+constexpr int kChunkKeysQ8 = 128;   // Q8 fast path: 4 waves x 32-key tiles
 
 int check_attn_shape(int num_q, int num_kv, int head_dim, int start_pos, int sub_n,
                      const uint32_t* tree_mask) {
@@ -250,13 +260,13 @@ struct FastGeom {
   int chunk_keys, n_chunks, n_slots;
   size_t header_off, ml_off, o_off, total;
 };
-// Chunks of 512*tpw keys, at most 128 per (kv head, query): one record per
+// Chunks of base*tpw keys, at most 128 per (kv head, query): one record per
 // chunk and q head, merged by the designated merger workgroups.
-FastGeom fast_geom(int num_q, int num_kv, int sub_n, int n_keys) {
+FastGeom fast_geom(int num_q, int num_kv, int sub_n, int n_keys, int base = kChunkKeys) {
   FastGeom g{};
-  const int c512 = (n_keys + kChunkKeys - 1) / kChunkKeys;
-  const int tpw = (c512 + 127) / 128;
-  g.chunk_keys = kChunkKeys * tpw;
+  const int cb = (n_keys + base - 1) / base;
+  const int tpw = (cb + 127) / 128;
+  g.chunk_keys = base * tpw;
   g.n_chunks = (n_keys + g.chunk_keys - 1) / g.chunk_keys;
   g.n_slots = g.n_chunks;
   const size_t rows = (size_t)num_q * sub_n * g.n_slots;
@@ -321,6 +331,55 @@ int qkv_decode_attn_tq3(const uint16_t* q, const qkv_block_tq3* k, const qkv_blo
   a.ws_ml_bytes = (uint32_t)(g.o_off - g.ml_off);
   a.ws_o_bytes = (uint32_t)(g.total - g.o_off);
   return launch_status(qkv::launch_tq3_attn(a, 0, out, stream));
+}
+
+size_t qkv_decode_attn_q8_workspace_bytes(int num_q, int num_kv, int sub_n, int n_keys) {
+  if (num_q <= 0 || num_kv <= 0 || sub_n <= 0 || n_keys <= 0) return 0;
+  return fast_geom(num_q, num_kv, sub_n, n_keys, kChunkKeysQ8).total;
+}
+
+int qkv_decode_attn_q8(const uint16_t* q, const qkv_block_q8* k, const qkv_block_q8* v,
+                       uint16_t* out, int num_q, int num_kv, int head_dim, int start_pos,
+                       int sub_n, float scale, void* workspace, size_t workspace_bytes,
+                       hipStream_t stream) {
+  int st = check_attn_shape(num_q, num_kv, head_dim, start_pos, sub_n, nullptr);
+  if (st) return st;
+  if (!q || !k || !v || !out) return QKV_ERR_NULL;
+  if (!aligned(q, 16) || !aligned(k, 4) || !aligned(v, 4) || !aligned(out, 16))
+    return QKV_ERR_ALIGN;
+  const int n_keys = start_pos + sub_n;
+  const FastGeom g = fast_geom(num_q, num_kv, sub_n, n_keys, kChunkKeysQ8);
+  if (!workspace || workspace_bytes < g.total) return QKV_ERR_WORKSPACE;
+  if (!aligned(workspace, 256)) return QKV_ERR_ALIGN;
+  char* ws = static_cast<char*>(workspace);
+  qkv::AttnArgs a{};
+  a.q = q;
+  a.k = reinterpret_cast<const uint32_t*>(k);
+  a.v = reinterpret_cast<const uint32_t*>(v);
+  a.num_q = num_q;
+  a.num_kv = num_kv;
+  a.start_pos = start_pos;
+  a.sub_n = sub_n;
+  a.sub_n_max = sub_n;
+  a.qpw = 1;
+  {
+    const uint64_t extent = (uint64_t)n_keys * num_kv * 8 * sizeof(qkv_block_q8);
+    if (extent > 0x7fffffffULL) return QKV_ERR_UNSUPPORTED;   // 32-bit buffer offsets
+    a.kv_bytes = (uint32_t)extent;
+  }
+  a.active_end_max = n_keys;
+  a.k_splits = 1;
+  a.n_chunks = g.n_chunks;
+  a.chunk_keys = g.chunk_keys;
+  a.n_slots = g.n_slots;
+  a.scale_log2 = scale * qkv::kLog2e;
+  a.ws_header = reinterpret_cast<int*>(ws + g.header_off);
+  a.ws_ml = reinterpret_cast<float*>(ws + g.ml_off);
+  a.ws_o = reinterpret_cast<float*>(ws + g.o_off);
+  if (g.total > 0xffffffffULL) return QKV_ERR_UNSUPPORTED;   // 32-bit buffer offsets
+  a.ws_ml_bytes = (uint32_t)(g.o_off - g.ml_off);
+  a.ws_o_bytes = (uint32_t)(g.total - g.o_off);
+  return launch_status(qkv::launch_q8_attn_fast(a, out, stream));
 }
 
 size_t qkv_decode_attn_tq3_paged_workspace_bytes(int num_q, int num_kv, int n_slots,

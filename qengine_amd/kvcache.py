@@ -81,6 +81,19 @@ def q8_append(x: torch.Tensor, out: torch.Tensor, stream=None) -> None:
           "qkv_q8_append")
 
 
+def q8_append_kv(k: torch.Tensor, v: torch.Tensor, k_out: torch.Tensor, v_out: torch.Tensor,
+                 stream=None) -> None:
+    """K and V in one launch (the two quantize_kv_q8_0_kern launches of
+    model.cuh:2316-2333)."""
+    assert k.dtype == torch.float16 and v.dtype == torch.float16 and k.numel() == v.numel()
+    n = k.numel() // 32
+    assert k.numel() == n * 32
+    assert k_out.numel() >= n * Q8_BLOCK_BYTES and v_out.numel() >= n * Q8_BLOCK_BYTES
+    check(lib().qkv_q8_append_kv(_dev_ptr(k, "k"), _dev_ptr(v, "v"), _dev_ptr(k_out, "k_out"),
+                                 _dev_ptr(v_out, "v_out"), n, _stream(stream)),
+          "qkv_q8_append_kv")
+
+
 def q8_dequant(blocks: torch.Tensor, out: torch.Tensor | None = None, stream=None) -> torch.Tensor:
     """attention.cuh:2614-2626."""
     n = blocks.numel() // Q8_BLOCK_BYTES
@@ -147,6 +160,22 @@ def decode_attn_tq3(q, k, v, out, workspace, *, num_q, num_kv, start_pos, sub_n,
         num_kv, head_dim, start_pos, sub_n, float(scale), sink_tok, window_tok,
         _opt_ptr(tree_mask), _dev_ptr(workspace, "workspace"),
         workspace.numel() * workspace.element_size(), _stream(stream)), "qkv_decode_attn_tq3")
+
+
+def decode_attn_q8_workspace(num_q, num_kv, sub_n, n_keys, device) -> torch.Tensor:
+    """Zero-filled workspace for decode_attn_q8."""
+    n = int(lib().qkv_decode_attn_q8_workspace_bytes(num_q, num_kv, sub_n, n_keys))
+    return torch.zeros(n, dtype=torch.uint8, device=device)
+
+
+def decode_attn_q8(q, k, v, out, workspace, *, num_q, num_kv, start_pos, sub_n, scale,
+                   head_dim=256, stream=None) -> None:
+    """Fast path over the Q8_0 cache: split-K decode with the merge inside the
+    same launch."""
+    check(lib().qkv_decode_attn_q8(
+        _dev_ptr(q, "q"), _dev_ptr(k, "k"), _dev_ptr(v, "v"), _dev_ptr(out, "out"), num_q,
+        num_kv, head_dim, start_pos, sub_n, float(scale), _dev_ptr(workspace, "workspace"),
+        workspace.numel() * workspace.element_size(), _stream(stream)), "qkv_decode_attn_q8")
 
 
 # ---------------------------------------------------------------------------

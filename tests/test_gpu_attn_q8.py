@@ -88,3 +88,64 @@ def test_q8_split_rejects_bad_shapes(dev):
     with pytest.raises(QKVError):   # sub_n > sub_n_max
         kvcache.attn_split_q8(q, kv, kv, pm, pm, po, num_q=16, num_kv=4, start_pos=9, sub_n=2,
                               sub_n_max=1, active_end_max=10, scale=1 / 16, k_splits=8)
+
+
+def _expected(q, kb, vb, n, num_q, sub_n):
+    kw = dict(num_q=num_q, num_kv=4, start_pos=n - sub_n, sub_n=sub_n, sub_n_max=sub_n,
+              active_end_max=n, scale=1 / 16, k_splits=8)
+    em, el, eo = O.attn_split(O.KV_Q8, q, kb, vb, hd=256, **kw)
+    return O.attn_split_merge(em, el, eo, num_q=num_q, num_kv=4, hd=256, sub_n=sub_n,
+                              sub_n_max=sub_n, k_splits=8).view(np.float16)
+
+
+@pytest.mark.parametrize("n,num_q,sub_n", [
+    (4097, 16, 1),     # config 2
+    (1, 16, 1), (127, 16, 1), (129, 16, 1), (16384, 16, 1), (20000, 16, 1),
+    (700, 24, 1),      # GQA 6
+    (530, 16, 16),     # 16 causal queries
+])
+def test_q8_fast_decode_vs_oracle(dev, n, num_q, sub_n):
+    """Single-launch Q8 decode (records merged in the kernel) against the
+    oracle's reference split + merge."""
+    from qengine_amd import kvcache
+    torch = _torch()
+    rng, kb, vb = _cache(700 + n + sub_n, n)
+    q = q_f16(rng, sub_n, num_q, 256)
+    ws = kvcache.decode_attn_q8_workspace(num_q, 4, sub_n, n, dev)
+    out = torch.zeros((sub_n, num_q, 256), dtype=torch.float16, device=dev)
+    kvcache.decode_attn_q8(_dev(q.view(np.uint16), dev), _dev(kb.view(np.uint8), dev),
+                           _dev(vb.view(np.uint8), dev), out, ws, num_q=num_q, num_kv=4,
+                           start_pos=n - sub_n, sub_n=sub_n, scale=1 / 16)
+    torch.cuda.synchronize()
+    assert rel_err(out.cpu().numpy(), _expected(q, kb, vb, n, num_q, sub_n)) < TOL
+
+
+def test_q8_fast_decode_workspace_reuse(dev):
+    """One workspace across calls of different lengths and query counts."""
+    from qengine_amd import kvcache
+    torch = _torch()
+    ws = kvcache.decode_attn_q8_workspace(16, 4, 4, 8192, dev)
+    for i, (n, sub_n) in enumerate([(8192, 1), (4097, 1), (1000, 4), (8192, 1), (300, 4)]):
+        rng, kb, vb = _cache(800 + i, n)
+        q = q_f16(rng, sub_n, 16, 256)
+        out = torch.zeros((sub_n, 16, 256), dtype=torch.float16, device=dev)
+        kvcache.decode_attn_q8(_dev(q.view(np.uint16), dev), _dev(kb.view(np.uint8), dev),
+                               _dev(vb.view(np.uint8), dev), out, ws, num_q=16, num_kv=4,
+                               start_pos=n - sub_n, sub_n=sub_n, scale=1 / 16)
+        torch.cuda.synchronize()
+        assert rel_err(out.cpu().numpy(), _expected(q, kb, vb, n, 16, sub_n)) < TOL, (n, sub_n)
+
+
+def test_q8_append_kv_matches_two_appends(dev):
+    from qengine_amd import kvcache
+    torch = _torch()
+    g = torch.Generator(device=dev).manual_seed(11)
+    k = torch.randn(3000 * 32, generator=g, device=dev).half()
+    v = torch.randn(3000 * 32, generator=g, device=dev).half()
+    a1, a2 = kvcache.q8_blocks(3000, dev), kvcache.q8_blocks(3000, dev)
+    b1, b2 = kvcache.q8_blocks(3000, dev), kvcache.q8_blocks(3000, dev)
+    kvcache.q8_append_kv(k, v, a1, a2)
+    kvcache.q8_append(k, b1)
+    kvcache.q8_append(v, b2)
+    torch.cuda.synchronize()
+    assert torch.equal(a1, b1) and torch.equal(a2, b2)
