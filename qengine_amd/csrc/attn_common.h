@@ -9,13 +9,13 @@ namespace qkv {
 constexpr float kLn2 = 0.69314718055994531f;
 constexpr float kLog2e = 1.44269504088896341f;
 
-// Fast-path workspace header: the launch epoch (records of the current call
-// carry tag epoch + 1) and, one 128-byte line further, the count of merger
-// workgroups that finished (the last one advances the epoch and resets it).
-constexpr int kWsEpoch = 0;          // ints
-constexpr int kWsFinished = 32;      // ints
+// Fast-path workspace: kWsHeaderBytes reserved at its start, then the record
+// scalars {m, l, tag of 128-block unit 0, tag of unit 1} (kRecMlBytes each)
+// and the record rows.  A tag is kTagValid while its record is waiting for
+// that unit's merger and 0 otherwise (the state of a zero-filled workspace).
 constexpr int kWsHeaderBytes = 256;
-constexpr int kRecMlBytes = 16;      // {m, l, tag, 0} per record
+constexpr int kRecMlBytes = 16;
+constexpr uint32_t kTagValid = 1u;
 
 struct AttnArgs {
   const uint16_t* q;        // [sub_n][num_q][256] fp16
@@ -46,9 +46,9 @@ struct AttnArgs {
   float* part_l;
   float* part_o;
   // fast-path workspace
-  float* ws_ml;             // [num_q][sub_n][n_slots] x {m (log2 units), l, tag, 0}
+  float* ws_ml;             // [num_q][sub_n][n_slots] x {m (log2 units), l, tag0, tag1}
   float* ws_o;              // [num_q][sub_n][n_slots][256] rotated coordinates
-  int* ws_header;           // epoch, finished-merger count (kWsHeaderBytes)
+  int* ws_header;           // reserved (kWsHeaderBytes)
   uint32_t ws_ml_bytes, ws_o_bytes;
 };
 

@@ -8,12 +8,16 @@
 // not coherent with each other) with buffer accesses carrying the sc0|sc1
 // cache policy: stores write through to the device coherence point and loads
 // read from it.  A writer stores a record's data, waits for those stores to
-// complete (s_waitcnt vmcnt(0)) and only then stores the record's tag; a
-// merger loads a record's data only after it has read the tag.  No workgroup
-// pays an L2 write-back or invalidate (what agent-scope fences cost on this
-// GPU), and no arrival counter is contended.  Only mergers wait, and they are
-// dispatched after every other workgroup, so progress does not depend on
-// workgroup co-residency.
+// complete (s_waitcnt vmcnt(0)) and only then stores the record's two tags
+// (one per 128-block unit); a merger loads a record's data only after it has
+// read its unit's tag.  Once a merger has seen every tag of its unit it clears
+// them (the other unit of the same records has tag words of its own), so that
+// after a launch every tag is clear again: the state the next launch, ordered
+// after this one on the stream, starts from, and the state of a zero-filled
+// workspace.  No counter, atomic or epoch is involved, and no workgroup pays an
+// L2 write-back or invalidate (what agent-scope fences cost on this GPU).
+// Only mergers wait, and they are dispatched after every other workgroup, so
+// progress does not depend on workgroup co-residency.
 #pragma once
 #include "attn_common.h"
 #include "qkv_device.h"
@@ -47,8 +51,9 @@ struct MergeLayout {
 // Merge all chunk records (n_chunks <= 128) of one unit (q head qh, query t,
 // 128-block blk) and write its fp16 output  o = sum w_c o_c / sum w_c l_c,
 // rotated back (o = rs*D*H*o per 128-block) when ROTATE.
-// 1. Threads 0..n-1 poll one record each ({m, l, tag} in one 16-byte load)
-//    until every tag is current; m and l go to LDS (mls, 128 entries).
+// 1. Threads 0..n-1 poll one record each ({m, l, tags} in one 16-byte load)
+//    until every tag of the unit is set; m and l go to LDS (mls, 128
+//    entries); then each clears its record's tag of this unit.
 // 2. Thread (record slice sl = tid/32, dim quad dq = tid%32) loads the rows
 //    of records sl, sl+slices, ... in one round and merges them through the
 //    LDS reduction area red.
@@ -56,8 +61,7 @@ struct MergeLayout {
 // the poll limit.
 template <int THREADS, bool ROTATE>
 __device__ bool merge_unit(float* red, f2_t* mls, const AttnArgs& p, __amdgpu_buffer_rsrc_t rml,
-                           __amdgpu_buffer_rsrc_t ro, int qh, int t, int blk, uint32_t tag,
-                           uint16_t* out) {
+                           __amdgpu_buffer_rsrc_t ro, int qh, int t, int blk, uint16_t* out) {
   using ML = MergeLayout<THREADS>;
   constexpr int kSlices = ML::kSlices, kRecPerThread = ML::kRecPerThread;
   constexpr int kRedM = ML::kRedM, kRedL = ML::kRedL, kRedSum = ML::kRedSum;
@@ -72,7 +76,7 @@ __device__ bool merge_unit(float* red, f2_t* mls, const AttnArgs& p, __amdgpu_bu
     if (!seen) {
       const f4_t r = __builtin_amdgcn_raw_buffer_load_b128(
           rml, (uint32_t)((base + tid) * kRecMlBytes), 0, kCoherent);
-      if (__float_as_uint(r[2]) == tag) {
+      if (__float_as_uint(blk ? r[3] : r[2]) == kTagValid) {
         seen = true;
         mls[tid] = f2_t{r[0], r[1]};
       }
@@ -84,6 +88,9 @@ __device__ bool merge_unit(float* red, f2_t* mls, const AttnArgs& p, __amdgpu_bu
     __builtin_amdgcn_s_sleep(1);
   }
   if (!complete) return false;
+  if (tid < n)   // this unit has seen its records: clear their tags for the next launch
+    __builtin_amdgcn_raw_buffer_store_b32(0u, rml, (uint32_t)((base + tid) * kRecMlBytes + 8 + 4 * blk), 0,
+                                          kCoherent);
   f4_t v[kRecPerThread];
 #pragma unroll
   for (int i = 0; i < kRecPerThread; i++) {
@@ -166,12 +173,11 @@ __device__ bool merge_unit(float* red, f2_t* mls, const AttnArgs& p, __amdgpu_bu
 // Store this workgroup's merged rows as records: row r = qi * gqa + hh (q head
 // h*gqa + hh of query t0 + qi) with data mo[r][256], maxima Mv[r] (log2
 // units) and sums Lv[r]; data first, then (once every thread's data stores
-// are complete) the tags.
+// are complete) the tags of both 128-block units.
 template <int THREADS>
 __device__ void store_records(const float* mo, const float* Mv, const float* Lv,
                               const AttnArgs& p, __amdgpu_buffer_rsrc_t rml,
-                              __amdgpu_buffer_rsrc_t ro, int h, int t0, int rows, int chunk,
-                              uint32_t tag) {
+                              __amdgpu_buffer_rsrc_t ro, int h, int t0, int rows, int chunk) {
   constexpr int kHD = 256;
   const int gqa = p.num_q / p.num_kv;
   for (int idx = threadIdx.x; idx < rows * 64; idx += THREADS) {
@@ -187,33 +193,24 @@ __device__ void store_records(const float* mo, const float* Mv, const float* Lv,
   __syncthreads();
   if ((int)threadIdx.x < rows) {
     const int r = threadIdx.x;
-    __builtin_amdgcn_raw_buffer_store_b32(
-        tag, rml, (uint32_t)(rec_index(p, h * gqa + r % gqa, t0 + r / gqa, chunk) * kRecMlBytes + 8),
-        0, kCoherent);
+    __builtin_amdgcn_raw_buffer_store_b64(
+        u2_t{kTagValid, kTagValid}, rml,
+        (uint32_t)(rec_index(p, h * gqa + r % gqa, t0 + r / gqa, chunk) * kRecMlBytes + 8), 0, kCoherent);
   }
 }
 
 // The designated mergers: the last min(units, grid) workgroups merge the
-// (q head, query, block) units; the last merger to finish advances the
-// workspace epoch (every workgroup of this launch has read it by then) and
-// resets the count.
+// (q head, query, block) units.
 template <int THREADS, bool ROTATE>
 __device__ void merge_phase(float* red, f2_t* mls, const AttnArgs& p, __amdgpu_buffer_rsrc_t rml,
-                            __amdgpu_buffer_rsrc_t ro, uint32_t tag, uint16_t* out) {
+                            __amdgpu_buffer_rsrc_t ro, uint16_t* out) {
   const int n_units = p.num_q * p.sub_n * 2;
   const int n_mergers = min(n_units, (int)gridDim.x);
   const int mid = (int)blockIdx.x - ((int)gridDim.x - n_mergers);
   if (mid < 0) return;
   for (int u = mid; u < n_units; u += n_mergers) {
     const int blk = u & 1, qh = (u >> 1) % p.num_q, t = (u >> 1) / p.num_q;
-    if (!merge_unit<THREADS, ROTATE>(red, mls, p, rml, ro, qh, t, blk, tag, out)) break;
-  }
-  if (threadIdx.x == 0) {
-    const int done = atomicAdd(&p.ws_header[kWsFinished], 1);
-    if (done == n_mergers - 1) {
-      __hip_atomic_store(&p.ws_header[kWsFinished], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      __hip_atomic_store(&p.ws_header[kWsEpoch], (int)tag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
+    if (!merge_unit<THREADS, ROTATE>(red, mls, p, rml, ro, qh, t, blk, out)) break;
   }
 }
 

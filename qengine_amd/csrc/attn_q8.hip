@@ -57,6 +57,7 @@ constexpr int kLdsTotal = kLdsMergeEnd > kLdsTotalTile ? kLdsMergeEnd : kLdsTota
 constexpr int kMlW0 = 0, kMlLw0 = 8 * kWaves;   // merge scalars: m[w][8], l[w][8], M[8], L[8]
 constexpr int kMlM = 16 * kWaves, kMlL = 16 * kWaves + 8;
 static_assert(kMlL + 8 <= 256, "merge scalars must fit the ML area");
+static_assert(kMlL + 8 <= 256, "merge scalars must fit the ML area");
 static_assert(kLdsMergeO + MergeLayout<kThreads>::kRedFloats * 4 <= kLdsMergeML,
               "merger reduction must fit the merge area");
 
@@ -158,11 +159,6 @@ __global__ __launch_bounds__(kThreads, 2) void q8_attn_kernel(AttnArgs p, uint16
     lo = split * p.chunk_keys;
     hi = has_work ? min(lo + p.chunk_keys, active_end) : lo;
   }
-  // launch epoch of the fast-path workspace (records of this call carry epoch + 1)
-  const uint32_t epoch =
-      MODE == 0 ? (uint32_t)__hip_atomic_load(&p.ws_header[kWsEpoch], __ATOMIC_RELAXED,
-                                              __HIP_MEMORY_SCOPE_AGENT)
-                : 0u;
 
   const __amdgpu_buffer_rsrc_t rk =
       __builtin_amdgcn_make_buffer_rsrc(const_cast<uint32_t*>(p.k), 0, p.kv_bytes, kBufferRsrcWord3);
@@ -352,11 +348,10 @@ __global__ __launch_bounds__(kThreads, 2) void q8_attn_kernel(AttnArgs p, uint16
       __builtin_amdgcn_make_buffer_rsrc(p.ws_ml, 0, p.ws_ml_bytes, kBufferRsrcWord3);
   const __amdgpu_buffer_rsrc_t ro =
       __builtin_amdgcn_make_buffer_rsrc(p.ws_o, 0, p.ws_o_bytes, kBufferRsrcWord3);
-  const uint32_t tag = epoch + 1u;
   if (has_work)
-    store_records<kThreads>(mo, ml + kMlM, ml + kMlL, p, rml, ro, h, t_idx, rows, split, tag);
+    store_records<kThreads>(mo, ml + kMlM, ml + kMlL, p, rml, ro, h, t_idx, rows, split);
   merge_phase<kThreads, false>(reinterpret_cast<float*>(lds + kLdsMergeO),
-                               reinterpret_cast<f2_t*>(lds + kLdsMergeML), p, rml, ro, tag, out);
+                               reinterpret_cast<f2_t*>(lds + kLdsMergeML), p, rml, ro, out);
 }
 
 }  // namespace

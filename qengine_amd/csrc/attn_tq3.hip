@@ -31,6 +31,8 @@
 // stores fp16.  Only mergers wait, so progress does not depend on workgroup
 // co-residency.  Split API: one workgroup per reference split, written in the
 // reference partial layout.
+#include <type_traits>
+
 #include "qkv_device.h"
 #include "attn_common.h"
 #include "attn_fastmerge.h"
@@ -65,7 +67,7 @@ constexpr int kStageBytes = (36 * kKeyPitch + 16) * 4;   // 9856
 constexpr int kLdsLut = 0;
 constexpr int kLdsLutBytes = 256 * 64 * 4;
 constexpr int kLdsStage = kLdsLut + kLdsLutBytes;            // per wave, kStageBytes
-constexpr int kLdsQ = kLdsStage + kWaves * kStageBytes;      // rotated query, [16][2][4][4][8] fp16
+constexpr int kLdsQ = kLdsStage + kWaves * kStageBytes;      // rotated query, 512 x 16 B (q_unit)
 constexpr int kLdsTileEnd = kLdsQ + 16 * 256 * 2;
 // After the tile loop the table and the staging areas are free: the merge
 // area starts at 0.
@@ -75,9 +77,17 @@ constexpr int kLdsMergeEnd = kLdsMergeML + 512 * 4;
 constexpr int kLdsTotal = kLdsTileEnd;
 static_assert(kLdsMergeEnd <= kLdsQ, "merge area must not reach the query scratch");
 
-// merge-area float offsets (ML): m[w][8], l[w][8], M[8], L[8]
+// merge-area float offsets (ML): m[w][16], l[w][16], M[16], L[16]
 constexpr int kMlW0 = 0, kMlLw0 = 16 * kWaves, kMlM = 32 * kWaves, kMlL = 32 * kWaves + 16;
 static_assert(kMlL + 16 <= 512, "merge scalars must fit the ML area");
+
+// 16-byte unit of the rotated-query scratch holding elements 8(4o+u)..+7 of
+// 128-block j of column c, s = 4j + u.  The column is swizzled with (u, o) so
+// that the 16 lanes of one WHT writing (fixed c, j) and the 16 lanes of one
+// MFMA row reading (fixed s, o) each touch 16 distinct 16-byte bank groups.
+__device__ __forceinline__ int q_unit(int c, int s, int o) {
+  return (s * 4 + o) * 16 + (c ^ (4 * (s & 3) + o));
+}
 
 __device__ __forceinline__ uint32_t lut_read(const uint8_t* lds, uint32_t addr) {
   return *reinterpret_cast<const uint32_t*>(lds + kLdsLut + addr);
@@ -126,31 +136,73 @@ __device__ __forceinline__ void score_group(const uint8_t* lds, uint32_t (&ac)[4
   }
 }
 
-// Values for one (32-key chunk, 128-block): centroid pair PP of the lane's
-// dim group gives tiles t0+2PP (low dim) and t0+2PP+1 (high dim).
-template <int PP>
-__device__ __forceinline__ void value_pipe(const uint8_t* lds, uint32_t (&ac)[4], const uint32_t (&x)[8],
-                                           const h8_t& a, f4_t (&acc)[16], int t0) {
-  if constexpr (PP < 4) {
-    uint32_t cp[8];
+// One value pass: a (32-key chunk c2, 128-block j) pair.  x[i]: code group
+// `col` (8 dims) of key 32*c2 + 4*row + i (i < 4) or 32*c2 + 16 + 4*row + i - 4;
+// a: A operand (p * value norm of those keys, head `col`).
+struct ValuePass {
+  uint32_t x[8];
+  h8_t a;
+};
+
+// Codes and A operand of pass c = 2*c2 + j from the tile's staging area.
+__device__ __forceinline__ void value_pass_load(const float* st, const uint32_t* stu, int c, int row,
+                                                int col, const float (&s)[4][4], ValuePass& vp) {
+  const int c2 = c >> 1, j = c & 1;
+  const f4_t va = *reinterpret_cast<const f4_t*>(st + kStVn + j * kKeyPitch + 32 * c2 + 4 * row);
+  const f4_t vb = *reinterpret_cast<const f4_t*>(st + kStVn + j * kKeyPitch + 32 * c2 + 16 + 4 * row);
+  const u4_t xa = *reinterpret_cast<const u4_t*>(stu + kStCodes + (16 * j + col) * kKeyPitch + 32 * c2 + 4 * row);
+  const u4_t xb =
+      *reinterpret_cast<const u4_t*>(stu + kStCodes + (16 * j + col) * kKeyPitch + 32 * c2 + 16 + 4 * row);
 #pragma unroll
-    for (int i = 0; i < 8; i++) {
-      const uint32_t xi = x[i];
-      ac[i & 3] = sdwa_index<6 * PP>(ac[i & 3], xi);
-      cp[i] = lut_read(lds, ac[i & 3]);
-    }
+  for (int r = 0; r < 4; r++) {
+    vp.a[r] = (_Float16)(s[2 * c2][r] * va[r]);
+    vp.a[4 + r] = (_Float16)(s[2 * c2 + 1][r] * vb[r]);
+    vp.x[r] = xa[r];
+    vp.x[4 + r] = xb[r];
+  }
+}
+
+// Table reads of centroid pair PP (dims 2PP, 2PP+1 of the group) of the 8 keys.
+template <int PP>
+__device__ __forceinline__ void value_pairs(const uint8_t* lds, uint32_t (&ac)[4], const uint32_t (&x)[8],
+                                            uint32_t (&cp)[8]) {
+#pragma unroll
+  for (int i = 0; i < 8; i++) {
+    ac[i & 3] = sdwa_index<6 * PP>(ac[i & 3], x[i]);
+    cp[i] = lut_read(lds, ac[i & 3]);
+  }
+}
+
+// Step K of the value phase (pass c = K / 4, centroid pair PP = K % 4): tiles
+// 8j + 2PP (low dim) and 8j + 2PP + 1 (high dim).  Software-pipelined two
+// steps deep: the table reads of step K+2 are issued before the perms and
+// MFMAs of step K (cp: step K's pairs, cq: step K+1's), and the codes and A
+// operand of pass c+1 are read during the first step of pass c.
+// FIRST: the workgroup's first tile, whose passes 0 and 1 write every
+// accumulator tile for the first time (zero C operand).
+template <int K, bool FIRST>
+__device__ __forceinline__ void value_steps(const uint8_t* lds, uint32_t (&ac)[4], ValuePass (&vp)[2],
+                                            const uint32_t (&cp)[8], const uint32_t (&cq)[8],
+                                            f4_t (&acc)[16], const float* st, const uint32_t* stu, int row,
+                                            int col, const float (&s)[4][4]) {
+  if constexpr (K < 16) {
+    constexpr int c = K >> 2, PP = K & 3;
+    if constexpr (PP == 0 && c < 3) value_pass_load(st, stu, c + 1, row, col, s, vp[(c + 1) & 1]);
+    uint32_t cn[8];
+    if constexpr (K + 2 < 16) value_pairs<(K + 2) & 3>(lds, ac, vp[((K + 2) >> 2) & 1].x, cn);
 #pragma unroll
     for (int e = 0; e < 2; e++) {
       u4_t bv;
 #pragma unroll
       for (int k2 = 0; k2 < 4; k2++)
         bv[k2] = __builtin_amdgcn_perm(cp[2 * k2 + 1], cp[2 * k2], e ? 0x07060302u : 0x05040100u);
-      const int tile = t0 + 2 * PP + e;
-      acc[tile] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, __builtin_bit_cast(h8_t, bv),
-                                                         acc[tile], 0, 0, 0);
+      constexpr int t0 = 8 * (c & 1) + 2 * PP;
+      const f4_t cin = (FIRST && c < 2) ? f4_t{0.f, 0.f, 0.f, 0.f} : acc[t0 + e];
+      acc[t0 + e] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vp[c & 1].a, __builtin_bit_cast(h8_t, bv),
+                                                           cin, 0, 0, 0);
     }
     __builtin_amdgcn_sched_barrier(0);
-    value_pipe<PP + 1>(lds, ac, x, a, acc, t0);
+    if constexpr (K < 15) value_steps<K + 1, FIRST>(lds, ac, vp, cq, cn, acc, st, stu, row, col, s);
   }
 }
 
@@ -314,7 +366,7 @@ __global__ __launch_bounds__(kThreads, 1) void tq3_attn_kernel(AttnArgs p, uint1
   // static LDS: table and tile offsets fold into the instructions' offset field
   __shared__ __attribute__((aligned(16))) uint8_t lds[kLdsTotal];
   const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int gqa = p.num_q / p.num_kv;
 
   // ---- work id (XCD-aware: the num_kv workgroups of one (query group, chunk)
@@ -363,25 +415,45 @@ __global__ __launch_bounds__(kThreads, 1) void tq3_attn_kernel(AttnArgs p, uint1
     hi_col = min((chunk + 1) * tps * 32, active_end);
     hi_first = min((chunk + 1) * tps * 32, active_first);
   }
+  lo = __builtin_amdgcn_readfirstlane(lo);
+  hi = __builtin_amdgcn_readfirstlane(hi);
+  hi_first = __builtin_amdgcn_readfirstlane(hi_first);
   // A dead column has a zero query: its scores are 0 and its accumulator rows
   // are never stored, so it needs no mask of its own.
   const KeyRule rule(p.start_pos, t_col, p.sink_tok, p.window_tok, p.tree_mask);
 
-  // ---- first tile's loads go out before the setup work ----------------------
+  // ---- setup: query load, centroid-pair table, rotated query --------------
+  // The query is loaded and rotated before any tile load is issued: a query
+  // load issued after the tile loads of the whole chip would wait behind
+  // them in the memory queues.
   const __amdgpu_buffer_rsrc_t rk =
       __builtin_amdgcn_make_buffer_rsrc(const_cast<uint32_t*>(p.k), 0, p.kv_bytes, kBufferRsrcWord3);
   const __amdgpu_buffer_rsrc_t rv =
       __builtin_amdgcn_make_buffer_rsrc(const_cast<uint32_t*>(p.v), 0, p.kv_bytes, kBufferRsrcWord3);
-
-  // ---- setup: centroid-pair table; rotated query ---------------------------
-  // entry e = (centroid[e & 7], centroid[e >> 3]) as fp16, from immediates
-  // (wave-uniform values); wave w writes every lane's copy of entries 8w..8w+7
-  // wave w writes every lane's copy of entries 32w .. 32w+31 (entry E holds
-  // the pair of E & 63: low code E & 7, high code (E >> 3) & 7)
+  // 32 WHTs of 128 (16 columns x 2 blocks), 16 lanes each
+  const int q_wht = threadIdx.x >> 4;
+  const int q_part = threadIdx.x & 15;
+  const int q_col = q_wht >> 1, q_blk = q_wht & 1;   // column, 128-block
+  u4_t q_raw;
+  {
+    // unconditional (rows past the buffer's extent read as zero): a load
+    // under a branch makes the compiler wait for every load at the join
+    const uint32_t q_extent = (uint32_t)(p.sub_n * p.num_q * kHD * 2);
+    const __amdgpu_buffer_rsrc_t rq =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(p.q), 0, q_extent, kBufferRsrcWord3);
+    const uint32_t qoff =
+        q_col < rows_used ? (uint32_t)((((t0 + q_col / gqa) * p.num_q + h * gqa + q_col % gqa) * kHD +
+                                        q_blk * 128 + q_part * 8) * 2)
+                          : q_extent;
+    q_raw = __builtin_amdgcn_raw_buffer_load_b128(rq, qoff, 0, 0);
+  }
+  // centroid-pair table: entry e = (centroid[e & 7], centroid[(e >> 3) & 7])
+  // as fp16, from immediates (wave-uniform values); wave w writes every lane's
+  // copy of entries 32w .. 32w+31
   static_assert(kWaves == 8, "8 waves x 32 entries");
   const uint32_t lane4 = 4u * (uint32_t)lane;
   {
-    const uint32_t w = (uint32_t)__builtin_amdgcn_readfirstlane(wave);
+    const uint32_t w = (uint32_t)wave;
 #pragma unroll
     for (int hk = 0; hk < 4; hk++) {
       const uint32_t hi = f2h(centroid_imm((4u * w + hk) & 7u)) << 16;
@@ -392,41 +464,22 @@ __global__ __launch_bounds__(kThreads, 1) void tq3_attn_kernel(AttnArgs p, uint1
     }
   }
   uint32_t ac[4] = {lane4, lane4, lane4, lane4};   // table address chains
-  TileRegs tr;
   {
-    // 32 WHTs of 128 (16 columns x 2 blocks), 16 lanes each; fp16 result in LDS
-    // scratch laid out [head][block][group u][octet o][8] so each lane's A
-    // operand slice is one 16-byte read.
+    // rotated query: fp16 in LDS scratch (q_unit), so that each lane's A
+    // operand slice is one 16-byte read
     uint16_t* qs = reinterpret_cast<uint16_t*>(lds + kLdsQ);
-    const int wht = threadIdx.x >> 4;
-    const int part = threadIdx.x & 15;
-    const int cq = wht >> 1, blk = wht & 1;   // column, 128-block
-    // The query is loaded and rotated before any tile load is issued: a
-    // query load issued after the tile loads of the whole chip would wait
-    // behind them in the memory queues.  The load is unconditional (rows
-    // past the buffer's extent read as zero): a load under a branch makes the
-    // compiler wait for every load at the join.
-    const uint32_t q_extent = (uint32_t)(p.sub_n * p.num_q * kHD * 2);
-    const __amdgpu_buffer_rsrc_t rq =
-        __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(p.q), 0, q_extent, kBufferRsrcWord3);
-    const uint32_t qoff =
-        cq < rows_used ? (uint32_t)((((t0 + cq / gqa) * p.num_q + h * gqa + cq % gqa) * kHD +
-                                     blk * 128 + part * 8) * 2)
-                       : q_extent;
-    const u4_t raw = __builtin_amdgcn_raw_buffer_load_b128(rq, qoff, 0, 0);
-    const int o = part >> 2, u = part & 3;   // elements part*8..+7 = code group 4*o + u
+    const int o = q_part >> 2, u = q_part & 3;   // elements part*8..+7 = code group 4*o + u
     if (2 * wave >= rows_used) {
       // a wave whose two columns are both dead writes zeros
-      *reinterpret_cast<uint4*>(qs + (((cq * 2 + blk) * 4 + u) * 4 + o) * 8) = make_uint4(0, 0, 0, 0);
+      *reinterpret_cast<uint4*>(qs + q_unit(q_col, 4 * q_blk + u, o) * 8) = make_uint4(0, 0, 0, 0);
     } else {
       float x[8];
-      const uint32_t wv[4] = {raw[0], raw[1], raw[2], raw[3]};
 #pragma unroll
       for (int i = 0; i < 4; i++) {
-        x[2 * i] = h2f(wv[i] & 0xffffu);
-        x[2 * i + 1] = h2f(wv[i] >> 16);
+        x[2 * i] = h2f(q_raw[i] & 0xffffu);
+        x[2 * i + 1] = h2f(q_raw[i] >> 16);
       }
-      const uint32_t sbits = sign_word_sel(part >> 2) >> (8 * (part & 3));   // elements part*8..+7
+      const uint32_t sbits = sign_word_sel(q_part >> 2) >> (8 * (q_part & 3));   // elements part*8..+7
 #pragma unroll
       for (int i = 0; i < 8; i++) {
         const bool pos = (sbits >> i) & 1u;
@@ -438,46 +491,40 @@ __global__ __launch_bounds__(kThreads, 1) void tq3_attn_kernel(AttnArgs p, uint1
       uint32_t pk[4];
 #pragma unroll
       for (int i = 0; i < 4; i++) pk[i] = f2h(x[2 * i] * rs) | (f2h(x[2 * i + 1] * rs) << 16);
-      *reinterpret_cast<uint4*>(qs + (((cq * 2 + blk) * 4 + u) * 4 + o) * 8) =
+      *reinterpret_cast<uint4*>(qs + q_unit(q_col, 4 * q_blk + u, o) * 8) =
           make_uint4(pk[0], pk[1], pk[2], pk[3]);
     }
   }
   __syncthreads();
-  load_tile(rk, rv, tile_row(p, t0, lo + wave * kTile, hi), p.num_kv, h, lane, row, col, tr);
-  // launch epoch of the fast-path workspace (records of this call carry
-  // epoch + 1); requested after the first tile so that it is in flight
-  // during the tile's compute and needed only when the records are stored
-  __builtin_amdgcn_sched_barrier(0);
-  const uint32_t epoch =
-      MODE == 0 ? (uint32_t)__hip_atomic_load(&p.ws_header[kWsEpoch], __ATOMIC_RELAXED,
-                                              __HIP_MEMORY_SCOPE_AGENT)
-                : 0u;
-  __builtin_amdgcn_sched_barrier(0);
+  // ---- first tile: the first wave of each SIMD (waves 0..3) issues its loads
+  // before the second (waves 4..7), so that across the chip the first waves'
+  // tiles arrive in the first half of the stream and are computed while the
+  // second waves' tiles are still in flight.
+  TileRegs tr;
+  if (wave < 4) load_tile(rk, rv, tile_row(p, t0, lo + wave * kTile, hi), p.num_kv, h, lane, row, col, tr);
+  __syncthreads();
+  if (wave >= 4) load_tile(rk, rv, tile_row(p, t0, lo + wave * kTile, hi), p.num_kv, h, lane, row, col, tr);
   // qa[s], slice s = 4j+u: column `col`, element i = dim 128j + 8(4*row+u) + i
   h8_t qa[8];
   {
     const uint16_t* qs = reinterpret_cast<const uint16_t*>(lds + kLdsQ);
 #pragma unroll
-    for (int s = 0; s < 8; s++) {
-      const int j = s >> 2, u = s & 3;
-      // dead columns were written as zeros
-      qa[s] = *reinterpret_cast<const h8_t*>(qs + (((col * 2 + j) * 4 + u) * 4 + row) * 8);
-    }
+    for (int s = 0; s < 8; s++)   // dead columns were written as zeros
+      qa[s] = *reinterpret_cast<const h8_t*>(qs + q_unit(col, s, row) * 8);
   }
 
   const float scale2 = p.scale_log2;
   float m2 = -INFINITY;   // running max of head `col` (base-2 units)
   float lsum = 0.0f;      // this lane's part of the running sum of head `col`
   f4_t acc[16];
-#pragma unroll
-  for (int t = 0; t < 16; t++) acc[t] = f4_t{0.f, 0.f, 0.f, 0.f};
 
   float* st = reinterpret_cast<float*>(lds + kLdsStage + wave * kStageBytes);
   uint32_t* stu = reinterpret_cast<uint32_t*>(st);
 
-  for (int ts = lo + wave * kTile; ts < hi; ts += kWaves * kTile) {
-    const bool first = ts == lo + wave * kTile;
-    if (!first) load_tile(rk, rv, tile_row(p, t0, ts, hi), p.num_kv, h, lane, row, col, tr);
+  // One 64-key tile.  The wave's first tile is a separate instance: its loads
+  // were issued with the setup, and its accumulators start at zero.
+  auto tile_body = [&](auto first_tag, int ts) {
+    constexpr bool first = decltype(first_tag)::value;
     auto& kq = tr.kq;
     auto& kn = tr.kn;
 
@@ -495,8 +542,8 @@ __global__ __launch_bounds__(kThreads, 1) void tq3_attn_kernel(AttnArgs p, uint1
     if (row == 0) {
 #pragma unroll
       for (int g = 0; g < 4; g++) {
-        st[kStKn + 16 * g + col] = kn[g][0];
-        st[kStKn + kKeyPitch + 16 * g + col] = kn[g][1];
+        st[kStKn + 16 * g + col] = kn[g][0] * scale2;   // key norms carry the softmax scale
+        st[kStKn + kKeyPitch + 16 * g + col] = kn[g][1] * scale2;
       }
     }
     {
@@ -533,7 +580,7 @@ __global__ __launch_bounds__(kThreads, 1) void tq3_attn_kernel(AttnArgs p, uint1
       const f4_t k0 = *reinterpret_cast<const f4_t*>(st + kStKn + 16 * g + 4 * row);
       const f4_t k1 = *reinterpret_cast<const f4_t*>(st + kStKn + kKeyPitch + 16 * g + 4 * row);
 #pragma unroll
-      for (int r = 0; r < 4; r++) s[g][r] = (k0[r] * sa[g][0][r] + k1[r] * sa[g][1][r]) * scale2;
+      for (int r = 0; r < 4; r++) s[g][r] = k0[r] * sa[g][0][r] + k1[r] * sa[g][1][r];
     }
     if (!dense) {
 #pragma unroll
@@ -566,7 +613,7 @@ __global__ __launch_bounds__(kThreads, 1) void tq3_attn_kernel(AttnArgs p, uint1
       }
     lsum = lsum * corr + ps;
     m2 = mn;
-    if (!first) {   // accumulators are still zero on the first tile
+    if constexpr (!first) {   // accumulators are still zero on the first tile
       // accumulator rows are heads 4*row + r: their factors come from lanes 4*row + r
       if (row == 0) st[kStCorr + col] = corr;
       __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
@@ -584,27 +631,30 @@ __global__ __launch_bounds__(kThreads, 1) void tq3_attn_kernel(AttnArgs p, uint1
     // 32*c2 + 16 + 4*row + (i - 4) (i >= 4), in both operands.  A = p * value
     // norm (head `col`, this lane's own probabilities), B = codes of 8 keys
     // in dim group `col`.
-#pragma unroll
-    for (int c2 = 0; c2 < 2; c2++) {
-#pragma unroll
-      for (int j = 0; j < 2; j++) {
-        const f4_t va = *reinterpret_cast<const f4_t*>(st + kStVn + j * kKeyPitch + 32 * c2 + 4 * row);
-        const f4_t vb = *reinterpret_cast<const f4_t*>(st + kStVn + j * kKeyPitch + 32 * c2 + 16 + 4 * row);
-        const u4_t xa = *reinterpret_cast<const u4_t*>(stu + kStCodes + (16 * j + col) * kKeyPitch + 32 * c2 + 4 * row);
-        const u4_t xb = *reinterpret_cast<const u4_t*>(stu + kStCodes + (16 * j + col) * kKeyPitch + 32 * c2 + 16 + 4 * row);
-        h8_t a;
-#pragma unroll
-        for (int r = 0; r < 4; r++) {
-          a[r] = (_Float16)(s[2 * c2][r] * va[r]);
-          a[4 + r] = (_Float16)(s[2 * c2 + 1][r] * vb[r]);
-        }
-        const uint32_t x[8] = {xa[0], xa[1], xa[2], xa[3], xb[0], xb[1], xb[2], xb[3]};
-        value_pipe<0>(lds, ac, x, a, acc, 8 * j);
-      }
+    {
+      ValuePass vp[2];
+      uint32_t cp[8], cq[8];
+      value_pass_load(st, stu, 0, row, col, s, vp[0]);
+      value_pairs<0>(lds, ac, vp[0].x, cp);
+      value_pairs<1>(lds, ac, vp[0].x, cq);
+      value_steps<0, first>(lds, ac, vp, cp, cq, acc, st, stu, row, col, s);
     }
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  };
+  // lo and hi are wave-uniform (a paged workgroup serves one query): the tile
+  // loop is a scalar loop
+  const int ts0 = lo + wave * kTile;
+  if (ts0 < hi) {
+    tile_body(std::true_type{}, ts0);
+    for (int ts = ts0 + kWaves * kTile; ts < hi; ts += kWaves * kTile) {
+      load_tile(rk, rv, tile_row(p, t0, ts, hi), p.num_kv, h, lane, row, col, tr);
+      tile_body(std::false_type{}, ts);
+    }
+  } else {
+#pragma unroll
+    for (int t = 0; t < 16; t++) acc[t] = f4_t{0.f, 0.f, 0.f, 0.f};
   }
   lsum = xrow_sum(lsum);
 
@@ -613,12 +663,15 @@ __global__ __launch_bounds__(kThreads, 1) void tq3_attn_kernel(AttnArgs p, uint1
   float* mo = reinterpret_cast<float*>(lds + kLdsMergeO);    // [wave][8][256]
   float* ml = reinterpret_cast<float*>(lds + kLdsMergeML);
   if (4 * row < rows_used) {   // accumulator rows 4*row + r; rows >= rows_used are unused
-    // acc tile t: rows 4*row+r, dim 128*(t>>3) + 8*col + (t&7)
+    // acc tile t: rows 4*row+r, dim 128*(t>>3) + 8*col + (t&7): 16-byte stores
 #pragma unroll
-    for (int t = 0; t < 16; t++)
+    for (int r = 0; r < 4; r++)
 #pragma unroll
-      for (int r = 0; r < 4; r++)
-        mo[(wave * 16 + 4 * row + r) * kHD + 128 * (t >> 3) + 8 * col + (t & 7)] = acc[t][r];
+      for (int q4 = 0; q4 < 4; q4++) {
+        const int t = 4 * q4;   // tiles t..t+3: dims 128*(q4>>1) + 8*col + 4*(q4&1) + 0..3
+        *reinterpret_cast<f4_t*>(mo + (wave * 16 + 4 * row + r) * kHD + 128 * (q4 >> 1) + 8 * col +
+                                 4 * (q4 & 1)) = f4_t{acc[t][r], acc[t + 1][r], acc[t + 2][r], acc[t + 3][r]};
+      }
   }
   if (row == 0) {
     ml[kMlW0 + wave * 16 + col] = m2;
@@ -637,11 +690,12 @@ __global__ __launch_bounds__(kThreads, 1) void tq3_attn_kernel(AttnArgs p, uint1
       const float mw = ml[kMlW0 + w * 16 + r];
       const float wt = (mw == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(mw - M);
       L += wt * ml[kMlLw0 + w * 16 + r];
+      const f4_t ow = *reinterpret_cast<const f4_t*>(mo + (w * 16 + r) * kHD + d4);
 #pragma unroll
-      for (int i = 0; i < 4; i++) o[i] += wt * mo[(w * 16 + r) * kHD + d4 + i];
+      for (int i = 0; i < 4; i++) o[i] += wt * ow[i];
     }
-#pragma unroll
-    for (int i = 0; i < 4; i++) mo[r * kHD + d4 + i] = o[i];   // wave-0 slot, own elements
+    // wave-0 slot, own elements
+    *reinterpret_cast<f4_t*>(mo + r * kHD + d4) = f4_t{o[0], o[1], o[2], o[3]};
     if (d4 == 0) {
       ml[kMlM + r] = M;
       ml[kMlL + r] = L;
@@ -660,16 +714,15 @@ __global__ __launch_bounds__(kThreads, 1) void tq3_attn_kernel(AttnArgs p, uint1
       __builtin_amdgcn_make_buffer_rsrc(p.ws_ml, 0, p.ws_ml_bytes, kBufferRsrcWord3);
   const __amdgpu_buffer_rsrc_t ro =
       __builtin_amdgcn_make_buffer_rsrc(p.ws_o, 0, p.ws_o_bytes, kBufferRsrcWord3);
-  const uint32_t tag = epoch + 1u;
   if (has_work) {
     const float* mlv = reinterpret_cast<const float*>(lds + kLdsMergeML);
     store_records<kThreads>(reinterpret_cast<const float*>(lds + kLdsMergeO), mlv + kMlM,
-                            mlv + kMlL, p, rml, ro, h, t0, rows, chunk, tag);
+                            mlv + kMlL, p, rml, ro, h, t0, rows, chunk);
   }
   using ML = MergeLayout<kThreads>;
   static_assert(kLdsMergeO + ML::kRedFloats * 4 <= kLdsMergeML, "merge reduction must fit");
   merge_phase<kThreads, true>(reinterpret_cast<float*>(lds + kLdsMergeO),
-                              reinterpret_cast<f2_t*>(lds + kLdsMergeML), p, rml, ro, tag, out);
+                              reinterpret_cast<f2_t*>(lds + kLdsMergeML), p, rml, ro, out);
 }
 
 size_t tq3_attn_lds_bytes() { return kLdsTotal; }

@@ -172,8 +172,9 @@ def _fast_expected(q, kb, vb, n, num_q, sub_n):
 
 
 def test_fast_decode_workspace_reuse(dev):
-    """One workspace across calls of different lengths and query counts: each
-    call's records are told apart from earlier calls' by the launch epoch."""
+    """One workspace across calls of different lengths and query counts: every
+    merger clears the record tags it consumed, so no call can take an earlier
+    call's records for its own."""
     from qengine_amd import kvcache
     torch = _torch()
     ws = kvcache.decode_attn_tq3_workspace(16, 4, 4, 32768, dev)
@@ -187,6 +188,28 @@ def test_fast_decode_workspace_reuse(dev):
                                 start_pos=n - sub_n, sub_n=sub_n, scale=1 / 16)
         torch.cuda.synchronize()
         assert rel_err(out.cpu().numpy(), _fast_expected(q, kb, vb, n, 16, sub_n)) < TOL, (n, sub_n)
+
+
+def test_fast_decode_leaves_record_tags_clear(dev):
+    """After a call every record tag of the workspace is clear again (the state
+    of a zero-filled workspace), while the record scalars were written."""
+    from qengine_amd import kvcache
+    torch = _torch()
+    n, num_q = 32768, 16
+    ws = kvcache.decode_attn_tq3_workspace(num_q, 4, 1, n, dev)
+    for i in range(2):
+        rng, kb, vb = _cache(900 + i, n)
+        q = q_f16(rng, 1, num_q, 256)
+        out = torch.zeros((1, num_q, 256), dtype=torch.float16, device=dev)
+        kvcache.decode_attn_tq3(_dev(q.view(np.uint16), dev), _dev(kb.view(np.uint8), dev),
+                                _dev(vb.view(np.uint8), dev), out, ws, num_q=num_q, num_kv=4,
+                                start_pos=n - 1, sub_n=1, scale=1 / 16)
+        torch.cuda.synchronize()
+        assert rel_err(out.cpu().numpy(), _fast_expected(q, kb, vb, n, num_q, 1)) < TOL
+        # 512-key chunks at this length: 64 records per q head after a 256-byte header
+        ml = ws.cpu().numpy()[256:256 + num_q * 64 * 16].view(np.uint32).reshape(num_q * 64, 4)
+        assert not ml[:, 2:].any(), "record tags left set"
+        assert (ml[:, 1].view(np.float32) > 0).all(), "record sums missing"
 
 
 def test_fast_decode_output_may_alias_query(dev):
