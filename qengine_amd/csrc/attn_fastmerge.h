@@ -38,35 +38,37 @@ constexpr int kMergeSpinLimit = 1 << 22;
 
 // Merger thread layout for a THREADS-thread workgroup: slices of 32 threads
 // (one dim quad of a 128-block each), 128/slices records per thread
-// (n_chunks <= 128).  The reduction area holds [slices][128] sums, then
-// maxima, sums of l and the 128 merged dims.
+// (n_chunks <= 128).  The reduction area holds one 128-float partial per wave.
 template <int THREADS>
 struct MergeLayout {
   static constexpr int kSlices = THREADS / 32;
   static constexpr int kRecPerThread = 128 / kSlices;
-  static constexpr int kRedM = kSlices * 128, kRedL = kRedM + kSlices, kRedSum = kRedL + kSlices;
-  static constexpr int kRedFloats = kRedSum + 128;
+  static constexpr int kWaves = THREADS / 64;
+  static constexpr int kRedFloats = kWaves * 128;
 };
 
 // Merge all chunk records (n_chunks <= 128) of one unit (q head qh, query t,
 // 128-block blk) and write its fp16 output  o = sum w_c o_c / sum w_c l_c,
-// rotated back (o = rs*D*H*o per 128-block) when ROTATE.
+// w_c = 2^(m_c - M), rotated back (o = rs*D*H*o per 128-block) when ROTATE.
 // 1. Threads 0..n-1 poll one record each ({m, l, tags} in one 16-byte load)
 //    until every tag of the unit is set; m and l go to LDS (mls, 128
 //    entries); then each clears its record's tag of this unit.
 // 2. Thread (record slice sl = tid/32, dim quad dq = tid%32) loads the rows
-//    of records sl, sl+slices, ... in one round and merges them through the
-//    LDS reduction area red.
+//    of records sl, sl+slices, ... in one round.  Every wave reduces the
+//    record scalars to M and L itself (lane l: records l and l+64), weights
+//    its rows, and folds its two slices together (lanes l and l^32); the
+//    waves' partials meet once in LDS, where 16 threads sum them, normalise,
+//    rotate and store.
 // Returns false (and writes nothing) if the records did not all appear within
 // the poll limit.
 template <int THREADS, bool ROTATE>
 __device__ bool merge_unit(float* red, f2_t* mls, const AttnArgs& p, __amdgpu_buffer_rsrc_t rml,
                            __amdgpu_buffer_rsrc_t ro, int qh, int t, int blk, uint16_t* out) {
   using ML = MergeLayout<THREADS>;
-  constexpr int kSlices = ML::kSlices, kRecPerThread = ML::kRecPerThread;
-  constexpr int kRedM = ML::kRedM, kRedL = ML::kRedL, kRedSum = ML::kRedSum;
+  constexpr int kSlices = ML::kSlices, kRecPerThread = ML::kRecPerThread, kWaves = ML::kWaves;
   constexpr int kHD = 256;
   const int tid = threadIdx.x;
+  const int lane = tid & 63, wave = tid >> 6;
   const int sl = tid >> 5, dq = tid & 31;
   const int n = p.n_chunks;
   const long base = rec_index(p, qh, t, 0);
@@ -99,49 +101,49 @@ __device__ bool merge_unit(float* red, f2_t* mls, const AttnArgs& p, __amdgpu_bu
                        ro, (uint32_t)(((base + c) * kHD + blk * 128 + 4 * dq) * 4), 0, kCoherent)
                  : f4_t{0.f, 0.f, 0.f, 0.f};
   }
-  // common max over all records (empty chunks, l = 0, carry no weight)
-  float M = -INFINITY;
-#pragma unroll
-  for (int i = 0; i < kRecPerThread; i++) {
-    const int c = sl + kSlices * i;
-    if (c < n && mls[c][1] > 0.f) M = fmaxf(M, mls[c][0]);
-  }
-  if (dq == 0) red[kRedM + sl] = M;
-  __syncthreads();
-  M = red[kRedM];
-#pragma unroll
-  for (int k = 1; k < kSlices; k++) M = fmaxf(M, red[kRedM + k]);
+  // common max M and weight sum L over the records (empty chunks, l = 0,
+  // carry no weight), in every wave
+  const f2_t r0 = lane < n ? mls[lane] : f2_t{-INFINITY, 0.f};
+  const f2_t r1 = lane + 64 < n ? mls[lane + 64] : f2_t{-INFINITY, 0.f};
+  const bool a0 = r0[1] > 0.f, a1 = r1[1] > 0.f;
+  const float M = wave_max(fmaxf(a0 ? r0[0] : -INFINITY, a1 ? r1[0] : -INFINITY));
+  const float L = wave_sum((a0 ? __builtin_amdgcn_exp2f(r0[0] - M) * r0[1] : 0.f) +
+                           (a1 ? __builtin_amdgcn_exp2f(r1[0] - M) * r1[1] : 0.f));
   f4_t acc = {0.f, 0.f, 0.f, 0.f};
-  float L = 0.f;
 #pragma unroll
   for (int i = 0; i < kRecPerThread; i++) {
     const int c = sl + kSlices * i;
-    if (c < n && mls[c][1] > 0.f) {
-      const float w = __builtin_amdgcn_exp2f(mls[c][0] - M);
-      L += w * mls[c][1];
-      acc += w * v[i];
+    if (c < n) {
+      const f2_t r = mls[c];
+      if (r[1] > 0.f) acc += __builtin_amdgcn_exp2f(r[0] - M) * v[i];
     }
   }
-  *reinterpret_cast<f4_t*>(&red[sl * 128 + 4 * dq]) = acc;
-  if (dq == 0) red[kRedL + sl] = L;
-  __syncthreads();
-  // sum the slices: thread d < 128 owns dim d
-  if (tid < 128) {
-    float sum = 0.f;
+  // the wave's two slices: lanes l and l^32 hold the same dim quad
 #pragma unroll
-    for (int k = 0; k < kSlices; k++) sum += red[k * 128 + tid];
-    red[kRedSum + tid] = sum;
+  for (int e = 0; e < 4; e++) {
+    const auto s2 = __builtin_amdgcn_permlane32_swap(__float_as_uint(acc[e]), __float_as_uint(acc[e]),
+                                                     false, false);
+    acc[e] = __uint_as_float(s2[0]) + __uint_as_float(s2[1]);
   }
+  if (lane < 32) *reinterpret_cast<f4_t*>(&red[wave * 128 + 4 * dq]) = acc;
   __syncthreads();
-  // 16 lanes x 8 elements (threads 0..15): normalise, rotate back, store fp16
+  // 16 lanes x 8 elements (threads 0..15): sum the waves' partials, normalise,
+  // rotate back, store fp16
   if (tid < 16) {
-    float Lt = 0.f;
+    const float inv = L > 0.f ? 1.0f / L : 0.f;
+    float x[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int k = 0; k < kSlices; k++) Lt += red[kRedL + k];
-    const float inv = Lt > 0.f ? 1.0f / Lt : 0.f;
-    float x[8];
+    for (int w = 0; w < kWaves; w++) {
+      const f4_t lo = *reinterpret_cast<const f4_t*>(&red[w * 128 + tid * 8]);
+      const f4_t hi = *reinterpret_cast<const f4_t*>(&red[w * 128 + tid * 8 + 4]);
 #pragma unroll
-    for (int i = 0; i < 8; i++) x[i] = red[kRedSum + tid * 8 + i] * inv;
+      for (int i = 0; i < 4; i++) {
+        x[i] += lo[i];
+        x[4 + i] += hi[i];
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < 8; i++) x[i] *= inv;
     uint32_t pk[4];
     if constexpr (ROTATE) {
       wht8_inreg(x);
@@ -166,7 +168,7 @@ __device__ bool merge_unit(float* red, f2_t* mls, const AttnArgs& p, __amdgpu_bu
     *reinterpret_cast<uint4*>(out + ((long)t * p.num_q + qh) * kHD + blk * 128 + tid * 8) =
         make_uint4(pk[0], pk[1], pk[2], pk[3]);
   }
-  __syncthreads();
+  __syncthreads();   // red and mls are reused by the next unit
   return true;
 }
 
