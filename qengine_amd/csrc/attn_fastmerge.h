@@ -201,6 +201,33 @@ __device__ void store_records(const float* mo, const float* Mv, const float* Lv,
   }
 }
 
+// One 4-float piece of a record (row of q head qh, query t, chunk), written
+// straight from a merge: data at dims d4..d4+3 and, from the thread with
+// d4 == 0, the scalars.  publish_records then tags the workgroup's records.
+__device__ __forceinline__ void store_record_piece(const AttnArgs& p, __amdgpu_buffer_rsrc_t rml,
+                                                   __amdgpu_buffer_rsrc_t ro, int qh, int t, int chunk,
+                                                   int d4, f4_t o, float M, float L) {
+  const long rec = rec_index(p, qh, t, chunk);
+  __builtin_amdgcn_raw_buffer_store_b128(o, ro, (uint32_t)((rec * 256 + d4) * 4), 0, kCoherent);
+  if (d4 == 0)
+    __builtin_amdgcn_raw_buffer_store_b64(f2_t{M, L}, rml, (uint32_t)(rec * kRecMlBytes), 0, kCoherent);
+}
+
+// Tag this workgroup's records (rows 0..rows-1 as in store_records) once every
+// thread's data stores are complete; every thread of the workgroup calls it.
+__device__ __forceinline__ void publish_records(const AttnArgs& p, __amdgpu_buffer_rsrc_t rml, int h,
+                                                int t0, int rows, int chunk) {
+  const int gqa = p.num_q / p.num_kv;
+  __builtin_amdgcn_s_waitcnt(0);  // this thread's data stores are complete
+  __syncthreads();
+  if ((int)threadIdx.x < rows) {
+    const int r = threadIdx.x;
+    __builtin_amdgcn_raw_buffer_store_b64(
+        u2_t{kTagValid, kTagValid}, rml,
+        (uint32_t)(rec_index(p, h * gqa + r % gqa, t0 + r / gqa, chunk) * kRecMlBytes + 8), 0, kCoherent);
+  }
+}
+
 // The designated mergers: the last min(units, grid) workgroups merge the
 // (q head, query, block) units.
 template <int THREADS, bool ROTATE>

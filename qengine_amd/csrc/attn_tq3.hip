@@ -679,46 +679,44 @@ __global__ __launch_bounds__(kThreads, 1) void tq3_attn_kernel(AttnArgs p, uint1
   }
   __syncthreads();
   const int rows = rows_used;
+  // fast path: every merged piece goes straight to its record
+  const __amdgpu_buffer_rsrc_t rml =
+      __builtin_amdgcn_make_buffer_rsrc(p.ws_ml, 0, MODE == 0 ? p.ws_ml_bytes : 0u, kBufferRsrcWord3);
+  const __amdgpu_buffer_rsrc_t ro =
+      __builtin_amdgcn_make_buffer_rsrc(p.ws_o, 0, MODE == 0 ? p.ws_o_bytes : 0u, kBufferRsrcWord3);
   for (int idx = threadIdx.x; idx < rows * 64; idx += kThreads) {
     const int r = idx >> 6, d4 = (idx & 63) * 4;
     float M = -INFINITY;
 #pragma unroll
     for (int w = 0; w < kWaves; w++) M = fmaxf(M, ml[kMlW0 + w * 16 + r]);
-    float L = 0.f, o[4] = {0.f, 0.f, 0.f, 0.f};
+    float L = 0.f;
+    f4_t o = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int w = 0; w < kWaves; w++) {
       const float mw = ml[kMlW0 + w * 16 + r];
       const float wt = (mw == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(mw - M);
       L += wt * ml[kMlLw0 + w * 16 + r];
-      const f4_t ow = *reinterpret_cast<const f4_t*>(mo + (w * 16 + r) * kHD + d4);
-#pragma unroll
-      for (int i = 0; i < 4; i++) o[i] += wt * ow[i];
+      o += wt * *reinterpret_cast<const f4_t*>(mo + (w * 16 + r) * kHD + d4);
     }
-    // wave-0 slot, own elements
-    *reinterpret_cast<f4_t*>(mo + r * kHD + d4) = f4_t{o[0], o[1], o[2], o[3]};
-    if (d4 == 0) {
-      ml[kMlM + r] = M;
-      ml[kMlL + r] = L;
+    if constexpr (MODE == 1) {
+      *reinterpret_cast<f4_t*>(mo + r * kHD + d4) = o;   // wave-0 slot, own elements only
+      if (d4 == 0) {
+        ml[kMlM + r] = M;
+        ml[kMlL + r] = L;
+      }
+    } else if (has_work) {
+      store_record_piece(p, rml, ro, h * gqa + r % gqa, t0 + r / gqa, chunk, d4, o, M, L);
     }
   }
-  __syncthreads();
 
-  if (MODE == 1) {
+  if constexpr (MODE == 1) {
+    __syncthreads();
     finish_rows(lds, p, h, t0, rows, false, chunk, nullptr);
     return;
   }
 
-
   // ---------------- fast path: tagged records, designated mergers ----------------
-  const __amdgpu_buffer_rsrc_t rml =
-      __builtin_amdgcn_make_buffer_rsrc(p.ws_ml, 0, p.ws_ml_bytes, kBufferRsrcWord3);
-  const __amdgpu_buffer_rsrc_t ro =
-      __builtin_amdgcn_make_buffer_rsrc(p.ws_o, 0, p.ws_o_bytes, kBufferRsrcWord3);
-  if (has_work) {
-    const float* mlv = reinterpret_cast<const float*>(lds + kLdsMergeML);
-    store_records<kThreads>(reinterpret_cast<const float*>(lds + kLdsMergeO), mlv + kMlM,
-                            mlv + kMlL, p, rml, ro, h, t0, rows, chunk);
-  }
+  if (has_work) publish_records(p, rml, h, t0, rows, chunk);
   using ML = MergeLayout<kThreads>;
   static_assert(kLdsMergeO + ML::kRedFloats * 4 <= kLdsMergeML, "merge reduction must fit");
   merge_phase<kThreads, true>(reinterpret_cast<float*>(lds + kLdsMergeO),
