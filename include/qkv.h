@@ -106,6 +106,19 @@ int qkv_q8_append_kv(const uint16_t* k_f16, const uint16_t* v_f16, qkv_block_q8*
 int qkv_q8_dequant(const qkv_block_q8* in, uint16_t* out_f16, int n_blocks,
                    hipStream_t stream);
 
+/* Token-row moves inside one slot of one layer's cache: replaces the per-token
+ * device copies of kv_move_token (model.cuh:7430-7471; its tree-verify
+ * acceptance calls it once per accepted token and layer).  For i = 0..n-1 in
+ * list order, row slot_row0 + to[i] := row slot_row0 + from[i] in both k and
+ * v, where from_to = {from0, to0, from1, to1, ...} (host array, 0 <= from, to
+ * < slot_rows) and a row is k_row_bytes / v_row_bytes (blocks_per_token x
+ * sizeof(qkv_block_tq3) or sizeof(qkv_block_q8); multiples of 4).  Works for
+ * either cache format.  n <= 64 per call; a move with from == to does
+ * nothing.  One launch; moves that touch no row another move writes run in
+ * parallel, otherwise in list order. */
+int qkv_kv_move_tokens(void* k, void* v, size_t k_row_bytes, size_t v_row_bytes, long slot_row0,
+                       long slot_rows, const int32_t* from_to, int n, hipStream_t stream);
+
 /* ---------------------------------------------------------------------------
  * Split-K flash decode over the packed caches
  *

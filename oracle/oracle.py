@@ -287,6 +287,18 @@ def key_visible(key, start_pos, t_idx, sink_tok=0, window_tok=0, tree_mask=None)
 # block_tokens keys; gathering a slot's rows and running the contiguous
 # reference decode on them is the paged decode's definition.
 
+def move_token_rows(cache_rows: np.ndarray, moves, slot_row0: int = 0) -> np.ndarray:
+    """kv_move_token (model.cuh:7430-7471) applied per move in list order, as
+    the reference's sequence of device copies: row slot_row0 + to := row
+    slot_row0 + from.  cache_rows: [rows][row_bytes] uint8 (K or V of one
+    layer).  Returns a new array."""
+    out = np.array(cache_rows, copy=True)
+    for f, t in moves:
+        if f != t:
+            out[slot_row0 + t] = out[slot_row0 + f]
+    return out
+
+
 def paged_rows(block_table, n_keys, block_tokens):
     """Cache rows of keys 0..n_keys-1 of one slot."""
     k = np.arange(n_keys, dtype=np.int64)

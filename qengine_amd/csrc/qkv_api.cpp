@@ -130,6 +130,41 @@ int qkv_q8_append_kv(const uint16_t* k_f16, const uint16_t* v_f16, qkv_block_q8*
     return QKV_ERR_ALIGN;
   return launch_status(qkv::launch_q8_append(k_f16, k_out, v_f16, v_out, n_blocks, 2, stream));
 }
+int qkv_kv_move_tokens(void* k, void* v, size_t k_row_bytes, size_t v_row_bytes, long slot_row0,
+                       long slot_rows, const int32_t* from_to, int n, hipStream_t stream) {
+  if (n < 0 || n > qkv::kMoveMax) return QKV_ERR_INVALID;
+  if (n == 0) return QKV_OK;
+  if (!k || !v || !from_to) return QKV_ERR_NULL;
+  if (k_row_bytes == 0 || v_row_bytes == 0 || k_row_bytes % 4 || v_row_bytes % 4 ||
+      k_row_bytes > 0xffffffffULL || v_row_bytes > 0xffffffffULL || slot_row0 < 0 || slot_rows <= 0)
+    return QKV_ERR_INVALID;
+  if (!aligned(k, 4) || !aligned(v, 4)) return QKV_ERR_ALIGN;
+  qkv::MoveArgs a{};
+  a.k = static_cast<uint8_t*>(k);
+  a.v = static_cast<uint8_t*>(v);
+  a.k_row_bytes = (uint32_t)k_row_bytes;
+  a.v_row_bytes = (uint32_t)v_row_bytes;
+  a.slot_row0 = slot_row0;
+  a.n = n;
+  for (int i = 0; i < n; i++) {
+    a.from[i] = from_to[2 * i];
+    a.to[i] = from_to[2 * i + 1];
+    if (a.from[i] < 0 || a.from[i] >= slot_rows || a.to[i] < 0 || a.to[i] >= slot_rows)
+      return QKV_ERR_INVALID;
+  }
+  // in list order unless no row written by one move is read or written by another
+  bool ordered = false;
+  for (int i = 0; i < n && !ordered; i++) {
+    if (a.from[i] == a.to[i]) continue;
+    for (int j = 0; j < n; j++)
+      if (j != i && a.from[j] != a.to[j] && (a.to[i] == a.from[j] || a.to[i] == a.to[j])) {
+        ordered = true;
+        break;
+      }
+  }
+  return launch_status(qkv::launch_kv_move(a, ordered, stream));
+}
+
 int qkv_q8_dequant(const qkv_block_q8* in, uint16_t* out_f16, int n_blocks, hipStream_t stream) {
   if (n_blocks < 0) return QKV_ERR_INVALID;
   if (n_blocks == 0) return QKV_OK;

@@ -25,6 +25,19 @@ hipError_t launch_q8_append(const void* in0, void* out0, const void* in1, void* 
                             int n_blocks, int n_tensors, hipStream_t stream);
 hipError_t launch_q8_dequant(const void* in, void* out, int n_blocks, hipStream_t stream);
 
+// Token-row moves inside one slot of one layer's cache (kv_move.hip): row
+// slot_row0 + to[i] := row slot_row0 + from[i] for i = 0..n-1, K and V.
+constexpr int kMoveMax = 64;
+struct MoveArgs {
+  uint8_t* k;
+  uint8_t* v;
+  uint32_t k_row_bytes, v_row_bytes;   // multiples of 4
+  long slot_row0;
+  int n;
+  int from[kMoveMax], to[kMoveMax];
+};
+hipError_t launch_kv_move(const MoveArgs& a, bool ordered, hipStream_t stream);
+
 // Chunked prefill over a TQ3 cache (prefill_tq3.hip).  Workspace pieces:
 // qr  rotated queries [n_tok][num_q][256] fp16
 // kr  rotated chunk keys [num_kv][n_pad][256] fp16

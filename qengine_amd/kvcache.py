@@ -104,6 +104,21 @@ def q8_dequant(blocks: torch.Tensor, out: torch.Tensor | None = None, stream=Non
     return out
 
 
+def kv_move_tokens(k: torch.Tensor, v: torch.Tensor, moves, *, k_row_bytes: int,
+                   v_row_bytes: int, slot_row0: int = 0, slot_rows: int | None = None,
+                   stream=None) -> None:
+    """kv_move_token (model.cuh:7430-7471) for a list of (from_pos, to_pos)
+    moves of one layer, applied in list order, in one launch."""
+    import ctypes
+    moves = list(moves)
+    if slot_rows is None:
+        slot_rows = k.numel() // k_row_bytes - slot_row0
+    flat = (ctypes.c_int32 * max(1, 2 * len(moves)))(*[int(x) for m in moves for x in m])
+    check(lib().qkv_kv_move_tokens(_dev_ptr(k, "k"), _dev_ptr(v, "v"), k_row_bytes, v_row_bytes,
+                                   slot_row0, slot_rows, ctypes.cast(flat, ctypes.c_void_p),
+                                   len(moves), _stream(stream)), "qkv_kv_move_tokens")
+
+
 # ---------------------------------------------------------------------------
 # attention
 # ---------------------------------------------------------------------------

@@ -85,3 +85,19 @@ def test_paged_argument_errors_without_gpu(L):
     assert app(hd=64) == -3
     assert app(pos=None) == -2
     assert app(k=p + 8) == -4
+
+
+def test_kv_move_tokens_argument_errors_without_gpu(L):
+    buf = ctypes.create_string_buffer(4096)
+    p = (ctypes.addressof(buf) + 15) & ~15
+    pairs = (ctypes.c_int32 * 4)(0, 1, 2, 3)
+    pp = ctypes.cast(pairs, ctypes.c_void_p)
+    assert L.qkv_kv_move_tokens(p, p, 416, 416, 0, 8, pp, 0, None) == 0       # empty list
+    assert L.qkv_kv_move_tokens(p, p, 416, 416, 0, 8, pp, -1, None) == -1
+    assert L.qkv_kv_move_tokens(p, p, 416, 416, 0, 8, pp, 65, None) == -1     # more than 64 moves
+    assert L.qkv_kv_move_tokens(None, p, 416, 416, 0, 8, pp, 2, None) == -2
+    assert L.qkv_kv_move_tokens(p, p, 416, 416, 0, 8, None, 2, None) == -2
+    assert L.qkv_kv_move_tokens(p, p, 418, 416, 0, 8, pp, 2, None) == -1      # rows of whole dwords
+    assert L.qkv_kv_move_tokens(p, p, 416, 416, 0, 3, pp, 2, None) == -1      # row 3 outside 3 rows
+    assert L.qkv_kv_move_tokens(p, p, 416, 416, -1, 8, pp, 2, None) == -1
+    assert L.qkv_kv_move_tokens(p + 2, p, 416, 416, 0, 8, pp, 2, None) == -4

@@ -351,3 +351,14 @@ def test_prescale_thresholds_one_ulp_off_fails(k, delta):
     lo, hi = max(0, thr[k] - (1 << 15)), min(0xFFFFFFFF, thr[k] + (1 << 15))
     assert O.prescale_threshold_mismatches(PRESCALE_THR, lo, hi) == 0
     assert O.prescale_threshold_mismatches(thr, lo, hi) > 0
+
+
+def test_move_token_rows_known_answer():
+    """The reference's per-token copies in list order (model.cuh:7430-7471):
+    rows A B C D E with moves 2->0, 0->3, 4->4 (no-op), 1->2 give C B B C E,
+    worked out by hand (the second move copies the row the first one wrote)."""
+    rows = np.array([[ord(c)] * 4 for c in "ABCDE"], np.uint8)
+    got = O.move_token_rows(rows, [(2, 0), (0, 3), (4, 4), (1, 2)])
+    assert bytes(got[:, 0]).decode() == "CBBCE"
+    got = O.move_token_rows(rows, [(0, 1)], slot_row0=2)     # slot starting at row 2
+    assert bytes(got[:, 0]).decode() == "ABCCE"
