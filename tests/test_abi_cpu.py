@@ -101,3 +101,18 @@ def test_kv_move_tokens_argument_errors_without_gpu(L):
     assert L.qkv_kv_move_tokens(p, p, 416, 416, 0, 3, pp, 2, None) == -1      # row 3 outside 3 rows
     assert L.qkv_kv_move_tokens(p, p, 416, 416, -1, 8, pp, 2, None) == -1
     assert L.qkv_kv_move_tokens(p + 2, p, 416, 416, 0, 8, pp, 2, None) == -4
+
+
+def test_decode_workspace_for_the_longest_call_covers_shorter_ones(L):
+    """The fast path's chunk size grows with the key count (one round of
+    workgroups), so its record area is not proportional to the length; a
+    workspace sized for the longest call must still cover every shorter one."""
+    for num_q, num_kv in [(16, 4), (24, 4), (16, 16), (8, 4), (32, 4)]:
+        for sub_n in (1, 4, 16):
+            for n_max in (4096, 40000, 131088, 262144):
+                top = L.qkv_decode_attn_tq3_workspace_bytes(num_q, num_kv, sub_n, n_max)
+                assert top > 0
+                for n in sorted({sub_n, 513, 4097, n_max // 3, n_max - 1, n_max}):
+                    if sub_n <= n <= n_max:
+                        assert L.qkv_decode_attn_tq3_workspace_bytes(num_q, num_kv, sub_n, n) <= top, \
+                            (num_q, num_kv, sub_n, n, n_max)
