@@ -240,19 +240,6 @@ __device__ __forceinline__ void load_tile(__amdgpu_buffer_rsrc_t rk, __amdgpu_bu
   tr.vr6 = __builtin_amdgcn_raw_buffer_load_b64(rv, vrow + 96, 0, 0);
 }
 
-// Cache row of key index ts (a multiple of 64) of query t: ts itself for a
-// contiguous cache; through the query's block table for a paged one (block
-// sizes are multiples of 64, so a 64-key tile never straddles two blocks).
-// The table is read only for a tile that has keys (ts < hi <= ctx_max, so the
-// entry lies inside the query's row of the table); rows outside the cache
-// extent read as zero (buffer range checks).
-__device__ __forceinline__ int tile_row(const AttnArgs& p, int t, int ts, int hi) {
-  if (p.block_tables == nullptr) return ts;
-  if (ts >= hi) return 0;
-  const int b = ts / p.block_tokens;
-  return p.block_tables[t * p.bt_stride + b] * p.block_tokens + (ts - b * p.block_tokens);
-}
-
 // Key visibility of one query (attention.cuh:1923-1929, 2101-2105): the
 // sink/window rule on 32-key tiles, then the tree bits for keys of the block.
 // Branch-free: every key of a tile is tested with the same instructions.
@@ -434,6 +421,37 @@ __global__ __launch_bounds__(kThreads, 1) void tq3_attn_kernel(AttnArgs p, uint1
   const int q_wht = threadIdx.x >> 4;
   const int q_part = threadIdx.x & 15;
   const int q_col = q_wht >> 1, q_blk = q_wht & 1;   // column, 128-block
+  // paged caches: the block-table entries of this wave's first 64 tiles (lane
+  // k: tile k, key lo + wave*64 + k*kStep), loaded now so that no tile load
+  // waits for a table read (rows past the table's extent read as 0)
+  constexpr int kStep = kWaves * kTile;
+  const int ts0 = lo + wave * kTile;
+  const __amdgpu_buffer_rsrc_t rbt = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<int32_t*>(p.block_tables), 0,
+      p.block_tables ? (uint32_t)(p.sub_n * p.bt_stride * 4) : 0u, kBufferRsrcWord3);
+  auto bt_batch = [&](int k0) -> int {   // entries of tiles k0 .. k0+63 (one per lane)
+    const int ts = ts0 + (k0 + lane) * kStep;
+    const uint32_t off = ts < hi ? (uint32_t)((t0 * p.bt_stride + ts / max(p.block_tokens, 1)) * 4)
+                                 : 0xffffffffu;
+    return (int)__builtin_amdgcn_raw_buffer_load_b32(rbt, off, 0, 0);
+  };
+  int bt_entry = bt_batch(0), bt_k0 = 0;
+  // cache row of this wave's tile starting at key ts: ts itself for a
+  // contiguous cache; through the query's block table for a paged one (block
+  // sizes are multiples of 64, so a 64-key tile never straddles two blocks);
+  // rows outside the cache extent read as zero (buffer range checks)
+  auto wave_tile_row = [&](int ts) -> int {
+    if (p.block_tables == nullptr) return ts;
+    if (ts >= hi) return 0;
+    const int k = (ts - ts0) / kStep;
+    if (k - bt_k0 >= 64) {
+      bt_k0 = k & ~63;
+      bt_entry = bt_batch(bt_k0);
+    }
+    const int e = __builtin_amdgcn_readlane(bt_entry, k - bt_k0);
+    const int b = ts / p.block_tokens;
+    return e * p.block_tokens + (ts - b * p.block_tokens);
+  };
   u4_t q_raw;
   {
     // unconditional (rows past the buffer's extent read as zero): a load
@@ -501,9 +519,9 @@ __global__ __launch_bounds__(kThreads, 1) void tq3_attn_kernel(AttnArgs p, uint1
   // tiles arrive in the first half of the stream and are computed while the
   // second waves' tiles are still in flight.
   TileRegs tr;
-  if (wave < 4) load_tile(rk, rv, tile_row(p, t0, lo + wave * kTile, hi), p.num_kv, h, lane, row, col, tr);
+  if (wave < 4) load_tile(rk, rv, wave_tile_row(ts0), p.num_kv, h, lane, row, col, tr);
   __syncthreads();
-  if (wave >= 4) load_tile(rk, rv, tile_row(p, t0, lo + wave * kTile, hi), p.num_kv, h, lane, row, col, tr);
+  if (wave >= 4) load_tile(rk, rv, wave_tile_row(ts0), p.num_kv, h, lane, row, col, tr);
   // qa[s], slice s = 4j+u: column `col`, element i = dim 128j + 8(4*row+u) + i
   h8_t qa[8];
   {
@@ -645,11 +663,10 @@ __global__ __launch_bounds__(kThreads, 1) void tq3_attn_kernel(AttnArgs p, uint1
   };
   // lo and hi are wave-uniform (a paged workgroup serves one query): the tile
   // loop is a scalar loop
-  const int ts0 = lo + wave * kTile;
   if (ts0 < hi) {
     tile_body(std::true_type{}, ts0);
-    for (int ts = ts0 + kWaves * kTile; ts < hi; ts += kWaves * kTile) {
-      load_tile(rk, rv, tile_row(p, t0, ts, hi), p.num_kv, h, lane, row, col, tr);
+    for (int ts = ts0 + kStep; ts < hi; ts += kStep) {
+      load_tile(rk, rv, wave_tile_row(ts), p.num_kv, h, lane, row, col, tr);
       tile_body(std::false_type{}, ts);
     }
   } else {
