@@ -31,6 +31,47 @@ __device__ __forceinline__ long rec_index(const AttnArgs& p, int qh, int t, int 
   return (long)(qh * p.sub_n + t) * p.n_slots + chunk;
 }
 
+// Ragged (paged) launches: the sub_n * n_chunks record shares of a kv head
+// are split over the slots in proportion to their key counts (every slot at
+// least one, at most 128), so that long slots get more workgroups than short
+// ones; every workgroup computes the same split.  Slot s owns the shares
+// first .. first+count-1, whose records sit at rec_index(p, qh, 0, share).
+__device__ __forceinline__ int slot_keys(const AttnArgs& p, int s) {
+  return min(max(p.ctx_lens[s], 0), p.ctx_max);
+}
+__device__ inline int share_count(const AttnArgs& p, int s, long total) {
+  const int extra = p.sub_n * p.n_chunks - p.sub_n;
+  return min(128, 1 + (total > 0 ? (int)((long)extra * slot_keys(p, s) / total) : 0));
+}
+__device__ inline long total_keys(const AttnArgs& p) {
+  long total = 0;
+  for (int i = 0; i < p.sub_n; i++) total += slot_keys(p, i);
+  return total;
+}
+__device__ inline void slot_shares(const AttnArgs& p, int s, int& first, int& count) {
+  const long total = total_keys(p);
+  int acc = 0;
+  for (int i = 0; i < s; i++) acc += share_count(p, i, total);
+  first = acc;
+  count = share_count(p, s, total);
+}
+// The slot of share g (-1 past the last slot's shares), its first share and count.
+__device__ inline int share_slot(const AttnArgs& p, int g, int& first, int& count) {
+  const long total = total_keys(p);
+  int acc = 0;
+  for (int i = 0; i < p.sub_n; i++) {
+    const int w = share_count(p, i, total);
+    if (g < acc + w) {
+      first = acc;
+      count = w;
+      return i;
+    }
+    acc += w;
+  }
+  first = count = 0;
+  return -1;
+}
+
 // Poll limit of a merger waiting for the records of one launch (each poll
 // sleeps ~64 cycles after two memory round trips; the limit is seconds, far
 // beyond any legitimate wait).
@@ -47,8 +88,8 @@ struct MergeLayout {
   static constexpr int kRedFloats = kWaves * 128;
 };
 
-// Merge all chunk records (n_chunks <= 128) of one unit (q head qh, query t,
-// 128-block blk) and write its fp16 output  o = sum w_c o_c / sum w_c l_c,
+// Merge the n <= 128 records base .. base+n-1 of one unit (q head qh, query
+// t, 128-block blk) and write its fp16 output  o = sum w_c o_c / sum w_c l_c,
 // w_c = 2^(m_c - M), rotated back (o = rs*D*H*o per 128-block) when ROTATE.
 // 1. Threads 0..n-1 poll one record each ({m, l, tags} in one 16-byte load)
 //    until every tag of the unit is set; m and l go to LDS (mls, 128
@@ -63,15 +104,14 @@ struct MergeLayout {
 // the poll limit.
 template <int THREADS, bool ROTATE>
 __device__ bool merge_unit(float* red, f2_t* mls, const AttnArgs& p, __amdgpu_buffer_rsrc_t rml,
-                           __amdgpu_buffer_rsrc_t ro, int qh, int t, int blk, uint16_t* out) {
+                           __amdgpu_buffer_rsrc_t ro, long base, int n, int qh, int t, int blk,
+                           uint16_t* out) {
   using ML = MergeLayout<THREADS>;
   constexpr int kSlices = ML::kSlices, kRecPerThread = ML::kRecPerThread, kWaves = ML::kWaves;
   constexpr int kHD = 256;
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
   const int sl = tid >> 5, dq = tid & 31;
-  const int n = p.n_chunks;
-  const long base = rec_index(p, qh, t, 0);
   bool seen = tid >= n;
   bool complete = false;
   for (int spins = 0; spins < kMergeSpinLimit; spins++) {
@@ -239,7 +279,14 @@ __device__ void merge_phase(float* red, f2_t* mls, const AttnArgs& p, __amdgpu_b
   if (mid < 0) return;
   for (int u = mid; u < n_units; u += n_mergers) {
     const int blk = u & 1, qh = (u >> 1) % p.num_q, t = (u >> 1) / p.num_q;
-    if (!merge_unit<THREADS, ROTATE>(red, mls, p, rml, ro, qh, t, blk, out)) break;
+    long base = rec_index(p, qh, t, 0);
+    int n = p.n_chunks;
+    if (p.ctx_lens) {   // ragged slots: the slot's shares of the kv head's records
+      int first;
+      slot_shares(p, t, first, n);
+      base = rec_index(p, qh, 0, first);
+    }
+    if (!merge_unit<THREADS, ROTATE>(red, mls, p, rml, ro, base, n, qh, t, blk, out)) break;
   }
 }
 

@@ -361,6 +361,8 @@ __global__ __launch_bounds__(kThreads, 1) void tq3_attn_kernel(AttnArgs p, uint1
   // one kv head: MFMA column c = qi * gqa + hh is q head h*gqa + hh of query
   // t0 + qi (columns past nq * gqa carry nothing).
   int h, t0, chunk;
+  int rec_t0, rec_chunk;      // record coordinates of this workgroup's rows
+  int chunk_keys = p.chunk_keys;
   bool has_work;
   {
     const int L = blockIdx.x;
@@ -369,9 +371,26 @@ __global__ __launch_bounds__(kThreads, 1) void tq3_attn_kernel(AttnArgs p, uint1
     const int g = (r / p.num_kv) * 8 + xcd;
     const int groups = (p.sub_n + p.qpw - 1) / p.qpw;
     has_work = g < groups * p.n_chunks;
-    const int tq = has_work ? g / p.n_chunks : 0;
-    chunk = has_work ? g - tq * p.n_chunks : 0;
-    t0 = tq * p.qpw;
+    if (MODE == 0 && p.ctx_lens) {
+      // ragged slots (one query each): share g of the length-proportional split
+      int first, count;
+      const int s = has_work ? share_slot(p, g, first, count) : -1;
+      has_work = s >= 0;
+      t0 = has_work ? s : 0;
+      chunk = has_work ? g - first : 0;
+      if (has_work) {   // the slot's keys in count chunks of whole 512-key steps
+        const int per = (slot_keys(p, s) + count - 1) / count;
+        chunk_keys = max(1, (per + kWaves * kTile - 1) / (kWaves * kTile)) * (kWaves * kTile);
+      }
+      rec_t0 = 0;
+      rec_chunk = g;
+    } else {
+      const int tq = has_work ? g / p.n_chunks : 0;
+      chunk = has_work ? g - tq * p.n_chunks : 0;
+      t0 = tq * p.qpw;
+      rec_t0 = t0;
+      rec_chunk = chunk;
+    }
   }
   if (MODE == 1 && !has_work) return;
   const int nq = min(p.qpw, p.sub_n - t0);
@@ -388,10 +407,10 @@ __global__ __launch_bounds__(kThreads, 1) void tq3_attn_kernel(AttnArgs p, uint1
   int lo = 0, hi = 0, hi_col = 0, hi_first = 0;
   if (MODE == 0) {
     if (has_work) {
-      lo = chunk * p.chunk_keys;
-      hi = min(lo + p.chunk_keys, active_last);
-      hi_col = min(lo + p.chunk_keys, active_end);
-      hi_first = min(lo + p.chunk_keys, active_first);
+      lo = chunk * chunk_keys;
+      hi = min(lo + chunk_keys, active_last);
+      hi_col = min(lo + chunk_keys, active_end);
+      hi_first = min(lo + chunk_keys, active_first);
     }
   } else {
     // reference split range (attention.cuh:1944-1951)
@@ -722,7 +741,7 @@ __global__ __launch_bounds__(kThreads, 1) void tq3_attn_kernel(AttnArgs p, uint1
         ml[kMlL + r] = L;
       }
     } else if (has_work) {
-      store_record_piece(p, rml, ro, h * gqa + r % gqa, t0 + r / gqa, chunk, d4, o, M, L);
+      store_record_piece(p, rml, ro, h * gqa + r % gqa, rec_t0 + r / gqa, rec_chunk, d4, o, M, L);
     }
   }
 
@@ -733,7 +752,7 @@ __global__ __launch_bounds__(kThreads, 1) void tq3_attn_kernel(AttnArgs p, uint1
   }
 
   // ---------------- fast path: tagged records, designated mergers ----------------
-  if (has_work) publish_records(p, rml, h, t0, rows, chunk);
+  if (has_work) publish_records(p, rml, h, rec_t0, rows, rec_chunk);
   using ML = MergeLayout<kThreads>;
   static_assert(kLdsMergeO + ML::kRedFloats * 4 <= kLdsMergeML, "merge reduction must fit");
   merge_phase<kThreads, true>(reinterpret_cast<float*>(lds + kLdsMergeO),
