@@ -10,27 +10,32 @@
 // accumulate sum_t p_t norm_t c[idx_t] in rotated coordinates and each output
 // row is rotated back once.
 //
-// Workgroup: 4 waves on one kv head; each wave takes 64-key tiles.  Per tile:
-//   scores  v_mfma_f32_16x16x32_f16, A = rotated query (rows = heads, held in
-//           32 VGPRs for the whole kernel), B = codes of 16 keys x 32 dims:
-//           lane (key, octet o) reads the 12 aligned bytes holding code groups
-//           4o..4o+3 of each 128-block and decodes centroid pairs through a
-//           64-entry LDS table.  One accumulator per 128-block, each scaled by
-//           its block norm.
-//   softmax online, per 16-lane row of the D layout (rows = heads), base 2.
-//   values  v_mfma_f32_16x16x32_f16, A = p*norm (fp16, LDS, rows = heads),
-//           B = codes of 32 keys x 16 dims.  The wave's value rows are loaded
-//           with aligned 16-byte loads (lane = key) and staged in LDS; lane
-//           (n, o) gathers dim group n of both blocks for 8 keys and pairs keys
-//           with v_perm.
-// Merging: the 4 waves merge in LDS.  Fast path: every workgroup writes one
-// record per q head {m, l, o[256]} (rotated) and counts itself in; the last
-// workgroups of the grid are designated mergers, one per (q head, query,
-// 128-block) unit: each waits for the full count (bounded poll), reads all of
-// its unit's records in one round of 16-byte loads, merges, rotates back and
-// stores fp16.  Only mergers wait, so progress does not depend on workgroup
-// co-residency.  Split API: one workgroup per reference split, written in the
-// reference partial layout.
+// Workgroup: 8 waves (two per SIMD) on one kv head and one key chunk; each
+// wave takes 64-key tiles.  The first wave of each SIMD issues its first
+// tile's loads before the second, so that its tile arrives first and is
+// computed while the second one streams.  Per tile:
+//   scores  v_mfma_f32_16x16x32_f16, A = key codes of 16 keys x 32 dims, B =
+//           rotated query (columns = heads, held in 32 VGPRs for the whole
+//           kernel): lane (key, octet o) reads the 12 aligned bytes holding
+//           code groups 4o..4o+3 of each 128-block and decodes centroid pairs
+//           through a per-lane LDS table.  One accumulator per 128-block, each
+//           scaled by its block norm (which carries the softmax scale).
+//   softmax online, per head, base 2.
+//   values  v_mfma_f32_16x16x32_f16, A = p*norm (fp16, the lane's own
+//           probabilities), B = codes of 32 keys x 16 dims.  The wave's value
+//           rows are loaded with aligned 16-byte loads (lane = key) and staged
+//           in LDS; lane (n, o) gathers dim group n of both blocks for 8 keys
+//           and pairs keys with v_perm; the table reads run two steps ahead.
+// Merging: the 8 waves merge in LDS and each merged piece goes straight to
+// its record {m, l, tags} + o[256] (rotated); the tags are set once the
+// workgroup's data stores are complete.  The last workgroups of the grid are
+// designated mergers, one per (q head, query, 128-block) unit: each polls its
+// unit's tags (bounded), clears them, reads the rows in one round of 16-byte
+// loads, merges, rotates back and stores fp16 (attn_fastmerge.h).  Only
+// mergers wait, so progress does not depend on workgroup co-residency.  Paged
+// (ragged) launches split each kv head's record shares over the slots in
+// proportion to their key counts.  Split API: one workgroup per reference
+// split, written in the reference partial layout.
 #include <type_traits>
 
 #include "qkv_device.h"
