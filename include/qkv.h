@@ -198,6 +198,21 @@ int qkv_decode_attn_q8(const uint16_t* q, const qkv_block_q8* k, const qkv_block
                        int sub_n, float scale, void* workspace, size_t workspace_bytes,
                        hipStream_t stream);
 
+/* V-only TurboQuant (TQ_KEYS_Q8=1): keys in Q8_0 (k, 8 blocks per kv head and
+ * token), values in TQ3 (v, 2 blocks per kv head and token).  Replaces the
+ * reference's unfused sequence for that mode (model.cuh:2574-2588:
+ * dequantize_kv_q8_0_kern into fp16 scratch, attn_score_kernel_h, softmax,
+ * then attn_value_kernel_tq3 over the TQ3 values; cache layout
+ * model.cuh:1735-1748, append model.cuh:2323-2333) with one fused launch:
+ * the qkv_decode_attn_q8 schedule, values accumulated in rotated coordinates
+ * and rotated back by the in-kernel mergers.  Same arguments, errors and
+ * workspace rules as qkv_decode_attn_q8. */
+size_t qkv_decode_attn_q8k_tq3v_workspace_bytes(int num_q, int num_kv, int sub_n, int n_keys);
+int qkv_decode_attn_q8k_tq3v(const uint16_t* q, const qkv_block_q8* k, const qkv_block_tq3* v,
+                             uint16_t* out, int num_q, int num_kv, int head_dim, int start_pos,
+                             int sub_n, float scale, void* workspace, size_t workspace_bytes,
+                             hipStream_t stream);
+
 /* Paged, ragged decode: one query per slot over per-slot block tables
  * This generalises the reference, which keeps every
  * slot contiguous and hands the attention launch a slot-base pointer

@@ -275,6 +275,27 @@ def attn_ref_f64(q, k_f16, v_f16, *, num_q, num_kv, hd, start_pos, sub_n, scale,
     return out
 
 
+def attn_q8k_tq3v_f64(q, k_q8, v_tq3, *, num_q, num_kv, hd, start_pos, sub_n, scale):
+    """V-only TurboQuant decode (TQ_KEYS_Q8, model.cuh:2574-2588): keys
+    dequantized from Q8_0 to fp16 (dequantize_kv_q8_0_kern,
+    attention.cuh:2614-2626) for attn_score_kernel_h, values decoded from TQ3
+    in fp32 as attn_value_kernel_tq3 does (attention.cuh:920-989); query t
+    attends keys 0 .. start_pos + t; softmax and sums in float64.
+    Returns [sub_n][num_q][hd] float64."""
+    k = f16_to_f32(q8_decode(k_q8)).astype(np.float64).reshape(-1, num_kv, hd)
+    v = tq3_decode_f32(v_tq3).astype(np.float64).reshape(-1, num_kv, hd)
+    qf = f16_to_f32(_u16(q)).astype(np.float64).reshape(sub_n, num_q, hd)
+    gqa = num_q // num_kv
+    out = np.zeros((sub_n, num_q, hd))
+    for t in range(sub_n):
+        n = start_pos + t + 1
+        for h in range(num_kv):
+            s = qf[t, h * gqa:(h + 1) * gqa] @ k[:n, h].T * scale     # [gqa][n]
+            w = np.exp(s - s.max(axis=1, keepdims=True))
+            out[t, h * gqa:(h + 1) * gqa] = (w @ v[:n, h]) / w.sum(axis=1, keepdims=True)
+    return out
+
+
 def key_visible(key, start_pos, t_idx, sink_tok=0, window_tok=0, tree_mask=None):
     tm = None if tree_mask is None else np.ascontiguousarray(tree_mask, np.uint32)
     return bool(lib().or_key_visible(key, start_pos, t_idx, sink_tok, window_tok, _ptr(tm)))

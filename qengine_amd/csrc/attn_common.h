@@ -22,6 +22,7 @@ struct AttnArgs {
   const uint32_t* k;        // slot-base key cache (blocks viewed as dwords)
   const uint32_t* v;        // slot-base value cache
   uint32_t kv_bytes;        // readable bytes of each cache from its base (buffer range)
+  uint32_t v_bytes;         // value cache range when its format differs from the keys' (else unused)
   int num_q, num_kv;
   int start_pos, sub_n, sub_n_max;
   int qpw;                  // queries per workgroup (MFMA columns = qpw * gqa <= 16)
@@ -155,6 +156,7 @@ __device__ __forceinline__ void wht_xor_lanes16(float (&x)[8], int lane) {
 hipError_t launch_tq3_attn(const AttnArgs& a, int mode, uint16_t* out, hipStream_t stream);
 hipError_t launch_q8_attn_split(const AttnArgs& a, hipStream_t stream);
 hipError_t launch_q8_attn_fast(const AttnArgs& a, uint16_t* out, hipStream_t stream);
+hipError_t launch_q8k_tq3v_attn_fast(const AttnArgs& a, uint16_t* out, hipStream_t stream);
 hipError_t launch_split_merge(const float* m, const float* l, const float* o, uint16_t* out,
                               int num_q, int sub_n, int sub_n_max, int k_splits,
                               hipStream_t stream);

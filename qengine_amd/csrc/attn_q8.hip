@@ -27,6 +27,13 @@
 // wave, or a multiple), tagged records and designated mergers in the same
 // launch (attn_fastmerge.h); values are not rotated, so the merge ends with a
 // plain fp16 store.
+// Mixed formats (VTQ3: keys Q8_0, values TQ3, the reference's TQ_KEYS_Q8
+// mode, model.cuh:1735-1748, 2323-2333, 2574-2588): the same scores; values
+// accumulate sum_t p_t norm_t c[idx_t] in rotated coordinates as in
+// attn_tq3.hip (A = p*norm per 128-block, B = centroid pairs from a per-lane
+// 64-entry LDS table), and the mergers rotate each output block back.  The
+// reference has no fused kernel for this mode: it dequantizes K to fp16 and
+// runs the unfused score, softmax and TQ3 value kernels.
 #include "qkv_device.h"
 #include "attn_common.h"
 #include "attn_fastmerge.h"
@@ -54,6 +61,19 @@ constexpr int kLdsMergeO = 0;
 constexpr int kLdsMergeML = kLdsMergeO + kWaves * 8 * kHD * 4;
 constexpr int kLdsMergeEnd = kLdsMergeML + 256 * 4;
 constexpr int kLdsTotal = kLdsMergeEnd > kLdsTotalTile ? kLdsMergeEnd : kLdsTotalTile;
+// mixed formats: centroid-pair table (entry E = codes E & 7, E >> 3 of lane L
+// at byte E * 256 + 4 * L, so each lane reads its own bank), then per-wave
+// staging (dwords): value code groups [block j][group g][kPitch] (3 bytes of
+// codes, dword-expanded), value block norms [j][kPitch], per-head rescale [16]
+constexpr int kTq3RowBytes = 104;              // one kv head of one token: 2 blocks x 52 B
+constexpr int kMxStCodes = 0;
+constexpr int kMxStNorm = 32 * kPitch;
+constexpr int kMxStCorr = 34 * kPitch;
+constexpr int kMxStageBytes = (34 * kPitch + 16) * 4;
+constexpr int kMxLdsLut = 0;
+constexpr int kMxLdsStage = 64 * 64 * 4;
+constexpr int kMxLdsTotalTile = kMxLdsStage + kWaves * kMxStageBytes;
+constexpr int kMxLdsTotal = kLdsMergeEnd > kMxLdsTotalTile ? kLdsMergeEnd : kMxLdsTotalTile;
 constexpr int kMlW0 = 0, kMlLw0 = 8 * kWaves;   // merge scalars: m[w][8], l[w][8], M[8], L[8]
 constexpr int kMlM = 16 * kWaves, kMlL = 16 * kWaves + 8;
 static_assert(kMlL + 8 <= 256, "merge scalars must fit the ML area");
@@ -63,9 +83,11 @@ static_assert(kLdsMergeO + MergeLayout<kThreads>::kRedFloats * 4 <= kLdsMergeML,
 
 struct TileQ8 {
   uint32_t k[2][18];   // key 16g+col: blocks 2*row and 2*row+1 (qs, pad|d, qs, pad|d)
-  u4_t v[9];           // key ts + (lane & 31): blocks 4*(lane>>5) .. +3 (36 dwords)
+  u4_t v[9];           // key ts + (lane & 31): blocks 4*(lane>>5) .. +3 (36 dwords);
+                       // TQ3 values: 128-block lane>>5 (norm + 12 code dwords in v[0..3])
 };
 
+template <bool VTQ3>
 __device__ __forceinline__ void load_tile_q8(__amdgpu_buffer_rsrc_t rk, __amdgpu_buffer_rsrc_t rv,
                                              int ts, int nkv, int h, int lane, int row, int col,
                                              TileQ8& t) {
@@ -82,10 +104,18 @@ __device__ __forceinline__ void load_tile_q8(__amdgpu_buffer_rsrc_t rk, __amdgpu
     t.k[g][16] = c[0];
     t.k[g][17] = c[1];
   }
-  const uint32_t voff =
-      (uint32_t)((ts + (lane & 31)) * nkv + h) * kRowBytes + 144u * (uint32_t)(lane >> 5);
+  if constexpr (VTQ3) {
+    const uint32_t voff =
+        (uint32_t)((ts + (lane & 31)) * nkv + h) * kTq3RowBytes + 52u * (uint32_t)(lane >> 5);
 #pragma unroll
-  for (int i = 0; i < 9; i++) t.v[i] = __builtin_amdgcn_raw_buffer_load_b128(rv, voff + 16 * i, 0, 0);
+    for (int i = 0; i < 3; i++) t.v[i] = __builtin_amdgcn_raw_buffer_load_b128(rv, voff + 16 * i, 0, 0);
+    t.v[3][0] = __builtin_amdgcn_raw_buffer_load_b32(rv, voff + 48, 0, 0);
+  } else {
+    const uint32_t voff =
+        (uint32_t)((ts + (lane & 31)) * nkv + h) * kRowBytes + 144u * (uint32_t)(lane >> 5);
+#pragma unroll
+    for (int i = 0; i < 9; i++) t.v[i] = __builtin_amdgcn_raw_buffer_load_b128(rv, voff + 16 * i, 0, 0);
+  }
 }
 
 __device__ __forceinline__ float scale_of(uint32_t pad_d) { return h2f(pad_d >> 16); }
@@ -125,9 +155,10 @@ __device__ __forceinline__ void wave_sync() {
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
-template <int MODE>
+template <int MODE, bool VTQ3 = false>
 __global__ __launch_bounds__(kThreads, 2) void q8_attn_kernel(AttnArgs p, uint16_t* out) {
-  __shared__ __attribute__((aligned(16))) uint8_t lds[kLdsTotal];
+  static_assert(!VTQ3 || MODE == 0, "mixed formats: fast path only");
+  __shared__ __attribute__((aligned(16))) uint8_t lds[VTQ3 ? kMxLdsTotal : kLdsTotal];
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int row = lane >> 4, col = lane & 15;
@@ -162,8 +193,8 @@ __global__ __launch_bounds__(kThreads, 2) void q8_attn_kernel(AttnArgs p, uint16
 
   const __amdgpu_buffer_rsrc_t rk =
       __builtin_amdgcn_make_buffer_rsrc(const_cast<uint32_t*>(p.k), 0, p.kv_bytes, kBufferRsrcWord3);
-  const __amdgpu_buffer_rsrc_t rv =
-      __builtin_amdgcn_make_buffer_rsrc(const_cast<uint32_t*>(p.v), 0, p.kv_bytes, kBufferRsrcWord3);
+  const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint32_t*>(p.v), 0, VTQ3 ? p.v_bytes : p.kv_bytes, kBufferRsrcWord3);
 
   // query operand, slice s: head `col`, dims (2*row + (s>>2))*32 + 8*(s&3) + i
   h8_t qa[8];
@@ -180,13 +211,26 @@ __global__ __launch_bounds__(kThreads, 2) void q8_attn_kernel(AttnArgs p, uint16
   f4_t acc[16];
 #pragma unroll
   for (int t = 0; t < 16; t++) acc[t] = f4_t{0.f, 0.f, 0.f, 0.f};
-  float* st = reinterpret_cast<float*>(lds + kLdsStage + wave * kStageBytes);
+  if constexpr (VTQ3) {
+    // centroid-pair table: wave w writes every lane's copy of entries 16w .. 16w+15
+    const uint32_t lane4 = 4u * (uint32_t)lane;
+#pragma unroll
+    for (int k = 0; k < 16; k++) {
+      const uint32_t e = 16u * (uint32_t)wave + k;
+      *reinterpret_cast<uint32_t*>(lds + kMxLdsLut + e * 256 + lane4) =
+          f2h(centroid_imm(e & 7u)) | (f2h(centroid_imm(e >> 3)) << 16);
+    }
+    __syncthreads();
+  }
+  constexpr int kCorr = VTQ3 ? kMxStCorr : kStCorr;
+  float* st = reinterpret_cast<float*>(lds + (VTQ3 ? kMxLdsStage + wave * kMxStageBytes
+                                                   : kLdsStage + wave * kStageBytes));
   uint32_t* stu = reinterpret_cast<uint32_t*>(st);
 
   bool first = true;
   for (int ts = lo + wave * kTile; ts < hi; ts += kWaves * kTile) {
     TileQ8 tr;
-    load_tile_q8(rk, rv, ts, p.num_kv, h, lane, row, col, tr);
+    load_tile_q8<VTQ3>(rk, rv, ts, p.num_kv, h, lane, row, col, tr);
 
     // ---- scores: D rows = keys 16g + 4*row + r, D col = head `col`
     f4_t sa[2];
@@ -205,7 +249,24 @@ __global__ __launch_bounds__(kThreads, 2) void q8_attn_kernel(AttnArgs p, uint16
     }
 
     // ---- value rows to LDS (keys past the range stage as zeros)
-    {
+    if constexpr (VTQ3) {
+      // lane (key kl, block j): its norm and code groups 0..15 (bytes 3g..3g+2)
+      const int kl = lane & 31, j = lane >> 5;
+      const bool live = ts + kl < hi;
+      uint32_t d[14];
+#pragma unroll
+      for (int i = 0; i < 3; i++)
+#pragma unroll
+        for (int e = 0; e < 4; e++) d[4 * i + e] = tr.v[i][e];
+      d[12] = tr.v[3][0];
+      d[13] = 0u;
+      st[kMxStNorm + j * kPitch + kl] = live ? __uint_as_float(d[0]) : 0.f;
+#pragma unroll
+      for (int g = 0; g < 16; g++) {
+        const int w = 1 + ((3 * g) >> 2), sh = (3 * g) & 3;
+        stu[kMxStCodes + (16 * j + g) * kPitch + kl] = sh ? __builtin_amdgcn_alignbyte(d[w + 1], d[w], sh) : d[w];
+      }
+    } else {
       const int kl = lane & 31, hf = lane >> 5;
       const bool live = ts + kl < hi;
 #pragma unroll
@@ -248,9 +309,9 @@ __global__ __launch_bounds__(kThreads, 2) void q8_attn_kernel(AttnArgs p, uint16
     lsum = lsum * corr + ps;
     m2 = mn;
     if (!first) {
-      if (row == 0) st[kStCorr + col] = corr;
+      if (row == 0) st[kCorr + col] = corr;
       wave_sync();
-      const f4_t cr = *reinterpret_cast<const f4_t*>(st + kStCorr + 4 * row);
+      const f4_t cr = *reinterpret_cast<const f4_t*>(st + kCorr + 4 * row);
 #pragma unroll
       for (int t = 0; t < 16; t++)
 #pragma unroll
@@ -259,6 +320,43 @@ __global__ __launch_bounds__(kThreads, 2) void q8_attn_kernel(AttnArgs p, uint16
     first = false;
 
     // ---- values: k index i <-> key 4*row + i (i < 4), 16 + 4*row + (i - 4)
+    if constexpr (VTQ3) {
+      // tile 8a+e, column col: dim 128a + 8col + e (code group col of block a);
+      // A = p * block norm, B = centroids of that dim for the 8 keys
+      const uint32_t lane4 = 4u * (uint32_t)lane;
+#pragma unroll
+      for (int a = 0; a < 2; a++) {
+        const f4_t na = *reinterpret_cast<const f4_t*>(st + kMxStNorm + a * kPitch + 4 * row);
+        const f4_t nb = *reinterpret_cast<const f4_t*>(st + kMxStNorm + a * kPitch + 16 + 4 * row);
+        h8_t pv;
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+          pv[r] = (_Float16)(s[0][r] * na[r]);
+          pv[4 + r] = (_Float16)(s[1][r] * nb[r]);
+        }
+        const u4_t xa = *reinterpret_cast<const u4_t*>(stu + kMxStCodes + (16 * a + col) * kPitch + 4 * row);
+        const u4_t xb =
+            *reinterpret_cast<const u4_t*>(stu + kMxStCodes + (16 * a + col) * kPitch + 16 + 4 * row);
+        const uint32_t x[8] = {xa[0], xa[1], xa[2], xa[3], xb[0], xb[1], xb[2], xb[3]};
+#pragma unroll
+        for (int pp = 0; pp < 4; pp++) {   // centroid pair pp: dims 2pp (low half), 2pp+1
+          uint32_t cp[8];
+#pragma unroll
+          for (int i = 0; i < 8; i++)
+            cp[i] = *reinterpret_cast<const uint32_t*>(lds + kMxLdsLut +
+                                                       ((((x[i] >> (6 * pp)) & 63u) << 8) | lane4));
+#pragma unroll
+          for (int e = 0; e < 2; e++) {
+            u4_t bv;
+#pragma unroll
+            for (int k2 = 0; k2 < 4; k2++)
+              bv[k2] = __builtin_amdgcn_perm(cp[2 * k2 + 1], cp[2 * k2], e ? 0x07060302u : 0x05040100u);
+            acc[8 * a + 2 * pp + e] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+                pv, __builtin_bit_cast(h8_t, bv), acc[8 * a + 2 * pp + e], 0, 0, 0);
+          }
+        }
+      }
+    } else {
     h8_t pa;
 #pragma unroll
     for (int r = 0; r < 4; r++) {
@@ -283,6 +381,7 @@ __global__ __launch_bounds__(kThreads, 2) void q8_attn_kernel(AttnArgs p, uint16
         acc[4 * a + e] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pa, b, acc[4 * a + e], 0, 0, 0);
       }
     }
+    }
     wave_sync();
   }
   lsum = xrow_sum(lsum);
@@ -291,7 +390,19 @@ __global__ __launch_bounds__(kThreads, 2) void q8_attn_kernel(AttnArgs p, uint16
   __syncthreads();
   float* mo = reinterpret_cast<float*>(lds + kLdsMergeO);
   float* ml = reinterpret_cast<float*>(lds + kLdsMergeML);
-  if (4 * row < gqa) {
+  if (VTQ3 && 4 * row < gqa) {
+    // tile 8a+e, row 4*row+r (head), column col: dim 128a + 8*col + e
+#pragma unroll
+    for (int a = 0; a < 2; a++)
+#pragma unroll
+      for (int r = 0; r < 4; r++)
+#pragma unroll
+        for (int hh = 0; hh < 2; hh++) {
+          const int t = 8 * a + 4 * hh;
+          f4_t v4 = {acc[t][r], acc[t + 1][r], acc[t + 2][r], acc[t + 3][r]};
+          *reinterpret_cast<f4_t*>(&mo[(wave * 8 + 4 * row + r) * kHD + 128 * a + 8 * col + 4 * hh]) = v4;
+        }
+  } else if (4 * row < gqa) {
     // tile 4a+e, row 4*row+r (head), column col: dim 64a + 4*col + e
 #pragma unroll
     for (int a = 0; a < 4; a++)
@@ -350,7 +461,7 @@ __global__ __launch_bounds__(kThreads, 2) void q8_attn_kernel(AttnArgs p, uint16
       __builtin_amdgcn_make_buffer_rsrc(p.ws_o, 0, p.ws_o_bytes, kBufferRsrcWord3);
   if (has_work)
     store_records<kThreads>(mo, ml + kMlM, ml + kMlL, p, rml, ro, h, t_idx, rows, split);
-  merge_phase<kThreads, false>(reinterpret_cast<float*>(lds + kLdsMergeO),
+  merge_phase<kThreads, VTQ3>(reinterpret_cast<float*>(lds + kLdsMergeO),
                                reinterpret_cast<f2_t*>(lds + kLdsMergeML), p, rml, ro, out);
 }
 
@@ -366,6 +477,13 @@ hipError_t launch_q8_attn_fast(const AttnArgs& a, uint16_t* out, hipStream_t str
   const int groups = a.sub_n * a.n_chunks;
   const int n_wg = ((groups + 7) / 8) * 8 * a.num_kv;
   hipLaunchKernelGGL((q8_attn_kernel<0>), dim3(n_wg), dim3(kThreads), 0, stream, a, out);
+  return hipGetLastError();
+}
+
+hipError_t launch_q8k_tq3v_attn_fast(const AttnArgs& a, uint16_t* out, hipStream_t stream) {
+  const int groups = a.sub_n * a.n_chunks;
+  const int n_wg = ((groups + 7) / 8) * 8 * a.num_kv;
+  hipLaunchKernelGGL((q8_attn_kernel<0, true>), dim3(n_wg), dim3(kThreads), 0, stream, a, out);
   return hipGetLastError();
 }
 

@@ -387,10 +387,11 @@ size_t qkv_decode_attn_q8_workspace_bytes(int num_q, int num_kv, int sub_n, int 
   return fast_geom(num_q, num_kv, sub_n, n_keys, kChunkKeysQ8).total;
 }
 
-int qkv_decode_attn_q8(const uint16_t* q, const qkv_block_q8* k, const qkv_block_q8* v,
-                       uint16_t* out, int num_q, int num_kv, int head_dim, int start_pos,
-                       int sub_n, float scale, void* workspace, size_t workspace_bytes,
-                       hipStream_t stream) {
+// Fast path over Q8_0 keys; values Q8_0 (v_tq3 false) or TQ3 (v_tq3 true).
+static int decode_q8_keys(const uint16_t* q, const void* k, const void* v, uint16_t* out,
+                          int num_q, int num_kv, int head_dim, int start_pos, int sub_n,
+                          float scale, void* workspace, size_t workspace_bytes, bool v_tq3,
+                          hipStream_t stream) {
   int st = check_attn_shape(num_q, num_kv, head_dim, start_pos, sub_n, nullptr);
   if (st) return st;
   if (!q || !k || !v || !out) return QKV_ERR_NULL;
@@ -415,6 +416,7 @@ int qkv_decode_attn_q8(const uint16_t* q, const qkv_block_q8* k, const qkv_block
     const uint64_t extent = (uint64_t)n_keys * num_kv * 8 * sizeof(qkv_block_q8);
     if (extent > 0x7fffffffULL) return QKV_ERR_UNSUPPORTED;   // 32-bit buffer offsets
     a.kv_bytes = (uint32_t)extent;
+    a.v_bytes = (uint32_t)((uint64_t)n_keys * num_kv * 2 * sizeof(qkv_block_tq3));
   }
   a.active_end_max = n_keys;
   a.k_splits = 1;
@@ -428,7 +430,28 @@ int qkv_decode_attn_q8(const uint16_t* q, const qkv_block_q8* k, const qkv_block
   if (g.total > 0xffffffffULL) return QKV_ERR_UNSUPPORTED;   // 32-bit buffer offsets
   a.ws_ml_bytes = (uint32_t)(g.o_off - g.ml_off);
   a.ws_o_bytes = (uint32_t)(g.total - g.o_off);
-  return launch_status(qkv::launch_q8_attn_fast(a, out, stream));
+  return launch_status(v_tq3 ? qkv::launch_q8k_tq3v_attn_fast(a, out, stream)
+                             : qkv::launch_q8_attn_fast(a, out, stream));
+}
+
+int qkv_decode_attn_q8(const uint16_t* q, const qkv_block_q8* k, const qkv_block_q8* v,
+                       uint16_t* out, int num_q, int num_kv, int head_dim, int start_pos,
+                       int sub_n, float scale, void* workspace, size_t workspace_bytes,
+                       hipStream_t stream) {
+  return decode_q8_keys(q, k, v, out, num_q, num_kv, head_dim, start_pos, sub_n, scale,
+                        workspace, workspace_bytes, false, stream);
+}
+
+size_t qkv_decode_attn_q8k_tq3v_workspace_bytes(int num_q, int num_kv, int sub_n, int n_keys) {
+  return qkv_decode_attn_q8_workspace_bytes(num_q, num_kv, sub_n, n_keys);
+}
+
+int qkv_decode_attn_q8k_tq3v(const uint16_t* q, const qkv_block_q8* k, const qkv_block_tq3* v,
+                             uint16_t* out, int num_q, int num_kv, int head_dim, int start_pos,
+                             int sub_n, float scale, void* workspace, size_t workspace_bytes,
+                             hipStream_t stream) {
+  return decode_q8_keys(q, k, v, out, num_q, num_kv, head_dim, start_pos, sub_n, scale,
+                        workspace, workspace_bytes, true, stream);
 }
 
 size_t qkv_decode_attn_tq3_paged_workspace_bytes(int num_q, int num_kv, int n_slots,

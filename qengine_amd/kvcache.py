@@ -193,6 +193,22 @@ def decode_attn_q8(q, k, v, out, workspace, *, num_q, num_kv, start_pos, sub_n, 
         workspace.numel() * workspace.element_size(), _stream(stream)), "qkv_decode_attn_q8")
 
 
+def decode_attn_q8k_tq3v_workspace(num_q, num_kv, sub_n, n_keys, device) -> torch.Tensor:
+    """Zero-filled workspace for decode_attn_q8k_tq3v."""
+    n = int(lib().qkv_decode_attn_q8k_tq3v_workspace_bytes(num_q, num_kv, sub_n, n_keys))
+    return torch.zeros(n, dtype=torch.uint8, device=device)
+
+
+def decode_attn_q8k_tq3v(q, k, v, out, workspace, *, num_q, num_kv, start_pos, sub_n, scale,
+                         head_dim=256, stream=None) -> None:
+    """V-only TurboQuant (reference TQ_KEYS_Q8 mode): keys in Q8_0 blocks, values
+    in TQ3 blocks; one fused decode launch with the merge inside it."""
+    check(lib().qkv_decode_attn_q8k_tq3v(
+        _dev_ptr(q, "q"), _dev_ptr(k, "k"), _dev_ptr(v, "v"), _dev_ptr(out, "out"), num_q,
+        num_kv, head_dim, start_pos, sub_n, float(scale), _dev_ptr(workspace, "workspace"),
+        workspace.numel() * workspace.element_size(), _stream(stream)), "qkv_decode_attn_q8k_tq3v")
+
+
 # ---------------------------------------------------------------------------
 # paged caches (per-slot int32 block tables)
 # ---------------------------------------------------------------------------

@@ -116,3 +116,21 @@ def test_decode_workspace_for_the_longest_call_covers_shorter_ones(L):
                     if sub_n <= n <= n_max:
                         assert L.qkv_decode_attn_tq3_workspace_bytes(num_q, num_kv, sub_n, n) <= top, \
                             (num_q, num_kv, sub_n, n, n_max)
+
+
+def test_mixed_decode_argument_errors_without_gpu(L):
+    """Q8_0-key / TQ3-value decode: the Q8 decode's workspace size and error
+    order (shape, then pointers, alignment, workspace); no call reaches a launch."""
+    buf = ctypes.create_string_buffer(4096)
+    p = (ctypes.addressof(buf) + 255) & ~255
+    n = L.qkv_decode_attn_q8k_tq3v_workspace_bytes(16, 4, 1, 4097)
+    assert n == L.qkv_decode_attn_q8_workspace_bytes(16, 4, 1, 4097) > 0
+
+    def call(q=p, hd=256, ws=p, wsb=n - 1, num_q=16):
+        return L.qkv_decode_attn_q8k_tq3v(q, p, p, p, num_q, 4, hd, 4096, 1, 1 / 16, ws, wsb, None)
+    assert call(q=None) == -2
+    assert call(hd=128) in (-1, -3)
+    assert call(num_q=18) in (-1, -3)          # 18 q heads over 4 kv heads
+    assert call(q=p + 2) == -4
+    assert call(ws=None) == -7
+    assert call() == -7                        # one byte short

@@ -194,3 +194,25 @@ def test_merge_skips_empty_and_nonfinite_splits():
                            np.zeros((1, 1, 2, hd), np.float32), num_q=1, num_kv=1, hd=hd,
                            sub_n=1, sub_n_max=1, k_splits=2)
     assert np.all(z == 0)
+
+
+def test_q8k_tq3v_vs_fp64_and_closed_form():
+    """Mixed-format oracle (Q8_0 keys, TQ3 values) against attn_ref_f64 over the
+    same decoded rows (values rounded to fp16 for it: within 2e-3), and the
+    closed form: with every key equal, each query's output is the mean of the
+    visible values."""
+    rng = np.random.default_rng(41)
+    n, nq, nkv, sub_n = 300, 16, 4, 3
+    k16, v16 = kv_f16(rng, n, nkv, 256), kv_f16(rng, n, nkv, 256)
+    kq, vt = O.q8_encode(k16), O.tq3_encode(v16)
+    q = q_f16(rng, sub_n, nq, 256)
+    kw = dict(num_q=nq, num_kv=nkv, hd=256, start_pos=n - sub_n, sub_n=sub_n, scale=1 / 16)
+    got = O.attn_q8k_tq3v_f64(q, kq, vt, **kw)
+    ref = O.attn_ref_f64(q, O.q8_decode(kq), O.tq3_decode(vt), **kw)
+    assert rel_err(got, ref) < 2e-3
+    same = O.q8_encode(np.tile(k16[:1], (n, 1, 1)))
+    flat = O.attn_q8k_tq3v_f64(q, same, vt, **kw)
+    v32 = O.tq3_decode_f32(vt).astype(np.float64).reshape(n, nkv, 256)
+    for t in range(sub_n):
+        mean = v32[:n - sub_n + t + 1].mean(axis=0)               # [nkv][256]
+        assert np.allclose(flat[t], np.repeat(mean, nq // nkv, axis=0), rtol=1e-9, atol=1e-12)
