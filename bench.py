@@ -242,6 +242,34 @@ def secondary(torch, kvcache, dev, stream):
                 "the TQ3 cache (131088 keys, the block's own keys read back quantized) through "
                 "qkv_decode_attn_tq3 with sub_n 16 (4 queries per workgroup pass); "
                 "prefill_path_us: the same through qkv_prefill_attn_tq3 in verify mode"}
+
+    # ---- V-only TurboQuant (keys Q8_0, values TQ3): one query over 32768 keys
+    # of config 3's head shape; 8 layers x 2 cache sets rotated ----
+    ctx, n_caches = 32768, 16
+    caches = []
+    for _ in range(n_caches):
+        kb = kvcache.q8_blocks(ctx * NUM_KV * HD // 32, dev)
+        vb = kvcache.tq3_blocks(ctx * NUM_KV * HD // 128, dev)
+        kvcache.q8_append(rnd(ctx, NUM_KV, HD), kb)
+        kvcache.tq3_append(rnd(ctx, NUM_KV, HD), vb)
+        caches.append((kb, vb))
+    q = rnd(1, NUM_Q, HD)
+    o = torch.empty(1, NUM_Q, HD, dtype=torch.float16, device=dev)
+    wsm = kvcache.decode_attn_q8k_tq3v_workspace(NUM_Q, NUM_KV, 1, ctx, dev)
+
+    def mixed_layer(i=0):
+        kb, vb = caches[i % n_caches]
+        kvcache.decode_attn_q8k_tq3v(q, kb, vb, o, wsm, num_q=NUM_Q, num_kv=NUM_KV,
+                                     start_pos=ctx - 1, sub_n=1, scale=scale)
+    ms = _time(torch, stream, mixed_layer, 320)
+    mbytes = ctx * NUM_KV * (8 * 36 + 2 * 52) + NUM_Q * HD * 2 * 2   # Q8_0 keys, TQ3 values
+    out["f4_mixed_decode_32k"] = {
+        "us_per_launch": round(ms * 1e3, 3), "bytes": mbytes,
+        "gbps": round(mbytes / (ms * 1e-3) / 1e9, 1),
+        "frac": round(mbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+        "note": "qkv_decode_attn_q8k_tq3v: one query (16 q / 4 kv heads, d 256) over 32768 keys, "
+                "keys Q8_0 (288 B per kv head and token), values TQ3 (104 B); 16 caches rotated"}
+    del caches
     return out
 
 
