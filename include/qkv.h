@@ -186,7 +186,7 @@ int qkv_decode_attn_tq3(const uint16_t* q, const qkv_block_tq3* k, const qkv_blo
                         hipStream_t stream);
 
 /* Fast path for qkv_attn_split_q8 + qkv_attn_split_merge over the Q8_0 cache
- * (model.cuh:5655-5665; attention.cuh:2633-2801 and 1837-1891) in ONE launch:
+ * (decode launch model.cuh:2430-2463; attention.cuh:2633-2801 and 1837-1891) in ONE launch:
  * chunks of 128*k keys, records merged inside the kernel as for
  * qkv_decode_attn_tq3 (values are not rotated).  Same argument meaning as
  * qkv_attn_split_q8 (no sink/window/tree rules, as in the reference) with the
