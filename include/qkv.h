@@ -50,7 +50,8 @@ typedef enum qkv_status {
   QKV_ERR_ALIGN = -4,       /* pointer not aligned as documented                       */
   QKV_ERR_DEVICE = -5,      /* no usable gfx950 device / HIP runtime error             */
   QKV_ERR_LAUNCH = -6,      /* kernel launch failed                                    */
-  QKV_ERR_WORKSPACE = -7    /* workspace missing or smaller than the query says         */
+  QKV_ERR_WORKSPACE = -7,   /* workspace missing or smaller than the query says         */
+  QKV_ERR_TIMEOUT = -8      /* an in-kernel merge timed out; reset the workspace        */
 } qkv_status;
 
 /* Library version (major*10000 + minor*100 + patch). */
@@ -184,6 +185,25 @@ int qkv_decode_attn_tq3(const uint16_t* q, const qkv_block_tq3* k, const qkv_blo
                         int sub_n, float scale, int sink_tok, int window_tok,
                         const uint32_t* tree_mask, void* workspace, size_t workspace_bytes,
                         hipStream_t stream);
+
+/* Health of a fast-path decode workspace (qkv_decode_attn_tq3, _q8, _q8k_tq3v,
+ * _tq3_paged).  The in-kernel merge waits for the records of its launch with
+ * a bounded poll; if the bound runs out (a launch starved of GPU time for
+ * seconds), the affected output rows are written as NaN and the workspace
+ * header keeps an error word, after which every later call on that workspace
+ * writes NaN rows until it is reset.  No counterpart in the reference (its
+ * merge is a separate launch, attention.cuh:1837-1891).
+ * qkv_decode_workspace_status synchronises `stream`, then returns QKV_OK or
+ * QKV_ERR_TIMEOUT.  qkv_decode_workspace_reset zero-fills `bytes` bytes of
+ * the workspace on `stream` (a fill kernel, no memset node: safe to capture). */
+int qkv_decode_workspace_status(const void* workspace, hipStream_t stream);
+int qkv_decode_workspace_reset(void* workspace, size_t bytes, hipStream_t stream);
+
+/* Test hook, no counterpart in the reference: the merger poll limit of every
+ * later fast-path decode launch in this process (limit >= 0; a negative value
+ * restores the default of 2^22 polls).  A limit of 0 makes every merger time
+ * out, so the error path can be exercised without a GPU fault or hang. */
+int qkv_debug_set_merge_spin_limit(int limit);
 
 /* Fast path for qkv_attn_split_q8 + qkv_attn_split_merge over the Q8_0 cache
  * (decode launch model.cuh:2430-2463; attention.cuh:2633-2801 and 1837-1891) in ONE launch:

@@ -18,6 +18,7 @@ QKV_OK = 0
 STATUS_NAMES = {
     0: "QKV_OK", -1: "QKV_ERR_INVALID", -2: "QKV_ERR_NULL", -3: "QKV_ERR_UNSUPPORTED",
     -4: "QKV_ERR_ALIGN", -5: "QKV_ERR_DEVICE", -6: "QKV_ERR_LAUNCH", -7: "QKV_ERR_WORKSPACE",
+    -8: "QKV_ERR_TIMEOUT",
 }
 
 
@@ -59,6 +60,9 @@ SIGNATURES = {
     "qkv_decode_attn_tq3_paged_workspace_bytes": (_SZ, [_I, _I, _I, _I]),
     "qkv_decode_attn_tq3_paged": (_I, [_P, _P, _P, _P, _I, _I, _I, _I, _P, _I, _I, _I, _P, _I,
                                       _F, _P, _SZ, _P]),
+    "qkv_decode_workspace_status": (_I, [_P, _P]),
+    "qkv_decode_workspace_reset": (_I, [_P, _SZ, _P]),
+    "qkv_debug_set_merge_spin_limit": (_I, [_I]),
     "qkv_prefill_attn_tq3_workspace_bytes": (_SZ, [_I, _I, _I, _I]),
     "qkv_prefill_attn_tq3": (_I, [_P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _F, _P, _SZ, _P]),
 }

@@ -9,20 +9,30 @@ namespace qkv {
 constexpr float kLn2 = 0.69314718055994531f;
 constexpr float kLog2e = 1.44269504088896341f;
 
-// Fast-path workspace: kWsHeaderBytes reserved at its start, then the record
-// scalars {m, l, tag of 128-block unit 0, tag of unit 1} (kRecMlBytes each)
-// and the record rows.  A tag is kTagValid while its record is waiting for
-// that unit's merger and 0 otherwise (the state of a zero-filled workspace).
+// Fast-path workspace: kWsHeaderBytes at its start, then the record scalars
+// {m, l, tag of 128-block unit 0, tag of unit 1} (kRecMlBytes each) and the
+// record rows.  A tag is kTagValid while its record is waiting for that unit's
+// merger and 0 otherwise (the state of a zero-filled workspace).  Header word
+// kWsErrorWord is 0 while the workspace is consistent; a merger whose bounded
+// wait ran out sets it to kWsErrorTimeout, and from then on every merge of a
+// launch on that workspace writes NaN rows until the workspace is zero-filled
+// again (records it could not account for may still carry set tags).
 constexpr int kWsHeaderBytes = 256;
 constexpr int kRecMlBytes = 16;
 constexpr uint32_t kTagValid = 1u;
+constexpr int kWsErrorWord = 0;
+constexpr int kWsErrorTimeout = 1;
+// Poll limit of a merger waiting for the records of one launch (each poll
+// sleeps ~64 cycles after two memory round trips; the default limit is
+// seconds, far beyond any legitimate wait).
+constexpr int kMergeSpinLimit = 1 << 22;
 
 struct AttnArgs {
   const uint16_t* q;        // [sub_n][num_q][256] fp16
   const uint32_t* k;        // slot-base key cache (blocks viewed as dwords)
   const uint32_t* v;        // slot-base value cache
-  uint32_t kv_bytes;        // readable bytes of each cache from its base (buffer range)
-  uint32_t v_bytes;         // value cache range when its format differs from the keys' (else unused)
+  uint64_t kv_bytes;        // readable bytes of each cache from its base
+  uint64_t v_bytes;         // value cache extent when its format differs from the keys' (else unused)
   int num_q, num_kv;
   int start_pos, sub_n, sub_n_max;
   int qpw;                  // queries per workgroup (MFMA columns = qpw * gqa <= 16)
@@ -49,9 +59,23 @@ struct AttnArgs {
   // fast-path workspace
   float* ws_ml;             // [num_q][sub_n][n_slots] x {m (log2 units), l, tag0, tag1}
   float* ws_o;              // [num_q][sub_n][n_slots][256] rotated coordinates
-  int* ws_header;           // reserved (kWsHeaderBytes)
+  int* ws_header;           // kWsHeaderBytes; word kWsErrorWord: sticky merge error
   uint32_t ws_ml_bytes, ws_o_bytes;
+  int spin_limit;           // merger poll limit (kMergeSpinLimit unless a test lowers it)
 };
+
+// Buffer resource over bytes [off, extent) of a cache, rebased at the 64-bit
+// byte offset `off` (wave-uniform) so that the in-tile offsets of a load stay
+// small: caches past 4 GiB are addressed exactly.  Bytes at or past `extent`
+// read as zero (the buffer range check), also for a tile that starts there.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t cache_rsrc(const void* base, uint64_t off,
+                                                             uint64_t extent) {
+  const bool in = off < extent;
+  const uint64_t rem = in ? extent - off : 0;
+  char* b = const_cast<char*>(static_cast<const char*>(base)) + (in ? off : 0);
+  return __builtin_amdgcn_make_buffer_rsrc(b, 0, (uint32_t)(rem < 0xffffffffull ? rem : 0xffffffffull),
+                                           0x00020000);
+}
 
 // ---- DPP wave reductions (result broadcast through lane 63) -------------
 template <int CTRL, int ROW_MASK = 0xf>

@@ -14,10 +14,14 @@
 // them (the other unit of the same records has tag words of its own), so that
 // after a launch every tag is clear again: the state the next launch, ordered
 // after this one on the stream, starts from, and the state of a zero-filled
-// workspace.  No counter, atomic or epoch is involved, and no workgroup pays an
-// L2 write-back or invalidate (what agent-scope fences cost on this GPU).
+// workspace.  No counter or epoch is involved, and no workgroup pays an L2
+// write-back or invalidate (what agent-scope fences cost on this GPU).
 // Only mergers wait, and they are dispatched after every other workgroup, so
-// progress does not depend on workgroup co-residency.
+// progress does not depend on workgroup co-residency.  Their wait is bounded:
+// a merger that runs out of polls writes NaN rows and sets the sticky error
+// word of the workspace header (one relaxed agent-scope store), which the host
+// reads with qkv_decode_workspace_status and clears with
+// qkv_decode_workspace_reset.
 #pragma once
 #include "attn_common.h"
 #include "qkv_device.h"
@@ -72,11 +76,6 @@ __device__ inline int share_slot(const AttnArgs& p, int g, int& first, int& coun
   return -1;
 }
 
-// Poll limit of a merger waiting for the records of one launch (each poll
-// sleeps ~64 cycles after two memory round trips; the limit is seconds, far
-// beyond any legitimate wait).
-constexpr int kMergeSpinLimit = 1 << 22;
-
 // Merger thread layout for a THREADS-thread workgroup: slices of 32 threads
 // (one dim quad of a 128-block each), 128/slices records per thread
 // (n_chunks <= 128).  The reduction area holds one 128-float partial per wave.
@@ -87,6 +86,13 @@ struct MergeLayout {
   static constexpr int kWaves = THREADS / 64;
   static constexpr int kRedFloats = kWaves * 128;
 };
+
+// NaN rows for unit (query t, q head qh, 128-block blk): threads 0..15 store 8 halves each.
+__device__ __forceinline__ void write_nan_unit(const AttnArgs& p, int t, int qh, int blk, uint16_t* out) {
+  if (threadIdx.x < 16)
+    *reinterpret_cast<uint4*>(out + ((long)t * p.num_q + qh) * 256 + blk * 128 + threadIdx.x * 8) =
+        make_uint4(0x7e007e00u, 0x7e007e00u, 0x7e007e00u, 0x7e007e00u);
+}
 
 // Merge the n <= 128 records base .. base+n-1 of one unit (q head qh, query
 // t, 128-block blk) and write its fp16 output  o = sum w_c o_c / sum w_c l_c,
@@ -100,8 +106,9 @@ struct MergeLayout {
 //    its rows, and folds its two slices together (lanes l and l^32); the
 //    waves' partials meet once in LDS, where 16 threads sum them, normalise,
 //    rotate and store.
-// Returns false (and writes nothing) if the records did not all appear within
-// the poll limit.
+// If the records did not all appear within the poll limit: clears the tags it
+// did see, writes NaN rows, records the error in the workspace header and
+// returns false.
 template <int THREADS, bool ROTATE>
 __device__ bool merge_unit(float* red, f2_t* mls, const AttnArgs& p, __amdgpu_buffer_rsrc_t rml,
                            __amdgpu_buffer_rsrc_t ro, long base, int n, int qh, int t, int blk,
@@ -114,7 +121,7 @@ __device__ bool merge_unit(float* red, f2_t* mls, const AttnArgs& p, __amdgpu_bu
   const int sl = tid >> 5, dq = tid & 31;
   bool seen = tid >= n;
   bool complete = false;
-  for (int spins = 0; spins < kMergeSpinLimit; spins++) {
+  for (int spins = 0; spins < p.spin_limit; spins++) {
     if (!seen) {
       const f4_t r = __builtin_amdgcn_raw_buffer_load_b128(
           rml, (uint32_t)((base + tid) * kRecMlBytes), 0, kCoherent);
@@ -129,7 +136,17 @@ __device__ bool merge_unit(float* red, f2_t* mls, const AttnArgs& p, __amdgpu_bu
     }
     __builtin_amdgcn_s_sleep(1);
   }
-  if (!complete) return false;
+  if (!complete) {
+    if (tid < n && seen)   // the tags this merger saw will not be read again
+      __builtin_amdgcn_raw_buffer_store_b32(0u, rml, (uint32_t)((base + tid) * kRecMlBytes + 8 + 4 * blk),
+                                            0, kCoherent);
+    write_nan_unit(p, t, qh, blk, out);
+    if (tid == 0)
+      __hip_atomic_store(p.ws_header + kWsErrorWord, kWsErrorTimeout, __ATOMIC_RELAXED,
+                         __HIP_MEMORY_SCOPE_AGENT);
+    __syncthreads();   // mls is reused by the next unit
+    return false;
+  }
   if (tid < n)   // this unit has seen its records: clear their tags for the next launch
     __builtin_amdgcn_raw_buffer_store_b32(0u, rml, (uint32_t)((base + tid) * kRecMlBytes + 8 + 4 * blk), 0,
                                           kCoherent);
@@ -277,6 +294,9 @@ __device__ void merge_phase(float* red, f2_t* mls, const AttnArgs& p, __amdgpu_b
   const int n_mergers = min(n_units, (int)gridDim.x);
   const int mid = (int)blockIdx.x - ((int)gridDim.x - n_mergers);
   if (mid < 0) return;
+  // a workspace left inconsistent by an earlier timeout yields NaN rows until it is reset
+  const bool poisoned = __hip_atomic_load(p.ws_header + kWsErrorWord, __ATOMIC_RELAXED,
+                                          __HIP_MEMORY_SCOPE_AGENT) != 0;
   for (int u = mid; u < n_units; u += n_mergers) {
     const int blk = u & 1, qh = (u >> 1) % p.num_q, t = (u >> 1) / p.num_q;
     long base = rec_index(p, qh, t, 0);
@@ -286,7 +306,10 @@ __device__ void merge_phase(float* red, f2_t* mls, const AttnArgs& p, __amdgpu_b
       slot_shares(p, t, first, n);
       base = rec_index(p, qh, 0, first);
     }
-    if (!merge_unit<THREADS, ROTATE>(red, mls, p, rml, ro, base, n, qh, t, blk, out)) break;
+    if (poisoned)
+      write_nan_unit(p, t, qh, blk, out);
+    else
+      merge_unit<THREADS, ROTATE>(red, mls, p, rml, ro, base, n, qh, t, blk, out);
   }
 }
 

@@ -4,7 +4,10 @@
 // splits; splits with non-finite m or l <= 0 are skipped; out = sum w*o /
 // sum w*l with w = exp(m_s - M), 0 when the sum is 0; fp16 output
 // [t][q_head][256].  One workgroup per (q head, t), one thread per dim.
+#include <algorithm>
+
 #include "attn_common.h"
+#include "qkv_launch.h"
 #include "qkv_device.h"
 
 namespace qkv {
@@ -36,6 +39,21 @@ hipError_t launch_split_merge(const float* m, const float* l, const float* o, ui
   dim3 grid(num_q, sub_n);
   hipLaunchKernelGGL(split_merge_kernel, grid, dim3(256), 0, stream, m, l, o, out, num_q,
                      sub_n_max, k_splits);
+  return hipGetLastError();
+}
+
+// Zero-fill by a kernel, so that a caller that captures the reset into a HIP
+// graph records a kernel node rather than a memset node.
+__global__ __launch_bounds__(256) void fill_zero_kernel(uint32_t* __restrict__ p, size_t n_words) {
+  for (size_t i = blockIdx.x * 256ul + threadIdx.x; i < n_words; i += (size_t)gridDim.x * 256)
+    p[i] = 0u;
+}
+
+hipError_t launch_fill_zero(void* p, size_t bytes, hipStream_t stream) {
+  const size_t n = bytes / 4;
+  const unsigned blocks = (unsigned)std::min<size_t>((n + 255) / 256, 4096);
+  hipLaunchKernelGGL(fill_zero_kernel, dim3(blocks), dim3(256), 0, stream,
+                     static_cast<uint32_t*>(p), n);
   return hipGetLastError();
 }
 

@@ -87,13 +87,18 @@ struct TileQ8 {
                        // TQ3 values: 128-block lane>>5 (norm + 12 code dwords in v[0..3])
 };
 
+// ts: the tile's first key (wave-uniform); the buffer resources are rebased at
+// its row (64-bit byte offsets)
 template <bool VTQ3>
-__device__ __forceinline__ void load_tile_q8(__amdgpu_buffer_rsrc_t rk, __amdgpu_buffer_rsrc_t rv,
-                                             int ts, int nkv, int h, int lane, int row, int col,
-                                             TileQ8& t) {
+__device__ __forceinline__ void load_tile_q8(const AttnArgs& p, int ts, int nkv, int h, int lane,
+                                             int row, int col, TileQ8& t) {
+  const uint64_t row0 = (uint64_t)(uint32_t)ts * (uint32_t)nkv;
+  const __amdgpu_buffer_rsrc_t rk = cache_rsrc(p.k, row0 * kRowBytes, p.kv_bytes);
+  const __amdgpu_buffer_rsrc_t rv = VTQ3 ? cache_rsrc(p.v, row0 * kTq3RowBytes, p.v_bytes)
+                                         : cache_rsrc(p.v, row0 * kRowBytes, p.kv_bytes);
 #pragma unroll
   for (int g = 0; g < 2; g++) {
-    const uint32_t off = (uint32_t)((ts + 16 * g + col) * nkv + h) * kRowBytes + 72u * row;
+    const uint32_t off = (uint32_t)((16 * g + col) * nkv + h) * kRowBytes + 72u * row;
 #pragma unroll
     for (int i = 0; i < 4; i++) {
       const u4_t c = __builtin_amdgcn_raw_buffer_load_b128(rk, off + 16 * i, 0, 0);
@@ -106,13 +111,13 @@ __device__ __forceinline__ void load_tile_q8(__amdgpu_buffer_rsrc_t rk, __amdgpu
   }
   if constexpr (VTQ3) {
     const uint32_t voff =
-        (uint32_t)((ts + (lane & 31)) * nkv + h) * kTq3RowBytes + 52u * (uint32_t)(lane >> 5);
+        (uint32_t)((lane & 31) * nkv + h) * kTq3RowBytes + 52u * (uint32_t)(lane >> 5);
 #pragma unroll
     for (int i = 0; i < 3; i++) t.v[i] = __builtin_amdgcn_raw_buffer_load_b128(rv, voff + 16 * i, 0, 0);
     t.v[3][0] = __builtin_amdgcn_raw_buffer_load_b32(rv, voff + 48, 0, 0);
   } else {
     const uint32_t voff =
-        (uint32_t)((ts + (lane & 31)) * nkv + h) * kRowBytes + 144u * (uint32_t)(lane >> 5);
+        (uint32_t)((lane & 31) * nkv + h) * kRowBytes + 144u * (uint32_t)(lane >> 5);
 #pragma unroll
     for (int i = 0; i < 9; i++) t.v[i] = __builtin_amdgcn_raw_buffer_load_b128(rv, voff + 16 * i, 0, 0);
   }
@@ -191,10 +196,6 @@ __global__ __launch_bounds__(kThreads, 2) void q8_attn_kernel(AttnArgs p, uint16
     hi = has_work ? min(lo + p.chunk_keys, active_end) : lo;
   }
 
-  const __amdgpu_buffer_rsrc_t rk =
-      __builtin_amdgcn_make_buffer_rsrc(const_cast<uint32_t*>(p.k), 0, p.kv_bytes, kBufferRsrcWord3);
-  const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(
-      const_cast<uint32_t*>(p.v), 0, VTQ3 ? p.v_bytes : p.kv_bytes, kBufferRsrcWord3);
 
   // query operand, slice s: head `col`, dims (2*row + (s>>2))*32 + 8*(s&3) + i
   h8_t qa[8];
@@ -230,7 +231,7 @@ __global__ __launch_bounds__(kThreads, 2) void q8_attn_kernel(AttnArgs p, uint16
   bool first = true;
   for (int ts = lo + wave * kTile; ts < hi; ts += kWaves * kTile) {
     TileQ8 tr;
-    load_tile_q8<VTQ3>(rk, rv, ts, p.num_kv, h, lane, row, col, tr);
+    load_tile_q8<VTQ3>(p, ts, p.num_kv, h, lane, row, col, tr);
 
     // ---- scores: D rows = keys 16g + 4*row + r, D col = head `col`
     f4_t sa[2];

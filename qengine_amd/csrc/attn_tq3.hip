@@ -221,15 +221,18 @@ struct TileRegs {
   float kn[4][2];        // key block norms, group g, block j
 };
 
-// prow: cache row of the tile's first key (64 consecutive rows)
-__device__ __forceinline__ void load_tile(__amdgpu_buffer_rsrc_t rk, __amdgpu_buffer_rsrc_t rv,
-                                          int prow, int nkv, int h, int lane, int row, int col,
-                                          TileRegs& tr) {
+// prow: cache row of the tile's first key (64 consecutive rows, wave-uniform);
+// the buffer resources are rebased at that row (64-bit byte offset)
+__device__ __forceinline__ void load_tile(const AttnArgs& p, int prow, int nkv, int h, int lane,
+                                          int row, int col, TileRegs& tr) {
+  const uint64_t off0 = (uint64_t)(uint32_t)prow * (uint32_t)nkv * 104u;
+  const __amdgpu_buffer_rsrc_t rk = cache_rsrc(p.k, off0, p.kv_bytes);
+  const __amdgpu_buffer_rsrc_t rv = cache_rsrc(p.v, off0, p.kv_bytes);
   // keys first (group by group): the score MFMAs of group g only wait for
   // group g, and values arrive while the scores are computed
 #pragma unroll
   for (int g = 0; g < 4; g++) {
-    const uint32_t krow = (uint32_t)((prow + 16 * g + col) * nkv + h) * 104u;
+    const uint32_t krow = (uint32_t)((16 * g + col) * nkv + h) * 104u;
 #pragma unroll
     for (int j = 0; j < 2; j++) {
       const u3_t c = __builtin_amdgcn_raw_buffer_load_b96(rk, krow + 52 * j + 4 + 12 * row, 0, 0);
@@ -239,7 +242,7 @@ __device__ __forceinline__ void load_tile(__amdgpu_buffer_rsrc_t rk, __amdgpu_bu
       tr.kn[g][j] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rk, krow + 52 * j, 0, 0));
     }
   }
-  const uint32_t vrow = (uint32_t)((prow + lane) * nkv + h) * 104u;
+  const uint32_t vrow = (uint32_t)(lane * nkv + h) * 104u;
 #pragma unroll
   for (int i = 0; i < 6; i++) tr.vr[i] = __builtin_amdgcn_raw_buffer_load_b128(rv, vrow + 16 * i, 0, 0);
   tr.vr6 = __builtin_amdgcn_raw_buffer_load_b64(rv, vrow + 96, 0, 0);
@@ -437,10 +440,6 @@ __global__ __launch_bounds__(kThreads, 1) void tq3_attn_kernel(AttnArgs p, uint1
   // The query is loaded and rotated before any tile load is issued: a query
   // load issued after the tile loads of the whole chip would wait behind
   // them in the memory queues.
-  const __amdgpu_buffer_rsrc_t rk =
-      __builtin_amdgcn_make_buffer_rsrc(const_cast<uint32_t*>(p.k), 0, p.kv_bytes, kBufferRsrcWord3);
-  const __amdgpu_buffer_rsrc_t rv =
-      __builtin_amdgcn_make_buffer_rsrc(const_cast<uint32_t*>(p.v), 0, p.kv_bytes, kBufferRsrcWord3);
   // 32 WHTs of 128 (16 columns x 2 blocks), 16 lanes each
   const int q_wht = threadIdx.x >> 4;
   const int q_part = threadIdx.x & 15;
@@ -543,9 +542,9 @@ __global__ __launch_bounds__(kThreads, 1) void tq3_attn_kernel(AttnArgs p, uint1
   // tiles arrive in the first half of the stream and are computed while the
   // second waves' tiles are still in flight.
   TileRegs tr;
-  if (wave < 4) load_tile(rk, rv, wave_tile_row(ts0), p.num_kv, h, lane, row, col, tr);
+  if (wave < 4) load_tile(p, wave_tile_row(ts0), p.num_kv, h, lane, row, col, tr);
   __syncthreads();
-  if (wave >= 4) load_tile(rk, rv, wave_tile_row(ts0), p.num_kv, h, lane, row, col, tr);
+  if (wave >= 4) load_tile(p, wave_tile_row(ts0), p.num_kv, h, lane, row, col, tr);
   // qa[s], slice s = 4j+u: column `col`, element i = dim 128j + 8(4*row+u) + i
   h8_t qa[8];
   {
@@ -690,7 +689,7 @@ __global__ __launch_bounds__(kThreads, 1) void tq3_attn_kernel(AttnArgs p, uint1
   if (ts0 < hi) {
     tile_body(std::true_type{}, ts0);
     for (int ts = ts0 + kStep; ts < hi; ts += kStep) {
-      load_tile(rk, rv, wave_tile_row(ts), p.num_kv, h, lane, row, col, tr);
+      load_tile(p, wave_tile_row(ts), p.num_kv, h, lane, row, col, tr);
       tile_body(std::false_type{}, ts);
     }
   } else {

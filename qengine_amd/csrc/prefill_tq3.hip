@@ -106,17 +106,21 @@ struct RawTile {
 
 // Loads of history tile ti (rows past start_pos read as zero; a tile index
 // past the history loads nothing useful and is never stored).
+// k0: the tile's first key (workgroup-uniform); the buffer resources are
+// rebased at its row (64-bit byte offsets).
 template <int NT>
-__device__ __forceinline__ void load_raw(RawTile<NT>& r, __amdgpu_buffer_rsrc_t rk,
-                                         __amdgpu_buffer_rsrc_t rv, int k0, int num_kv, int h,
-                                         int tid) {
+__device__ __forceinline__ void load_raw(RawTile<NT>& r, const PrefillArgs& p, int k0, int num_kv,
+                                         int h, int tid) {
+  const uint64_t off0 = (uint64_t)(uint32_t)k0 * (uint32_t)num_kv * 104u;
+  const __amdgpu_buffer_rsrc_t rk = cache_rsrc(p.k_cache, off0, p.kv_bytes);
+  const __amdgpu_buffer_rsrc_t rv = cache_rsrc(p.v_cache, off0, p.kv_bytes);
 #pragma unroll
   for (int j = 0; j < RawTile<NT>::kPer; j++) {
     const int i = tid + NT * j;
     const int tv = i >= kKeys * 13;
     const int jj = i - tv * kKeys * 13;
     const int key = jj / 13, piece = jj - key * 13;
-    const uint32_t off = (uint32_t)(((long)(k0 + key) * num_kv + h) * 104 + piece * 8);
+    const uint32_t off = (uint32_t)((key * num_kv + h) * 104 + piece * 8);
     r.d[j] = (i < kRawPieces) ? __builtin_amdgcn_raw_buffer_load_b64(tv ? rv : rk, off, 0, 0)
                               : u2_t{0u, 0u};
   }
@@ -266,10 +270,6 @@ __global__ __launch_bounds__(64 * WAVES, 1) void prefill_attn_kernel(PrefillArgs
             h8_t, __builtin_amdgcn_raw_buffer_load_b128(rq, base + (b * 128 + 16 * s + 8 * hh) * 2, 0, 0));
   }
 
-  const __amdgpu_buffer_rsrc_t rk =
-      __builtin_amdgcn_make_buffer_rsrc(const_cast<uint32_t*>(p.k_cache), 0, p.kv_bytes, kBufferRsrcWord3);
-  const __amdgpu_buffer_rsrc_t rv =
-      __builtin_amdgcn_make_buffer_rsrc(const_cast<uint32_t*>(p.v_cache), 0, p.kv_bytes, kBufferRsrcWord3);
 
   f16x_t acc[8];
 #pragma unroll
@@ -281,7 +281,7 @@ __global__ __launch_bounds__(64 * WAVES, 1) void prefill_attn_kernel(PrefillArgs
 
   // the first tile's raw rows (history tiles only; a chunk tile loads nothing)
   RawTile<NT> raw;
-  if (tlo < min(thi, th)) load_raw(raw, rk, rv, tlo * kKeys, p.num_kv, h, tid);
+  if (tlo < min(thi, th)) load_raw(raw, p, tlo * kKeys, p.num_kv, h, tid);
 
   for (int ti = tlo; ti < thi; ti++) {
     const bool cached = ti < th;
@@ -293,7 +293,7 @@ __global__ __launch_bounds__(64 * WAVES, 1) void prefill_attn_kernel(PrefillArgs
       // the previous tile; rows past start_pos read as zero (buffer range)
       store_raw(raw, lds, tid);
       // the next history tile's rows go out now and arrive during this tile
-      if (ti + 1 < min(thi, th)) load_raw(raw, rk, rv, (ti + 1) * kKeys, p.num_kv, h, tid);
+      if (ti + 1 < min(thi, th)) load_raw(raw, p, (ti + 1) * kKeys, p.num_kv, h, tid);
       __syncthreads();
       uint32_t ac[4] = {lane4, lane4, lane4, lane4};
       // keys: item (key, quarter): block quarter >> 1, codes 64*(quarter & 1) ..

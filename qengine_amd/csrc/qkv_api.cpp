@@ -6,6 +6,7 @@
 
 #include <hip/hip_runtime.h>
 
+#include <atomic>
 #include <cstring>
 #include <mutex>
 
@@ -24,6 +25,7 @@ inline int launch_status(hipError_t e) { return e == hipSuccess ? QKV_OK : QKV_E
 
 std::mutex g_init_mu;
 bool g_init_ok[64];
+std::atomic<int> g_spin_limit{qkv::kMergeSpinLimit};
 
 }  // namespace
 
@@ -41,6 +43,7 @@ const char* qkv_status_string(int s) {
     case QKV_ERR_DEVICE: return "no usable gfx950 device";
     case QKV_ERR_LAUNCH: return "kernel launch failed";
     case QKV_ERR_WORKSPACE: return "workspace missing or too small";
+    case QKV_ERR_TIMEOUT: return "in-kernel merge timed out; reset the workspace";
     default: return "unknown status";
   }
 }
@@ -224,8 +227,7 @@ int qkv_attn_split_tq3(const uint16_t* q, const qkv_block_tq3* k, const qkv_bloc
   a.qpw = 16 / (num_q / num_kv);   // queries share the MFMA columns
   {
     const uint64_t extent = (uint64_t)(start_pos + sub_n) * num_kv * 104;
-    if (extent > 0x7fffffffULL) return QKV_ERR_UNSUPPORTED;   // 32-bit buffer offsets
-    a.kv_bytes = (uint32_t)extent;
+    a.kv_bytes = extent;
   }
   a.active_end_max = active_end_max;
   a.k_splits = k_splits;
@@ -264,8 +266,7 @@ int qkv_attn_split_q8(const uint16_t* q, const qkv_block_q8* k, const qkv_block_
   a.sub_n_max = sub_n_max;
   {
     const uint64_t extent = (uint64_t)(start_pos + sub_n) * num_kv * 8 * sizeof(qkv_block_q8);
-    if (extent > 0x7fffffffULL) return QKV_ERR_UNSUPPORTED;   // 32-bit buffer offsets
-    a.kv_bytes = (uint32_t)extent;
+    a.kv_bytes = extent;
   }
   a.active_end_max = active_end_max;
   a.k_splits = k_splits;
@@ -361,8 +362,7 @@ int qkv_decode_attn_tq3(const uint16_t* q, const qkv_block_tq3* k, const qkv_blo
   a.qpw = 16 / (num_q / num_kv);   // queries share the MFMA columns
   {
     const uint64_t extent = (uint64_t)n_keys * num_kv * 104;
-    if (extent > 0x7fffffffULL) return QKV_ERR_UNSUPPORTED;   // 32-bit buffer offsets
-    a.kv_bytes = (uint32_t)extent;
+    a.kv_bytes = extent;
   }
   a.active_end_max = n_keys;
   a.k_splits = 1;
@@ -374,6 +374,7 @@ int qkv_decode_attn_tq3(const uint16_t* q, const qkv_block_tq3* k, const qkv_blo
   a.window_tok = window_tok;
   a.tree_mask = tree_mask;
   a.ws_header = reinterpret_cast<int*>(ws + g.header_off);
+  a.spin_limit = g_spin_limit.load(std::memory_order_relaxed);
   a.ws_ml = reinterpret_cast<float*>(ws + g.ml_off);
   a.ws_o = reinterpret_cast<float*>(ws + g.o_off);
   if (g.total > 0xffffffffULL) return QKV_ERR_UNSUPPORTED;   // 32-bit buffer offsets
@@ -414,9 +415,8 @@ static int decode_q8_keys(const uint16_t* q, const void* k, const void* v, uint1
   a.qpw = 1;
   {
     const uint64_t extent = (uint64_t)n_keys * num_kv * 8 * sizeof(qkv_block_q8);
-    if (extent > 0x7fffffffULL) return QKV_ERR_UNSUPPORTED;   // 32-bit buffer offsets
-    a.kv_bytes = (uint32_t)extent;
-    a.v_bytes = (uint32_t)((uint64_t)n_keys * num_kv * 2 * sizeof(qkv_block_tq3));
+    a.kv_bytes = extent;
+    a.v_bytes = (uint64_t)n_keys * num_kv * 2 * sizeof(qkv_block_tq3);
   }
   a.active_end_max = n_keys;
   a.k_splits = 1;
@@ -425,6 +425,7 @@ static int decode_q8_keys(const uint16_t* q, const void* k, const void* v, uint1
   a.n_slots = g.n_slots;
   a.scale_log2 = scale * qkv::kLog2e;
   a.ws_header = reinterpret_cast<int*>(ws + g.header_off);
+  a.spin_limit = g_spin_limit.load(std::memory_order_relaxed);
   a.ws_ml = reinterpret_cast<float*>(ws + g.ml_off);
   a.ws_o = reinterpret_cast<float*>(ws + g.o_off);
   if (g.total > 0xffffffffULL) return QKV_ERR_UNSUPPORTED;   // 32-bit buffer offsets
@@ -491,8 +492,7 @@ int qkv_decode_attn_tq3_paged(const uint16_t* q, const qkv_block_tq3* k_pool,
   a.qpw = 1;   // slots read different caches
   {
     const uint64_t extent = (uint64_t)pool_rows * num_kv * 104;
-    if (extent > 0x7fffffffULL) return QKV_ERR_UNSUPPORTED;   // 32-bit buffer offsets
-    a.kv_bytes = (uint32_t)extent;
+    a.kv_bytes = extent;
   }
   a.active_end_max = max_ctx;
   a.k_splits = 1;
@@ -506,12 +506,36 @@ int qkv_decode_attn_tq3_paged(const uint16_t* q, const qkv_block_tq3* k_pool,
   a.ctx_lens = ctx_lens;
   a.ctx_max = max_ctx;
   a.ws_header = reinterpret_cast<int*>(ws + g.header_off);
+  a.spin_limit = g_spin_limit.load(std::memory_order_relaxed);
   a.ws_ml = reinterpret_cast<float*>(ws + g.ml_off);
   a.ws_o = reinterpret_cast<float*>(ws + g.o_off);
   if (g.total > 0xffffffffULL) return QKV_ERR_UNSUPPORTED;   // 32-bit buffer offsets
   a.ws_ml_bytes = (uint32_t)(g.o_off - g.ml_off);
   a.ws_o_bytes = (uint32_t)(g.total - g.o_off);
   return launch_status(qkv::launch_tq3_attn(a, 0, out, stream));
+}
+
+int qkv_decode_workspace_status(const void* workspace, hipStream_t stream) {
+  if (!workspace) return QKV_ERR_NULL;
+  if (!aligned(workspace, 256)) return QKV_ERR_ALIGN;
+  if (hipStreamSynchronize(stream) != hipSuccess) return QKV_ERR_DEVICE;
+  int word = 0;
+  if (hipMemcpy(&word, static_cast<const char*>(workspace) + 4 * qkv::kWsErrorWord, sizeof(word),
+                hipMemcpyDeviceToHost) != hipSuccess)
+    return QKV_ERR_DEVICE;
+  return word == 0 ? QKV_OK : QKV_ERR_TIMEOUT;
+}
+
+int qkv_decode_workspace_reset(void* workspace, size_t bytes, hipStream_t stream) {
+  if (!workspace) return QKV_ERR_NULL;
+  if (!aligned(workspace, 256) || bytes % 4) return QKV_ERR_ALIGN;
+  if (bytes == 0) return QKV_OK;
+  return launch_status(qkv::launch_fill_zero(workspace, bytes, stream));
+}
+
+int qkv_debug_set_merge_spin_limit(int limit) {
+  g_spin_limit.store(limit < 0 ? qkv::kMergeSpinLimit : limit, std::memory_order_relaxed);
+  return QKV_OK;
 }
 
 size_t qkv_prefill_attn_tq3_workspace_bytes(int num_q, int num_kv, int n_tok, int start_pos) {
@@ -541,12 +565,12 @@ int qkv_prefill_attn_tq3(const uint16_t* q, const qkv_block_tq3* k_cache,
   if (!aligned(workspace, 256)) return QKV_ERR_ALIGN;
   const uint64_t hist = (uint64_t)(start_pos + (from_cache ? n_tok : 0)) * num_kv * 104;
   const uint64_t qbytes = (uint64_t)n_tok * num_q * 256 * 2;
-  if (hist > 0x7fffffffULL || qbytes > 0x7fffffffULL) return QKV_ERR_UNSUPPORTED;   // 32-bit offsets
+  if (qbytes > 0x7fffffffULL) return QKV_ERR_UNSUPPORTED;   // 32-bit query offsets
   char* ws = static_cast<char*>(workspace);
   qkv::PrefillArgs a{};
   a.k_cache = reinterpret_cast<const uint32_t*>(k_cache);
   a.v_cache = reinterpret_cast<const uint32_t*>(v_cache);
-  a.kv_bytes = (uint32_t)hist;
+  a.kv_bytes = hist;
   a.qr = reinterpret_cast<uint16_t*>(ws + g.qr_off);
   a.kr = reinterpret_cast<uint16_t*>(ws + g.kr_off);
   a.vt = reinterpret_cast<uint16_t*>(ws + g.vt_off);

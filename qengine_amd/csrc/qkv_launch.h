@@ -24,6 +24,8 @@ hipError_t launch_tq3_dequant(const void* in, void* out, int n_blocks, hipStream
 hipError_t launch_q8_append(const void* in0, void* out0, const void* in1, void* out1,
                             int n_blocks, int n_tensors, hipStream_t stream);
 hipError_t launch_q8_dequant(const void* in, void* out, int n_blocks, hipStream_t stream);
+// Zero-fill of `bytes` (a multiple of 4) bytes by a kernel (graph-capture safe).
+hipError_t launch_fill_zero(void* p, size_t bytes, hipStream_t stream);
 
 // Token-row moves inside one slot of one layer's cache (kv_move.hip): row
 // slot_row0 + to[i] := row slot_row0 + from[i] for i = 0..n-1, K and V.
@@ -48,7 +50,7 @@ struct PrefillArgs {
   const uint32_t* k_cache;   // slot-base TQ3 caches (rows 0 .. start_pos-1, or
                              // 0 .. start_pos+n_tok-1 when from_cache)
   const uint32_t* v_cache;
-  uint32_t kv_bytes;         // readable history bytes from the slot base
+  uint64_t kv_bytes;         // readable history bytes from the slot base
   uint16_t* qr;
   uint16_t* kr;
   uint16_t* vt;

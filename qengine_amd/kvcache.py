@@ -209,6 +209,25 @@ def decode_attn_q8k_tq3v(q, k, v, out, workspace, *, num_q, num_kv, start_pos, s
         workspace.numel() * workspace.element_size(), _stream(stream)), "qkv_decode_attn_q8k_tq3v")
 
 
+def decode_workspace_status(workspace, stream=None) -> int:
+    """Synchronises the stream and returns QKV_OK (0) or QKV_ERR_TIMEOUT (-8): an
+    in-kernel merge on this workspace ran out of polls and its rows were NaN."""
+    return int(lib().qkv_decode_workspace_status(_dev_ptr(workspace, "workspace"),
+                                                 _stream(stream)))
+
+
+def decode_workspace_reset(workspace, stream=None) -> None:
+    """Zero-fill a fast-path decode workspace (clears a sticky merge error)."""
+    check(lib().qkv_decode_workspace_reset(_dev_ptr(workspace, "workspace"),
+                                           workspace.numel() * workspace.element_size(),
+                                           _stream(stream)), "qkv_decode_workspace_reset")
+
+
+def debug_set_merge_spin_limit(limit: int) -> None:
+    """Test hook: merger poll limit of later fast-path launches (negative = default)."""
+    check(lib().qkv_debug_set_merge_spin_limit(int(limit)), "qkv_debug_set_merge_spin_limit")
+
+
 # ---------------------------------------------------------------------------
 # paged caches (per-slot int32 block tables)
 # ---------------------------------------------------------------------------

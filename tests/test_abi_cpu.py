@@ -134,3 +134,16 @@ def test_mixed_decode_argument_errors_without_gpu(L):
     assert call(q=p + 2) == -4
     assert call(ws=None) == -7
     assert call() == -7                        # one byte short
+
+
+def test_workspace_health_argument_errors(L):
+    buf = ctypes.create_string_buffer(4096)
+    p = (ctypes.addressof(buf) + 255) & ~255
+    assert L.qkv_decode_workspace_status(None, None) == -2
+    assert L.qkv_decode_workspace_status(p + 4, None) == -4
+    assert L.qkv_decode_workspace_reset(None, 256, None) == -2
+    assert L.qkv_decode_workspace_reset(p + 4, 256, None) == -4
+    assert L.qkv_decode_workspace_reset(p, 6, None) == -4      # whole words only
+    assert L.qkv_decode_workspace_reset(p, 0, None) == 0       # nothing to clear
+    assert L.qkv_debug_set_merge_spin_limit(-1) == 0
+    assert L.qkv_status_string(-8) == b"in-kernel merge timed out; reset the workspace"

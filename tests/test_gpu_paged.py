@@ -220,3 +220,56 @@ def test_config4_step_append_then_decode(dev):
     got = out.cpu().numpy()
     for s in range(n_slots):
         assert rel_err(got[s], exp[s]) < TOL, s
+
+
+def test_pool_beyond_4gib(dev):
+    """A paged pool larger than 4 GiB per tensor (10.5M token rows of 416 B):
+    the append writes, and the decode reads, blocks at the top of the pool
+    (64-bit row offsets).  Results are bit-identical to the same slots in a
+    small pool, which in turn is checked against the oracle."""
+    from qengine_amd import kvcache
+    torch = _torch()
+    rng = np.random.default_rng(4242)
+    num_q, num_kv, bt_tok = 16, 4, 256
+    ctx = [2900, 1700]
+    max_blocks = 12
+    n_tok = max(ctx)
+    k16 = kv_f16(rng, 2 * n_tok, num_kv, HD).reshape(2, n_tok, num_kv, HD)
+    v16 = kv_f16(rng, 2 * n_tok, num_kv, HD).reshape(2, n_tok, num_kv, HD)
+    q = q_f16(rng, 2, num_q, HD)
+    big_rows = 10_500_000 // bt_tok * bt_tok          # 4.37e9 bytes per tensor
+    assert big_rows * num_kv * 104 > 2 ** 32
+    top = big_rows // bt_tok - 2 * max_blocks         # first block index used at the top
+    bt_small = np.arange(2 * max_blocks, dtype=np.int32).reshape(2, max_blocks)
+    bt_big = bt_small + np.int32(top)
+    out = {}
+    blocks = {}
+    for name, rows, bt in (("small", 2 * max_blocks * bt_tok, bt_small), ("big", big_rows, bt_big)):
+        kp = torch.zeros((rows * 8, 52), dtype=torch.uint8, device=dev)
+        vp = torch.zeros((rows * 8, 52), dtype=torch.uint8, device=dev)
+        btd = _dev(bt, dev)
+        kvcache.tq3_append_kv_paged(_dev(k16, dev), _dev(v16, dev), kp, vp, btd,
+                                    _dev(np.zeros(2, np.int32), dev), block_tokens=bt_tok)
+        ws = kvcache.decode_attn_tq3_paged_workspace(num_q, num_kv, 2, max(ctx), dev)
+        o = torch.zeros((2, num_q, HD), dtype=torch.float16, device=dev)
+        kvcache.decode_attn_tq3_paged(_dev(q, dev), kp, vp, o, ws, btd,
+                                      _dev(np.asarray(ctx, np.int32), dev), num_q=num_q,
+                                      num_kv=num_kv, max_ctx=max(ctx), block_tokens=bt_tok,
+                                      scale=1 / 16)
+        torch.cuda.synchronize()
+        out[name] = o.cpu().numpy()
+        r0 = int(bt[0, 0]) * bt_tok
+        blocks[name] = (kp[r0 * 8:(r0 + 2 * max_blocks * bt_tok) * 8].cpu().numpy(),
+                        vp[r0 * 8:(r0 + 2 * max_blocks * bt_tok) * 8].cpu().numpy())
+        del kp, vp
+        torch.cuda.empty_cache()
+    assert np.array_equal(blocks["big"][0], blocks["small"][0])
+    assert np.array_equal(blocks["big"][1], blocks["small"][1])
+    assert np.array_equal(out["big"].view(np.uint16), out["small"].view(np.uint16))
+    kb, vb = blocks["small"]
+    ref = O.decode_paged(O.KV_TQ3, q, np.ascontiguousarray(kb).view(O.BLOCK_TQ3).reshape(-1),
+                         np.ascontiguousarray(vb).view(O.BLOCK_TQ3).reshape(-1), bt_small,
+                         np.asarray(ctx, np.int32), num_q=num_q, num_kv=num_kv, hd=HD,
+                         block_tokens=bt_tok, scale=1 / 16)
+    assert rel_err(out["small"].astype(np.float64),
+                   ref.view(np.float16).astype(np.float64)) < TOL
