@@ -66,8 +66,10 @@ const char* qkv_status_string(int status);
 
 /* Replaces tq3_init_signs(gpu) (turboquant.cuh:288-302).  The sign vector is a
  * compile-time constant of this library (same seed and generator), so this call
- * only validates `device` as a gfx950 GPU.  Idempotent; optional before the
- * other calls. */
+ * validates `device` as a gfx950 GPU and prepares (zero-fills, synchronously)
+ * the scratch of qkv_decode_attn_tq3_noalloc on it.  Optional before the
+ * other calls; must not run while a qkv_decode_attn_tq3_noalloc call is in
+ * flight on that device. */
 int qkv_tq3_init(int device);
 
 /* Replaces tq3_quantize_kernel<<<(n+31)/32, 32, 0, stream>>>(in, out, n_blocks)
@@ -204,6 +206,25 @@ int qkv_decode_workspace_reset(void* workspace, size_t bytes, hipStream_t stream
  * restores the default of 2^22 polls).  A limit of 0 makes every merger time
  * out, so the error path can be exercised without a GPU fault or hang. */
 int qkv_debug_set_merge_spin_limit(int limit);
+
+/* Allocation-free variant of qkv_decode_attn_tq3 (same arguments without the
+ * workspace, same results).  No counterpart in the reference: it is for
+ * callers that cannot allocate or own device memory (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc).  The
+ * workspace lives in a fixed 8 MiB scratch array that the library holds on
+ * each GPU it runs on until the process ends; the call itself allocates
+ * nothing.  qkv_tq3_init(device) looks the array up and zero-fills it (so
+ * does the first call on a device if init was not called; it also re-clears
+ * it, the reset after a merge timeout).  Shapes whose workspace
+ * (qkv_decode_attn_tq3_workspace_bytes) exceeds 8 MiB return
+ * QKV_ERR_WORKSPACE.  Every call on one GPU shares that GPU's scratch, which
+ * each completed call leaves ready for the next: calls that overlap on one
+ * GPU (different streams, or a concurrent qkv_tq3_init) race and must not be
+ * issued. */
+int qkv_decode_attn_tq3_noalloc(const uint16_t* q, const qkv_block_tq3* k,
+                                const qkv_block_tq3* v, uint16_t* out, int num_q, int num_kv,
+                                int head_dim, int start_pos, int sub_n, float scale, int sink_tok,
+                                int window_tok, const uint32_t* tree_mask, hipStream_t stream);
 
 /* Fast path for qkv_attn_split_q8 + qkv_attn_split_merge over the Q8_0 cache
  * (decode launch model.cuh:2430-2463; attention.cuh:2633-2801 and 1837-1891) in ONE launch:

@@ -52,6 +52,8 @@ SIGNATURES = {
     "qkv_decode_attn_tq3_workspace_bytes": (_SZ, [_I, _I, _I, _I]),
     "qkv_decode_attn_tq3": (_I, [_P, _P, _P, _P, _I, _I, _I, _I, _I, _F, _I, _I, _P, _P, _SZ,
                                 _P]),
+    "qkv_decode_attn_tq3_noalloc": (_I, [_P, _P, _P, _P, _I, _I, _I, _I, _I, _F, _I, _I, _P,
+                                        _P]),
     "qkv_decode_attn_q8_workspace_bytes": (_SZ, [_I, _I, _I, _I]),
     "qkv_decode_attn_q8": (_I, [_P, _P, _P, _P, _I, _I, _I, _I, _I, _F, _P, _SZ, _P]),
     "qkv_decode_attn_q8k_tq3v_workspace_bytes": (_SZ, [_I, _I, _I, _I]),

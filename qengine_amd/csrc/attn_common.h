@@ -178,6 +178,12 @@ __device__ __forceinline__ void wht_xor_lanes16(float (&x)[8], int lane) {
 }
 
 hipError_t launch_tq3_attn(const AttnArgs& a, int mode, uint16_t* out, hipStream_t stream);
+// Scratch of the allocation-free TQ3 decode (attn_tq3.hip): this device's copy
+// of a file-scope device array of kNoAllocScratchBytes.  The first call for a
+// device (that device current) looks its address up; with `clear`, or on that
+// first call, the scratch is zero-filled on `stream` (a fill kernel).
+constexpr size_t kNoAllocScratchBytes = 8u << 20;
+hipError_t noalloc_scratch(int device, bool clear, hipStream_t stream, void** ptr);
 hipError_t launch_q8_attn_split(const AttnArgs& a, hipStream_t stream);
 hipError_t launch_q8_attn_fast(const AttnArgs& a, uint16_t* out, hipStream_t stream);
 hipError_t launch_q8k_tq3v_attn_fast(const AttnArgs& a, uint16_t* out, hipStream_t stream);

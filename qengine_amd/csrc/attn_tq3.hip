@@ -36,11 +36,13 @@
 // (ragged) launches split each kv head's record shares over the slots in
 // proportion to their key counts.  Split API: one workgroup per reference
 // split, written in the reference partial layout.
+#include <mutex>
 #include <type_traits>
 
 #include "qkv_device.h"
 #include "attn_common.h"
 #include "attn_fastmerge.h"
+#include "qkv_launch.h"
 
 namespace qkv {
 
@@ -764,6 +766,35 @@ __global__ __launch_bounds__(kThreads, 1) void tq3_attn_kernel(AttnArgs p, uint1
 }
 
 size_t tq3_attn_lds_bytes() { return kLdsTotal; }
+
+// ---- the allocation-free decode's scratch ----------------------------------
+// One fixed-size array per GPU, holding the fast path's workspace layout
+// (header, record scalars, record rows).  In host code `scratch` names a
+// host-side stand-in, not a device address: kernels only ever receive the
+// address hipGetSymbolAddress returns for the current device, kept per device.
+static __device__ __align__(256) uint8_t scratch[kNoAllocScratchBytes];
+
+namespace {
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[64];
+}  // namespace
+
+hipError_t noalloc_scratch(int device, bool clear, hipStream_t stream, void** ptr) {
+  if (device < 0 || device >= 64) return hipErrorInvalidDevice;
+  std::lock_guard<std::mutex> lk(g_scratch_mu);
+  bool fresh = false;
+  if (g_scratch_ptr[device] == nullptr) {
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return e;
+    if (p == nullptr) return hipErrorInvalidSymbol;
+    g_scratch_ptr[device] = p;
+    fresh = true;
+  }
+  *ptr = g_scratch_ptr[device];
+  if (clear || fresh) return launch_fill_zero(*ptr, kNoAllocScratchBytes, stream);
+  return hipSuccess;
+}
 
 hipError_t launch_tq3_attn(const AttnArgs& a, int mode, uint16_t* out, hipStream_t stream) {
   const int groups = (a.sub_n + a.qpw - 1) / a.qpw * a.n_chunks;

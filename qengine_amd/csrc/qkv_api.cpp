@@ -51,13 +51,20 @@ const char* qkv_status_string(int s) {
 int qkv_tq3_init(int device) {
   if (device < 0 || device >= 64) return QKV_ERR_INVALID;
   std::lock_guard<std::mutex> lk(g_init_mu);
-  if (g_init_ok[device]) return QKV_OK;
   int n = 0;
   if (hipGetDeviceCount(&n) != hipSuccess || device >= n) return QKV_ERR_DEVICE;
   hipDeviceProp_t prop;
   if (hipGetDeviceProperties(&prop, device) != hipSuccess) return QKV_ERR_DEVICE;
   if (std::strncmp(prop.gcnArchName, "gfx950", 6) != 0) return QKV_ERR_DEVICE;
   g_init_ok[device] = true;
+  // the allocation-free decode's scratch on this device: looked up and zero-filled
+  int cur = 0;
+  if (hipGetDevice(&cur) != hipSuccess) return QKV_ERR_DEVICE;
+  if (hipSetDevice(device) != hipSuccess) return QKV_ERR_DEVICE;
+  void* ptr = nullptr;
+  const bool ok = qkv::noalloc_scratch(device, true, nullptr, &ptr) == hipSuccess &&
+                  hipStreamSynchronize(nullptr) == hipSuccess;
+  if (hipSetDevice(cur) != hipSuccess || !ok) return QKV_ERR_DEVICE;
   return QKV_OK;
 }
 
@@ -334,11 +341,12 @@ size_t qkv_decode_attn_tq3_workspace_bytes(int num_q, int num_kv, int sub_n, int
   return fast_geom(num_q, num_kv, sub_n, n_keys, kChunkKeys, tq3_groups(num_q, num_kv, sub_n)).total;
 }
 
-int qkv_decode_attn_tq3(const uint16_t* q, const qkv_block_tq3* k, const qkv_block_tq3* v,
-                        uint16_t* out, int num_q, int num_kv, int head_dim, int start_pos,
-                        int sub_n, float scale, int sink_tok, int window_tok,
-                        const uint32_t* tree_mask, void* workspace, size_t workspace_bytes,
-                        hipStream_t stream) {
+// The TQ3 fast path with its workspace at `workspace` (caller-owned, or the
+// allocation-free entry point's scratch when `noalloc`).
+static int decode_tq3(const uint16_t* q, const qkv_block_tq3* k, const qkv_block_tq3* v,
+                      uint16_t* out, int num_q, int num_kv, int head_dim, int start_pos, int sub_n,
+                      float scale, int sink_tok, int window_tok, const uint32_t* tree_mask,
+                      void* workspace, size_t workspace_bytes, bool noalloc, hipStream_t stream) {
   int st = check_attn_shape(num_q, num_kv, head_dim, start_pos, sub_n, tree_mask);
   if (st) return st;
   if (sink_tok < 0 || window_tok < 0) return QKV_ERR_INVALID;
@@ -347,6 +355,15 @@ int qkv_decode_attn_tq3(const uint16_t* q, const qkv_block_tq3* k, const qkv_blo
     return QKV_ERR_ALIGN;
   const int n_keys = start_pos + sub_n;
   const FastGeom g = fast_geom(num_q, num_kv, sub_n, n_keys, kChunkKeys, tq3_groups(num_q, num_kv, sub_n));
+  if (noalloc) {
+    // no allocation: this device's scratch (looked up, and zero-filled on
+    // `stream`, by the device's first qkv_tq3_init or first call here)
+    if (g.total > qkv::kNoAllocScratchBytes) return QKV_ERR_WORKSPACE;
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return QKV_ERR_DEVICE;
+    if (qkv::noalloc_scratch(dev, false, stream, &workspace) != hipSuccess) return QKV_ERR_DEVICE;
+    workspace_bytes = qkv::kNoAllocScratchBytes;
+  }
   if (!workspace || workspace_bytes < g.total) return QKV_ERR_WORKSPACE;
   if (!aligned(workspace, 256)) return QKV_ERR_ALIGN;
   char* ws = static_cast<char*>(workspace);
@@ -381,6 +398,23 @@ int qkv_decode_attn_tq3(const uint16_t* q, const qkv_block_tq3* k, const qkv_blo
   a.ws_ml_bytes = (uint32_t)(g.o_off - g.ml_off);
   a.ws_o_bytes = (uint32_t)(g.total - g.o_off);
   return launch_status(qkv::launch_tq3_attn(a, 0, out, stream));
+}
+
+int qkv_decode_attn_tq3(const uint16_t* q, const qkv_block_tq3* k, const qkv_block_tq3* v,
+                        uint16_t* out, int num_q, int num_kv, int head_dim, int start_pos,
+                        int sub_n, float scale, int sink_tok, int window_tok,
+                        const uint32_t* tree_mask, void* workspace, size_t workspace_bytes,
+                        hipStream_t stream) {
+  return decode_tq3(q, k, v, out, num_q, num_kv, head_dim, start_pos, sub_n, scale, sink_tok,
+                    window_tok, tree_mask, workspace, workspace_bytes, false, stream);
+}
+
+int qkv_decode_attn_tq3_noalloc(const uint16_t* q, const qkv_block_tq3* k,
+                                const qkv_block_tq3* v, uint16_t* out, int num_q, int num_kv,
+                                int head_dim, int start_pos, int sub_n, float scale, int sink_tok,
+                                int window_tok, const uint32_t* tree_mask, hipStream_t stream) {
+  return decode_tq3(q, k, v, out, num_q, num_kv, head_dim, start_pos, sub_n, scale, sink_tok,
+                    window_tok, tree_mask, nullptr, 0, true, stream);
 }
 
 size_t qkv_decode_attn_q8_workspace_bytes(int num_q, int num_kv, int sub_n, int n_keys) {

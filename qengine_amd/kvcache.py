@@ -177,6 +177,17 @@ def decode_attn_tq3(q, k, v, out, workspace, *, num_q, num_kv, start_pos, sub_n,
         workspace.numel() * workspace.element_size(), _stream(stream)), "qkv_decode_attn_tq3")
 
 
+def decode_attn_tq3_noalloc(q, k, v, out, *, num_q, num_kv, start_pos, sub_n, scale,
+                            sink_tok=0, window_tok=0, tree_mask=None, head_dim=256,
+                            stream=None) -> None:
+    """decode_attn_tq3 without a workspace argument: the library's fixed
+    per-GPU scratch serves as the workspace (no allocation in the call)."""
+    check(lib().qkv_decode_attn_tq3_noalloc(
+        _dev_ptr(q, "q"), _dev_ptr(k, "k"), _dev_ptr(v, "v"), _dev_ptr(out, "out"), num_q,
+        num_kv, head_dim, start_pos, sub_n, float(scale), sink_tok, window_tok,
+        _opt_ptr(tree_mask), _stream(stream)), "qkv_decode_attn_tq3_noalloc")
+
+
 def decode_attn_q8_workspace(num_q, num_kv, sub_n, n_keys, device) -> torch.Tensor:
     """Zero-filled workspace for decode_attn_q8."""
     n = int(lib().qkv_decode_attn_q8_workspace_bytes(num_q, num_kv, sub_n, n_keys))
