@@ -175,7 +175,7 @@ size_t qkv_decode_attn_tq3_workspace_bytes(int num_q, int num_kv, int sub_n, int
  * (model.cuh:2472-2491) in ONE launch: the key range is cut into chunks of
  * 512*k keys, partials stay in rotated coordinates and are merged inside the
  * kernel (the last workgroups of the grid do the merge), and each output row
- * is rotated back once.  Up to 16/GQA queries of a multi-token call (verify,
+ * is rotated back once.  Up to 8/GQA queries of a multi-token call (verify,
  * sub_n > 1) share one pass over the cache.  out [sub_n][num_q][256] fp16
  * (16-byte aligned).
  * workspace: caller-owned device memory of at least

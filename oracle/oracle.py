@@ -80,6 +80,8 @@ def _declare(L):
     L.or_attn_split_merge.argtypes = [_P, _P, _P, _P, _I, _I, _I, _I, _I, _I]
     L.or_attn_ref_f64.argtypes = [_P, _P, _P, _P, _I, _I, _I, _I, _I, ctypes.c_double,
                                   _I, _I, _P]
+    L.or_attn_ref_f64_f32kv.argtypes = [_P, _P, _P, _P, _I, _I, _I, _I, _I, ctypes.c_double,
+                                  _I, _I, _P]
     L.or_key_visible.restype = _I
     L.or_key_visible.argtypes = [_I, _I, _I, _I, _I, _P]
 
@@ -272,6 +274,32 @@ def attn_ref_f64(q, k_f16, v_f16, *, num_q, num_kv, hd, start_pos, sub_n, scale,
     tm = None if tree_mask is None else np.ascontiguousarray(tree_mask, np.uint32)
     lib().or_attn_ref_f64(_ptr(q), _ptr(k_f16), _ptr(v_f16), _ptr(out), num_q, num_kv, hd,
                           start_pos, sub_n, float(scale), sink_tok, window_tok, _ptr(tm))
+    return out
+
+
+def attn_exact_tq3(q, k_tq3, v_tq3, *, num_q, num_kv, hd, start_pos, sub_n, scale,
+                   sink_tok=0, window_tok=0, tree_mask=None):
+    """fp64 attention over the EXACT dequantization of TQ3 caches
+    (norm * rs * sign * (H c), turboquant.cuh:169-200 without its final fp16
+    rounding; tq3_decode_f32), same visibility rules as attn_ref_f64.  The
+    reference's own numerics round every dequantized element to fp16; this is
+    the mathematical value both approximate.  Returns [sub_n][num_q][hd]."""
+    return attn_ref_f64_f32kv(q, tq3_decode_f32(k_tq3), tq3_decode_f32(v_tq3), num_q=num_q,
+                              num_kv=num_kv, hd=hd, start_pos=start_pos, sub_n=sub_n,
+                              scale=scale, sink_tok=sink_tok, window_tok=window_tok,
+                              tree_mask=tree_mask)
+
+
+def attn_ref_f64_f32kv(q, k_f32, v_f32, *, num_q, num_kv, hd, start_pos, sub_n, scale,
+                       sink_tok=0, window_tok=0, tree_mask=None):
+    """attn_ref_f64 over float K/V rows [n][num_kv][hd] (same core)."""
+    q = _u16(q)
+    k = np.ascontiguousarray(k_f32, np.float32)
+    v = np.ascontiguousarray(v_f32, np.float32)
+    out = np.zeros((sub_n, num_q, hd), np.float64)
+    tm = None if tree_mask is None else np.ascontiguousarray(tree_mask, np.uint32)
+    lib().or_attn_ref_f64_f32kv(_ptr(q), _ptr(k), _ptr(v), _ptr(out), num_q, num_kv, hd,
+                                start_pos, sub_n, float(scale), sink_tok, window_tok, _ptr(tm))
     return out
 
 

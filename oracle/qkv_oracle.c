@@ -39,6 +39,8 @@
  *                                   dense, causal-verify, tree, sink/window
  *                                   inputs; split-count invariance
  *   or_attn_ref_f64                 brute-force numpy softmax on tiny inputs
+ *   or_attn_ref_f64_f32kv           equals or_attn_ref_f64 bit for bit on
+ *                                   fp16-representable float inputs (same core)
  * No function is "parity unpinned".
  */
 #include "qkv_oracle.h"
@@ -592,16 +594,21 @@ void or_attn_split_merge(const float* part_m, const float* part_l, const float* 
 }
 
 /* Independent fp64 reference (tools/dflash_attn_bench.cu:185-211 pattern). */
-void or_attn_ref_f64(const uint16_t* q, const uint16_t* k_f16, const uint16_t* v_f16,
-                     double* out, int num_q, int num_kv, int hd, int start_pos,
-                     int sub_n, double scale, int sink_tok, int window_tok,
-                     const uint32_t* tree_mask) {
+/* fp64 attention of query t over keys 0 .. start_pos + t that pass the
+ * visibility rule; K/V elements are fp16 bits (kv_f32 = 0) or floats
+ * (kv_f32 = 1: e.g. the exact, unrounded TQ3 dequantization).  Parallel over
+ * (query, q head); each output row is a plain softmax in double. */
+static void attn_ref_f64_any(const uint16_t* q, const void* k, const void* v, int kv_f32,
+                             double* out, int num_q, int num_kv, int hd, int start_pos,
+                             int sub_n, double scale, int sink_tok, int window_tok,
+                             const uint32_t* tree_mask) {
     const int gqa = num_q / num_kv;
+    #pragma omp parallel for collapse(2) schedule(dynamic)
     for (int t = 0; t < sub_n; t++) {
-        int n_keys = start_pos + t + 1;
-        double* sc = (double*)malloc(sizeof(double) * (n_keys > 0 ? n_keys : 1));
         for (int qh = 0; qh < num_q; qh++) {
-            int kvh = qh / gqa;
+            const int n_keys = start_pos + t + 1;
+            double* sc = (double*)malloc(sizeof(double) * (n_keys > 0 ? n_keys : 1));
+            const int kvh = qh / gqa;
             const uint16_t* qv = q + ((int64_t)t * num_q + qh) * hd;
             double mx = -INFINITY;
             for (int key = 0; key < n_keys; key++) {
@@ -609,26 +616,47 @@ void or_attn_ref_f64(const uint16_t* q, const uint16_t* k_f16, const uint16_t* v
                     sc[key] = -INFINITY;
                     continue;
                 }
-                const uint16_t* kr = k_f16 + ((int64_t)key * num_kv + kvh) * hd;
+                const int64_t kr = ((int64_t)key * num_kv + kvh) * hd;
                 double d = 0.0;
-                for (int c = 0; c < hd; c++)
-                    d += (double)or_f16_to_f32(qv[c]) * (double)or_f16_to_f32(kr[c]);
+                for (int c = 0; c < hd; c++) {
+                    const double kc = kv_f32 ? (double)((const float*)k)[kr + c]
+                                             : (double)or_f16_to_f32(((const uint16_t*)k)[kr + c]);
+                    d += (double)or_f16_to_f32(qv[c]) * kc;
+                }
                 sc[key] = d * scale;
                 if (sc[key] > mx) mx = sc[key];
             }
             double den = 0.0;
             double* o = out + ((int64_t)t * num_q + qh) * hd;
             for (int c = 0; c < hd; c++) o[c] = 0.0;
-            if (mx == -INFINITY) continue;
-            for (int key = 0; key < n_keys; key++) {
-                if (sc[key] == -INFINITY) continue;
-                double w = exp(sc[key] - mx);
-                den += w;
-                const uint16_t* vr = v_f16 + ((int64_t)key * num_kv + kvh) * hd;
-                for (int c = 0; c < hd; c++) o[c] += w * (double)or_f16_to_f32(vr[c]);
+            if (mx != -INFINITY) {
+                for (int key = 0; key < n_keys; key++) {
+                    if (sc[key] == -INFINITY) continue;
+                    double w = exp(sc[key] - mx);
+                    den += w;
+                    const int64_t vr = ((int64_t)key * num_kv + kvh) * hd;
+                    for (int c = 0; c < hd; c++)
+                        o[c] += w * (kv_f32 ? (double)((const float*)v)[vr + c]
+                                            : (double)or_f16_to_f32(((const uint16_t*)v)[vr + c]));
+                }
+                for (int c = 0; c < hd; c++) o[c] /= den;
             }
-            for (int c = 0; c < hd; c++) o[c] /= den;
+            free(sc);
         }
-        free(sc);
     }
+}
+
+void or_attn_ref_f64(const uint16_t* q, const uint16_t* k_f16, const uint16_t* v_f16,
+                     double* out, int num_q, int num_kv, int hd, int start_pos,
+                     int sub_n, double scale, int sink_tok, int window_tok,
+                     const uint32_t* tree_mask) {
+    attn_ref_f64_any(q, k_f16, v_f16, 0, out, num_q, num_kv, hd, start_pos, sub_n, scale,
+                     sink_tok, window_tok, tree_mask);
+}
+
+void or_attn_ref_f64_f32kv(const uint16_t* q, const float* k, const float* v, double* out,
+                           int num_q, int num_kv, int hd, int start_pos, int sub_n, double scale,
+                           int sink_tok, int window_tok, const uint32_t* tree_mask) {
+    attn_ref_f64_any(q, k, v, 1, out, num_q, num_kv, hd, start_pos, sub_n, scale, sink_tok,
+                     window_tok, tree_mask);
 }

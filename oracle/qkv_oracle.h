@@ -112,6 +112,11 @@ void or_attn_ref_f64(const uint16_t* q, const uint16_t* k_f16, const uint16_t* v
                      double* out, int num_q, int num_kv, int hd, int start_pos,
                      int sub_n, double scale, int sink_tok, int window_tok,
                      const uint32_t* tree_mask);
+/* The same fp64 attention over float K/V (e.g. the exact TQ3 dequantization
+ * before its fp16 rounding): the truth the rotated-domain kernels are held to. */
+void or_attn_ref_f64_f32kv(const uint16_t* q, const float* k, const float* v, double* out,
+                           int num_q, int num_kv, int hd, int start_pos, int sub_n, double scale,
+                           int sink_tok, int window_tok, const uint32_t* tree_mask);
 
 /* Visibility rule shared by the split kernel and the fp64 reference:
  * attention.cuh:1941-1951 (causal), 1985-1994 (sink/window tile skip),

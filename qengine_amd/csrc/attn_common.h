@@ -126,6 +126,24 @@ __device__ __forceinline__ float centroid_imm(uint32_t i) {
   return (i & 4) ? mpos : -mneg;
 }
 
+// Scaled centroid table of the rotated-domain consumers.  The fp16 LUT holds
+// the Lloyd-Max levels (turboquant.cuh:27-30) times kCenScale, a factor chosen
+// so that all four magnitudes land within 2.6e-5 (relative) of an fp16 value
+// (unscaled, the fp16 levels are up to 2.0e-4 off, enough to move attention
+// rows by ~1e-3); scores and value sums are divided by kCenScale again in
+// fp32 (key norms carry kCenScaleInv, outputs are multiplied by it).
+constexpr float kCenScale = 1.14951002597808838f;
+constexpr float kCenScaleInv = 1.0f / kCenScale;
+// fp16 bits of kCenScale * |centroid| for magnitude index 0..3 (round to nearest)
+constexpr uint16_t kCenScaledH[4] = {0x2660, 0x2ceb, 0x305f, 0x3300};
+__device__ __forceinline__ uint32_t centroid_scaled_h(uint32_t i) {
+  // i >= 4: +m[i-4]; i < 4: -m[3-i] (symmetric table)
+  const uint32_t m = (i & 4u) ? (i & 3u) : (3u - (i & 3u));
+  const uint32_t mag = (m & 2u) ? ((m & 1u) ? kCenScaledH[3] : kCenScaledH[2])
+                                : ((m & 1u) ? kCenScaledH[1] : kCenScaledH[0]);
+  return (i & 4u) ? mag : (mag | 0x8000u);
+}
+
 // ---- 128-point Walsh-Hadamard pieces (butterflies (a,b) -> (a+b, a-b)) ----
 // Element e = part*8 + i of a 128-block lives in register i of lane `part`
 // (16 consecutive lanes per block).

@@ -187,7 +187,8 @@ __device__ bool merge_unit(float* red, f2_t* mls, const AttnArgs& p, __amdgpu_bu
   // 16 lanes x 8 elements (threads 0..15): sum the waves' partials, normalise,
   // rotate back, store fp16
   if (tid < 16) {
-    const float inv = L > 0.f ? 1.0f / L : 0.f;
+    // TQ3 values (ROTATE) were summed over the kCenScale-scaled centroid table
+    const float inv = (L > 0.f ? 1.0f / L : 0.f) * (ROTATE ? kCenScaleInv : 1.0f);
     float x[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int w = 0; w < kWaves; w++) {

@@ -219,7 +219,7 @@ __global__ __launch_bounds__(kThreads, 2) void q8_attn_kernel(AttnArgs p, uint16
     for (int k = 0; k < 16; k++) {
       const uint32_t e = 16u * (uint32_t)wave + k;
       *reinterpret_cast<uint32_t*>(lds + kMxLdsLut + e * 256 + lane4) =
-          f2h(centroid_imm(e & 7u)) | (f2h(centroid_imm(e >> 3)) << 16);
+          centroid_scaled_h(e & 7u) | (centroid_scaled_h(e >> 3) << 16);
     }
     __syncthreads();
   }

@@ -321,7 +321,8 @@ __device__ void finish_rows(const uint8_t* lds, const AttnArgs& p, int h, int t,
     const int r = wht >> 1, blk = wht & 1;
     const bool live = wht < rows * 2;
     const float L = live ? ml[kMlL + r] : 0.f;
-    const float scale = final ? (L > 0.f ? 1.0f / L : 0.f) : 1.0f;
+    // the centroid table is scaled by kCenScale: undo it here (fp32)
+    const float scale = (final ? (L > 0.f ? 1.0f / L : 0.f) : 1.0f) * kCenScaleInv;
     float x[8];
 #pragma unroll
     for (int i = 0; i < 8; i++) x[i] = live ? mo[r * kHD + blk * 128 + part * 8 + i] * scale : 0.f;
@@ -499,22 +500,29 @@ __global__ __launch_bounds__(kThreads, 1) void tq3_attn_kernel(AttnArgs p, uint1
     const uint32_t w = (uint32_t)wave;
 #pragma unroll
     for (int hk = 0; hk < 4; hk++) {
-      const uint32_t hi = f2h(centroid_imm((4u * w + hk) & 7u)) << 16;
+      const uint32_t hi = centroid_scaled_h((4u * w + hk) & 7u) << 16;
 #pragma unroll
       for (int k = 0; k < 8; k++)
         *reinterpret_cast<uint32_t*>(lds + kLdsLut + (w * 32 + hk * 8 + k) * 256 + lane4) =
-            f2h(centroid_imm(k)) | hi;
+            centroid_scaled_h(k) | hi;
     }
   }
   uint32_t ac[4] = {lane4, lane4, lane4, lane4};   // table address chains
   {
     // rotated query: fp16 in LDS scratch (q_unit), so that each lane's A
     // operand slice is one 16-byte read
+    // Column c < 8 holds the fp16 rounding of the rotated query (hi) and
+    // column c + 8 the fp16 rounding of its remainder (lo): the score MFMA
+    // computes both against the same decoded keys and the two halves are added
+    // in fp32, so the rotated query is carried to ~2^-22 (real columns <= 8).
     uint16_t* qs = reinterpret_cast<uint16_t*>(lds + kLdsQ);
     const int o = q_part >> 2, u = q_part & 3;   // elements part*8..+7 = code group 4*o + u
-    if (2 * wave >= rows_used) {
-      // a wave whose two columns are both dead writes zeros
+    if (q_col >= 8) {
+      // columns 8..15 are written by the waves of columns 0..7
+    } else if (2 * wave >= rows_used) {
+      // a wave whose two columns are both dead writes zeros (hi and lo)
       *reinterpret_cast<uint4*>(qs + q_unit(q_col, 4 * q_blk + u, o) * 8) = make_uint4(0, 0, 0, 0);
+      *reinterpret_cast<uint4*>(qs + q_unit(q_col + 8, 4 * q_blk + u, o) * 8) = make_uint4(0, 0, 0, 0);
     } else {
       float x[8];
 #pragma unroll
@@ -531,11 +539,18 @@ __global__ __launch_bounds__(kThreads, 1) void tq3_attn_kernel(AttnArgs p, uint1
       wht8_inreg(x);
       wht_xor_lanes16(x, lane);
       const float rs = wht_scale();
-      uint32_t pk[4];
+      uint32_t pk[4], pl[4];
 #pragma unroll
-      for (int i = 0; i < 4; i++) pk[i] = f2h(x[2 * i] * rs) | (f2h(x[2 * i + 1] * rs) << 16);
+      for (int i = 0; i < 4; i++) {
+        const float a = x[2 * i] * rs, b = x[2 * i + 1] * rs;
+        const uint32_t ha = f2h(a), hb = f2h(b);
+        pk[i] = ha | (hb << 16);
+        pl[i] = f2h(a - h2f(ha)) | (f2h(b - h2f(hb)) << 16);
+      }
       *reinterpret_cast<uint4*>(qs + q_unit(q_col, 4 * q_blk + u, o) * 8) =
           make_uint4(pk[0], pk[1], pk[2], pk[3]);
+      *reinterpret_cast<uint4*>(qs + q_unit(q_col + 8, 4 * q_blk + u, o) * 8) =
+          make_uint4(pl[0], pl[1], pl[2], pl[3]);
     }
   }
   __syncthreads();
@@ -556,7 +571,7 @@ __global__ __launch_bounds__(kThreads, 1) void tq3_attn_kernel(AttnArgs p, uint1
       qa[s] = *reinterpret_cast<const h8_t*>(qs + q_unit(col, s, row) * 8);
   }
 
-  const float scale2 = p.scale_log2;
+  const float scale2 = p.scale_log2 * kCenScaleInv;
   float m2 = -INFINITY;   // running max of head `col` (base-2 units)
   float lsum = 0.0f;      // this lane's part of the running sum of head `col`
   f4_t acc[16];
@@ -585,7 +600,8 @@ __global__ __launch_bounds__(kThreads, 1) void tq3_attn_kernel(AttnArgs p, uint1
     if (row == 0) {
 #pragma unroll
       for (int g = 0; g < 4; g++) {
-        st[kStKn + 16 * g + col] = kn[g][0] * scale2;   // key norms carry the softmax scale
+        // key norms carry the softmax scale and undo the table scale
+        st[kStKn + 16 * g + col] = kn[g][0] * scale2;
         st[kStKn + kKeyPitch + 16 * g + col] = kn[g][1] * scale2;
       }
     }
@@ -623,7 +639,10 @@ __global__ __launch_bounds__(kThreads, 1) void tq3_attn_kernel(AttnArgs p, uint1
       const f4_t k0 = *reinterpret_cast<const f4_t*>(st + kStKn + 16 * g + 4 * row);
       const f4_t k1 = *reinterpret_cast<const f4_t*>(st + kStKn + kKeyPitch + 16 * g + 4 * row);
 #pragma unroll
-      for (int r = 0; r < 4; r++) s[g][r] = k0[r] * sa[g][0][r] + k1[r] * sa[g][1][r];
+      for (int r = 0; r < 4; r++) {
+        s[g][r] = k0[r] * sa[g][0][r] + k1[r] * sa[g][1][r];
+        s[g][r] += dpp_f<0x128>(s[g][r]);   // + the lo half of the query (column + 8, row_ror:8)
+      }
     }
     if (!dense) {
 #pragma unroll

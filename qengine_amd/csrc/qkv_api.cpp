@@ -231,7 +231,7 @@ int qkv_attn_split_tq3(const uint16_t* q, const qkv_block_tq3* k, const qkv_bloc
   a.start_pos = start_pos;
   a.sub_n = sub_n;
   a.sub_n_max = sub_n_max;
-  a.qpw = 16 / (num_q / num_kv);   // queries share the MFMA columns
+  a.qpw = 8 / (num_q / num_kv);   // queries share MFMA columns 0..7 (8..15: query remainders)
   {
     const uint64_t extent = (uint64_t)(start_pos + sub_n) * num_kv * 104;
     a.kv_bytes = extent;
@@ -309,7 +309,7 @@ struct FastGeom {
 // Query groups of a contiguous TQ3 fast-path launch (16 / GQA queries share a
 // workgroup's MFMA columns).
 int tq3_groups(int num_q, int num_kv, int sub_n) {
-  const int qpw = 16 / (num_q / num_kv);
+  const int qpw = 8 / (num_q / num_kv);
   return (sub_n + qpw - 1) / qpw;
 }
 
@@ -376,7 +376,7 @@ static int decode_tq3(const uint16_t* q, const qkv_block_tq3* k, const qkv_block
   a.start_pos = start_pos;
   a.sub_n = sub_n;
   a.sub_n_max = sub_n;
-  a.qpw = 16 / (num_q / num_kv);   // queries share the MFMA columns
+  a.qpw = 8 / (num_q / num_kv);   // queries share MFMA columns 0..7 (8..15: query remainders)
   {
     const uint64_t extent = (uint64_t)n_keys * num_kv * 104;
     a.kv_bytes = extent;

@@ -6,7 +6,7 @@ import numpy as np
 import pytest
 
 from oracle import oracle as O
-from tests._data import kv_f16, q_f16, rel_err
+from tests._data import assert_tq3_attn, kv_f16, q_f16, rel_err, rel_err_global
 
 pytestmark = pytest.mark.gpu
 TOL = 2e-3
@@ -57,7 +57,14 @@ def _check_partials(pm, pl, po, em, el, eo, sub_n):
     # compare l and o after bringing both to the reference max
     w = np.exp(pm[live] - em[live])
     assert np.max(np.abs(pl[live] * w - el[live]) / el[live]) < TOL
-    assert rel_err(po[live] * w[:, None], eo[live]) < TOL
+    assert rel_err_global(po[live] * w[:, None], eo[live]) < TOL
+
+
+def _exact(q, kb, vb, *, num_q, num_kv=4, start_pos, sub_n, scale=1 / 16, sink_tok=0,
+           window_tok=0, tree_mask=None, **_):
+    return O.attn_exact_tq3(q, kb, vb, num_q=num_q, num_kv=num_kv, hd=256, start_pos=start_pos,
+                            sub_n=sub_n, scale=scale, sink_tok=sink_tok, window_tok=window_tok,
+                            tree_mask=tree_mask)
 
 
 @pytest.mark.parametrize("n,k_splits,num_q", [(4097, 8, 16), (1000, 8, 16), (33, 8, 16),
@@ -72,7 +79,7 @@ def test_split_decode_vs_oracle(dev, n, k_splits, num_q):
     exp = O.attn_split_merge(em, el, eo, num_q=num_q, num_kv=4, hd=256, sub_n=1, sub_n_max=16,
                              k_splits=k_splits)
     _check_partials(pm, pl, po, em, el, eo, 1)
-    assert rel_err(out, exp.view(np.float16)) < TOL
+    assert_tq3_attn(out, exp.view(np.float16), _exact(q, kb, vb, **kw))
 
 
 @pytest.mark.parametrize("sink,window,tree", [(0, 0, False), (0, 0, True), (64, 256, False),
@@ -92,7 +99,7 @@ def test_split_verify_masks(dev, sink, window, tree):
     exp = O.attn_split_merge(em, el, eo, num_q=16, num_kv=4, hd=256, sub_n=sub_n, sub_n_max=16,
                              k_splits=8)
     _check_partials(pm, pl, po, em, el, eo, sub_n)
-    assert rel_err(out, exp.view(np.float16)) < TOL
+    assert_tq3_attn(out, exp.view(np.float16), _exact(q, kb, vb, tree_mask=tm, **kw))
 
 
 @pytest.mark.parametrize("n,num_q,sub_n", [(4097, 16, 1), (32768, 16, 1), (1, 16, 1),
@@ -114,7 +121,8 @@ def test_fast_decode_vs_oracle(dev, n, num_q, sub_n):
                               scale=1 / 16, k_splits=8)
     exp = O.attn_split_merge(em, el, eo, num_q=num_q, num_kv=4, hd=256, sub_n=sub_n,
                              sub_n_max=sub_n, k_splits=8)
-    assert rel_err(out.cpu().numpy(), exp.view(np.float16)) < TOL
+    assert_tq3_attn(out.cpu().numpy(), exp.view(np.float16),
+                    _exact(q, kb, vb, num_q=num_q, start_pos=start, sub_n=sub_n))
 
 
 @pytest.mark.parametrize("n,num_q,sub_n,sink,window,tree", [
@@ -150,7 +158,9 @@ def test_fast_decode_multi_query(dev, n, num_q, sub_n, sink, window, tree):
                               tree_mask=tm)
     exp = O.attn_split_merge(em, el, eo, num_q=num_q, num_kv=num_kv, hd=256, sub_n=sub_n,
                              sub_n_max=sub_n, k_splits=8)
-    assert rel_err(out.cpu().numpy(), exp.view(np.float16)) < TOL
+    assert_tq3_attn(out.cpu().numpy(), exp.view(np.float16),
+                    _exact(q, kb, vb, num_q=num_q, num_kv=num_kv, start_pos=start, sub_n=sub_n,
+                           sink_tok=sink, window_tok=window, tree_mask=tm))
 
 
 def test_fast_decode_rejects_small_workspace(dev):
@@ -189,7 +199,8 @@ def test_fast_decode_workspace_reuse(dev):
                                 _dev(vb.view(np.uint8), dev), out, ws, num_q=16, num_kv=4,
                                 start_pos=n - sub_n, sub_n=sub_n, scale=1 / 16)
         torch.cuda.synchronize()
-        assert rel_err(out.cpu().numpy(), _fast_expected(q, kb, vb, n, 16, sub_n)) < TOL, (n, sub_n)
+        assert_tq3_attn(out.cpu().numpy(), _fast_expected(q, kb, vb, n, 16, sub_n),
+                        _exact(q, kb, vb, num_q=16, start_pos=n - sub_n, sub_n=sub_n), what=(n, sub_n))
 
 
 def test_fast_decode_leaves_record_tags_clear(dev):
@@ -207,7 +218,8 @@ def test_fast_decode_leaves_record_tags_clear(dev):
                                 _dev(vb.view(np.uint8), dev), out, ws, num_q=num_q, num_kv=4,
                                 start_pos=n - 1, sub_n=1, scale=1 / 16)
         torch.cuda.synchronize()
-        assert rel_err(out.cpu().numpy(), _fast_expected(q, kb, vb, n, num_q, 1)) < TOL
+        assert_tq3_attn(out.cpu().numpy(), _fast_expected(q, kb, vb, n, num_q, 1),
+                        _exact(q, kb, vb, num_q=num_q, start_pos=n - 1, sub_n=1))
         # 512-key chunks at this length: 64 records per q head after a 256-byte header
         ml = ws.cpu().numpy()[256:256 + num_q * 64 * 16].view(np.uint32).reshape(num_q * 64, 4)
         assert not ml[:, 2:].any(), "record tags left set"
@@ -226,4 +238,5 @@ def test_fast_decode_output_may_alias_query(dev):
     kvcache.decode_attn_tq3(qt, _dev(kb.view(np.uint8), dev), _dev(vb.view(np.uint8), dev), qt, ws,
                             num_q=16, num_kv=4, start_pos=n - 1, sub_n=1, scale=1 / 16)
     torch.cuda.synchronize()
-    assert rel_err(qt.cpu().numpy(), _fast_expected(q, kb, vb, n, 16, 1)) < TOL
+    assert_tq3_attn(qt.cpu().numpy(), _fast_expected(q, kb, vb, n, 16, 1),
+                    _exact(q, kb, vb, num_q=16, start_pos=n - 1, sub_n=1))

@@ -9,7 +9,7 @@ import numpy as np
 import pytest
 
 from oracle import oracle as O
-from tests._data import kv_f16, q_f16, rel_err
+from tests._data import assert_tq3_attn, kv_f16, q_f16, rel_err
 
 pytestmark = pytest.mark.gpu
 TOL = 2e-3
@@ -53,6 +53,22 @@ def _tables(rng, ctx_lens, block_tokens, max_blocks, n_phys, shared_prefix_block
                 bt[s, b] = -1   # never read: beyond the slot's context
     assert nxt <= n_phys
     return bt
+
+
+def _exact_paged(q, kp, vp, bt, ctx, *, num_q, num_kv, block_tokens):
+    """Exact fp64 attention of each slot over its gathered rows (zero row for ctx 0)."""
+    q = np.ascontiguousarray(q).view(np.uint16).reshape(len(ctx), num_q, HD)
+    out = np.zeros((len(ctx), num_q, HD))
+    bpr = num_kv * HD // 128
+    for s, c in enumerate(ctx):
+        c = int(c)
+        if c <= 0:
+            continue
+        rows = O.paged_rows(bt[s], c, block_tokens)
+        out[s] = O.attn_exact_tq3(q[s:s + 1], O.gather_rows(kp, rows, bpr),
+                                  O.gather_rows(vp, rows, bpr), num_q=num_q, num_kv=num_kv, hd=HD,
+                                  start_pos=c - 1, sub_n=1, scale=1 / 16)[0]
+    return out
 
 
 def _decode(dev, q, kp, vp, bt, ctx, *, num_q, num_kv, max_ctx, block_tokens, ws=None):
@@ -109,8 +125,9 @@ def test_ragged_shared_prefix_vs_oracle(dev, block_tokens, num_q):
                   block_tokens=block_tokens)
     exp = O.decode_paged(O.KV_TQ3, q, kp, vp, bt, ctx, num_q=num_q, num_kv=4, hd=HD,
                          block_tokens=block_tokens, scale=1 / 16).view(np.float16)
+    ex = _exact_paged(q, kp, vp, bt, ctx, num_q=num_q, num_kv=4, block_tokens=block_tokens)
     for s in range(len(ctx)):
-        assert rel_err(got[s], exp[s]) < TOL, s
+        assert_tq3_attn(got[s], exp[s], ex[s], what=s)
 
 
 def test_zero_and_clamped_context(dev):
@@ -126,7 +143,10 @@ def test_zero_and_clamped_context(dev):
     assert np.all(got[0] == 0)
     exp = O.decode_paged(O.KV_TQ3, q, kp, vp, bt, [0, max_ctx, max_ctx], num_q=16, num_kv=4,
                          hd=HD, block_tokens=bt_tok, scale=1 / 16).view(np.float16)
-    assert rel_err(got[1], exp[1]) < TOL and rel_err(got[2], exp[2]) < TOL
+    ex = _exact_paged(q, kp, vp, bt, [0, max_ctx, max_ctx], num_q=16, num_kv=4,
+                      block_tokens=bt_tok)
+    assert_tq3_attn(got[1], exp[1], ex[1])
+    assert_tq3_attn(got[2], exp[2], ex[2])
 
 
 @pytest.mark.parametrize("n_tok", [1, 3, 300])
@@ -218,8 +238,9 @@ def test_config4_step_append_then_decode(dev):
     exp = O.decode_paged(O.KV_TQ3, q, kp2, vp2, bt, ctx_new, num_q=num_q, num_kv=num_kv, hd=HD,
                          block_tokens=bt_tok, scale=1 / 16).view(np.float16)
     got = out.cpu().numpy()
+    ex = _exact_paged(q, kp2, vp2, bt, ctx_new, num_q=num_q, num_kv=num_kv, block_tokens=bt_tok)
     for s in range(n_slots):
-        assert rel_err(got[s], exp[s]) < TOL, s
+        assert_tq3_attn(got[s], exp[s], ex[s], what=s)
 
 
 def test_pool_beyond_4gib(dev):
@@ -271,5 +292,7 @@ def test_pool_beyond_4gib(dev):
                          np.ascontiguousarray(vb).view(O.BLOCK_TQ3).reshape(-1), bt_small,
                          np.asarray(ctx, np.int32), num_q=num_q, num_kv=num_kv, hd=HD,
                          block_tokens=bt_tok, scale=1 / 16)
-    assert rel_err(out["small"].astype(np.float64),
-                   ref.view(np.float16).astype(np.float64)) < TOL
+    ex = _exact_paged(q, np.ascontiguousarray(kb).view(O.BLOCK_TQ3).reshape(-1),
+                      np.ascontiguousarray(vb).view(O.BLOCK_TQ3).reshape(-1), bt_small, ctx,
+                      num_q=num_q, num_kv=num_kv, block_tokens=bt_tok)
+    assert_tq3_attn(out["small"].astype(np.float64), ref.view(np.float16).astype(np.float64), ex)

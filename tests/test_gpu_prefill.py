@@ -11,7 +11,7 @@ import numpy as np
 import pytest
 
 from oracle import oracle as O
-from tests._data import kv_f16, q_f16, rel_err
+from tests._data import kv_f16, q_f16, rel_err_global as rel_err
 
 pytestmark = pytest.mark.gpu
 TOL = 2e-3

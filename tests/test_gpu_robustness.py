@@ -9,7 +9,7 @@ import numpy as np
 import pytest
 
 from oracle import oracle as O
-from tests._data import kv_f16, q_f16, rel_err
+from tests._data import assert_tq3_attn, kv_f16, q_f16, rel_err
 
 pytestmark = pytest.mark.gpu
 TOL = 2e-3
@@ -28,7 +28,7 @@ def _oracle(kind, q, kb, vb, nq, nkv, n):
                               k_splits=8).view(np.float16).astype(np.float64)
 
 
-def _timeout_cycle(dev, call, ws, ref):
+def _timeout_cycle(dev, call, ws, ref, exact=None):
     from qengine_amd import kvcache
     import torch
     assert kvcache.decode_workspace_status(ws) == 0
@@ -48,7 +48,10 @@ def _timeout_cycle(dev, call, ws, ref):
     out = call()
     torch.cuda.synchronize()
     assert not np.any(np.isnan(out))
-    assert rel_err(out, ref) < TOL
+    if exact is None:
+        assert rel_err(out, ref) < TOL
+    else:
+        assert_tq3_attn(out, ref, exact)
     assert kvcache.decode_workspace_status(ws) == 0
 
 
@@ -61,6 +64,8 @@ def test_tq3_decode_merge_timeout(dev):
     kb, vb = O.tq3_encode(k16), O.tq3_encode(v16)
     q = q_f16(rng, 1, nq, 256)
     ref = _oracle(O.KV_TQ3, q, kb, vb, nq, nkv, n)
+    exact = O.attn_exact_tq3(q, kb, vb, num_q=nq, num_kv=nkv, hd=256, start_pos=n - 1, sub_n=1,
+                             scale=1 / 16)
     ws = kvcache.decode_attn_tq3_workspace(nq, nkv, 1, n, dev)
     qd, kd, vd = _dev(q.view(np.uint16), dev), _dev(kb.view(np.uint8), dev), _dev(vb.view(np.uint8), dev)
 
@@ -70,7 +75,7 @@ def test_tq3_decode_merge_timeout(dev):
                                 sub_n=1, scale=1 / 16)
         torch.cuda.synchronize()
         return out.cpu().numpy().astype(np.float64)
-    _timeout_cycle(dev, call, ws, ref)
+    _timeout_cycle(dev, call, ws, ref, exact)
 
 
 def test_q8_decode_merge_timeout(dev):

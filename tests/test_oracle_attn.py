@@ -216,3 +216,25 @@ def test_q8k_tq3v_vs_fp64_and_closed_form():
     for t in range(sub_n):
         mean = v32[:n - sub_n + t + 1].mean(axis=0)               # [nkv][256]
         assert np.allclose(flat[t], np.repeat(mean, nq // nkv, axis=0), rtol=1e-9, atol=1e-12)
+
+
+def test_attn_ref_f32kv_matches_f16_core():
+    """The float-input fp64 reference is the fp16-input one on fp16-representable
+    rows (bit for bit), masks included; the exact-TQ3 truth is that reference
+    over tq3_decode_f32 (pinned in test_oracle_codec), which differs from the
+    fp16-rounded dequantization by the reference's own rounding only."""
+    rng = np.random.default_rng(11)
+    n, nq, nkv = 300, 8, 2
+    k16, v16 = kv_f16(rng, n, nkv, 256), kv_f16(rng, n, nkv, 256)
+    q = q_f16(rng, 4, nq, 256)
+    kw = dict(num_q=nq, num_kv=nkv, hd=256, start_pos=n - 4, sub_n=4, scale=1 / 16)
+    tm = np.array([1, 3, 5, 15], np.uint32)
+    for extra in ({}, {"sink_tok": 32, "window_tok": 64}, {"tree_mask": tm}):
+        a = O.attn_ref_f64(q, k16, v16, **kw, **extra)
+        b = O.attn_ref_f64_f32kv(q, O.f16_to_f32(k16.view(np.uint16)),
+                                 O.f16_to_f32(v16.view(np.uint16)), **kw, **extra)
+        assert np.array_equal(a, b)
+    kb, vb = O.tq3_encode(k16), O.tq3_encode(v16)
+    ex = O.attn_exact_tq3(q, kb, vb, **kw)
+    rd = O.attn_ref_f64(q, O.tq3_decode(kb), O.tq3_decode(vb), **kw)
+    assert 0 < rel_err(rd, ex) < 5e-3

@@ -2,15 +2,15 @@
 through the C ABI, against the workspace entry point qkv_decode_attn_tq3 on
 the same inputs: two calls in a row, the second with a smaller input (the
 scratch keeps the first call's contents).  Both run the same kernels with the
-same geometry, so the outputs must be bit-identical (and within 2e-3 of the
-oracle, the decode's own bar)."""
+same geometry, so the outputs must be bit-identical (and meet the decode's
+own bar, tests/_data.assert_tq3_attn)."""
 import ctypes
 
 import numpy as np
 import pytest
 
 from oracle import oracle as O
-from tests._data import kv_f16, q_f16, rel_err
+from tests._data import assert_tq3_attn, kv_f16, q_f16
 
 pytestmark = pytest.mark.gpu
 TOL = 2e-3
@@ -51,7 +51,9 @@ def _case(dev, seed, n_keys, sub_n, num_q, num_kv):
                               scale=1 / 16, k_splits=ks)
     ref = O.attn_split_merge(pm, pl, po, num_q=num_q, num_kv=num_kv, hd=256, sub_n=sub_n,
                              sub_n_max=sub_n, k_splits=ks).view(np.float16)
-    assert rel_err(b, ref) < TOL
+    exact = O.attn_exact_tq3(q, kb, vb, num_q=num_q, num_kv=num_kv, hd=256, start_pos=start,
+                             sub_n=sub_n, scale=1 / 16)
+    assert_tq3_attn(b, ref, exact)
 
 
 def test_noalloc_matches_workspace_entry_point(dev):
