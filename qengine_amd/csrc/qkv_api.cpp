@@ -597,16 +597,14 @@ int qkv_prefill_attn_tq3(const uint16_t* q, const qkv_block_tq3* k_cache,
   const qkv::PrefillGeom g = qkv::prefill_geom(num_q, num_kv, n_tok, start_pos);
   if (!workspace || workspace_bytes < g.total) return QKV_ERR_WORKSPACE;
   if (!aligned(workspace, 256)) return QKV_ERR_ALIGN;
-  const uint64_t hist = (uint64_t)(start_pos + (from_cache ? n_tok : 0)) * num_kv * 104;
   const uint64_t qbytes = (uint64_t)n_tok * num_q * 256 * 2;
   if (qbytes > 0x7fffffffULL) return QKV_ERR_UNSUPPORTED;   // 32-bit query offsets
+  if ((int64_t)start_pos + n_tok > (int64_t)INT32_MAX - 128) return QKV_ERR_INVALID;
   char* ws = static_cast<char*>(workspace);
   qkv::PrefillArgs a{};
   a.k_cache = reinterpret_cast<const uint32_t*>(k_cache);
   a.v_cache = reinterpret_cast<const uint32_t*>(v_cache);
-  a.kv_bytes = hist;
-  a.qr = reinterpret_cast<uint16_t*>(ws + g.qr_off);
-  a.kr = reinterpret_cast<uint16_t*>(ws + g.kr_off);
+  a.kx = reinterpret_cast<uint16_t*>(ws + g.kx_off);
   a.vt = reinterpret_cast<uint16_t*>(ws + g.vt_off);
   a.part_ml = reinterpret_cast<float*>(ws + g.ml_off);
   a.part_o = reinterpret_cast<float*>(ws + g.o_off);
@@ -614,7 +612,9 @@ int qkv_prefill_attn_tq3(const uint16_t* q, const qkv_block_tq3* k_cache,
   a.num_kv = num_kv;
   a.start_pos = start_pos;
   a.n_tok = n_tok;
-  a.n_pad = from_cache ? 0 : g.n_pad;   // no chunk keys to rotate or tile
+  a.hist = from_cache ? start_pos + n_tok : start_pos;
+  a.h_pad = (a.hist + 63) / 64 * 64;
+  a.n_pad = from_cache ? 0 : g.n_pad;   // no chunk rows to stage
   a.n_split = g.n_split;
   a.from_cache = from_cache ? 1 : 0;
   a.scale_log2 = scale * qkv::kLog2e;

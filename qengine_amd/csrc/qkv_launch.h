@@ -41,28 +41,30 @@ struct MoveArgs {
 hipError_t launch_kv_move(const MoveArgs& a, bool ordered, hipStream_t stream);
 
 // Chunked prefill over a TQ3 cache (prefill_tq3.hip).  Workspace pieces:
-// qr  rotated queries [n_tok][num_q][256] fp16
-// kr  rotated chunk keys [num_kv][n_pad][256] fp16
-// vt  rotated chunk values, 64-key tiles [num_kv][n_pad/64][256 dims][64] fp16
-// part_ml / part_o  key-split partials {m (log2 units), l} and rotated o
+// kx  keys [num_kv][h_pad + n_pad][256] fp16: the history rows dequantized
+//     exactly as the reference's bulk dequantization, padded to whole 64-row
+//     tiles, then the chunk's own keys
+// vt  values in 64-key tiles [num_kv][(h_pad + n_pad)/64][256 dims][64] fp16
+// part_ml / part_o  key-split partials {m (log2 units), l} and o
 //                   [n_split][n_tok][num_q] (x 256 for o)
 struct PrefillArgs {
-  const uint32_t* k_cache;   // slot-base TQ3 caches (rows 0 .. start_pos-1, or
-                             // 0 .. start_pos+n_tok-1 when from_cache)
+  const uint32_t* k_cache;   // slot-base TQ3 caches, rows 0 .. hist-1
   const uint32_t* v_cache;
-  uint64_t kv_bytes;         // readable history bytes from the slot base
-  uint16_t* qr;
-  uint16_t* kr;
+  uint16_t* kx;
   uint16_t* vt;
   float* part_ml;
   float* part_o;
-  int num_q, num_kv, start_pos, n_tok, n_pad, n_split;
+  int num_q, num_kv, start_pos, n_tok;
+  int hist;                  // cache rows attended: start_pos, or start_pos + n_tok (verify)
+  int h_pad;                 // hist rounded up to 64
+  int n_pad;                 // chunk rows staged: n_tok rounded up to 64, 0 in verify mode
+  int n_split;
   int from_cache;            // 1: the chunk's keys are cache rows too (verify)
   float scale_log2;
 };
 struct PrefillGeom {
-  int n_pad, n_split;
-  size_t qr_off, kr_off, vt_off, ml_off, o_off, total;
+  int n_pad, h_pad, n_split;
+  size_t kx_off, vt_off, ml_off, o_off, total;
 };
 PrefillGeom prefill_geom(int num_q, int num_kv, int n_tok, int start_pos);
 hipError_t launch_prefill_tq3(const PrefillArgs& a, int gqa, const uint16_t* q, const uint16_t* k,

@@ -45,19 +45,26 @@ def rel_err_global(out, ref):
 
 
 def assert_tq3_attn(got, ref, exact, tol=2e-3, what=""):
-    """Bar of the TQ3 attention consumers (rotated-domain arithmetic, fp32
-    accumulation), two parts:
+    """Bar of the TQ3 decode consumers (rotated-domain arithmetic, fp32
+    accumulation):
       - every (query, head) output row within `tol` of the exact fp64
         attention over the exactly dequantized cache (rel_err, per row);
       - the whole output within `tol` of the reference-order oracle
         (fp16-rounded dequantization, the reference's split order;
-        rel_err_global).
-    The reference's own numerics round every dequantized element to fp16,
-    which puts its rows up to 2.4e-3 (per row, 20 seeds at 4097 keys) from the
-    exact attention; a per-row bar against the reference would therefore
-    reject even the exact result.  Returns (per-row vs exact, global vs
-    reference)."""
+        rel_err_global), or, where the reference itself lies further than
+        that from the exact attention, no further from the reference than
+        `tol` plus the reference's own distance d_ref from the exact result.
+    The reference's numerics round every dequantized element to fp16 before
+    its fp32 dot products (attention.cuh:2036-2072 in the split decode,
+    turboquant.cuh:199 in the bulk dequantization), which puts its rows up to
+    2.4e-3 (per row, 20 seeds at 4097 keys) and its whole output up to ~2.3e-3
+    (32768 keys, 16 verify queries) from the exact attention; the rotated-domain kernels never form those fp16 elements and
+    are held to the exact values instead.  The second part guards the exact
+    oracle path itself (a mistake shared by the kernel and attn_exact_tq3
+    would show up against the independently computed reference order).
+    Returns (per-row vs exact, global vs reference, d_ref)."""
     e_row = rel_err(got, exact)
     e_ref = rel_err_global(got, ref)
-    assert e_row < tol and e_ref < tol, (what, e_row, e_ref)
-    return e_row, e_ref
+    d_ref = rel_err_global(ref, exact)
+    assert e_row < tol and e_ref < max(tol, tol + d_ref), (what, e_row, e_ref, d_ref)
+    return e_row, e_ref, d_ref

@@ -5,13 +5,16 @@ Reference numerics (model.cuh:5189-5214, 5256-5330; attention.cuh:1690-1831):
 the history is dequantized to fp16 (tq3_dequantize_kernel), the chunk's own
 keys and values stay fp16, and the chunk attends causally (token t sees keys
 0 .. start_pos + t).  The oracle builds exactly that fp16 key/value array and
-runs its split-K reference decode + merge over it.  Bar: within 2e-3 relative
-error (max |diff| / max |ref|), fp32 accumulation."""
+runs its split-K reference decode + merge over it.  The kernel reproduces those
+numerics (the history bit-exact to the reference's fp16 dequantization, exact
+fp16 products, fp32 sums), so the bar is per row: every (token, head) output
+row within 2e-3 of the oracle's, relative to the row's largest magnitude
+(tests/_data.rel_err)."""
 import numpy as np
 import pytest
 
 from oracle import oracle as O
-from tests._data import kv_f16, q_f16, rel_err_global as rel_err
+from tests._data import kv_f16, q_f16, rel_err
 
 pytestmark = pytest.mark.gpu
 TOL = 2e-3
@@ -120,39 +123,12 @@ def test_prefill_causal_rows_ignore_later_tokens(dev):
     assert not np.array_equal(a[50:].view(np.uint16), b[50:].view(np.uint16))
 
 
-def _exact_rows(q, kb, vb, ck, cv, rows, *, num_q, num_kv, start_pos, scale):
-    """fp64 attention over the cache's exactly dequantized history
-    (turboquant.cuh:169-200 in fp32, before the fp16 rounding) and the raw
-    fp16 chunk, for the given chunk tokens."""
-    kx = np.concatenate([O.tq3_decode_f32(kb).reshape(-1, num_kv, 256),
-                         ck.astype(np.float32)]).astype(np.float64)
-    vx = np.concatenate([O.tq3_decode_f32(vb).reshape(-1, num_kv, 256),
-                         cv.astype(np.float32)]).astype(np.float64)
-    gqa = num_q // num_kv
-    out = {}
-    for t in rows:
-        n = start_pos + t + 1
-        o = np.zeros((num_q, 256))
-        for qh in range(num_q):
-            s = kx[:n, qh // gqa] @ q[t, qh].astype(np.float64) * scale
-            p = np.exp(s - s.max())
-            o[qh] = (p[:, None] * vx[:n, qh // gqa]).sum(0) / p.sum()
-        out[t] = o
-    return out
-
-
-def test_prefill_config5_sampled_rows(dev):
+def test_prefill_config5_full_size(dev):
     """BASELINE config 5(i) at full size: a 131072-token TQ3 history (built by
-    the GPU append) and a 2048-token chunk, checked on sampled rows.
-
-    At this length the reference's own numerics -- every dequantized history
-    element rounded to fp16 (turboquant.cuh:199) before the fp32 dot products --
-    drift from the attention over the exactly dequantized cache by up to ~2e-3
-    (measured with the oracle), and the rotated-domain kernel does not round
-    dequantized elements.  The bar is therefore applied against the fp64
-    attention over the exactly dequantized values (2e-3), and the distance to
-    the reference numerics is bounded by 2e-3 plus the reference's own
-    measured distance from those exact values."""
+    the GPU append) and a 2048-token chunk.  64 rows -- eight runs of eight
+    consecutive tokens spread over the chunk, its first and last tokens
+    included -- against the reference numerics (the oracle over the fp16
+    scratch of dequantized history + raw chunk), per row."""
     from qengine_amd import kvcache
     torch = _torch()
     num_q, num_kv, start_pos, n_tok, scale = 16, 4, 131072, 2048, 1 / 16
@@ -174,16 +150,16 @@ def test_prefill_config5_sampled_rows(dev):
     assert np.all(np.isfinite(got))
     kb = kbt.cpu().numpy().view(O.BLOCK_TQ3).reshape(-1)
     vb = vbt.cpu().numpy().view(O.BLOCK_TQ3).reshape(-1)
-    rows = (0, 1, 777, 2047)
-    exact = _exact_rows(q, kb, vb, ck, cv, rows, num_q=num_q, num_kv=num_kv,
-                        start_pos=start_pos, scale=scale)
     k_all, v_all = _oracle_kv(kb, vb, ck, cv, num_kv)
-    for t in rows:
-        ref = _oracle(q[t:t + 1], k_all[:start_pos + t + 1], v_all[:start_pos + t + 1],
-                      num_q=num_q, num_kv=num_kv, start_pos=start_pos + t, scale=scale,
-                      k_splits=32)[0]
-        assert rel_err(got[t], exact[t]) < TOL, t
-        assert rel_err(got[t], ref) < TOL + rel_err(ref, exact[t]), t
+    worst = 0.0
+    for t0 in (0, 293, 585, 877, 1169, 1461, 1753, 2040):
+        end = start_pos + t0 + 8
+        ref = _oracle(q[t0:t0 + 8], k_all[:end], v_all[:end], num_q=num_q, num_kv=num_kv,
+                      start_pos=start_pos + t0, scale=scale, k_splits=32)
+        e = rel_err(got[t0:t0 + 8], ref)
+        worst = max(worst, e)
+        assert e < TOL, (t0, e)
+    print(f"config 5(i): worst per-row rel err over 64 rows {worst:.3e}")
 
 
 # ---------------------------------------------------------------------------
@@ -225,9 +201,12 @@ def test_verify_from_cache_vs_oracle(dev, start_pos, n_tok, num_q):
 
 
 def test_verify_matches_decode_path(dev):
-    """The MFMA verify and the split-K decode kernel (sub_n = 16) compute the
-    same rows over a 32768-token cache."""
+    """The MFMA verify and the split-K decode kernel (sub_n = 16) over a
+    32768-token cache: the verify per row against the reference oracle, the
+    decode to its own bar (tests/_data.assert_tq3_attn), and the two within
+    the sum of their bars of each other."""
     from qengine_amd import kvcache
+    from tests._data import assert_tq3_attn
     torch = _torch()
     num_q, num_kv, start_pos, n_tok, scale = 16, 4, 32768, 16, 1 / 16
     rng = np.random.default_rng(9)
@@ -246,4 +225,16 @@ def test_verify_matches_decode_path(dev):
     kvcache.decode_attn_tq3(qt, kbt, vbt, b, wsd, num_q=num_q, num_kv=num_kv, start_pos=start_pos,
                             sub_n=n_tok, scale=scale)
     torch.cuda.synchronize()
-    assert rel_err(a.cpu().numpy(), b.cpu().numpy()) < TOL
+    a, b = a.cpu().numpy(), b.cpu().numpy()
+    kb = kbt.cpu().numpy().view(O.BLOCK_TQ3).reshape(-1)
+    vb = vbt.cpu().numpy().view(O.BLOCK_TQ3).reshape(-1)
+    pm, pl, po = O.attn_split(O.KV_TQ3, q, kb, vb, num_q=num_q, num_kv=num_kv, hd=256,
+                              start_pos=start_pos, sub_n=n_tok, sub_n_max=n_tok,
+                              active_end_max=n, scale=scale, k_splits=8)
+    ref = O.attn_split_merge(pm, pl, po, num_q=num_q, num_kv=num_kv, hd=256, sub_n=n_tok,
+                             sub_n_max=n_tok, k_splits=8).view(np.float16)
+    exact = O.attn_exact_tq3(q, kb, vb, num_q=num_q, num_kv=num_kv, hd=256, start_pos=start_pos,
+                             sub_n=n_tok, scale=scale)
+    assert rel_err(a, ref) < TOL
+    assert_tq3_attn(b, ref, exact)
+    assert rel_err(a, b) < 2 * TOL
