@@ -109,6 +109,34 @@ int qkv_q8_append_kv(const uint16_t* k_f16, const uint16_t* v_f16, qkv_block_q8*
 int qkv_q8_dequant(const qkv_block_q8* in, uint16_t* out_f16, int n_blocks,
                    hipStream_t stream);
 
+/* ---------------------------------------------------------------------------
+ * KV inject from a DFK2 plane (int8 rows, one fp16 scale per 128 elements)
+ * ------------------------------------------------------------------------- */
+
+/* Replaces dfki2_dequant_kernel<<<(n + 255) / 256, 256>>>(q, scales, out, n,
+ * kv_dim) (model.cuh:149-159; launched at model.cuh:3189-3192):
+ * out[i] = half(float(q[i]) * float(scales[i / 128])), the scales of a row of
+ * kv_dim elements being scales[row * kv_dim / 128 ...].  kv_dim a multiple of
+ * 128, n a multiple of 8; q 8-byte and out 16-byte aligned. */
+int qkv_dfk2_dequant(const int8_t* q, const uint16_t* scales, uint16_t* out_f16, long long n,
+                     int kv_dim, hipStream_t stream);
+
+/* The inject's dequantize-then-quantize pair fused into one launch: the
+ * dfki2_dequant_kernel into the fp16 scratch followed by
+ * tq3_quantize_kernel<<<(blocks + 31) / 32, 32>>>(scratch, dst, blocks)
+ * (model.cuh:3189-3192, 3218-3226; the value planes, and key planes that need
+ * no RoPE).  Block i is quantized from q[128 i .. 128 i + 127] with scale
+ * scales[i]; the codes and norms are bit-identical to that pair's.  q 16-byte
+ * aligned. */
+int qkv_tq3_append_dfk2(const int8_t* q, const uint16_t* scales, qkv_block_tq3* out,
+                        int n_blocks, hipStream_t stream);
+
+/* The same for a Q8_0 cache (model.cuh:3189-3192 then 3227-3233 /
+ * 3209-3217): 32-element block i from q[32 i ..] with scale scales[i / 4];
+ * n_blocks a multiple of 4; q 8-byte aligned. */
+int qkv_q8_append_dfk2(const int8_t* q, const uint16_t* scales, qkv_block_q8* out, int n_blocks,
+                       hipStream_t stream);
+
 /* Token-row moves inside one slot of one layer's cache: replaces the per-token
  * device copies of kv_move_token (model.cuh:7430-7471; its tree-verify
  * acceptance calls it once per accepted token and layer).  For i = 0..n-1 in

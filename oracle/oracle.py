@@ -84,6 +84,8 @@ def _declare(L):
                                   _I, _I, _P]
     L.or_key_visible.restype = _I
     L.or_key_visible.argtypes = [_I, _I, _I, _I, _I, _P]
+    L.or_legacy_decode.restype = _I
+    L.or_legacy_decode.argtypes = [_I, _I, _I, _P, _P, _P, _P, _P, _I, _I, _I, _I, _F]
 
 
 def _ptr(a):
@@ -322,6 +324,29 @@ def attn_q8k_tq3v_f64(q, k_q8, v_tq3, *, num_q, num_kv, hd, start_pos, sub_n, sc
             w = np.exp(s - s.max(axis=1, keepdims=True))
             out[t, h * gqa:(h + 1) * gqa] = (w @ v[:n, h]) / w.sum(axis=1, keepdims=True)
     return out
+
+
+def legacy_decode(k_kind, v_kind, q, k, v, *, num_q, num_kv, hd, seq_len, scale,
+                  tq_fused=False, return_probs=False):
+    """The reference's short-context decode (model.cuh:2544-2664) of one query
+    token over cache rows 0 .. seq_len-1: K and V dequantized to an fp16
+    scratch, attn_score_kernel_h, softmax_kernel (sum + 1e-10),
+    attn_value_kernel_h (attention.cuh:277-316, 531-575, 885-907); with
+    tq_fused, TQ3 operands go through attn_score_kernel_tq3 /
+    attn_value_kernel_tq3 (attention.cuh:400-483, 920-989).  q [1][num_q][hd]
+    or [num_q][hd] fp16; k / v in the layout of their kind (KV_TQ3 blocks,
+    KV_Q8 blocks, KV_F16 fp16 rows).  Returns fp16 bits [num_q][hd] (and the
+    softmax rows [num_q][seq_len] float32 when return_probs)."""
+    qq = _u16(q).reshape(num_q, hd)
+    kk = np.ascontiguousarray(k)
+    vv = np.ascontiguousarray(v)
+    out = np.zeros((num_q, hd), np.uint16)
+    probs = np.zeros((num_q, seq_len), np.float32)
+    rc = lib().or_legacy_decode(k_kind, v_kind, int(bool(tq_fused)), _ptr(qq), _ptr(kk), _ptr(vv),
+                                _ptr(out), _ptr(probs), num_q, num_kv, hd, seq_len, float(scale))
+    if rc != 0:
+        raise ValueError("legacy_decode: unsupported shape")
+    return (out, probs) if return_probs else out
 
 
 def key_visible(key, start_pos, t_idx, sink_tok=0, window_tok=0, tree_mask=None):

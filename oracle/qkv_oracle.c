@@ -660,3 +660,210 @@ void or_attn_ref_f64_f32kv(const uint16_t* q, const float* k, const float* v, do
     attn_ref_f64_any(q, k, v, 1, out, num_q, num_kv, hd, start_pos, sub_n, scale, sink_tok,
                      window_tok, tree_mask);
 }
+
+/* ===================================================================== */
+/* Legacy short-context decode (model.cuh:2544-2664)                      */
+/* ===================================================================== */
+/* Below 4096 cache rows the reference decodes one query token without the
+ * fused split kernel: the keys (and later the values) are dequantized to an
+ * fp16 scratch, then attn_score_kernel_h, softmax_kernel and
+ * attn_value_kernel_h run over all seq_len rows (every row visible).  With
+ * TQ_FUSED set, TQ3 keys / values go through attn_score_kernel_tq3 /
+ * attn_value_kernel_tq3 instead, which dequantize to fp32 without the fp16
+ * rounding.  `sum += a * b` in these kernels is taken as contracted to one
+ * fused multiply-add (nvcc's default -fmad=true); fmaf states it here. */
+
+/* lane 0's value after `for (off = 16; off > 0; off >>= 1) x += shfl_xor(x, off)`
+ * over 32 lanes (attention.cuh:300-301) */
+static float warp_butterfly_lane0(const float* x32) {
+    float part[32];
+    memcpy(part, x32, sizeof(part));
+    for (int off = 16; off > 0; off >>= 1) {
+        float nxt[32];
+        for (int l = 0; l < 32; l++) nxt[l] = part[l] + part[l ^ off];
+        memcpy(part, nxt, sizeof(part));
+    }
+    return part[0];
+}
+
+/* block-wide sum of per-thread values v[0..bd) (bd a multiple of 32): per
+ * warp the butterfly, then warp 0 reduces the warp sums, lanes at or above
+ * n_warps contributing 0 (attention.cuh:300-314) */
+static float block_sum_legacy(const float* v, int bd) {
+    const int n_warps = bd / 32;
+    float ws[32];
+    for (int l = 0; l < 32; l++) ws[l] = 0.0f;
+    for (int w = 0; w < n_warps; w++) ws[w] = warp_butterfly_lane0(v + 32 * w);
+    return warp_butterfly_lane0(ws);
+}
+
+/* attn_score_kernel_h (attention.cuh:277-316): blockDim = min(hd, 256), thread
+ * t sums elements t, t + blockDim, ...; score = sum * scale. */
+static void legacy_scores_h(const uint16_t* q, const uint16_t* k16, float* scores, int num_q,
+                            int num_kv, int hd, int seq_len, float scale) {
+    const int bd = hd < 256 ? hd : 256;
+    const int gqa = num_q / num_kv;
+    #pragma omp parallel for collapse(2) schedule(static)
+    for (int qh = 0; qh < num_q; qh++) {
+        for (int pos = 0; pos < seq_len; pos++) {
+            float th[256];
+            const uint16_t* qv = q + (int64_t)qh * hd;
+            const uint16_t* kv = k16 + ((int64_t)pos * num_kv + qh / gqa) * hd;
+            for (int t = 0; t < bd; t++) {
+                float s = 0.0f;
+                for (int i = t; i < hd; i += bd)
+                    s = fmaf(or_f16_to_f32(qv[i]), or_f16_to_f32(kv[i]), s);
+                th[t] = s;
+            }
+            scores[(int64_t)qh * seq_len + pos] = block_sum_legacy(th, bd) * scale;
+        }
+    }
+}
+
+/* One TQ3 block dequantized as attn_score_kernel_tq3 / attn_value_kernel_tq3
+ * do (attention.cuh:420-445, 941-963): centroids, the butterflies, then
+ * x * (sign * (rsqrtf(128) * norm)), fp32, no fp16 rounding. */
+static void legacy_tq3_block_f32(const or_block_tq3* b, float* x) {
+    const float* sg = signs();
+    for (int g = 0; g < OR_TQ_BLOCK / 8; g++) {
+        uint8_t idx[8];
+        or_unpack_3bit_8(&b->qs[3 * g], idx);
+        for (int j = 0; j < 8; j++) x[8 * g + j] = k_centroids[idx[j]];
+    }
+    for (int step = 1; step < OR_TQ_BLOCK; step <<= 1)
+        for (int i = 0; i < OR_TQ_BLOCK; i += 2 * step)
+            for (int j = i; j < i + step; j++) {
+                const float a = x[j], c = x[j + step];
+                x[j] = a + c;
+                x[j + step] = a - c;
+            }
+    const float scale_norm = or_tq3_wht_scale() * b->norm;
+    for (int i = 0; i < OR_TQ_BLOCK; i++) x[i] *= sg[i] * scale_norm;
+}
+
+/* attn_score_kernel_tq3 (attention.cuh:400-483): blockDim = hd, thread t holds
+ * K element t; prod = fp16(q_t) * k_t, reduced as above, times scale. */
+static void legacy_scores_tq3(const uint16_t* q, const or_block_tq3* k, float* scores, int num_q,
+                              int num_kv, int hd, int seq_len, float scale) {
+    const int gqa = num_q / num_kv, bpk = hd / OR_TQ_BLOCK;
+    #pragma omp parallel for collapse(2) schedule(static)
+    for (int kvh = 0; kvh < num_kv; kvh++) {
+        for (int pos = 0; pos < seq_len; pos++) {
+            float kx[512], th[512];
+            for (int j = 0; j < bpk; j++)
+                legacy_tq3_block_f32(k + ((int64_t)pos * num_kv + kvh) * bpk + j,
+                                     kx + j * OR_TQ_BLOCK);
+            for (int qi = 0; qi < gqa; qi++) {
+                const int qh = kvh * gqa + qi;
+                for (int t = 0; t < hd; t++) th[t] = or_f16_to_f32(q[(int64_t)qh * hd + t]) * kx[t];
+                scores[(int64_t)qh * seq_len + pos] = block_sum_legacy(th, hd) * scale;
+            }
+        }
+    }
+}
+
+/* softmax_kernel (attention.cuh:531-575) with st threads, st the least power
+ * of two >= min(seq_len, 256): max, e = expf(x - max), per-thread strided
+ * sums, a shared-memory tree, row *= 1 / (sum + 1e-10). */
+static void legacy_softmax(float* scores, int num_q, int seq_len) {
+    int st = 1;
+    while (st < seq_len && st < 256) st <<= 1;
+    for (int qh = 0; qh < num_q; qh++) {
+        float* row = scores + (int64_t)qh * seq_len;
+        float mx = -1e30f;
+        for (int i = 0; i < seq_len; i++) mx = fmaxf(mx, row[i]);
+        float sd[256];
+        for (int t = 0; t < st; t++) {
+            float s = 0.0f;
+            for (int i = t; i < seq_len; i += st) {
+                const float e = expf(row[i] - mx);
+                row[i] = e;
+                s += e;
+            }
+            sd[t] = s;
+        }
+        for (int s = st / 2; s > 0; s >>= 1)
+            for (int t = 0; t < s; t++) sd[t] += sd[t + s];
+        const float inv = 1.0f / (sd[0] + 1e-10f);
+        for (int i = 0; i < seq_len; i++) row[i] *= inv;
+    }
+}
+
+/* attn_value_kernel_h (attention.cuh:885-907): out[d] = fp16(sequential sum
+ * over pos of p * v). */
+static void legacy_values_h(const float* probs, const uint16_t* v16, uint16_t* out, int num_q,
+                            int num_kv, int hd, int seq_len) {
+    const int gqa = num_q / num_kv;
+    #pragma omp parallel for schedule(static)
+    for (int qh = 0; qh < num_q; qh++) {
+        const float* sc = probs + (int64_t)qh * seq_len;
+        for (int d = 0; d < hd; d++) {
+            float s = 0.0f;
+            for (int pos = 0; pos < seq_len; pos++)
+                s = fmaf(sc[pos], or_f16_to_f32(v16[((int64_t)pos * num_kv + qh / gqa) * hd + d]), s);
+            out[(int64_t)qh * hd + d] = or_f32_to_f16(s);
+        }
+    }
+}
+
+/* attn_value_kernel_tq3 (attention.cuh:920-989): per (kv head, 128-dim
+ * block), acc += p * v over pos with v dequantized in fp32. */
+static void legacy_values_tq3(const float* probs, const or_block_tq3* v, uint16_t* out,
+                              int num_q, int num_kv, int hd, int seq_len) {
+    const int gqa = num_q / num_kv, bpk = hd / OR_TQ_BLOCK;
+    #pragma omp parallel for collapse(2) schedule(static)
+    for (int kvh = 0; kvh < num_kv; kvh++) {
+        for (int db = 0; db < bpk; db++) {
+            float acc[8][OR_TQ_BLOCK];
+            memset(acc, 0, sizeof(acc));
+            float x[OR_TQ_BLOCK];
+            for (int pos = 0; pos < seq_len; pos++) {
+                legacy_tq3_block_f32(v + ((int64_t)pos * num_kv + kvh) * bpk + db, x);
+                for (int qi = 0; qi < gqa && qi < 8; qi++) {
+                    const float p = probs[(int64_t)(kvh * gqa + qi) * seq_len + pos];
+                    for (int l = 0; l < OR_TQ_BLOCK; l++) acc[qi][l] = fmaf(p, x[l], acc[qi][l]);
+                }
+            }
+            for (int qi = 0; qi < gqa && qi < 8; qi++)
+                for (int l = 0; l < OR_TQ_BLOCK; l++)
+                    out[(int64_t)(kvh * gqa + qi) * hd + db * OR_TQ_BLOCK + l] = or_f32_to_f16(acc[qi][l]);
+        }
+    }
+}
+
+/* The fp16 scratch a legacy consumer reads: dequantized rows (TQ3 bulk
+ * dequantization turboquant.cuh:169-200, Q8 attention.cuh:2614-2626) or the
+ * fp16 cache itself. */
+static uint16_t* legacy_scratch(int kind, const void* cache, int num_kv, int hd, int seq_len) {
+    uint16_t* s = (uint16_t*)malloc(sizeof(uint16_t) * (size_t)seq_len * num_kv * hd);
+    #pragma omp parallel for schedule(static)
+    for (int pos = 0; pos < seq_len; pos++)
+        for (int h = 0; h < num_kv; h++)
+            decode_row(kind, cache, pos, num_kv, h, hd, s + ((int64_t)pos * num_kv + h) * hd);
+    return s;
+}
+
+int or_legacy_decode(int k_kind, int v_kind, int tq_fused, const uint16_t* q, const void* k,
+                     const void* v, uint16_t* out, float* probs, int num_q, int num_kv, int hd,
+                     int seq_len, float scale) {
+    if (seq_len < 1 || hd % 32 || hd > 512 || num_q % num_kv || num_q / num_kv > 8) return -1;
+    if (tq_fused && (k_kind == OR_KV_TQ3 || v_kind == OR_KV_TQ3) && hd % OR_TQ_BLOCK) return -1;
+    float* sc = probs ? probs : (float*)malloc(sizeof(float) * (size_t)num_q * seq_len);
+    if (k_kind == OR_KV_TQ3 && tq_fused) {
+        legacy_scores_tq3(q, (const or_block_tq3*)k, sc, num_q, num_kv, hd, seq_len, scale);
+    } else {
+        uint16_t* k16 = legacy_scratch(k_kind, k, num_kv, hd, seq_len);
+        legacy_scores_h(q, k16, sc, num_q, num_kv, hd, seq_len, scale);
+        free(k16);
+    }
+    legacy_softmax(sc, num_q, seq_len);
+    if (v_kind == OR_KV_TQ3 && tq_fused) {
+        legacy_values_tq3(sc, (const or_block_tq3*)v, out, num_q, num_kv, hd, seq_len);
+    } else {
+        uint16_t* v16 = legacy_scratch(v_kind, v, num_kv, hd, seq_len);
+        legacy_values_h(sc, v16, out, num_q, num_kv, hd, seq_len);
+        free(v16);
+    }
+    if (!probs) free(sc);
+    return 0;
+}

@@ -124,6 +124,17 @@ void or_attn_ref_f64_f32kv(const uint16_t* q, const float* k, const float* v, do
 int or_key_visible(int key, int start_pos, int t_idx, int sink_tok, int window_tok,
                    const uint32_t* tree_mask);
 
+/* Legacy short-context decode of one query token over seq_len rows
+ * (model.cuh:2544-2664): fp16 scratch + attn_score_kernel_h + softmax_kernel +
+ * attn_value_kernel_h, or with tq_fused the fp32 TQ3 kernels
+ * (attention.cuh:400-483, 920-989) for TQ3 operands.  k_kind / v_kind are
+ * OR_KV_*; q [num_q][hd] fp16; out [num_q][hd] fp16; probs (optional)
+ * receives the normalized softmax rows [num_q][seq_len].  Returns 0, or -1 for
+ * an unsupported shape. */
+int or_legacy_decode(int k_kind, int v_kind, int tq_fused, const uint16_t* q, const void* k,
+                     const void* v, uint16_t* out, float* probs, int num_q, int num_kv, int hd,
+                     int seq_len, float scale);
+
 #ifdef __cplusplus
 }
 #endif

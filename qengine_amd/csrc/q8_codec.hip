@@ -30,23 +30,39 @@ __device__ __forceinline__ uint32_t q8_code(float v, float inv) {
   return (uint32_t)q & 0xffu;
 }
 
-// gridDim.y selects (in, out) so K and V can share one launch.
+// gridDim.y selects (in, out) so K and V can share one launch.  kDfk2: the
+// input is DFK2 int8 rows (8 bytes per 8-element group) with one fp16 scale
+// per 128 elements (sc0/sc1), each element first dequantized as
+// dfki2_dequant_kernel does (model.cuh:149-159): half(float(q) * float(s)).
+template <bool kDfk2>
 __global__ __launch_bounds__(kQ8Threads) void q8_append_kernel(
-    const uint4* __restrict__ in0, uint8_t* __restrict__ out0, const uint4* __restrict__ in1,
-    uint8_t* __restrict__ out1, int n_blocks) {
-  const uint4* __restrict__ in = blockIdx.y ? in1 : in0;
+    const void* __restrict__ in0, uint8_t* __restrict__ out0, const void* __restrict__ in1,
+    uint8_t* __restrict__ out1, int n_blocks, const uint16_t* __restrict__ sc0,
+    const uint16_t* __restrict__ sc1) {
   uint8_t* __restrict__ out = blockIdx.y ? out1 : out0;
   const long g = (long)blockIdx.x * kQ8Threads + threadIdx.x;  // 8-element group
   const long blk = g >> 2;
   const int part = (int)(g & 3);
   const bool live = blk < n_blocks;
-  uint4 w = live ? in[g] : make_uint4(0, 0, 0, 0);
   float v[8];
-  const uint32_t ww[4] = {w.x, w.y, w.z, w.w};
+  if constexpr (kDfk2) {
+    const uint2* __restrict__ in = static_cast<const uint2*>(blockIdx.y ? in1 : in0);
+    const uint16_t* __restrict__ sc = blockIdx.y ? sc1 : sc0;
+    const uint2 w = live ? in[g] : make_uint2(0, 0);
+    const float s = live ? h2f(sc[g >> 4]) : 0.0f;   // 16 groups of 8 per scale
+    const uint32_t ww[2] = {w.x, w.y};
 #pragma unroll
-  for (int k = 0; k < 4; k++) {
-    v[2 * k] = h2f(ww[k] & 0xffffu);
-    v[2 * k + 1] = h2f(ww[k] >> 16);
+    for (int k = 0; k < 8; k++)
+      v[k] = h2f(f2h((float)(int8_t)((ww[k >> 2] >> (8 * (k & 3))) & 0xffu) * s));
+  } else {
+    const uint4* __restrict__ in = static_cast<const uint4*>(blockIdx.y ? in1 : in0);
+    const uint4 w = live ? in[g] : make_uint4(0, 0, 0, 0);
+    const uint32_t ww[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+      v[2 * k] = h2f(ww[k] & 0xffffu);
+      v[2 * k + 1] = h2f(ww[k] >> 16);
+    }
   }
   float amax = fabsf(v[0]);
 #pragma unroll
@@ -92,12 +108,48 @@ __global__ __launch_bounds__(kQ8Threads) void q8_dequant_kernel(const uint8_t* _
 }
 
 hipError_t launch_q8_append(const void* in0, void* out0, const void* in1, void* out1,
-                            int n_blocks, int n_tensors, hipStream_t stream) {
+                            int n_blocks, int n_tensors, hipStream_t stream,
+                            const uint16_t* sc0, const uint16_t* sc1) {
   const long groups = (long)n_blocks * 4;
   dim3 grid((unsigned)((groups + kQ8Threads - 1) / kQ8Threads), n_tensors);
-  hipLaunchKernelGGL(q8_append_kernel, grid, dim3(kQ8Threads), 0, stream,
-                     static_cast<const uint4*>(in0), static_cast<uint8_t*>(out0),
-                     static_cast<const uint4*>(in1), static_cast<uint8_t*>(out1), n_blocks);
+  if (sc0 != nullptr)
+    hipLaunchKernelGGL(q8_append_kernel<true>, grid, dim3(kQ8Threads), 0, stream, in0,
+                       static_cast<uint8_t*>(out0), in1, static_cast<uint8_t*>(out1), n_blocks,
+                       sc0, sc1);
+  else
+    hipLaunchKernelGGL(q8_append_kernel<false>, grid, dim3(kQ8Threads), 0, stream, in0,
+                       static_cast<uint8_t*>(out0), in1, static_cast<uint8_t*>(out1), n_blocks,
+                       nullptr, nullptr);
+  return hipGetLastError();
+}
+
+// dfki2_dequant_kernel (model.cuh:149-159): 8 elements per thread.
+__global__ __launch_bounds__(kQ8Threads) void dfk2_dequant_kernel(
+    const uint2* __restrict__ q, const uint16_t* __restrict__ sc, uint4* __restrict__ out,
+    long n_groups) {
+  const long g = (long)blockIdx.x * kQ8Threads + threadIdx.x;
+  if (g >= n_groups) return;
+  const uint2 w = q[g];
+  const float s = h2f(sc[g >> 4]);
+  const uint32_t ww[2] = {w.x, w.y};
+  uint32_t o[4];
+#pragma unroll
+  for (int k = 0; k < 4; k++) {
+    const uint32_t word = ww[k >> 1];
+    const int sh = 16 * (k & 1);
+    o[k] = f2h((float)(int8_t)((word >> sh) & 0xffu) * s) |
+           (f2h((float)(int8_t)((word >> (sh + 8)) & 0xffu) * s) << 16);
+  }
+  out[g] = make_uint4(o[0], o[1], o[2], o[3]);
+}
+
+hipError_t launch_dfk2_dequant(const void* q, const uint16_t* sc, void* out, long n_elems,
+                               hipStream_t stream) {
+  const long groups = n_elems / 8;
+  if (groups == 0) return hipSuccess;
+  hipLaunchKernelGGL(dfk2_dequant_kernel, dim3((unsigned)((groups + kQ8Threads - 1) / kQ8Threads)),
+                     dim3(kQ8Threads), 0, stream, static_cast<const uint2*>(q), sc,
+                     static_cast<uint4*>(out), groups);
   return hipGetLastError();
 }
 

@@ -140,6 +140,36 @@ int qkv_q8_append_kv(const uint16_t* k_f16, const uint16_t* v_f16, qkv_block_q8*
     return QKV_ERR_ALIGN;
   return launch_status(qkv::launch_q8_append(k_f16, k_out, v_f16, v_out, n_blocks, 2, stream));
 }
+int qkv_dfk2_dequant(const int8_t* q, const uint16_t* scales, uint16_t* out_f16, long long n,
+                     int kv_dim, hipStream_t stream) {
+  if (n < 0 || kv_dim <= 0) return QKV_ERR_INVALID;
+  if (kv_dim % 128 != 0 || n % 8 != 0) return QKV_ERR_UNSUPPORTED;
+  if (n == 0) return QKV_OK;
+  if (!q || !scales || !out_f16) return QKV_ERR_NULL;
+  if (!aligned(q, 8) || !aligned(scales, 2) || !aligned(out_f16, 16)) return QKV_ERR_ALIGN;
+  return launch_status(qkv::launch_dfk2_dequant(q, scales, out_f16, (long)n, stream));
+}
+
+int qkv_tq3_append_dfk2(const int8_t* q, const uint16_t* scales, qkv_block_tq3* out,
+                        int n_blocks, hipStream_t stream) {
+  if (n_blocks < 0) return QKV_ERR_INVALID;
+  if (n_blocks == 0) return QKV_OK;
+  if (!q || !scales || !out) return QKV_ERR_NULL;
+  if (!aligned(q, 16) || !aligned(scales, 2) || !aligned(out, 4)) return QKV_ERR_ALIGN;
+  return launch_status(
+      qkv::launch_tq3_append(q, out, q, out, n_blocks, 1, stream, nullptr, scales, scales));
+}
+
+int qkv_q8_append_dfk2(const int8_t* q, const uint16_t* scales, qkv_block_q8* out, int n_blocks,
+                       hipStream_t stream) {
+  if (n_blocks < 0) return QKV_ERR_INVALID;
+  if (n_blocks % 4 != 0) return QKV_ERR_UNSUPPORTED;
+  if (n_blocks == 0) return QKV_OK;
+  if (!q || !scales || !out) return QKV_ERR_NULL;
+  if (!aligned(q, 8) || !aligned(scales, 2) || !aligned(out, 4)) return QKV_ERR_ALIGN;
+  return launch_status(qkv::launch_q8_append(q, out, q, out, n_blocks, 1, stream, scales, scales));
+}
+
 int qkv_kv_move_tokens(void* k, void* v, size_t k_row_bytes, size_t v_row_bytes, long slot_row0,
                        long slot_rows, const int32_t* from_to, int n, hipStream_t stream) {
   if (n < 0 || n > qkv::kMoveMax) return QKV_ERR_INVALID;

@@ -17,12 +17,19 @@ struct PagedRows {
   long pool_rows;
 };
 
+// sc0/sc1 non-null: in0/in1 are DFK2 int8 rows with one fp16 scale per
+// 128-element block (re-quantizing append)
 hipError_t launch_tq3_append(const void* in0, void* out0, const void* in1, void* out1,
                              int n_blocks, int n_tensors, hipStream_t stream,
-                             const PagedRows* paged = nullptr);
+                             const PagedRows* paged = nullptr, const uint16_t* sc0 = nullptr,
+                             const uint16_t* sc1 = nullptr);
 hipError_t launch_tq3_dequant(const void* in, void* out, int n_blocks, hipStream_t stream);
 hipError_t launch_q8_append(const void* in0, void* out0, const void* in1, void* out1,
-                            int n_blocks, int n_tensors, hipStream_t stream);
+                            int n_blocks, int n_tensors, hipStream_t stream,
+                            const uint16_t* sc0 = nullptr, const uint16_t* sc1 = nullptr);
+// DFK2 int8 rows (group-128 fp16 scales) to fp16; n_elems a multiple of 128
+hipError_t launch_dfk2_dequant(const void* q, const uint16_t* sc, void* out, long n_elems,
+                               hipStream_t stream);
 hipError_t launch_q8_dequant(const void* in, void* out, int n_blocks, hipStream_t stream);
 // Zero-fill of `bytes` (a multiple of 4) bytes by a kernel (graph-capture safe).
 hipError_t launch_fill_zero(void* p, size_t bytes, hipStream_t stream);

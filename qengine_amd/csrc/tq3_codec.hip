@@ -171,6 +171,37 @@ __device__ __forceinline__ void load_tile32(uint32_t (&pre)[32], const uint4* __
   }
 }
 
+// DFK2 source (int8 rows with one fp16 scale per 128 elements, i.e. per TQ3
+// block): 4 coalesced 16-byte loads of the tile's int8 codes -- chunk
+// j*64+lane is piece (lane & 7) (16 elements) of block 8j + (lane >> 3) --
+// and that block's scale in the high half of pre[16 + j].  Past the last
+// block the loads read zero.
+__device__ __forceinline__ void load_tile32_dfk2(uint32_t (&pre)[32], const uint4* __restrict__ in,
+                                                 const uint16_t* __restrict__ sc, int b0, int nb,
+                                                 int lane) {
+  const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint4*>(in + (long)b0 * 8), 0, nb * 128, kBufferRsrcWord3);
+  const __amdgpu_buffer_rsrc_t rsc = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint16_t*>(sc + b0), 0, nb * 2, kBufferRsrcWord3);
+#pragma unroll
+  for (int j = 0; j < 4; j++) {
+    const u4_t v = __builtin_amdgcn_raw_buffer_load_b128(rs, lane * 16, j * 1024, 0);
+    pre[4 * j] = v.x;
+    pre[4 * j + 1] = v.y;
+    pre[4 * j + 2] = v.z;
+    pre[4 * j + 3] = v.w;
+    pre[16 + j] = __builtin_amdgcn_raw_buffer_load_b16(rsc, (8 * j + (lane >> 3)) * 2, 0, 0);
+  }
+}
+
+// dfki2_dequant_kernel's element (model.cuh:149-159): half(float(q) * float(s));
+// the product of an int8 and an fp16 is exact in fp32, then one rounding.
+__device__ __forceinline__ uint32_t dfk2_pair(uint32_t word, int byte, float s) {
+  const float a = (float)(int8_t)((word >> (8 * byte)) & 0xffu) * s;
+  const float b = (float)(int8_t)((word >> (8 * byte + 8)) & 0xffu) * s;
+  return f2h(a) | (f2h(b) << 16);
+}
+
 template <int CTRL>
 __device__ __forceinline__ float lane_dpp(float v) {
   return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(
@@ -200,9 +231,13 @@ __device__ __forceinline__ void cross_stage8(float (&x)[N], int k0, float s) {
       : "v"(s));
 }
 
+// kDfk2: the input is DFK2 int8 rows (in0/in1) with per-block fp16 scales
+// (sc0/sc1), dequantized to the reference's fp16 values on the way into LDS.
+template <bool kDfk2>
 __global__ __launch_bounds__(kAp2Threads, 3) void tq3_append2_kernel(
     const uint4* __restrict__ in0, uint32_t* __restrict__ out0, const uint4* __restrict__ in1,
-    uint32_t* __restrict__ out1, int n_blocks, int n_tensors, PagedRows pr) {
+    uint32_t* __restrict__ out1, int n_blocks, int n_tensors, PagedRows pr,
+    const uint16_t* __restrict__ sc0, const uint16_t* __restrict__ sc1) {
   __shared__ uint32_t lds[kAp2Waves * kAp2WaveLdsDw];
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -225,7 +260,11 @@ __global__ __launch_bounds__(kAp2Threads, 3) void tq3_append2_kernel(
   uint32_t pre[32];
   {
     const int b0 = (t % tiles) * kAp2Tile;
-    load_tile32(pre, t < tiles ? in0 : in1, b0, min(kAp2Tile, n_blocks - b0), lane);
+    if constexpr (kDfk2)
+      load_tile32_dfk2(pre, t < tiles ? in0 : in1, t < tiles ? sc0 : sc1, b0,
+                       min(kAp2Tile, n_blocks - b0), lane);
+    else
+      load_tile32(pre, t < tiles ? in0 : in1, b0, min(kAp2Tile, n_blocks - b0), lane);
   }
   for (;;) {
     const bool second = t >= tiles;
@@ -233,13 +272,27 @@ __global__ __launch_bounds__(kAp2Threads, 3) void tq3_append2_kernel(
     const int b0 = (t % tiles) * kAp2Tile;
     const int nb = min(kAp2Tile, n_blocks - b0);
 
-    // 1. prefetched tile into LDS
+    // 1. prefetched tile into LDS (fp16)
+    if constexpr (kDfk2) {
 #pragma unroll
-    for (int j = 0; j < 8; j++) {
-      const int chunk = j * 64 + lane;
-      const int b = chunk >> 4, part = chunk & 15;
-      *reinterpret_cast<uint4*>(wl + b * kInPitchDw + part * 4) =
-          make_uint4(pre[4 * j], pre[4 * j + 1], pre[4 * j + 2], pre[4 * j + 3]);
+      for (int j = 0; j < 4; j++) {
+        const int b = 8 * j + (lane >> 3), piece = lane & 7;
+        const float sc = h2f(pre[16 + j] & 0xffffu);
+        uint32_t h[8];
+#pragma unroll
+        for (int k = 0; k < 8; k++) h[k] = dfk2_pair(pre[4 * j + (k >> 1)], 2 * (k & 1), sc);
+        uint32_t* dst = wl + b * kInPitchDw + piece * 8;
+        *reinterpret_cast<uint4*>(dst) = make_uint4(h[0], h[1], h[2], h[3]);
+        *reinterpret_cast<uint4*>(dst + 4) = make_uint4(h[4], h[5], h[6], h[7]);
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < 8; j++) {
+        const int chunk = j * 64 + lane;
+        const int b = chunk >> 4, part = chunk & 15;
+        *reinterpret_cast<uint4*>(wl + b * kInPitchDw + part * 4) =
+            make_uint4(pre[4 * j], pre[4 * j + 1], pre[4 * j + 2], pre[4 * j + 3]);
+      }
     }
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "workgroup");
@@ -248,7 +301,11 @@ __global__ __launch_bounds__(kAp2Threads, 3) void tq3_append2_kernel(
     const int tn = t + stride;
     if (tn < total) {
       const int nb0 = (tn % tiles) * kAp2Tile;
-      load_tile32(pre, tn < tiles ? in0 : in1, nb0, min(kAp2Tile, n_blocks - nb0), lane);
+      if constexpr (kDfk2)
+        load_tile32_dfk2(pre, tn < tiles ? in0 : in1, tn < tiles ? sc0 : sc1, nb0,
+                         min(kAp2Tile, n_blocks - nb0), lane);
+      else
+        load_tile32(pre, tn < tiles ? in0 : in1, nb0, min(kAp2Tile, n_blocks - nb0), lane);
     }
 
     // 3. this lane's half block
@@ -452,7 +509,7 @@ __global__ __launch_bounds__(kCodecThreads) void tq3_dequant_kernel(
 // ---------------------------------------------------------------------------
 hipError_t launch_tq3_append(const void* in0, void* out0, const void* in1, void* out1,
                              int n_blocks, int n_tensors, hipStream_t stream,
-                             const PagedRows* paged) {
+                             const PagedRows* paged, const uint16_t* sc0, const uint16_t* sc1) {
   // Persistent grid: two workgroups (8 waves) per CU, fewer when the work
   // list is shorter.
   static std::atomic<int> cus[64];
@@ -472,10 +529,16 @@ hipError_t launch_tq3_append(const void* in0, void* out0, const void* in1, void*
   const int grid = (int)std::min<long>(wgs_needed, 3L * n_cu);
   if (grid == 0) return hipSuccess;
   const PagedRows pr = paged ? *paged : PagedRows{};
-  hipLaunchKernelGGL(tq3_append2_kernel, dim3(grid), dim3(kAp2Threads), 0, stream,
-                     static_cast<const uint4*>(in0), static_cast<uint32_t*>(out0),
-                     static_cast<const uint4*>(in1), static_cast<uint32_t*>(out1), n_blocks,
-                     n_tensors, pr);
+  if (sc0 != nullptr)
+    hipLaunchKernelGGL(tq3_append2_kernel<true>, dim3(grid), dim3(kAp2Threads), 0, stream,
+                       static_cast<const uint4*>(in0), static_cast<uint32_t*>(out0),
+                       static_cast<const uint4*>(in1), static_cast<uint32_t*>(out1), n_blocks,
+                       n_tensors, pr, sc0, sc1);
+  else
+    hipLaunchKernelGGL(tq3_append2_kernel<false>, dim3(grid), dim3(kAp2Threads), 0, stream,
+                       static_cast<const uint4*>(in0), static_cast<uint32_t*>(out0),
+                       static_cast<const uint4*>(in1), static_cast<uint32_t*>(out1), n_blocks,
+                       n_tensors, pr, nullptr, nullptr);
   return hipGetLastError();
 }
 
