@@ -137,6 +137,32 @@ int qkv_tq3_append_dfk2(const int8_t* q, const uint16_t* scales, qkv_block_tq3* 
 int qkv_q8_append_dfk2(const int8_t* q, const uint16_t* scales, qkv_block_q8* out, int n_blocks,
                        hipStream_t stream);
 
+/* Slot snapshot and restore over a paged pool.  The reference saves a slot's
+ * first N rows of K and V with one device-to-host copy each
+ * (save_prefix_snapshot, model.cuh:3394-3417: N * blocks_per_token blocks from
+ * kv_slot_offset(slot) * blocks_per_token) and restores them with the reverse
+ * copy (restore_snapshot_into_slot, model.cuh:3314-3335).  A contiguous slot
+ * keeps those plain copies.  In a paged pool (qkv_decode_attn_tq3_paged) the
+ * slot's logical row r is pool row
+ *   block_table[r / block_tokens] * block_tokens + r % block_tokens,
+ * and these two calls move rows 0 .. n_rows-1 between the pool and a flat
+ * device buffer [n_rows][row_bytes] (then copied to / from the host as in the
+ * reference).  Any packed format: row_bytes = blocks_per_token * 52 (TQ3),
+ * * 36 (Q8_0) or kv_dim * 2 (fp16), a multiple of 4.  block_table is the
+ * slot's row of max_blocks int32 entries (device).  Rows whose table entry is
+ * negative or lands outside [0, pool_rows) are gathered as zeros and skipped
+ * by the scatter.  v_pool and v_flat may both be NULL (keys only).  Rows of a
+ * block shared with other slots (a common prefix) are written by the scatter
+ * like any other row. */
+int qkv_kv_gather_rows(const void* k_pool, const void* v_pool, void* k_flat, void* v_flat,
+                       size_t k_row_bytes, size_t v_row_bytes, long pool_rows,
+                       const int32_t* block_table, int max_blocks, int block_tokens, int n_rows,
+                       hipStream_t stream);
+int qkv_kv_scatter_rows(void* k_pool, void* v_pool, const void* k_flat, const void* v_flat,
+                        size_t k_row_bytes, size_t v_row_bytes, long pool_rows,
+                        const int32_t* block_table, int max_blocks, int block_tokens, int n_rows,
+                        hipStream_t stream);
+
 /* Token-row moves inside one slot of one layer's cache: replaces the per-token
  * device copies of kv_move_token (model.cuh:7430-7471; its tree-verify
  * acceptance calls it once per accepted token and layer).  For i = 0..n-1 in

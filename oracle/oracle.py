@@ -84,6 +84,7 @@ def _declare(L):
                                   _I, _I, _P]
     L.or_key_visible.restype = _I
     L.or_key_visible.argtypes = [_I, _I, _I, _I, _I, _P]
+    L.or_dfk2_dequant.argtypes = [_P, _P, _P, _I64, _I]
     L.or_legacy_decode.restype = _I
     L.or_legacy_decode.argtypes = [_I, _I, _I, _P, _P, _P, _P, _P, _I, _I, _I, _I, _F]
 
@@ -347,6 +348,16 @@ def legacy_decode(k_kind, v_kind, q, k, v, *, num_q, num_kv, hd, seq_len, scale,
     if rc != 0:
         raise ValueError("legacy_decode: unsupported shape")
     return (out, probs) if return_probs else out
+
+
+def dfk2_dequant(q_i8, scales_f16, kv_dim):
+    """dfki2_dequant_kernel (model.cuh:149-159): int8 rows [n_rows][kv_dim]
+    with fp16 scales [n_rows][kv_dim / 128] to fp16 bits of the same shape."""
+    q = np.ascontiguousarray(q_i8, np.int8)
+    s = _u16(scales_f16)
+    out = np.zeros(q.shape, np.uint16)
+    lib().or_dfk2_dequant(_ptr(q), _ptr(s), _ptr(out), q.size, kv_dim)
+    return out
 
 
 def key_visible(key, start_pos, t_idx, sink_tok=0, window_tok=0, tree_mask=None):

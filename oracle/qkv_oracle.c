@@ -867,3 +867,17 @@ int or_legacy_decode(int k_kind, int v_kind, int tq_fused, const uint16_t* q, co
     if (!probs) free(sc);
     return 0;
 }
+
+/* ===================================================================== */
+/* DFK2 KV-inject planes                                                  */
+/* ===================================================================== */
+/* dfki2_dequant_kernel (model.cuh:149-159): out[i] = half(float(q[i]) *
+ * float(s[row * (kv_dim / 128) + col / 128])), row = i / kv_dim. */
+void or_dfk2_dequant(const int8_t* q, const uint16_t* s, uint16_t* out, int64_t n, int kv_dim) {
+    for (int64_t i = 0; i < n; i++) {
+        const int col = (int)(i % kv_dim);
+        const int64_t row = i / kv_dim;
+        const float sc = or_f16_to_f32(s[row * (kv_dim / 128) + col / 128]);
+        out[i] = or_f32_to_f16((float)q[i] * sc);
+    }
+}

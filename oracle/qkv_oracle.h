@@ -135,6 +135,10 @@ int or_legacy_decode(int k_kind, int v_kind, int tq_fused, const uint16_t* q, co
                      const void* v, uint16_t* out, float* probs, int num_q, int num_kv, int hd,
                      int seq_len, float scale);
 
+/* dfki2_dequant_kernel (model.cuh:149-159): DFK2 int8 plane rows of kv_dim
+ * elements with one fp16 scale per 128 to fp16. */
+void or_dfk2_dequant(const int8_t* q, const uint16_t* s, uint16_t* out, int64_t n, int kv_dim);
+
 #ifdef __cplusplus
 }
 #endif

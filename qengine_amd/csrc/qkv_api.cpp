@@ -205,6 +205,58 @@ int qkv_kv_move_tokens(void* k, void* v, size_t k_row_bytes, size_t v_row_bytes,
   return launch_status(qkv::launch_kv_move(a, ordered, stream));
 }
 
+static int kv_page_copy(void* k_pool, void* v_pool, void* k_flat, void* v_flat,
+                        size_t k_row_bytes, size_t v_row_bytes, long pool_rows,
+                        const int32_t* block_table, int max_blocks, int block_tokens, int n_rows,
+                        bool scatter, hipStream_t stream) {
+  if (n_rows < 0 || max_blocks <= 0 || block_tokens <= 0 || pool_rows < 0) return QKV_ERR_INVALID;
+  if (n_rows == 0) return QKV_OK;
+  if (!k_pool || !k_flat || !block_table) return QKV_ERR_NULL;
+  if ((v_pool == nullptr) != (v_flat == nullptr)) return QKV_ERR_NULL;
+  const int n_tensors = v_pool ? 2 : 1;
+  if (k_row_bytes == 0 || k_row_bytes % 4 || k_row_bytes > 0x7fffffffULL) return QKV_ERR_INVALID;
+  if (n_tensors == 2 && (v_row_bytes == 0 || v_row_bytes % 4 || v_row_bytes > 0x7fffffffULL))
+    return QKV_ERR_INVALID;
+  if ((long)(n_rows - 1) / block_tokens >= max_blocks) return QKV_ERR_INVALID;
+  if (!aligned(k_pool, 4) || !aligned(k_flat, 4) || !aligned(block_table, 4) ||
+      (n_tensors == 2 && (!aligned(v_pool, 4) || !aligned(v_flat, 4))))
+    return QKV_ERR_ALIGN;
+  qkv::PageCopyArgs a{};
+  a.pool[0] = static_cast<uint8_t*>(k_pool);
+  a.flat[0] = static_cast<uint8_t*>(k_flat);
+  a.row_bytes[0] = (uint32_t)k_row_bytes;
+  a.pool[1] = n_tensors == 2 ? static_cast<uint8_t*>(v_pool) : a.pool[0];
+  a.flat[1] = n_tensors == 2 ? static_cast<uint8_t*>(v_flat) : a.flat[0];
+  a.row_bytes[1] = n_tensors == 2 ? (uint32_t)v_row_bytes : a.row_bytes[0];
+  a.table = block_table;
+  a.max_blocks = max_blocks;
+  a.block_tokens = block_tokens;
+  a.n_rows = n_rows;
+  a.n_tensors = n_tensors;
+  a.pool_rows = pool_rows;
+  a.aligned16 = aligned(a.pool[0], 16) && aligned(a.pool[1], 16) && aligned(a.flat[0], 16) &&
+                aligned(a.flat[1], 16);
+  return launch_status(qkv::launch_kv_page_copy(a, scatter, stream));
+}
+
+int qkv_kv_gather_rows(const void* k_pool, const void* v_pool, void* k_flat, void* v_flat,
+                       size_t k_row_bytes, size_t v_row_bytes, long pool_rows,
+                       const int32_t* block_table, int max_blocks, int block_tokens, int n_rows,
+                       hipStream_t stream) {
+  return kv_page_copy(const_cast<void*>(k_pool), const_cast<void*>(v_pool), k_flat, v_flat,
+                      k_row_bytes, v_row_bytes, pool_rows, block_table, max_blocks, block_tokens,
+                      n_rows, false, stream);
+}
+
+int qkv_kv_scatter_rows(void* k_pool, void* v_pool, const void* k_flat, const void* v_flat,
+                        size_t k_row_bytes, size_t v_row_bytes, long pool_rows,
+                        const int32_t* block_table, int max_blocks, int block_tokens, int n_rows,
+                        hipStream_t stream) {
+  return kv_page_copy(k_pool, v_pool, const_cast<void*>(k_flat), const_cast<void*>(v_flat),
+                      k_row_bytes, v_row_bytes, pool_rows, block_table, max_blocks, block_tokens,
+                      n_rows, true, stream);
+}
+
 int qkv_q8_dequant(const qkv_block_q8* in, uint16_t* out_f16, int n_blocks, hipStream_t stream) {
   if (n_blocks < 0) return QKV_ERR_INVALID;
   if (n_blocks == 0) return QKV_OK;

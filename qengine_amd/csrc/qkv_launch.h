@@ -47,6 +47,19 @@ struct MoveArgs {
 };
 hipError_t launch_kv_move(const MoveArgs& a, bool ordered, hipStream_t stream);
 
+// Paged slot snapshot (gather) / restore (scatter), kv_move.hip.  Tensor t
+// (0: K, 1: V) has rows of row_bytes[t] (a multiple of 4).
+struct PageCopyArgs {
+  uint8_t* pool[2];
+  uint8_t* flat[2];
+  uint32_t row_bytes[2];
+  const int32_t* table;      // the slot's block-table row
+  int max_blocks, block_tokens, n_rows, n_tensors;
+  long pool_rows;
+  bool aligned16;            // every pointer 16-byte aligned
+};
+hipError_t launch_kv_page_copy(const PageCopyArgs& a, bool scatter, hipStream_t stream);
+
 // Chunked prefill over a TQ3 cache (prefill_tq3.hip).  Workspace pieces:
 // kx  keys [num_kv][h_pad + n_pad][256] fp16: the history rows dequantized
 //     exactly as the reference's bulk dequantization, padded to whole 64-row

@@ -123,6 +123,63 @@ def kv_move_tokens(k: torch.Tensor, v: torch.Tensor, moves, *, k_row_bytes: int,
 # attention
 # ---------------------------------------------------------------------------
 
+def _pool_rows(k_pool, v_pool, k_row_bytes, v_row_bytes):
+    rows = k_pool.numel() * k_pool.element_size() // k_row_bytes
+    if v_pool is not None:
+        rows = min(rows, v_pool.numel() * v_pool.element_size() // v_row_bytes)
+    return rows
+
+
+def kv_gather_rows(k_pool, v_pool, k_flat, v_flat, block_table, *, n_rows, block_tokens,
+                   k_row_bytes, v_row_bytes=0, stream=None) -> None:
+    """Slot snapshot over a paged pool: logical rows 0 .. n_rows-1 of the slot
+    whose block-table row is `block_table` (int32 device tensor) into the flat
+    buffers [n_rows][row_bytes] (model.cuh:3394-3417 for the contiguous
+    layout).  v_pool / v_flat may be None (keys only)."""
+    pool_rows = _pool_rows(k_pool, v_pool, k_row_bytes, v_row_bytes)
+    check(lib().qkv_kv_gather_rows(
+        _dev_ptr(k_pool, "k_pool"), _opt_ptr(v_pool), _dev_ptr(k_flat, "k_flat"),
+        _opt_ptr(v_flat), k_row_bytes, v_row_bytes, pool_rows,
+        _i32(block_table, "block_table"), block_table.numel(),
+        block_tokens, n_rows, _stream(stream)), "qkv_kv_gather_rows")
+
+
+def kv_scatter_rows(k_pool, v_pool, k_flat, v_flat, block_table, *, n_rows, block_tokens,
+                    k_row_bytes, v_row_bytes=0, stream=None) -> None:
+    """Slot restore over a paged pool: the inverse of kv_gather_rows
+    (model.cuh:3314-3335 for the contiguous layout)."""
+    pool_rows = _pool_rows(k_pool, v_pool, k_row_bytes, v_row_bytes)
+    check(lib().qkv_kv_scatter_rows(
+        _dev_ptr(k_pool, "k_pool"), _opt_ptr(v_pool), _dev_ptr(k_flat, "k_flat"),
+        _opt_ptr(v_flat), k_row_bytes, v_row_bytes, pool_rows,
+        _i32(block_table, "block_table"), block_table.numel(),
+        block_tokens, n_rows, _stream(stream)), "qkv_kv_scatter_rows")
+
+
+def dfk2_dequant(q, scales, out, *, kv_dim, stream=None) -> None:
+    """dfki2_dequant_kernel (model.cuh:149-159): int8 plane rows with
+    group-128 fp16 scales to fp16."""
+    check(lib().qkv_dfk2_dequant(_dev_ptr(q, "q"), _dev_ptr(scales, "scales"),
+                                 _dev_ptr(out, "out"), q.numel(), kv_dim, _stream(stream)),
+          "qkv_dfk2_dequant")
+
+
+def tq3_append_dfk2(q, scales, out, stream=None) -> None:
+    """KV-inject re-quantization into TQ3 (model.cuh:3189-3192 + 3218-3226 in
+    one launch): block i from q[128 i ..] with scale scales[i]."""
+    check(lib().qkv_tq3_append_dfk2(_dev_ptr(q, "q"), _dev_ptr(scales, "scales"),
+                                    _dev_ptr(out, "out"), q.numel() // 128, _stream(stream)),
+          "qkv_tq3_append_dfk2")
+
+
+def q8_append_dfk2(q, scales, out, stream=None) -> None:
+    """KV-inject re-quantization into Q8_0 (model.cuh:3189-3192 + 3227-3233):
+    32-element block i with scale scales[i // 4]."""
+    check(lib().qkv_q8_append_dfk2(_dev_ptr(q, "q"), _dev_ptr(scales, "scales"),
+                                   _dev_ptr(out, "out"), q.numel() // 32, _stream(stream)),
+          "qkv_q8_append_dfk2")
+
+
 def _opt_ptr(t):
     return 0 if t is None else _dev_ptr(t, "tensor")
 

@@ -147,3 +147,33 @@ def test_workspace_health_argument_errors(L):
     assert L.qkv_decode_workspace_reset(p, 0, None) == 0       # nothing to clear
     assert L.qkv_debug_set_merge_spin_limit(-1) == 0
     assert L.qkv_status_string(-8) == b"in-kernel merge timed out; reset the workspace"
+
+
+def test_inject_and_page_copy_argument_errors_without_gpu(L):
+    """DFK2 re-quantizing appends and paged snapshot copies: shape, pointer
+    and alignment errors before any launch."""
+    buf = ctypes.create_string_buffer(8192)
+    p = (ctypes.addressof(buf) + 255) & ~255
+    assert L.qkv_dfk2_dequant(p, p, p, 0, 1024, None) == 0
+    assert L.qkv_dfk2_dequant(p, p, p, -8, 1024, None) == -1
+    assert L.qkv_dfk2_dequant(p, p, p, 1024, 1000, None) == -3     # kv_dim not a multiple of 128
+    assert L.qkv_dfk2_dequant(p, p, p, 1020, 1024, None) == -3
+    assert L.qkv_dfk2_dequant(None, p, p, 1024, 1024, None) == -2
+    assert L.qkv_dfk2_dequant(p + 4, p, p, 1024, 1024, None) == -4
+    assert L.qkv_tq3_append_dfk2(p, p, p, 0, None) == 0
+    assert L.qkv_tq3_append_dfk2(p, p, p, -1, None) == -1
+    assert L.qkv_tq3_append_dfk2(p, None, p, 8, None) == -2
+    assert L.qkv_tq3_append_dfk2(p + 8, p, p, 8, None) == -4
+    assert L.qkv_q8_append_dfk2(p, p, p, 6, None) == -3            # 32-element blocks in fours
+    assert L.qkv_q8_append_dfk2(p, p, None, 8, None) == -2
+    assert L.qkv_q8_append_dfk2(p + 4, p, p, 8, None) == -4
+    g = L.qkv_kv_gather_rows
+    assert g(p, p, p, p, 416, 416, 100, p, 4, 16, 0, None) == 0
+    assert g(p, p, p, p, 416, 416, 100, p, 4, 16, -1, None) == -1
+    assert g(p, p, p, p, 418, 416, 100, p, 4, 16, 8, None) == -1     # rows of whole dwords
+    assert g(p, p, p, p, 416, 416, 100, p, 4, 16, 65, None) == -1    # past the table's 4 blocks
+    assert g(p, p, p, p, 416, 416, 100, p, 4, 0, 8, None) == -1
+    assert g(p, None, p, p, 416, 416, 100, p, 4, 16, 8, None) == -2  # V pool without V buffer
+    assert g(p, p, p, p, 416, 416, 100, None, 4, 16, 8, None) == -2
+    assert g(p + 2, p, p, p, 416, 416, 100, p, 4, 16, 8, None) == -4
+    assert L.qkv_kv_scatter_rows(p, p, None, p, 416, 416, 100, p, 4, 16, 8, None) == -2
