@@ -214,6 +214,54 @@ int qkv_attn_split_q8(const uint16_t* q, const qkv_block_q8* k, const qkv_block_
                       int head_dim, int start_pos, int sub_n, int sub_n_max, int active_end_max,
                       float scale, int k_splits, hipStream_t stream);
 
+/* ---------------------------------------------------------------------------
+ * Block-sparse TQ3 verify (the DFLASH_VERIFY_BLOCKSPARSE path of
+ * model.cuh:4589-4662): per layer, a pool of 64-token key-block signatures is
+ * kept up to date, each verify query picks its top_k blocks, and the split
+ * kernel attends only those blocks; the partials merge with
+ * qkv_attn_split_merge.
+ * ------------------------------------------------------------------------- */
+
+/* Replaces tq3_kpool_ms_update_kern<256, 256><<<dim3(num_kv, cur_blocks -
+ * blk_lo), 256, block_size_n * 512>>>(k_tq, k_pool, k_pool_max, num_kv,
+ * total_kv, blk_lo, n_blocks_stride, block_size_n) (attention.cuh:2445-2533;
+ * launched at model.cuh:4616-4623).  For position blocks blk_lo ..
+ * ceil(total_kv / block_size_n) - 1 of each kv head: the fp16 mean and the
+ * sign-preserving max-abs over the block's dequantized keys, into
+ * k_pool / k_pool_max [num_kv][n_blocks_stride][256] fp16.  Bit-identical to
+ * the reference.  block_size_n <= 64. */
+int qkv_tq3_kpool_update(const qkv_block_tq3* k_cache, uint16_t* k_pool, uint16_t* k_pool_max,
+                         int num_kv, int head_dim, int total_kv, int blk_lo, int n_blocks_stride,
+                         int block_size_n, hipStream_t stream);
+
+/* Replaces build_block_index_ms_kern<256, GQA, 256><<<dim3(num_kv, sub_n),
+ * 256, ...>>>(q, k_pool, k_pool_max, block_index, num_q, num_kv, sub_n,
+ * sub_n_max, start_pos, top_k, block_size_n, n_blocks, n_blocks_stride, beta)
+ * (sparse_attn/sparse_index.cuh:214-330; launched at model.cuh:4634-4637,
+ * 4649-4652).  block_index [num_kv][sub_n_max][top_k] int32: per (kv head,
+ * query t) the top_k blocks by max(q_avg . mean, beta * q_avg . maxabs) among
+ * blocks 0 .. (start_pos + t) / block_size_n, ascending, -1 padded; ties go to
+ * the lower block.  Bit-identical selection.  n_blocks <= 32768. */
+int qkv_block_index_ms(const uint16_t* q, const uint16_t* k_pool, const uint16_t* k_pool_max,
+                       int32_t* block_index, int num_q, int num_kv, int head_dim, int sub_n,
+                       int sub_n_max, int start_pos, int top_k, int block_size_n, int n_blocks,
+                       int n_blocks_stride, float beta, hipStream_t stream);
+
+/* Replaces flash_attn_chunk_block_sparse_split_tq3<256, GQA, 32, 256,
+ * K_SPLITS><<<dim3(num_kv, sub_n, K_SPLITS), ...>>>(q, k_tq, v_tq,
+ * block_index, part_m, part_l, part_o, num_q, num_kv, start_pos, sub_n,
+ * sub_n_max, scale, top_k, block_size_n, tree_mask) (attention.cuh:2193-2433;
+ * launched at model.cuh:4638-4644, 4653-4659): split z attends the blocks
+ * block_index[...][z * ceil(top_k / k_splits) ...] (up to its first -1),
+ * causal (and tree-masked) within the query's reach; partials in the
+ * qkv_attn_split_tq3 layout.  block_size_n = 64; ceil(top_k / k_splits) <= 64. */
+int qkv_attn_block_sparse_split_tq3(const uint16_t* q, const qkv_block_tq3* k,
+                                    const qkv_block_tq3* v, const int32_t* block_index,
+                                    float* part_m, float* part_l, float* part_o, int num_q,
+                                    int num_kv, int head_dim, int start_pos, int sub_n,
+                                    int sub_n_max, float scale, int top_k, int block_size_n,
+                                    int k_splits, const uint32_t* tree_mask, hipStream_t stream);
+
 /* Replaces flash_attn_split_merge<256, GQA, 256, K_SPLITS><<<(num_kv, sub_n), 256>>>
  * (attention.cuh:1837-1891).  out [sub_n][num_q][256] fp16; may alias q of the
  * preceding split call (model.cuh:2479-2482 merges in place). */

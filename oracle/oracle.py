@@ -85,6 +85,10 @@ def _declare(L):
     L.or_key_visible.restype = _I
     L.or_key_visible.argtypes = [_I, _I, _I, _I, _I, _P]
     L.or_dfk2_dequant.argtypes = [_P, _P, _P, _I64, _I]
+    L.or_tq3_kpool_update.argtypes = [_P, _P, _P, _I, _I, _I, _I, _I, _I]
+    L.or_block_index_ms.argtypes = [_P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _I, _I, _I, _F]
+    L.or_attn_block_sparse_split.argtypes = [_P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I,
+                                             _F, _I, _I, _I, _P]
     L.or_legacy_decode.restype = _I
     L.or_legacy_decode.argtypes = [_I, _I, _I, _P, _P, _P, _P, _P, _I, _I, _I, _I, _F]
 
@@ -358,6 +362,49 @@ def dfk2_dequant(q_i8, scales_f16, kv_dim):
     out = np.zeros(q.shape, np.uint16)
     lib().or_dfk2_dequant(_ptr(q), _ptr(s), _ptr(out), q.size, kv_dim)
     return out
+
+
+def tq3_kpool_update(k_tq3, k_pool, k_pool_max, *, num_kv, hd, total_kv, blk_lo,
+                     block_size_n=64):
+    """tq3_kpool_ms_update_kern (attention.cuh:2445-2533), in place on the fp16
+    pools [num_kv][n_blocks_stride][hd] (uint16 bits): blocks blk_lo ..
+    ceil(total_kv / block_size_n) - 1 get the mean / signed max-abs of their
+    dequantized K rows."""
+    assert k_pool.dtype == np.uint16 and k_pool_max.dtype == np.uint16
+    assert k_pool.flags.c_contiguous and k_pool_max.flags.c_contiguous
+    stride = k_pool.shape[1]
+    lib().or_tq3_kpool_update(_ptr(np.ascontiguousarray(k_tq3)), _ptr(k_pool), _ptr(k_pool_max),
+                              num_kv, hd, total_kv, blk_lo, stride, block_size_n)
+
+
+def block_index_ms(q, k_pool, k_pool_max, *, num_q, num_kv, hd, sub_n, sub_n_max, start_pos,
+                   top_k, n_blocks, block_size_n=64, beta=0.5):
+    """build_block_index_ms_kern (sparse_attn/sparse_index.cuh:214-330):
+    int32 [num_kv][sub_n_max][top_k], rows sorted ascending, -1 padded."""
+    qq = _u16(q)
+    out = np.full((num_kv, sub_n_max, top_k), -1, np.int32)
+    lib().or_block_index_ms(_ptr(qq), _ptr(_u16(k_pool)), _ptr(_u16(k_pool_max)), _ptr(out),
+                            num_q, num_kv, hd, sub_n, sub_n_max, start_pos, top_k, block_size_n,
+                            n_blocks, k_pool.shape[1], float(beta))
+    return out
+
+
+def attn_block_sparse_split(q, k_tq3, v_tq3, block_index, *, num_q, num_kv, hd, start_pos, sub_n,
+                            sub_n_max, scale, top_k, k_splits, block_size_n=64, tree_mask=None):
+    """flash_attn_chunk_block_sparse_split_tq3 (attention.cuh:2193-2433):
+    partials (m, l, o) in the split layout; merge with attn_split_merge."""
+    qq = _u16(q)
+    pm = np.zeros((num_q, sub_n_max, k_splits), np.float32)
+    pl = np.zeros_like(pm)
+    po = np.zeros((num_q, sub_n_max, k_splits, hd), np.float32)
+    tm = None if tree_mask is None else np.ascontiguousarray(tree_mask, np.uint32)
+    bi = np.ascontiguousarray(block_index, np.int32)
+    lib().or_attn_block_sparse_split(_ptr(qq), _ptr(np.ascontiguousarray(k_tq3)),
+                                     _ptr(np.ascontiguousarray(v_tq3)), _ptr(bi), _ptr(pm),
+                                     _ptr(pl), _ptr(po), num_q, num_kv, hd, start_pos, sub_n,
+                                     sub_n_max, float(scale), top_k, block_size_n, k_splits,
+                                     _ptr(tm))
+    return pm, pl, po
 
 
 def key_visible(key, start_pos, t_idx, sink_tok=0, window_tok=0, tree_mask=None):

@@ -454,6 +454,102 @@ static float score_dot(const float* qf, const float* kf, int hd) {
     return part[0];
 }
 
+/* Online-softmax state of one (kv_head, t_idx, split): gqa rows. */
+typedef struct {
+    float* qf;     /* [gqa][hd] query */
+    float* acc;    /* [gqa][hd] unnormalized output */
+    float* m;      /* [gqa] running max */
+    float* l;      /* [gqa] running sum */
+    uint16_t* krow; uint16_t* vrow;   /* [OR_BM][hd] tile rows (fp16) */
+    float* kf; float* vf;             /* [OR_BM][hd] as floats */
+} split_state;
+
+static void split_state_init(split_state* st, const uint16_t* q, int num_q, int num_kv, int hd,
+                             int kv_head, int t_idx) {
+    const int gqa = num_q / num_kv;
+    st->qf = (float*)malloc(sizeof(float) * gqa * hd);
+    st->acc = (float*)calloc((size_t)gqa * hd, sizeof(float));
+    st->m = (float*)malloc(sizeof(float) * gqa);
+    st->l = (float*)calloc(gqa, sizeof(float));
+    st->krow = (uint16_t*)malloc(sizeof(uint16_t) * OR_BM * hd);
+    st->vrow = (uint16_t*)malloc(sizeof(uint16_t) * OR_BM * hd);
+    st->kf = (float*)malloc(sizeof(float) * OR_BM * hd);
+    st->vf = (float*)malloc(sizeof(float) * OR_BM * hd);
+    for (int g = 0; g < gqa; g++) {
+        st->m[g] = -INFINITY;
+        int qh = kv_head * gqa + g;
+        for (int c = 0; c < hd; c++)
+            st->qf[g * hd + c] = or_f16_to_f32(q[((int64_t)t_idx * num_q + qh) * hd + c]);
+    }
+}
+
+static void split_state_store(split_state* st, float* part_m, float* part_l, float* part_o,
+                              int num_q, int num_kv, int hd, int sub_n_max, int k_splits,
+                              int kv_head, int t_idx, int split) {
+    const int gqa = num_q / num_kv;
+    for (int g = 0; g < gqa; g++) {
+        int qh = kv_head * gqa + g;
+        int64_t ml = ((int64_t)qh * sub_n_max + t_idx) * k_splits + split;
+        part_m[ml] = st->m[g];
+        part_l[ml] = st->l[g];
+        memcpy(part_o + ml * hd, st->acc + g * hd, sizeof(float) * hd);
+    }
+    free(st->qf); free(st->acc); free(st->m); free(st->l);
+    free(st->krow); free(st->vrow); free(st->kf); free(st->vf);
+}
+
+/* One BM = 32 key tile [ts, ts + len) of the split kernels' loop body
+ * (attention.cuh:2009-2150): decode to fp16, scores (score_dot) * scale with
+ * invisible keys -inf (key >= start_pos and its tree bit clear), online
+ * softmax with expf, the xor-butterfly sum of p, sequential acc += p * v. */
+static void split_tile(split_state* st, int kind, const void* k, const void* v, int num_kv,
+                       int hd, int gqa, int start_pos, float scale, const uint32_t* tree_mask,
+                       int kv_head, int t_idx, int ts, int len) {
+    float s[OR_BM], p[OR_BM];
+    for (int r = 0; r < len; r++) {
+        decode_row(kind, k, ts + r, num_kv, kv_head, hd, st->krow + r * hd);
+        decode_row(kind, v, ts + r, num_kv, kv_head, hd, st->vrow + r * hd);
+    }
+    for (int i = 0; i < len * hd; i++) {
+        st->kf[i] = or_f16_to_f32(st->krow[i]);
+        st->vf[i] = or_f16_to_f32(st->vrow[i]);
+    }
+    for (int g = 0; g < gqa; g++) {
+        float mrow = -INFINITY;
+        for (int r = 0; r < OR_BM; r++) {
+            float val = -INFINITY;
+            if (r < len) {
+                int key = ts + r;
+                int vis = (key < start_pos) ||
+                          (tree_mask ? (int)((tree_mask[t_idx] >> (key - start_pos)) & 1u) : 1);
+                if (vis) val = score_dot(st->qf + g * hd, st->kf + r * hd, hd) * scale;
+            }
+            s[r] = val;
+            mrow = fmaxf(mrow, val);
+        }
+        float mnew = fmaxf(st->m[g], mrow);
+        float corr = expf(st->m[g] - mnew);
+        float sum = 0.0f;
+        for (int r = 0; r < OR_BM; r++) { p[r] = expf(s[r] - mnew); }
+        /* xor-butterfly sum over 32 lanes (attention.cuh:2121-2123) */
+        {
+            float part[32];
+            for (int r = 0; r < 32; r++) part[r] = r < OR_BM ? p[r] : 0.0f;
+            for (int off = 16; off > 0; off >>= 1) {
+                float nxt[32];
+                for (int r = 0; r < 32; r++) nxt[r] = part[r] + part[r ^ off];
+                memcpy(part, nxt, sizeof(part));
+            }
+            sum = part[0];
+        }
+        for (int c = 0; c < hd; c++) st->acc[g * hd + c] *= corr;
+        st->l[g] = st->l[g] * corr + sum;
+        for (int r = 0; r < len; r++)
+            for (int c = 0; c < hd; c++) st->acc[g * hd + c] += p[r] * st->vf[r * hd + c];
+        st->m[g] = mnew;
+    }
+}
+
 /* attention.cuh:1905-2177 / 2633-2801 for one (kv_head, t_idx, split). */
 static void split_one(int kind, const uint16_t* q, const void* k, const void* v,
                       float* part_m, float* part_l, float* part_o, int num_q, int num_kv,
@@ -469,78 +565,19 @@ static void split_one(int kind, const uint16_t* q, const void* k, const void* v,
     int tile_hi = (split + 1) * tps * OR_BM;
     if (tile_hi > active_end_t) tile_hi = active_end_t;
 
-    float* qf = (float*)malloc(sizeof(float) * gqa * hd);
-    float* acc = (float*)calloc((size_t)gqa * hd, sizeof(float));
-    float* m = (float*)malloc(sizeof(float) * gqa);
-    float* l = (float*)calloc(gqa, sizeof(float));
-    uint16_t* krow = (uint16_t*)malloc(sizeof(uint16_t) * OR_BM * hd);
-    uint16_t* vrow = (uint16_t*)malloc(sizeof(uint16_t) * OR_BM * hd);
-    float* kf = (float*)malloc(sizeof(float) * OR_BM * hd);
-    float* vf = (float*)malloc(sizeof(float) * OR_BM * hd);
-    float s[OR_BM], p[OR_BM];
-    for (int g = 0; g < gqa; g++) {
-        m[g] = -INFINITY;
-        int qh = kv_head * gqa + g;
-        for (int c = 0; c < hd; c++)
-            qf[g * hd + c] = or_f16_to_f32(q[((int64_t)t_idx * num_q + qh) * hd + c]);
-    }
+    split_state st;
+    split_state_init(&st, q, num_q, num_kv, hd, kv_head, t_idx);
     const int sparse = (sink_tok > 0 || window_tok > 0);
     const int win_lo = sparse ? active_end_t - window_tok : 0;
     for (int ts = tile_lo; ts < tile_hi; ts += OR_BM) {
         int te = ts + OR_BM < tile_hi ? ts + OR_BM : tile_hi;
         int len = te - ts;
         if (sparse && !(ts < sink_tok) && !(te > win_lo)) continue;
-        for (int r = 0; r < len; r++) {
-            decode_row(kind, k, ts + r, num_kv, kv_head, hd, krow + r * hd);
-            decode_row(kind, v, ts + r, num_kv, kv_head, hd, vrow + r * hd);
-        }
-        for (int i = 0; i < len * hd; i++) {
-            kf[i] = or_f16_to_f32(krow[i]);
-            vf[i] = or_f16_to_f32(vrow[i]);
-        }
-        for (int g = 0; g < gqa; g++) {
-            float mrow = -INFINITY;
-            for (int r = 0; r < OR_BM; r++) {
-                float val = -INFINITY;
-                if (r < len) {
-                    int key = ts + r;
-                    int vis = (key < start_pos) ||
-                              (tree_mask ? (int)((tree_mask[t_idx] >> (key - start_pos)) & 1u) : 1);
-                    if (vis) val = score_dot(qf + g * hd, kf + r * hd, hd) * scale;
-                }
-                s[r] = val;
-                mrow = fmaxf(mrow, val);
-            }
-            float mnew = fmaxf(m[g], mrow);
-            float corr = expf(m[g] - mnew);
-            float sum = 0.0f;
-            for (int r = 0; r < OR_BM; r++) { p[r] = expf(s[r] - mnew); }
-            /* xor-butterfly sum over 32 lanes (attention.cuh:2121-2123) */
-            {
-                float part[32];
-                for (int r = 0; r < 32; r++) part[r] = r < OR_BM ? p[r] : 0.0f;
-                for (int off = 16; off > 0; off >>= 1) {
-                    float nxt[32];
-                    for (int r = 0; r < 32; r++) nxt[r] = part[r] + part[r ^ off];
-                    memcpy(part, nxt, sizeof(part));
-                }
-                sum = part[0];
-            }
-            for (int c = 0; c < hd; c++) acc[g * hd + c] *= corr;
-            l[g] = l[g] * corr + sum;
-            for (int r = 0; r < len; r++)
-                for (int c = 0; c < hd; c++) acc[g * hd + c] += p[r] * vf[r * hd + c];
-            m[g] = mnew;
-        }
+        split_tile(&st, kind, k, v, num_kv, hd, gqa, start_pos, scale, tree_mask, kv_head, t_idx,
+                   ts, len);
     }
-    for (int g = 0; g < gqa; g++) {
-        int qh = kv_head * gqa + g;
-        int64_t ml = ((int64_t)qh * sub_n_max + t_idx) * k_splits + split;
-        part_m[ml] = m[g];
-        part_l[ml] = l[g];
-        memcpy(part_o + ml * hd, acc + g * hd, sizeof(float) * hd);
-    }
-    free(qf); free(acc); free(m); free(l); free(krow); free(vrow); free(kf); free(vf);
+    split_state_store(&st, part_m, part_l, part_o, num_q, num_kv, hd, sub_n_max, k_splits,
+                      kv_head, t_idx, split);
 }
 
 void or_attn_split(int kind, const uint16_t* q, const void* k, const void* v,
@@ -879,5 +916,152 @@ void or_dfk2_dequant(const int8_t* q, const uint16_t* s, uint16_t* out, int64_t 
         const int64_t row = i / kv_dim;
         const float sc = or_f16_to_f32(s[row * (kv_dim / 128) + col / 128]);
         out[i] = or_f32_to_f16((float)q[i] * sc);
+    }
+}
+
+/* ===================================================================== */
+/* Block-sparse TQ3 verify (attention.cuh:2193-2533; sparse_index.cuh:214) */
+/* ===================================================================== */
+
+/* tq3_kpool_ms_update_kern (attention.cuh:2445-2533): for position blocks
+ * n = blk_lo .. ceil(total_kv / bsn) - 1 of each kv head, the fp16 mean and
+ * sign-preserving max-abs over the block's dequantized fp16 K rows (the same
+ * values as the bulk dequantization): sum += x in position order, mean =
+ * sum / n_pos; max-abs keeps the first largest |x|, starting from 0. */
+void or_tq3_kpool_update(const or_block_tq3* k, uint16_t* k_pool, uint16_t* k_pool_max,
+                         int num_kv, int hd, int total_kv, int blk_lo, int n_blocks_stride,
+                         int bsn) {
+    const int cur_blocks = (total_kv + bsn - 1) / bsn;
+    const int bpk = hd / OR_TQ_BLOCK;
+    #pragma omp parallel for collapse(2) schedule(static)
+    for (int h = 0; h < num_kv; h++) {
+        for (int n = blk_lo; n < cur_blocks; n++) {
+            const int t_lo = n * bsn;
+            const int t_hi = t_lo + bsn < total_kv ? t_lo + bsn : total_kv;
+            const int64_t ob = ((int64_t)h * n_blocks_stride + n) * hd;
+            if (t_lo >= t_hi) {
+                for (int c = 0; c < hd; c++) k_pool[ob + c] = k_pool_max[ob + c] = 0;
+                continue;
+            }
+            const int n_pos = t_hi - t_lo;
+            uint16_t* rows = (uint16_t*)malloc(sizeof(uint16_t) * (size_t)n_pos * hd);
+            for (int pp = 0; pp < n_pos; pp++)
+                for (int j = 0; j < bpk; j++)
+                    tq3_decode_one(k + ((int64_t)(t_lo + pp) * num_kv + h) * bpk + j,
+                                   rows + (int64_t)pp * hd + j * OR_TQ_BLOCK, NULL);
+            for (int c = 0; c < hd; c++) {
+                float sum = 0.0f, best_mag = 0.0f, best_val = 0.0f;
+                for (int pp = 0; pp < n_pos; pp++) {
+                    const float x = or_f16_to_f32(rows[(int64_t)pp * hd + c]);
+                    sum += x;
+                    const float mg = fabsf(x);
+                    if (mg > best_mag) { best_mag = mg; best_val = x; }
+                }
+                k_pool[ob + c] = or_f32_to_f16(sum / (float)n_pos);
+                k_pool_max[ob + c] = or_f32_to_f16(best_val);
+            }
+            free(rows);
+        }
+    }
+}
+
+/* build_block_index_ms_kern (sparse_attn/sparse_index.cuh:214-330) for one
+ * (kv_head, t_idx): q_avg = fp16(sum over the GQA heads * (1/GQA)); block
+ * score max(q_avg . mean, beta * q_avg . maxabs) over half2 pairs (each pair
+ * sum rounded once, products exact), -inf past the causal block
+ * (start_pos + t_idx) / bsn; top_k picks of the highest score, the lower
+ * block index on ties, never a -inf (or NaN) score; the picks sorted
+ * ascending, then -1 padding. */
+void or_block_index_ms(const uint16_t* q, const uint16_t* k_pool, const uint16_t* k_pool_max,
+                       int32_t* block_index, int num_q, int num_kv, int hd, int sub_n,
+                       int sub_n_max, int start_pos, int top_k, int bsn, int n_blocks,
+                       int n_blocks_stride, float beta) {
+    const int gqa = num_q / num_kv;
+    const float inv_g = 1.0f / (float)gqa;
+    #pragma omp parallel for collapse(2) schedule(static)
+    for (int h = 0; h < num_kv; h++) {
+        for (int t = 0; t < sub_n; t++) {
+            float* qa = (float*)malloc(sizeof(float) * hd);
+            float* sc = (float*)malloc(sizeof(float) * (n_blocks > 0 ? n_blocks : 1));
+            for (int c = 0; c < hd; c++) {
+                float s = 0.0f;
+                for (int g = 0; g < gqa; g++)
+                    s += or_f16_to_f32(q[((int64_t)t * num_q + h * gqa + g) * hd + c]);
+                qa[c] = or_f16_to_f32(or_f32_to_f16(s * inv_g));
+            }
+            const int causal_max = (start_pos + t) / bsn;
+            for (int n = 0; n < n_blocks; n++) {
+                const uint16_t* mn = k_pool + ((int64_t)h * n_blocks_stride + n) * hd;
+                const uint16_t* mx = k_pool_max + ((int64_t)h * n_blocks_stride + n) * hd;
+                float s_mean = 0.0f, s_max = 0.0f;
+                for (int c = 0; c < hd; c += 2) {
+                    s_mean += qa[c] * or_f16_to_f32(mn[c]) + qa[c + 1] * or_f16_to_f32(mn[c + 1]);
+                    s_max += qa[c] * or_f16_to_f32(mx[c]) + qa[c + 1] * or_f16_to_f32(mx[c + 1]);
+                }
+                float s = fmaxf(s_mean, beta * s_max);
+                if (n > causal_max) s = -INFINITY;
+                sc[n] = s;
+            }
+            int32_t* row = block_index + ((int64_t)h * sub_n_max + t) * top_k;
+            int k = 0;
+            for (; k < top_k; k++) {
+                float lb = -INFINITY;
+                int li = -1;
+                for (int n = 0; n < n_blocks; n++)
+                    if (sc[n] > lb) { lb = sc[n]; li = n; }
+                if (li < 0) break;
+                row[k] = li;
+                sc[li] = -INFINITY;
+            }
+            for (int kk = k; kk < top_k; kk++) row[kk] = -1;
+            for (int i = 1; i < k; i++) {      /* ascending */
+                const int32_t x = row[i];
+                int j = i;
+                while (j > 0 && row[j - 1] > x) { row[j] = row[j - 1]; j--; }
+                row[j] = x;
+            }
+            free(qa);
+            free(sc);
+        }
+    }
+}
+
+/* flash_attn_chunk_block_sparse_split_tq3 (attention.cuh:2193-2433): split
+ * z takes entries [z * per, min((z + 1) * per, top_k)) of the query's block
+ * list (per = ceil(top_k / k_splits)), stops at a -1, and runs the dense
+ * kernel's tile body over each block's BM = 32 tiles up to start_pos + t. */
+void or_attn_block_sparse_split(const uint16_t* q, const or_block_tq3* k, const or_block_tq3* v,
+                                const int32_t* block_index, float* part_m, float* part_l,
+                                float* part_o, int num_q, int num_kv, int hd, int start_pos,
+                                int sub_n, int sub_n_max, float scale, int top_k, int bsn,
+                                int k_splits, const uint32_t* tree_mask) {
+    const int gqa = num_q / num_kv;
+    #pragma omp parallel for collapse(3) schedule(dynamic)
+    for (int h = 0; h < num_kv; h++) {
+        for (int t = 0; t < sub_n; t++) {
+            for (int z = 0; z < k_splits; z++) {
+                const int abs_pos = start_pos + t, active_end_t = abs_pos + 1;
+                const int per = (top_k + k_splits - 1) / k_splits;
+                const int tk_lo = z * per;
+                const int tk_hi = (z + 1) * per < top_k ? (z + 1) * per : top_k;
+                const int32_t* bi = block_index + ((int64_t)h * sub_n_max + t) * top_k;
+                split_state st;
+                split_state_init(&st, q, num_q, num_kv, hd, h, t);
+                for (int tk = tk_lo; tk < tk_hi; tk++) {
+                    const int blk = bi[tk];
+                    if (blk < 0) break;
+                    for (int inner = 0; inner < bsn / OR_BM; inner++) {
+                        const int ts = blk * bsn + inner * OR_BM;
+                        if (ts > abs_pos) break;
+                        const int te = ts + OR_BM < active_end_t ? ts + OR_BM : active_end_t;
+                        if (te - ts <= 0) continue;
+                        split_tile(&st, OR_KV_TQ3, k, v, num_kv, hd, gqa, start_pos, scale,
+                                   tree_mask, h, t, ts, te - ts);
+                    }
+                }
+                split_state_store(&st, part_m, part_l, part_o, num_q, num_kv, hd, sub_n_max,
+                                  k_splits, h, t, z);
+            }
+        }
     }
 }

@@ -139,6 +139,22 @@ int or_legacy_decode(int k_kind, int v_kind, int tq_fused, const uint16_t* q, co
  * elements with one fp16 scale per 128 to fp16. */
 void or_dfk2_dequant(const int8_t* q, const uint16_t* s, uint16_t* out, int64_t n, int kv_dim);
 
+/* Block-sparse TQ3 verify: K-pool signatures (attention.cuh:2445-2533), the
+ * MS top-k block index (sparse_attn/sparse_index.cuh:214-330) and the sparse
+ * split kernel (attention.cuh:2193-2433; merge with or_attn_split_merge). */
+void or_tq3_kpool_update(const or_block_tq3* k, uint16_t* k_pool, uint16_t* k_pool_max,
+                         int num_kv, int hd, int total_kv, int blk_lo, int n_blocks_stride,
+                         int bsn);
+void or_block_index_ms(const uint16_t* q, const uint16_t* k_pool, const uint16_t* k_pool_max,
+                       int32_t* block_index, int num_q, int num_kv, int hd, int sub_n,
+                       int sub_n_max, int start_pos, int top_k, int bsn, int n_blocks,
+                       int n_blocks_stride, float beta);
+void or_attn_block_sparse_split(const uint16_t* q, const or_block_tq3* k, const or_block_tq3* v,
+                                const int32_t* block_index, float* part_m, float* part_l,
+                                float* part_o, int num_q, int num_kv, int hd, int start_pos,
+                                int sub_n, int sub_n_max, float scale, int top_k, int bsn,
+                                int k_splits, const uint32_t* tree_mask);
+
 #ifdef __cplusplus
 }
 #endif

@@ -4,6 +4,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "qkv_device.h"
+
 namespace qkv {
 
 constexpr float kLn2 = 0.69314718055994531f;
@@ -52,6 +54,11 @@ struct AttnArgs {
   int bt_stride, block_tokens;
   const int32_t* ctx_lens;
   int ctx_max;
+  // block-sparse split (tq3_attn_kernel<2>): query t of kv head h attends the
+  // 64-key blocks block_index[(h * sub_n_max + t) * top_k + i] (ascending,
+  // -1 after the last); split z takes entries z * ceil(top_k / k_splits) ..
+  const int32_t* block_index;
+  int top_k;
   // split API partials (reference layout)
   float* part_m;
   float* part_l;
@@ -193,6 +200,47 @@ __device__ __forceinline__ void wht_xor_lanes16(float (&x)[8], int lane) {
   wht_xor_stage<2>(x, lane);
   wht_xor_stage<4>(x, lane);
   wht_xor_stage<8>(x, lane);
+}
+
+// fp32 Lloyd-Max level i (turboquant.cuh:27-30), selected without a memory
+// lookup: i >= 4: +m[i-4], i < 4: -m[3-i].
+__device__ __forceinline__ float centroid_f32(uint32_t i) {
+  const uint32_t m = (i & 4u) ? (i & 3u) : (3u - (i & 3u));
+  const float mag = (m & 2u) ? ((m & 1u) ? 0.190303f : 0.118828f) : ((m & 1u) ? 0.066847f : 0.021664f);
+  return (i & 4u) ? mag : -mag;
+}
+
+// The reference's TQ3 dequantization of one 52-byte block (turboquant.cuh:
+// 169-200), bit for bit, spread over 16 consecutive lanes: lane `part` of the
+// group gets elements part*8 .. part*8+7 as four fp16 pairs.  fp32 centroids,
+// the seven butterfly stages in the reference's pairing (three in registers,
+// four across the lanes), * rs, sign, * norm kept an fp32 product, fp16.
+__device__ __forceinline__ void tq3_dequant_exact8(const uint8_t* blk, int part, int lane,
+                                                   uint32_t (&pk)[4]) {
+  const float norm = *reinterpret_cast<const float*>(blk);
+  // code group `part`: bytes 3*part .. 3*part+2 of the 48 code bytes
+  const int b0 = 3 * part, w0 = b0 >> 2;
+  const uint32_t* cw = reinterpret_cast<const uint32_t*>(blk + 4);
+  const uint32_t lo = cw[w0], hi = cw[min(w0 + 1, 11)];
+  const uint32_t g = __builtin_amdgcn_alignbyte(hi, lo, b0 & 3);
+  float x[8];
+#pragma unroll
+  for (int i = 0; i < 8; i++) x[i] = centroid_f32((g >> (3 * i)) & 7u);
+  wht8_inreg(x);
+  wht_xor_lanes16(x, lane);
+  const float rs = wht_scale();
+  const uint32_t sbits = sign_word_sel(part >> 2) >> (8 * (part & 3));   // elements part*8..+7
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+    float a = x[2 * i] * rs, b = x[2 * i + 1] * rs;
+    a = ((sbits >> (2 * i)) & 1u) ? a : -a;
+    b = ((sbits >> (2 * i + 1)) & 1u) ? b : -b;
+    // the reference rounds v*norm to fp32, then to fp16: the empty asm keeps
+    // the fp32 product (no fused fp16-rounding mixed FMA)
+    float pa = a * norm, pb = b * norm;
+    asm volatile("" : "+v"(pa), "+v"(pb));
+    pk[i] = f2h(pa) | (f2h(pb) << 16);
+  }
 }
 
 hipError_t launch_tq3_attn(const AttnArgs& a, int mode, uint16_t* out, hipStream_t stream);

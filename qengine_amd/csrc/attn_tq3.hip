@@ -359,6 +359,8 @@ __device__ void finish_rows(const uint8_t* lds, const AttnArgs& p, int h, int t,
 }
 
 // MODE 0: fast path (final fp16 rows).  MODE 1: reference split partials.
+// MODE 2: block-sparse split partials (attention.cuh:2193-2433): one query
+// per workgroup (qpw = 1), split z over the query's selected 64-key blocks.
 template <int MODE>
 __global__ __launch_bounds__(kThreads, 1) void tq3_attn_kernel(AttnArgs p, uint16_t* out) {
   // static LDS: table and tile offsets fold into the instructions' offset field
@@ -403,7 +405,7 @@ __global__ __launch_bounds__(kThreads, 1) void tq3_attn_kernel(AttnArgs p, uint1
       rec_chunk = chunk;
     }
   }
-  if (MODE == 1 && !has_work) return;
+  if (MODE >= 1 && !has_work) return;
   const int nq = min(p.qpw, p.sub_n - t0);
   const int rows_used = nq * gqa;   // accumulator rows (columns) that hold heads
   const int row = lane >> 4;        // 16-lane row of the MFMA D layout
@@ -423,6 +425,12 @@ __global__ __launch_bounds__(kThreads, 1) void tq3_attn_kernel(AttnArgs p, uint1
       hi_col = min(lo + chunk_keys, active_end);
       hi_first = min(lo + chunk_keys, active_first);
     }
+  } else if (MODE == 2) {
+    // the selected blocks bound the keys; the query's causal end masks them
+    lo = 0;
+    hi = active_end;
+    hi_col = active_end;
+    hi_first = active_end;
   } else {
     // reference split range (attention.cuh:1944-1951)
     const int total_tiles = (p.active_end_max + 31) / 32;
@@ -451,7 +459,26 @@ __global__ __launch_bounds__(kThreads, 1) void tq3_attn_kernel(AttnArgs p, uint1
   // k: tile k, key lo + wave*64 + k*kStep), loaded now so that no tile load
   // waits for a table read (rows past the table's extent read as 0)
   constexpr int kStep = kWaves * kTile;
-  const int ts0 = lo + wave * kTile;
+  // block-sparse: lane k holds entry k of this split's block list; the list
+  // ends at its first -1 (n_sel entries); wave w takes entries w, w + 8, ...
+  int sel = -1, n_sel = 0;
+  if constexpr (MODE == 2) {
+    const int per = (p.top_k + p.k_splits - 1) / p.k_splits;
+    const int tk_lo = chunk * per, tk_n = max(0, min(per, p.top_k - tk_lo));
+    const __amdgpu_buffer_rsrc_t rbi = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<int32_t*>(p.block_index), 0, (uint32_t)(p.num_kv * p.sub_n_max * p.top_k * 4),
+        kBufferRsrcWord3);
+    // unconditional load (an out-of-range offset reads 0), masked after
+    const uint32_t off = lane < tk_n
+        ? (uint32_t)((((h * p.sub_n_max + t0) * p.top_k) + tk_lo + lane) * 4) : 0xffffffffu;
+    const int ld = (int)__builtin_amdgcn_raw_buffer_load_b32(rbi, off, 0, 0);
+    const int e = lane < tk_n ? ld : -1;
+    const uint64_t ends = __builtin_amdgcn_ballot_w64(e < 0);
+    n_sel = ends ? (int)__builtin_ctzll(ends) : 64;
+    sel = e;
+  }
+  const int ts0 = MODE == 2 ? (wave < n_sel ? __builtin_amdgcn_readlane(sel, wave) * kTile : 0)
+                            : lo + wave * kTile;
   const __amdgpu_buffer_rsrc_t rbt = __builtin_amdgcn_make_buffer_rsrc(
       const_cast<int32_t*>(p.block_tables), 0,
       p.block_tables ? (uint32_t)(p.sub_n * p.bt_stride * 4) : 0u, kBufferRsrcWord3);
@@ -707,7 +734,19 @@ __global__ __launch_bounds__(kThreads, 1) void tq3_attn_kernel(AttnArgs p, uint1
   };
   // lo and hi are wave-uniform (a paged workgroup serves one query): the tile
   // loop is a scalar loop
-  if (ts0 < hi) {
+  if constexpr (MODE == 2) {
+    if (wave < n_sel) {
+      tile_body(std::true_type{}, ts0);
+      for (int k = wave + kWaves; k < n_sel; k += kWaves) {
+        const int ts = __builtin_amdgcn_readlane(sel, k) * kTile;
+        load_tile(p, ts, p.num_kv, h, lane, row, col, tr);
+        tile_body(std::false_type{}, ts);
+      }
+    } else {
+#pragma unroll
+      for (int t = 0; t < 16; t++) acc[t] = f4_t{0.f, 0.f, 0.f, 0.f};
+    }
+  } else if (ts0 < hi) {
     tile_body(std::true_type{}, ts0);
     for (int ts = ts0 + kStep; ts < hi; ts += kStep) {
       load_tile(p, wave_tile_row(ts), p.num_kv, h, lane, row, col, tr);
@@ -759,7 +798,7 @@ __global__ __launch_bounds__(kThreads, 1) void tq3_attn_kernel(AttnArgs p, uint1
       L += wt * ml[kMlLw0 + w * 16 + r];
       o += wt * *reinterpret_cast<const f4_t*>(mo + (w * 16 + r) * kHD + d4);
     }
-    if constexpr (MODE == 1) {
+    if constexpr (MODE >= 1) {
       *reinterpret_cast<f4_t*>(mo + r * kHD + d4) = o;   // wave-0 slot, own elements only
       if (d4 == 0) {
         ml[kMlM + r] = M;
@@ -770,7 +809,7 @@ __global__ __launch_bounds__(kThreads, 1) void tq3_attn_kernel(AttnArgs p, uint1
     }
   }
 
-  if constexpr (MODE == 1) {
+  if constexpr (MODE >= 1) {
     __syncthreads();
     finish_rows(lds, p, h, t0, rows, false, chunk, nullptr);
     return;
@@ -821,8 +860,10 @@ hipError_t launch_tq3_attn(const AttnArgs& a, int mode, uint16_t* out, hipStream
   dim3 grid(n_wg), block(kThreads);
   if (mode == 0)
     hipLaunchKernelGGL((tq3_attn_kernel<0>), grid, block, 0, stream, a, out);
-  else
+  else if (mode == 1)
     hipLaunchKernelGGL((tq3_attn_kernel<1>), grid, block, 0, stream, a, out);
+  else
+    hipLaunchKernelGGL((tq3_attn_kernel<2>), grid, block, 0, stream, a, out);
   return hipGetLastError();
 }
 

@@ -69,14 +69,6 @@ __device__ __forceinline__ int value_pos(int key32) {
   return 16 * (a >> 1) + 8 * h + 4 * (a & 1) + c;
 }
 
-// fp32 Lloyd-Max level i (turboquant.cuh:27-30), selected without a memory
-// lookup: i >= 4: +m[i-4], i < 4: -m[3-i].
-__device__ __forceinline__ float centroid_f32(uint32_t i) {
-  const uint32_t m = (i & 4u) ? (i & 3u) : (3u - (i & 3u));
-  const float mag = (m & 2u) ? ((m & 1u) ? 0.190303f : 0.118828f) : ((m & 1u) ? 0.066847f : 0.021664f);
-  return (i & 4u) ? mag : -mag;
-}
-
 // Placement of the attention workgroups: the qtiles of one pair (kv head,
 // head group, key split) stream the same tiles, so they go to consecutive
 // slots of `span` XCDs (a power of two, 32 slots -- one per CU -- each);
@@ -120,33 +112,9 @@ __global__ __launch_bounds__(256) void prefill_stage_kernel(PrefillArgs p, const
   uint32_t pk[4] = {0u, 0u, 0u, 0u};    // pad rows stay zero
   if (row < p.hist) {
     // history: the reference's dequantization (turboquant.cuh:169-200)
-    const uint8_t* base = reinterpret_cast<const uint8_t*>(tv ? p.v_cache : p.k_cache) +
-                          ((uint64_t)(uint32_t)row * (uint32_t)p.num_kv + h) * 104u + blk * 52u;
-    const float norm = *reinterpret_cast<const float*>(base);
-    // code group `part`: bytes 3*part .. 3*part+2 of the 48 code bytes
-    const int b0 = 3 * part, w0 = b0 >> 2;
-    const uint32_t* cw = reinterpret_cast<const uint32_t*>(base + 4);
-    const uint32_t lo = cw[w0], hi = cw[min(w0 + 1, 11)];
-    const uint32_t g = __builtin_amdgcn_alignbyte(hi, lo, b0 & 3);
-    float x[8];
-#pragma unroll
-    for (int i = 0; i < 8; i++) x[i] = centroid_f32((g >> (3 * i)) & 7u);
-    // inverse WHT: the same butterfly pairs, stage by stage, as fast_iwht_128
-    wht8_inreg(x);
-    wht_xor_lanes16(x, lane);
-    const float rs = wht_scale();
-    const uint32_t sbits = sign_word_sel(part >> 2) >> (8 * (part & 3));   // elements part*8..+7
-#pragma unroll
-    for (int i = 0; i < 4; i++) {
-      float a = x[2 * i] * rs, b = x[2 * i + 1] * rs;
-      a = ((sbits >> (2 * i)) & 1u) ? a : -a;
-      b = ((sbits >> (2 * i + 1)) & 1u) ? b : -b;
-      // the reference rounds v*norm to fp32, then to fp16: the empty asm keeps
-      // the fp32 product (no fused fp16-rounding mixed FMA)
-      float pa = a * norm, pb = b * norm;
-      asm volatile("" : "+v"(pa), "+v"(pb));
-      pk[i] = f2h(pa) | (f2h(pb) << 16);
-    }
+    tq3_dequant_exact8(reinterpret_cast<const uint8_t*>(tv ? p.v_cache : p.k_cache) +
+                           ((uint64_t)(uint32_t)row * (uint32_t)p.num_kv + h) * 104u + blk * 52u,
+                       part, lane, pk);
   } else if (row >= p.h_pad && row - p.h_pad < p.n_tok) {
     // the chunk's own keys / values, as given
     const uint16_t* src = (tv ? v : k) + ((long)(row - p.h_pad) * p.num_kv + h) * kHD + dim0;

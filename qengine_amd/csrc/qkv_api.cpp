@@ -331,6 +331,101 @@ int qkv_attn_split_tq3(const uint16_t* q, const qkv_block_tq3* k, const qkv_bloc
   return launch_status(qkv::launch_tq3_attn(a, 1, nullptr, stream));
 }
 
+int qkv_tq3_kpool_update(const qkv_block_tq3* k_cache, uint16_t* k_pool, uint16_t* k_pool_max,
+                         int num_kv, int head_dim, int total_kv, int blk_lo, int n_blocks_stride,
+                         int block_size_n, hipStream_t stream) {
+  if (head_dim != 256) return QKV_ERR_UNSUPPORTED;
+  if (block_size_n < 1 || block_size_n > 64) return QKV_ERR_UNSUPPORTED;
+  if (num_kv <= 0 || total_kv < 0 || blk_lo < 0 || n_blocks_stride <= 0) return QKV_ERR_INVALID;
+  const int cur_blocks = (int)(((long)total_kv + block_size_n - 1) / block_size_n);
+  if (cur_blocks > n_blocks_stride) return QKV_ERR_INVALID;
+  if (blk_lo >= cur_blocks) return QKV_OK;
+  if ((long)num_kv * (cur_blocks - blk_lo) > 0x7fffffffL) return QKV_ERR_UNSUPPORTED;
+  if (!k_cache || !k_pool || !k_pool_max) return QKV_ERR_NULL;
+  if (!aligned(k_cache, 4) || !aligned(k_pool, 2) || !aligned(k_pool_max, 2)) return QKV_ERR_ALIGN;
+  qkv::KpoolArgs a{};
+  a.k = reinterpret_cast<const uint32_t*>(k_cache);
+  a.k_pool = k_pool;
+  a.k_pool_max = k_pool_max;
+  a.num_kv = num_kv;
+  a.total_kv = total_kv;
+  a.blk_lo = blk_lo;
+  a.cur_blocks = cur_blocks;
+  a.stride = n_blocks_stride;
+  a.bsn = block_size_n;
+  return launch_status(qkv::launch_tq3_kpool(a, stream));
+}
+
+int qkv_block_index_ms(const uint16_t* q, const uint16_t* k_pool, const uint16_t* k_pool_max,
+                       int32_t* block_index, int num_q, int num_kv, int head_dim, int sub_n,
+                       int sub_n_max, int start_pos, int top_k, int block_size_n, int n_blocks,
+                       int n_blocks_stride, float beta, hipStream_t stream) {
+  if (head_dim != 256) return QKV_ERR_UNSUPPORTED;
+  if (num_kv <= 0 || num_q <= 0 || num_q % num_kv != 0 || sub_n < 1 || sub_n > sub_n_max ||
+      start_pos < 0 || top_k < 1 || block_size_n < 1 || n_blocks < 0 ||
+      n_blocks > n_blocks_stride)
+    return QKV_ERR_INVALID;
+  if (n_blocks > 32768) return QKV_ERR_UNSUPPORTED;   // block scores live in LDS
+  if (!q || !k_pool || !k_pool_max || !block_index) return QKV_ERR_NULL;
+  if (!aligned(q, 4) || !aligned(k_pool, 4) || !aligned(k_pool_max, 4) || !aligned(block_index, 4))
+    return QKV_ERR_ALIGN;
+  qkv::BlockIndexArgs a{};
+  a.q = q;
+  a.k_pool = k_pool;
+  a.k_pool_max = k_pool_max;
+  a.block_index = block_index;
+  a.num_q = num_q;
+  a.num_kv = num_kv;
+  a.sub_n = sub_n;
+  a.sub_n_max = sub_n_max;
+  a.start_pos = start_pos;
+  a.top_k = top_k;
+  a.bsn = block_size_n;
+  a.n_blocks = n_blocks;
+  a.stride = n_blocks_stride;
+  a.beta = beta;
+  return launch_status(qkv::launch_block_index(a, stream));
+}
+
+int qkv_attn_block_sparse_split_tq3(const uint16_t* q, const qkv_block_tq3* k,
+                                    const qkv_block_tq3* v, const int32_t* block_index,
+                                    float* part_m, float* part_l, float* part_o, int num_q,
+                                    int num_kv, int head_dim, int start_pos, int sub_n,
+                                    int sub_n_max, float scale, int top_k, int block_size_n,
+                                    int k_splits, const uint32_t* tree_mask, hipStream_t stream) {
+  int st = check_attn_shape(num_q, num_kv, head_dim, start_pos, sub_n, tree_mask);
+  if (st) return st;
+  if (block_size_n != 64) return QKV_ERR_UNSUPPORTED;   // one 64-key tile per block
+  if (sub_n > sub_n_max || top_k < 1 || k_splits < 1 || k_splits > 65536) return QKV_ERR_INVALID;
+  if ((top_k + k_splits - 1) / k_splits > 64) return QKV_ERR_UNSUPPORTED;   // <= 64 blocks per split
+  if (!q || !k || !v || !block_index || !part_m || !part_l || !part_o) return QKV_ERR_NULL;
+  if (!aligned(q, 16) || !aligned(k, 4) || !aligned(v, 4) || !aligned(block_index, 4) ||
+      !aligned(part_m, 4) || !aligned(part_l, 4) || !aligned(part_o, 4))
+    return QKV_ERR_ALIGN;
+  qkv::AttnArgs a{};
+  a.q = q;
+  a.k = reinterpret_cast<const uint32_t*>(k);
+  a.v = reinterpret_cast<const uint32_t*>(v);
+  a.num_q = num_q;
+  a.num_kv = num_kv;
+  a.start_pos = start_pos;
+  a.sub_n = sub_n;
+  a.sub_n_max = sub_n_max;
+  a.qpw = 1;   // every query has its own block list
+  a.kv_bytes = (uint64_t)(start_pos + sub_n) * num_kv * 104;
+  a.active_end_max = start_pos + sub_n;
+  a.k_splits = k_splits;
+  a.n_chunks = k_splits;
+  a.scale_log2 = scale * qkv::kLog2e;
+  a.tree_mask = tree_mask;
+  a.block_index = block_index;
+  a.top_k = top_k;
+  a.part_m = part_m;
+  a.part_l = part_l;
+  a.part_o = part_o;
+  return launch_status(qkv::launch_tq3_attn(a, 2, nullptr, stream));
+}
+
 int qkv_attn_split_q8(const uint16_t* q, const qkv_block_q8* k, const qkv_block_q8* v,
                       float* part_m, float* part_l, float* part_o, int num_q, int num_kv,
                       int head_dim, int start_pos, int sub_n, int sub_n_max, int active_end_max,

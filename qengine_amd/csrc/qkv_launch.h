@@ -60,6 +60,25 @@ struct PageCopyArgs {
 };
 hipError_t launch_kv_page_copy(const PageCopyArgs& a, bool scatter, hipStream_t stream);
 
+// Block-sparse TQ3 verify (sparse_tq3.hip): K-pool signatures and the top-k
+// block index.  Pools are fp16 [num_kv][stride][256].
+struct KpoolArgs {
+  const uint32_t* k;         // slot-base TQ3 key cache
+  uint16_t* k_pool;
+  uint16_t* k_pool_max;
+  int num_kv, total_kv, blk_lo, cur_blocks, stride, bsn;
+};
+hipError_t launch_tq3_kpool(const KpoolArgs& a, hipStream_t stream);
+struct BlockIndexArgs {
+  const uint16_t* q;         // [sub_n][num_q][256]
+  const uint16_t* k_pool;
+  const uint16_t* k_pool_max;
+  int32_t* block_index;      // [num_kv][sub_n_max][top_k]
+  int num_q, num_kv, sub_n, sub_n_max, start_pos, top_k, bsn, n_blocks, stride;
+  float beta;
+};
+hipError_t launch_block_index(const BlockIndexArgs& a, hipStream_t stream);
+
 // Chunked prefill over a TQ3 cache (prefill_tq3.hip).  Workspace pieces:
 // kx  keys [num_kv][h_pad + n_pad][256] fp16: the history rows dequantized
 //     exactly as the reference's bulk dequantization, padded to whole 64-row

@@ -214,6 +214,40 @@ def attn_split_merge(part_m, part_l, part_o, out, *, num_q, num_kv, sub_n, sub_n
         _stream(stream)), "qkv_attn_split_merge")
 
 
+def tq3_kpool_update(k_cache, k_pool, k_pool_max, *, num_kv, total_kv, blk_lo, block_size_n=64,
+                     head_dim=256, stream=None) -> None:
+    """Block signatures of the TQ3 keys (attention.cuh:2445-2533): pools are
+    fp16 tensors [num_kv][n_blocks_stride][256]; blocks blk_lo ..
+    ceil(total_kv / block_size_n) - 1 are rebuilt."""
+    check(lib().qkv_tq3_kpool_update(
+        _dev_ptr(k_cache, "k_cache"), _dev_ptr(k_pool, "k_pool"), _dev_ptr(k_pool_max, "k_pool_max"),
+        num_kv, head_dim, total_kv, blk_lo, k_pool.shape[1], block_size_n, _stream(stream)),
+        "qkv_tq3_kpool_update")
+
+
+def block_index_ms(q, k_pool, k_pool_max, block_index, *, num_q, num_kv, sub_n, start_pos,
+                   top_k, n_blocks, block_size_n=64, beta=0.5, head_dim=256, stream=None) -> None:
+    """Top-k block selection (sparse_attn/sparse_index.cuh:214-330) into the
+    int32 tensor block_index [num_kv][sub_n_max][top_k]."""
+    check(lib().qkv_block_index_ms(
+        _dev_ptr(q, "q"), _dev_ptr(k_pool, "k_pool"), _dev_ptr(k_pool_max, "k_pool_max"),
+        _i32(block_index, "block_index"), num_q, num_kv, head_dim, sub_n, block_index.shape[1],
+        start_pos, top_k, block_size_n, n_blocks, k_pool.shape[1], float(beta), _stream(stream)),
+        "qkv_block_index_ms")
+
+
+def attn_block_sparse_split_tq3(q, k, v, block_index, part_m, part_l, part_o, *, num_q, num_kv,
+                                start_pos, sub_n, sub_n_max, scale, top_k, k_splits,
+                                block_size_n=64, tree_mask=None, head_dim=256,
+                                stream=None) -> None:
+    """attention.cuh:2193-2433: split partials over each query's selected blocks."""
+    check(lib().qkv_attn_block_sparse_split_tq3(
+        _dev_ptr(q, "q"), _dev_ptr(k, "k"), _dev_ptr(v, "v"), _i32(block_index, "block_index"),
+        _dev_ptr(part_m, "part_m"), _dev_ptr(part_l, "part_l"), _dev_ptr(part_o, "part_o"),
+        num_q, num_kv, head_dim, start_pos, sub_n, sub_n_max, float(scale), top_k, block_size_n,
+        k_splits, _opt_ptr(tree_mask), _stream(stream)), "qkv_attn_block_sparse_split_tq3")
+
+
 def decode_attn_tq3_workspace_bytes(num_q, num_kv, sub_n, n_keys) -> int:
     return int(lib().qkv_decode_attn_tq3_workspace_bytes(num_q, num_kv, sub_n, n_keys))
 

@@ -177,3 +177,27 @@ def test_inject_and_page_copy_argument_errors_without_gpu(L):
     assert g(p, p, p, p, 416, 416, 100, None, 4, 16, 8, None) == -2
     assert g(p + 2, p, p, p, 416, 416, 100, p, 4, 16, 8, None) == -4
     assert L.qkv_kv_scatter_rows(p, p, None, p, 416, 416, 100, p, 4, 16, 8, None) == -2
+
+
+def test_block_sparse_argument_errors_without_gpu(L):
+    buf = ctypes.create_string_buffer(8192)
+    p = (ctypes.addressof(buf) + 255) & ~255
+    kp = L.qkv_tq3_kpool_update
+    assert kp(p, p, p, 4, 256, 0, 0, 8, 64, None) == 0            # nothing to build
+    assert kp(p, p, p, 4, 128, 100, 0, 8, 64, None) == -3
+    assert kp(p, p, p, 4, 256, 100, 0, 8, 65, None) == -3          # blocks of at most 64 rows
+    assert kp(p, p, p, 4, 256, 64 * 9, 0, 8, 64, None) == -1        # 9 blocks in a stride of 8
+    assert kp(None, p, p, 4, 256, 100, 0, 8, 64, None) == -2
+    assert kp(p, p + 1, p, 4, 256, 100, 0, 8, 64, None) == -4
+    bi = L.qkv_block_index_ms
+    assert bi(p, p, p, p, 16, 4, 256, 2, 1, 100, 8, 64, 2, 2, 0.5, None) == -1   # sub_n > sub_n_max
+    assert bi(p, p, p, p, 16, 4, 256, 1, 1, 100, 0, 64, 2, 2, 0.5, None) == -1   # top_k 0
+    assert bi(p, p, p, p, 16, 4, 256, 1, 1, 100, 8, 64, 3, 2, 0.5, None) == -1   # n_blocks > stride
+    assert bi(p, p, p, p, 16, 4, 256, 1, 1, 100, 8, 64, 40000, 40000, 0.5, None) == -3
+    assert bi(p, None, p, p, 16, 4, 256, 1, 1, 100, 8, 64, 2, 2, 0.5, None) == -2
+    sp = L.qkv_attn_block_sparse_split_tq3
+    assert sp(p, p, p, p, p, p, p, 16, 4, 256, 100, 1, 1, 1.0, 8, 32, 8, None, None) == -3
+    assert sp(p, p, p, p, p, p, p, 16, 4, 256, 100, 1, 1, 1.0, 600, 64, 8, None, None) == -3
+    assert sp(p, p, p, p, p, p, p, 16, 4, 256, 100, 1, 1, 1.0, 0, 64, 8, None, None) == -1
+    assert sp(p, p, p, None, p, p, p, 16, 4, 256, 100, 1, 1, 1.0, 8, 64, 8, None, None) == -2
+    assert sp(p + 8, p, p, p, p, p, p, 16, 4, 256, 100, 1, 1, 1.0, 8, 64, 8, None, None) == -4
