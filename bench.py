@@ -14,9 +14,18 @@ Prints one JSON line (value = microseconds per token, lower is better) with:
                 around the timed region, which holds only these launches),
                 against 8 TB/s; traffic = HBM bytes per launch from rocprofv3
                 counters (profiles/traffic.json)
+  step_stats    per-step median / p10 / p90 over the timed steps (an event
+                pair around every step)
+  hbm_read_peak measured streaming-read bandwidth (qkv_hbm_read_bench over a
+                2 GiB buffer); every fraction is also given against it
   append        TQ3 append (K+V) throughput of the cache build
-  cpu_baseline  the CPU oracle (C port of the reference arithmetic, OpenMP)
-                on a bounded sample: one decode token over the 8 layers
+  config1       (CPU leg) the CPU-plumbing config: TQ3 roundtrip MSE, code
+                histogram, codes checked against the oracle, and the elements
+                within one fp32 ulp of a decision boundary
+  cpu_baseline  the CPU oracle (C port of the reference arithmetic, OpenMP) on
+                bounded samples, at all usable cores and at one thread: one
+                decode token over the 8 layers (the reported value) and the
+                TQ3 encode of one layer's K and V
 """
 import argparse
 import json
@@ -42,8 +51,8 @@ APPEND_REPS = 5
 def parse():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=100)
-    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-secondary", action="store_true",
                     help="skip the configs 2, 4 and 5 measurements")
@@ -243,6 +252,39 @@ def secondary(torch, kvcache, dev, stream):
                 "qkv_decode_attn_tq3 with sub_n 16 (4 queries per workgroup pass); "
                 "prefill_path_us: the same through qkv_prefill_attn_tq3 in verify mode"}
 
+    # ---- f2: block-sparse verify of the same 16 queries (DFLASH_VERIFY_BLOCKSPARSE
+    # defaults: top_k = 10% of the blocks capped at 64, beta 0.5, K_SPLITS 8) ----
+    n_all = hist + nv
+    nb = (n_all + 63) // 64
+    kp = torch.zeros((NUM_KV, nb + 64, HD), dtype=torch.float16, device=dev)
+    kx = torch.zeros_like(kp)
+    kvcache.tq3_kpool_update(kb, kp, kx, num_kv=NUM_KV, total_kv=hist, blk_lo=0)
+    top_k = min(64, max(1, int(nb * 0.10)))
+    bi = torch.zeros((NUM_KV, nv, top_k), dtype=torch.int32, device=dev)
+    spm = torch.empty(NUM_Q, nv, 8, device=dev)
+    spl = torch.empty(NUM_Q, nv, 8, device=dev)
+    spo = torch.empty(NUM_Q, nv, 8, HD, device=dev)
+
+    def sparse_verify(i=0):
+        append16()
+        kvcache.tq3_kpool_update(kb, kp, kx, num_kv=NUM_KV, total_kv=n_all,
+                                 blk_lo=(hist - 1) // 64)
+        kvcache.block_index_ms(qv, kp, kx, bi, num_q=NUM_Q, num_kv=NUM_KV, sub_n=nv,
+                               start_pos=hist, top_k=top_k, n_blocks=nb)
+        kvcache.attn_block_sparse_split_tq3(qv, kb, vb, bi, spm, spl, spo, num_q=NUM_Q,
+                                            num_kv=NUM_KV, start_pos=hist, sub_n=nv, sub_n_max=nv,
+                                            scale=scale, top_k=top_k, k_splits=8)
+        kvcache.attn_split_merge(spm, spl, spo, ov, num_q=NUM_Q, num_kv=NUM_KV, sub_n=nv,
+                                 sub_n_max=nv, k_splits=8)
+    ms = _time(torch, stream, sparse_verify, 50)
+    out["f2_sparse_verify16"] = {
+        "us": round(ms * 1e3, 3), "top_k": top_k, "n_blocks": nb,
+        "note": "append of the 16 verify tokens, incremental key-block signatures (the last "
+                "two 64-row blocks), top-k block index (10% of 2049 blocks -> 64), block-sparse "
+                "split attention (K_SPLITS 8) and merge: 5 launches over the 131088-key TQ3 "
+                "cache of config 5"}
+    del kp, kx
+
     # ---- V-only TurboQuant (keys Q8_0, values TQ3): one query over 32768 keys
     # of config 3's head shape; 8 layers x 2 cache sets rotated ----
     ctx, n_caches = 32768, 16
@@ -271,6 +313,127 @@ def secondary(torch, kvcache, dev, stream):
                 "keys Q8_0 (288 B per kv head and token), values TQ3 (104 B); 16 caches rotated"}
     del caches
     return out
+
+
+def hbm_read_peak(torch, kvcache, dev, stream):
+    """Sustained streaming-read bandwidth: qkv_hbm_read_bench over a 2 GiB
+    buffer (8x the Infinity Cache), 2 warm-up + 10 timed reads."""
+    buf = torch.ones(2 << 30, dtype=torch.uint8, device=dev)
+    sink = torch.zeros(1, dtype=torch.int32, device=dev)
+    for _ in range(2):
+        kvcache.hbm_read_bench(buf, sink)
+    reps = 10
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    a.record(stream)
+    for _ in range(reps):
+        kvcache.hbm_read_bench(buf, sink)
+    b.record(stream)
+    torch.cuda.synchronize()
+    ms = a.elapsed_time(b) / reps
+    gbps = buf.numel() / (ms * 1e-3) / 1e9
+    del buf
+    return {"gbps": round(gbps, 1), "frac_of_nominal": round(gbps / HBM_PEAK_GBS, 4),
+            "bytes": 2 << 30, "kernel": "stream_read_kernel (qkv_hbm_read_bench)"}
+
+
+def config1_report(torch, kvcache, dev):
+    """BASELINE config 1 (seed 0): K and V [1024][4][256] fp16 ~ N(0,1) with 5
+    fixed x8 outlier channels per head, TQ3-encoded on the GPU (append) and
+    decoded (dequant).  Reports the roundtrip MSE, the relative MSE, the
+    8-bin code histogram, whether the codes equal the oracle's, and how many
+    elements sit within one fp32 ulp of a decision boundary (where the
+    reference's rsqrtf(128) / contraction could move a code)."""
+    import numpy as np
+    from oracle import oracle as O
+    rng = np.random.default_rng(0)
+    planes = []
+    for _ in range(2):
+        x = rng.standard_normal((1024, NUM_KV, HD)).astype(np.float32)
+        for h in range(NUM_KV):
+            x[:, h, rng.choice(HD, 5, replace=False)] *= 8.0
+        planes.append(x.astype(np.float16))
+    codes_all, sq, ref_sq, equal, near, n_el = [], 0.0, 0.0, True, 0, 0
+    bounds = O.tq3_bounds().astype(np.float32)
+    for x in planes:
+        n = x.size // 128
+        blocks = kvcache.tq3_blocks(n, dev)
+        kvcache.tq3_append(torch.from_numpy(x.reshape(-1)).to(dev), blocks)
+        dec = kvcache.tq3_dequant(blocks).float().cpu().numpy().reshape(-1)
+        got = blocks.cpu().numpy().view(O.BLOCK_TQ3).reshape(-1)
+        exp, rot = O.tq3_encode_rotated(x)
+        equal = equal and bool(np.array_equal(got.view(np.uint8), exp.view(np.uint8)))
+        xf = x.astype(np.float64).reshape(-1)
+        sq += float(((dec - xf) ** 2).sum())
+        ref_sq += float((xf ** 2).sum())
+        n_el += xf.size
+        qs = got["qs"].reshape(n, 16, 3).astype(np.uint32)
+        w = qs[..., 0] | (qs[..., 1] << 8) | (qs[..., 2] << 16)
+        codes_all.append(((w[..., None] >> (3 * np.arange(8))) & 7).reshape(-1))
+        lo = np.nextafter(rot, np.float32(-np.inf))
+        hi = np.nextafter(rot, np.float32(np.inf))
+        near += int(((lo[..., None] <= bounds) & (bounds <= hi[..., None])).any(-1).sum())
+    hist = np.bincount(np.concatenate(codes_all), minlength=8)
+    return {"elements": n_el, "mse": sq / n_el, "rel_mse": sq / ref_sq,
+            "code_hist": [int(c) for c in hist],
+            "code_frac": [round(float(c) / hist.sum(), 4) for c in hist],
+            "codes_equal_oracle": equal, "near_boundary_1ulp": near,
+            "note": "K and V of config 1 (2 x 8192 blocks of 128), GPU append + dequant; "
+                    "near_boundary_1ulp: rotated values whose one-ulp neighbourhood holds a "
+                    "decision bound (oracle rotation)"}
+
+
+def cpu_baselines(torch, caches, q, scale):
+    """The oracle (C, -O3, OpenMP) on the GPU box's host: one decode token over
+    the 8 layers of cache set 0 (split-K 32 + merge) and the TQ3 encode of one
+    layer's 32768-token K and V, each at all usable cores and at one thread."""
+    import numpy as np
+    from oracle import oracle as O
+    nproc = os.cpu_count()
+    affinity = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else nproc
+    omp = os.environ.get("OMP_NUM_THREADS")
+    cores = max(1, min(affinity, int(omp) if omp and omp.isdigit() else affinity))
+    host = [(caches[0][l][0].cpu().numpy().view(O.BLOCK_TQ3).reshape(-1),
+             caches[0][l][1].cpu().numpy().view(O.BLOCK_TQ3).reshape(-1),
+             q[l].cpu().numpy().view(np.uint16)) for l in range(LAYERS)]
+
+    def decode(threads, layers):
+        t = time.perf_counter()
+        for kb, vb, qh in host[:layers]:
+            pm, pl, po = O.attn_split(O.KV_TQ3, qh, kb, vb, num_q=NUM_Q, num_kv=NUM_KV, hd=HD,
+                                      start_pos=CTX - 1, sub_n=1, sub_n_max=1, active_end_max=CTX,
+                                      scale=scale, k_splits=32, nthreads=threads)
+            O.attn_split_merge(pm, pl, po, num_q=NUM_Q, num_kv=NUM_KV, hd=HD, sub_n=1,
+                               sub_n_max=1, k_splits=32)
+        return (time.perf_counter() - t) * LAYERS / layers
+
+    dec_all = min(decode(cores, LAYERS) for _ in range(CPU_REPS)) * 1e6
+    dec_one = decode(1, 2) * 1e6            # two layers at one thread, scaled to eight
+    gen = torch.Generator().manual_seed(11)
+    xk = torch.randn(CTX, NUM_KV, HD, generator=gen).to(torch.float16).numpy()
+    xv = torch.randn(CTX, NUM_KV, HD, generator=gen).to(torch.float16).numpy()
+
+    def encode(threads):
+        t = time.perf_counter()
+        O.tq3_encode(xk, nthreads=threads)
+        O.tq3_encode(xv, nthreads=threads)
+        return time.perf_counter() - t
+
+    enc_all = min(encode(cores) for _ in range(3))
+    enc_one = encode(1)
+    return {"value": round(dec_all, 1), "unit": "us/token", "cores": cores, "kind": "port",
+            "sample": f"1 decode token x 8 layers at 32768 ctx ({CPU_REPS} reps, best), oracle C "
+                      "port of the reference split-K decode (32 splits) + merge, OpenMP over "
+                      "(kv head, split)",
+            "gbps": round(ATTN_BYTES * LAYERS / (dec_all * 1e-6) / 1e9, 3),
+            "one_thread_us_per_token": round(dec_one, 1),
+            "one_thread_sample": "2 of the 8 layers at one thread, scaled to 8",
+            "nproc": nproc, "affinity_cores": affinity, "omp_num_threads": omp,
+            "encode": {"unit": "M token-layers/s (K+V of one token in one layer)",
+                       "all_cores": round(CTX / enc_all / 1e6, 3),
+                       "one_thread": round(CTX / enc_one / 1e6, 3),
+                       "sample": "TQ3 encode (oracle C port of tq3_quantize_kernel) of one "
+                                 "layer's K and V, 32768 tokens x 4 kv heads x 256"}}
 
 
 def main():
@@ -344,17 +507,18 @@ def main():
         step(i)
     torch.cuda.synchronize()
 
-    # ---- timed region: K steps ----
-    t0 = torch.cuda.Event(enable_timing=True)
-    t1 = torch.cuda.Event(enable_timing=True)
+    # ---- timed region: K steps, an event between consecutive steps ----
+    evs_step = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps + 1)]
     torch.cuda.synchronize()
-    t0.record(stream)
+    evs_step[0].record(stream)
     for i in range(args.steps):
         step(i)
-    t1.record(stream)
+        evs_step[i + 1].record(stream)
     torch.cuda.synchronize()
-    ms_per_step = t0.elapsed_time(t1) / args.steps
+    ms_per_step = evs_step[0].elapsed_time(evs_step[-1]) / args.steps
     us_per_token = ms_per_step * 1e3
+    step_us = sorted(evs_step[i].elapsed_time(evs_step[i + 1]) * 1e3 for i in range(args.steps))
+    pct = lambda f: step_us[min(len(step_us) - 1, int(f * (len(step_us) - 1) + 0.5))]
 
     # ---- roofline: the timed region holds only attention launches (LAYERS per
     # step, back to back on `stream`), so its events give the kernel's average
@@ -379,32 +543,13 @@ def main():
         with open(tpath) as f:
             traffic = json.load(f).get("attn_tq3_32k_bytes_per_launch")
 
-    # ---- CPU baseline: the oracle on one decode token over the 8 layers ----
-    cpu = None
+    read_peak = hbm_read_peak(torch, kvcache, dev, stream)
+    # CPU leg (the oracle as baseline and checker): CPU baselines, and config 1
+    # -- the reference's CPU-runnable roundtrip case -- checked against it
+    cpu = cfg1 = None
     if not args.no_cpu_baseline:
-        from oracle import oracle as O
-        import numpy as np
-        cores = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else os.cpu_count()
-        cores = max(1, min(cores, 16))
-        host = [(caches[0][l][0].cpu().numpy().view(O.BLOCK_TQ3).reshape(-1),
-                 caches[0][l][1].cpu().numpy().view(O.BLOCK_TQ3).reshape(-1),
-                 q[l].cpu().numpy().view(np.uint16)) for l in range(LAYERS)]
-        times = []
-        for rep in range(CPU_REPS):
-            t = time.perf_counter()
-            for kb, vb, qh in host:
-                pm, pl, po = O.attn_split(O.KV_TQ3, qh, kb, vb, num_q=NUM_Q, num_kv=NUM_KV,
-                                          hd=HD, start_pos=CTX - 1, sub_n=1, sub_n_max=1,
-                                          active_end_max=CTX, scale=scale, k_splits=32,
-                                          nthreads=cores)
-                O.attn_split_merge(pm, pl, po, num_q=NUM_Q, num_kv=NUM_KV, hd=HD, sub_n=1,
-                                   sub_n_max=1, k_splits=32)
-            times.append(time.perf_counter() - t)
-        cpu_us = min(times) * 1e6
-        cpu = {"value": round(cpu_us, 1), "unit": "us/token", "cores": cores, "kind": "port",
-               "sample": f"1 decode token x 8 layers at 32768 ctx ({CPU_REPS} reps, best), oracle C "
-                         "port of the reference split-K decode, OpenMP over (kv head, split)",
-               "gbps": round(ATTN_BYTES * LAYERS / (cpu_us * 1e-6) / 1e9, 3)}
+        cpu = cpu_baselines(torch, caches, q, scale)
+        cfg1 = config1_report(torch, kvcache, dev)
 
     sec = None if args.no_secondary else secondary(torch, kvcache, dev, stream)
 
@@ -427,15 +572,25 @@ def main():
                    "bytes_per_layer": ATTN_BYTES},
         "hbm_gbps": round(ATTN_BYTES * LAYERS / (us_per_token * 1e-6) / 1e9, 1),
         "hbm_frac": round(ATTN_BYTES * LAYERS / (us_per_token * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+        "hbm_frac_of_measured_peak": round(ATTN_BYTES * LAYERS / (us_per_token * 1e-6) / 1e9
+                                           / read_peak["gbps"], 4),
+        "step_stats": {"unit": "us/token", "n": args.steps, "median": round(pct(0.5), 3),
+                       "p10": round(pct(0.1), 3), "p90": round(pct(0.9), 3),
+                       "min": round(step_us[0], 3), "max": round(step_us[-1], 3)},
+        "hbm_read_peak": read_peak,
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
                      "traffic": traffic, "kernel": "tq3_attn_kernel<0>",
+                     "frac_of_measured_peak": round(achieved / read_peak["gbps"], 4),
                      "avg_launch_us": round(launch_ms * 1e3, 3),
                      "isolated_launch_median_us": round(durs[len(durs) // 2] * 1e3, 3)},
         "append": {"mtok_layers_per_s": round(append_tok_layers / append_s / 1e6, 1),
                    "gbps": round(append_tok_layers * APPEND_BYTES_PER_TOKEN / append_s / 1e9, 1),
                    "frac": round(append_tok_layers * APPEND_BYTES_PER_TOKEN / append_s / 1e9
-                                 / HBM_PEAK_GBS, 4)},
+                                 / HBM_PEAK_GBS, 4),
+                   "frac_of_measured_peak": round(append_tok_layers * APPEND_BYTES_PER_TOKEN
+                                                  / append_s / 1e9 / read_peak["gbps"], 4)},
+        "config1": cfg1,
         "cpu_baseline": cpu,
         "secondary": sec,
     }

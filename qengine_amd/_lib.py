@@ -48,6 +48,7 @@ SIGNATURES = {
     "qkv_kv_gather_rows": (_I, [_P, _P, _P, _P, _SZ, _SZ, ctypes.c_long, _P, _I, _I, _I, _P]),
     "qkv_kv_scatter_rows": (_I, [_P, _P, _P, _P, _SZ, _SZ, ctypes.c_long, _P, _I, _I, _I, _P]),
     "qkv_dfk2_dequant": (_I, [_P, _P, _P, ctypes.c_longlong, _I, _P]),
+    "qkv_hbm_read_bench": (_I, [_P, _SZ, _P, _P]),
     "qkv_tq3_append_dfk2": (_I, [_P, _P, _P, _I, _P]),
     "qkv_q8_append_dfk2": (_I, [_P, _P, _P, _I, _P]),
     "qkv_attn_split_tq3": (_I, [_P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _F, _I, _I,

@@ -180,6 +180,12 @@ def q8_append_dfk2(q, scales, out, stream=None) -> None:
           "qkv_q8_append_dfk2")
 
 
+def hbm_read_bench(buf, sink, stream=None) -> None:
+    """One streaming read of the whole tensor `buf` (bandwidth measurement)."""
+    check(lib().qkv_hbm_read_bench(_dev_ptr(buf, "buf"), buf.numel() * buf.element_size(),
+                                   _dev_ptr(sink, "sink"), _stream(stream)), "qkv_hbm_read_bench")
+
+
 def _opt_ptr(t):
     return 0 if t is None else _dev_ptr(t, "tensor")
 
