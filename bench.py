@@ -17,7 +17,7 @@ Prints one JSON line (value = microseconds per token, lower is better) with:
   step_stats    per-step median / p10 / p90 over the timed steps (an event
                 pair around every step)
   hbm_read_peak measured streaming-read bandwidth (qkv_hbm_read_bench over a
-                2 GiB buffer); every fraction is also given against it
+                1 GiB buffer); every fraction is also given against it
   append        TQ3 append (K+V) throughput of the cache build
   config1       (CPU leg) the CPU-plumbing config: TQ3 roundtrip MSE, code
                 histogram, codes checked against the oracle, and the elements
@@ -316,9 +316,9 @@ def secondary(torch, kvcache, dev, stream):
 
 
 def hbm_read_peak(torch, kvcache, dev, stream):
-    """Sustained streaming-read bandwidth: qkv_hbm_read_bench over a 2 GiB
-    buffer (8x the Infinity Cache), 2 warm-up + 10 timed reads."""
-    buf = torch.ones(2 << 30, dtype=torch.uint8, device=dev)
+    """Sustained streaming-read bandwidth: qkv_hbm_read_bench over a 1 GiB
+    buffer (4x the Infinity Cache), 2 warm-up + 10 timed reads."""
+    buf = torch.ones(1 << 30, dtype=torch.uint8, device=dev)
     sink = torch.zeros(1, dtype=torch.int32, device=dev)
     for _ in range(2):
         kvcache.hbm_read_bench(buf, sink)
@@ -334,7 +334,7 @@ def hbm_read_peak(torch, kvcache, dev, stream):
     gbps = buf.numel() / (ms * 1e-3) / 1e9
     del buf
     return {"gbps": round(gbps, 1), "frac_of_nominal": round(gbps / HBM_PEAK_GBS, 4),
-            "bytes": 2 << 30, "kernel": "stream_read_kernel (qkv_hbm_read_bench)"}
+            "bytes": 1 << 30, "kernel": "stream_read_kernel (qkv_hbm_read_bench)"}
 
 
 def config1_report(torch, kvcache, dev):

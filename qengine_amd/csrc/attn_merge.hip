@@ -58,20 +58,15 @@ hipError_t launch_fill_zero(void* p, size_t bytes, hipStream_t stream) {
 }
 
 // Streaming read of `bytes` (a multiple of 64): every 16-byte piece loaded
-// once, four loads in flight per thread; the xor of the data is written only
-// if it equals a value no test buffer produces, so no store traffic is added
-// and the loads cannot be elided.  The measurement the reference makes with
-// its bandwidth tool (tools/bench_hbm_bandwidth.cu k_read_f4).
+// once by a grid-stride loop; the xor of the data is written only if it
+// equals a value no test buffer produces, so no store traffic is added and
+// the loads cannot be elided.  The measurement the reference makes with its
+// bandwidth tool (tools/bench_hbm_bandwidth.cu k_read_f4).
 __global__ __launch_bounds__(256) void stream_read_kernel(const uint4* __restrict__ p, size_t n4,
                                                           uint32_t* __restrict__ sink) {
   const size_t stride = (size_t)gridDim.x * 256;
   uint32_t acc = 0u;
-  size_t i = blockIdx.x * 256ul + threadIdx.x;
-  for (; i + 3 * stride < n4; i += 4 * stride) {
-    const uint4 a = p[i], b = p[i + stride], c = p[i + 2 * stride], d = p[i + 3 * stride];
-    acc ^= a.x ^ a.y ^ a.z ^ a.w ^ b.x ^ b.y ^ b.z ^ b.w ^ c.x ^ c.y ^ c.z ^ c.w ^ d.x ^ d.y ^ d.z ^ d.w;
-  }
-  for (; i < n4; i += stride) {
+  for (size_t i = blockIdx.x * 256ul + threadIdx.x; i < n4; i += stride) {
     const uint4 a = p[i];
     acc ^= a.x ^ a.y ^ a.z ^ a.w;
   }
