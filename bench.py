@@ -264,13 +264,15 @@ def secondary(torch, kvcache, dev, stream):
     spm = torch.empty(NUM_Q, nv, 8, device=dev)
     spl = torch.empty(NUM_Q, nv, 8, device=dev)
     spo = torch.empty(NUM_Q, nv, 8, HD, device=dev)
+    wsb = kvcache.lib().qkv_block_index_ms_workspace_bytes(NUM_KV, nv, nb)
+    wsi = torch.empty(wsb, dtype=torch.uint8, device=dev)
 
     def sparse_verify(i=0):
         append16()
         kvcache.tq3_kpool_update(kb, kp, kx, num_kv=NUM_KV, total_kv=n_all,
                                  blk_lo=(hist - 1) // 64)
         kvcache.block_index_ms(qv, kp, kx, bi, num_q=NUM_Q, num_kv=NUM_KV, sub_n=nv,
-                               start_pos=hist, top_k=top_k, n_blocks=nb)
+                               start_pos=hist, top_k=top_k, n_blocks=nb, workspace=wsi)
         kvcache.attn_block_sparse_split_tq3(qv, kb, vb, bi, spm, spl, spo, num_q=NUM_Q,
                                             num_kv=NUM_KV, start_pos=hist, sub_n=nv, sub_n_max=nv,
                                             scale=scale, top_k=top_k, k_splits=8)

@@ -250,11 +250,20 @@ int qkv_tq3_kpool_update(const qkv_block_tq3* k_cache, uint16_t* k_pool, uint16_
  * 4649-4652).  block_index [num_kv][sub_n_max][top_k] int32: per (kv head,
  * query t) the top_k blocks by max(q_avg . mean, beta * q_avg . maxabs) among
  * blocks 0 .. (start_pos + t) / block_size_n, ascending, -1 padded; ties go to
- * the lower block.  Bit-identical selection.  n_blocks <= 32768. */
+ * the lower block.  Bit-identical selection.  Unlike the reference (which
+ * keeps one query's block scores in shared memory and rereads the pool per
+ * query), the pool is read once for all sub_n queries and the scores pass
+ * through a caller-provided workspace of
+ * qkv_block_index_ms_workspace_bytes(num_kv, sub_n, n_blocks) bytes
+ * (256-byte aligned, no initialisation needed).  k_pool / k_pool_max 16-byte
+ * aligned.  n_blocks <= 32768 (with top_k <= 64; a longer pick list shares
+ * that 128 KiB of LDS). */
+size_t qkv_block_index_ms_workspace_bytes(int num_kv, int sub_n, int n_blocks);
 int qkv_block_index_ms(const uint16_t* q, const uint16_t* k_pool, const uint16_t* k_pool_max,
                        int32_t* block_index, int num_q, int num_kv, int head_dim, int sub_n,
                        int sub_n_max, int start_pos, int top_k, int block_size_n, int n_blocks,
-                       int n_blocks_stride, float beta, hipStream_t stream);
+                       int n_blocks_stride, float beta, void* workspace, size_t workspace_bytes,
+                       hipStream_t stream);
 
 /* Replaces flash_attn_chunk_block_sparse_split_tq3<256, GQA, 32, 256,
  * K_SPLITS><<<dim3(num_kv, sub_n, K_SPLITS), ...>>>(q, k_tq, v_tq,

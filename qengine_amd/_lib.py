@@ -56,7 +56,9 @@ SIGNATURES = {
     "qkv_attn_split_q8": (_I, [_P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _F, _I, _P]),
     "qkv_attn_split_merge": (_I, [_P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _P]),
     "qkv_tq3_kpool_update": (_I, [_P, _P, _P, _I, _I, _I, _I, _I, _I, _P]),
-    "qkv_block_index_ms": (_I, [_P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _I, _I, _I, _F, _P]),
+    "qkv_block_index_ms_workspace_bytes": (_SZ, [_I, _I, _I]),
+    "qkv_block_index_ms": (_I, [_P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _I, _I, _I, _F, _P, _SZ,
+                               _P]),
     "qkv_attn_block_sparse_split_tq3": (_I, [_P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I,
                                             _F, _I, _I, _I, _P, _P]),
     "qkv_decode_attn_tq3_workspace_bytes": (_SZ, [_I, _I, _I, _I]),

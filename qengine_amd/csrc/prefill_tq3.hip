@@ -90,52 +90,61 @@ __host__ __device__ inline Placement placement(int qtiles, int pairs) {
 }  // namespace
 
 // ---------------------------------------------------------------------------
-// staging: 16 lanes per 128-element block; lane `part` owns elements
-// part*8 .. part*8+7.  Work item = (tensor K/V, row, kv head, block).
+// staging: one workgroup per (kv head, 64-row tile).  Units (tensor, row,
+// 128-block) of 16 lanes; lane `part` of a unit owns elements part*8 ..
+// part*8+7.  Keys go straight to their kx row; values are transposed through
+// LDS ([dim][value position], 132-byte dim pitch: 2-way banks on the 2-byte
+// stores) and leave as whole 16-byte pieces of the tile.
 // ---------------------------------------------------------------------------
+constexpr int kStVPitch = 132;   // bytes per staged value dim row (64 keys fp16 + 4)
+
 __global__ __launch_bounds__(256) void prefill_stage_kernel(PrefillArgs p, const uint16_t* k,
                                                             const uint16_t* v) {
-  const int lane = threadIdx.x & 63;
-  const int part = threadIdx.x & 15;
-  const long item = (long)blockIdx.x * 16 + (threadIdx.x >> 4);
+  __shared__ __attribute__((aligned(16))) uint8_t vt_lds[kHD * kStVPitch];
+  const int tid = threadIdx.x, lane = tid & 63, part = tid & 15;
   const long rows = (long)p.h_pad + p.n_pad;
-  const long per_tensor = rows * p.num_kv * 2;
-  if (item >= 2 * per_tensor) return;   // 16-lane groups leave together
-  const int tv = item >= per_tensor;    // 0: keys, 1: values
-  const long rest = item - tv * per_tensor;
-  const int blk = (int)(rest & 1);
-  const long rh = rest >> 1;             // row * num_kv + h
-  const int h = (int)(rh % p.num_kv);
-  const int row = (int)(rh / p.num_kv);
-  const int dim0 = blk * 128 + part * 8;
-
-  uint32_t pk[4] = {0u, 0u, 0u, 0u};    // pad rows stay zero
-  if (row < p.hist) {
-    // history: the reference's dequantization (turboquant.cuh:169-200)
-    tq3_dequant_exact8(reinterpret_cast<const uint8_t*>(tv ? p.v_cache : p.k_cache) +
-                           ((uint64_t)(uint32_t)row * (uint32_t)p.num_kv + h) * 104u + blk * 52u,
-                       part, lane, pk);
-  } else if (row >= p.h_pad && row - p.h_pad < p.n_tok) {
-    // the chunk's own keys / values, as given
-    const uint16_t* src = (tv ? v : k) + ((long)(row - p.h_pad) * p.num_kv + h) * kHD + dim0;
-    const uint4 raw = *reinterpret_cast<const uint4*>(src);
-    pk[0] = raw.x;
-    pk[1] = raw.y;
-    pk[2] = raw.z;
-    pk[3] = raw.w;
-  }
-  if (!tv) {
-    *reinterpret_cast<uint4*>(p.kx + ((long)h * rows + row) * kHD + dim0) =
-        make_uint4(pk[0], pk[1], pk[2], pk[3]);
-    return;
-  }
-  // values: tile (h, row / 64), [dim][value position of row % 64]
-  uint16_t* tile = p.vt + ((long)h * (rows / kKeys) + row / kKeys) * kHD * kKeys;
-  const int key64 = row % kKeys;
-  const int pos = (key64 >> 5) * 32 + value_pos(key64 & 31);
+  const int tiles = (int)(rows / kKeys);
+  const int h = blockIdx.x / tiles, tile = blockIdx.x - h * tiles;
+  // 256 units: tensor (K: 0..127, V: 128..255), row r = (u & 127) >> 1, block u & 1
+  for (int u = tid >> 4; u < 256; u += 16) {
+    const int tv = u >> 7, r = (u & 127) >> 1, blk = u & 1;
+    const int row = tile * kKeys + r;
+    const int dim0 = blk * 128 + part * 8;
+    uint32_t pk[4] = {0u, 0u, 0u, 0u};   // pad rows stay zero
+    if (row < p.hist) {
+      // history: the reference's dequantization (turboquant.cuh:169-200)
+      tq3_dequant_exact8(reinterpret_cast<const uint8_t*>(tv ? p.v_cache : p.k_cache) +
+                             ((uint64_t)(uint32_t)row * (uint32_t)p.num_kv + h) * 104u + blk * 52u,
+                         part, lane, pk);
+    } else if (row >= p.h_pad && row - p.h_pad < p.n_tok) {
+      // the chunk's own keys / values, as given
+      const uint16_t* src = (tv ? v : k) + ((long)(row - p.h_pad) * p.num_kv + h) * kHD + dim0;
+      const uint4 raw = *reinterpret_cast<const uint4*>(src);
+      pk[0] = raw.x;
+      pk[1] = raw.y;
+      pk[2] = raw.z;
+      pk[3] = raw.w;
+    }
+    if (!tv) {
+      *reinterpret_cast<uint4*>(p.kx + ((long)h * rows + row) * kHD + dim0) =
+          make_uint4(pk[0], pk[1], pk[2], pk[3]);
+    } else {
+      const int pos = (r >> 5) * 32 + value_pos(r & 31);
 #pragma unroll
-  for (int i = 0; i < 8; i++)
-    tile[(dim0 + i) * kKeys + pos] = (uint16_t)((pk[i >> 1] >> (16 * (i & 1))) & 0xffffu);
+      for (int i = 0; i < 8; i++)
+        *reinterpret_cast<uint16_t*>(vt_lds + (dim0 + i) * kStVPitch + pos * 2) =
+            (uint16_t)((pk[i >> 1] >> (16 * (i & 1))) & 0xffffu);
+    }
+  }
+  __syncthreads();
+  // the value tile: 256 dims x 128 bytes = 2048 16-byte pieces, 8 per thread
+  uint4* dst = reinterpret_cast<uint4*>(p.vt + ((long)h * tiles + tile) * kHD * kKeys);
+#pragma unroll
+  for (int i = 0; i < 8; i++) {
+    const int piece = i * 256 + tid, dim = piece >> 3, q = piece & 7;
+    const uint32_t* src = reinterpret_cast<const uint32_t*>(vt_lds + dim * kStVPitch + q * 16);
+    dst[piece] = make_uint4(src[0], src[1], src[2], src[3]);
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -384,8 +393,8 @@ PrefillGeom prefill_geom(int num_q, int num_kv, int n_tok, int start_pos) {
 hipError_t launch_prefill_tq3(const PrefillArgs& a, int gqa, const uint16_t* q, const uint16_t* k,
                               const uint16_t* v, uint16_t* out, hipStream_t stream) {
   {
-    const long items = 2L * ((long)a.h_pad + a.n_pad) * a.num_kv * 2;
-    hipLaunchKernelGGL(prefill_stage_kernel, dim3((unsigned)((items + 15) / 16)), dim3(256), 0,
+    const long tiles = ((long)a.h_pad + a.n_pad) / kKeys;
+    hipLaunchKernelGGL(prefill_stage_kernel, dim3((unsigned)(a.num_kv * tiles)), dim3(256), 0,
                        stream, a, k, v);
   }
   const int qtiles = (a.n_tok + kToks - 1) / kToks;

@@ -364,19 +364,30 @@ int qkv_tq3_kpool_update(const qkv_block_tq3* k_cache, uint16_t* k_pool, uint16_
   return launch_status(qkv::launch_tq3_kpool(a, stream));
 }
 
+size_t qkv_block_index_ms_workspace_bytes(int num_kv, int sub_n, int n_blocks) {
+  if (num_kv <= 0 || sub_n <= 0 || n_blocks <= 0) return 0;
+  return ((size_t)num_kv * sub_n * n_blocks * 4 + 255) & ~(size_t)255;
+}
+
 int qkv_block_index_ms(const uint16_t* q, const uint16_t* k_pool, const uint16_t* k_pool_max,
                        int32_t* block_index, int num_q, int num_kv, int head_dim, int sub_n,
                        int sub_n_max, int start_pos, int top_k, int block_size_n, int n_blocks,
-                       int n_blocks_stride, float beta, hipStream_t stream) {
+                       int n_blocks_stride, float beta, void* workspace, size_t workspace_bytes,
+                       hipStream_t stream) {
   if (head_dim != 256) return QKV_ERR_UNSUPPORTED;
   if (num_kv <= 0 || num_q <= 0 || num_q % num_kv != 0 || sub_n < 1 || sub_n > sub_n_max ||
-      start_pos < 0 || top_k < 1 || block_size_n < 1 || n_blocks < 0 ||
+      start_pos < 0 || top_k < 1 || block_size_n < 1 || n_blocks < 1 ||
       n_blocks > n_blocks_stride)
     return QKV_ERR_INVALID;
-  if (n_blocks > 32768) return QKV_ERR_UNSUPPORTED;   // block scores live in LDS
+  // the selection keeps up to n_blocks scores and top_k picks in LDS
+  if ((long)n_blocks * 4 + (top_k > 64 ? (long)top_k * 4 : 0) > 128 * 1024) return QKV_ERR_UNSUPPORTED;
   if (!q || !k_pool || !k_pool_max || !block_index) return QKV_ERR_NULL;
-  if (!aligned(q, 4) || !aligned(k_pool, 4) || !aligned(k_pool_max, 4) || !aligned(block_index, 4))
+  if (!aligned(q, 4) || !aligned(k_pool, 16) || !aligned(k_pool_max, 16) ||
+      !aligned(block_index, 4))
     return QKV_ERR_ALIGN;
+  if (!workspace || workspace_bytes < qkv_block_index_ms_workspace_bytes(num_kv, sub_n, n_blocks))
+    return QKV_ERR_WORKSPACE;
+  if (!aligned(workspace, 256)) return QKV_ERR_ALIGN;
   qkv::BlockIndexArgs a{};
   a.q = q;
   a.k_pool = k_pool;
@@ -392,7 +403,7 @@ int qkv_block_index_ms(const uint16_t* q, const uint16_t* k_pool, const uint16_t
   a.n_blocks = n_blocks;
   a.stride = n_blocks_stride;
   a.beta = beta;
-  return launch_status(qkv::launch_block_index(a, stream));
+  return launch_status(qkv::launch_block_index(a, static_cast<float*>(workspace), stream));
 }
 
 int qkv_attn_block_sparse_split_tq3(const uint16_t* q, const qkv_block_tq3* k,

@@ -78,7 +78,8 @@ struct BlockIndexArgs {
   int num_q, num_kv, sub_n, sub_n_max, start_pos, top_k, bsn, n_blocks, stride;
   float beta;
 };
-hipError_t launch_block_index(const BlockIndexArgs& a, hipStream_t stream);
+// scores: workspace of block_index_workspace_bytes (block scores [num_kv][sub_n][n_blocks])
+hipError_t launch_block_index(const BlockIndexArgs& a, float* scores, hipStream_t stream);
 
 // Chunked prefill over a TQ3 cache (prefill_tq3.hip).  Workspace pieces:
 // kx  keys [num_kv][h_pad + n_pad][256] fp16: the history rows dequantized

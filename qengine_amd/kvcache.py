@@ -232,14 +232,20 @@ def tq3_kpool_update(k_cache, k_pool, k_pool_max, *, num_kv, total_kv, blk_lo, b
 
 
 def block_index_ms(q, k_pool, k_pool_max, block_index, *, num_q, num_kv, sub_n, start_pos,
-                   top_k, n_blocks, block_size_n=64, beta=0.5, head_dim=256, stream=None) -> None:
+                   top_k, n_blocks, block_size_n=64, beta=0.5, head_dim=256, workspace=None,
+                   stream=None) -> None:
     """Top-k block selection (sparse_attn/sparse_index.cuh:214-330) into the
-    int32 tensor block_index [num_kv][sub_n_max][top_k]."""
+    int32 tensor block_index [num_kv][sub_n_max][top_k]; the block scores pass
+    through `workspace` (allocated here when None)."""
+    if workspace is None:
+        n = int(lib().qkv_block_index_ms_workspace_bytes(num_kv, sub_n, n_blocks))
+        workspace = torch.empty(max(n, 256), dtype=torch.uint8, device=block_index.device)
     check(lib().qkv_block_index_ms(
         _dev_ptr(q, "q"), _dev_ptr(k_pool, "k_pool"), _dev_ptr(k_pool_max, "k_pool_max"),
         _i32(block_index, "block_index"), num_q, num_kv, head_dim, sub_n, block_index.shape[1],
-        start_pos, top_k, block_size_n, n_blocks, k_pool.shape[1], float(beta), _stream(stream)),
-        "qkv_block_index_ms")
+        start_pos, top_k, block_size_n, n_blocks, k_pool.shape[1], float(beta),
+        _dev_ptr(workspace, "workspace"), workspace.numel() * workspace.element_size(),
+        _stream(stream)), "qkv_block_index_ms")
 
 
 def attn_block_sparse_split_tq3(q, k, v, block_index, part_m, part_l, part_o, *, num_q, num_kv,

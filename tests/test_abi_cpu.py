@@ -190,11 +190,15 @@ def test_block_sparse_argument_errors_without_gpu(L):
     assert kp(None, p, p, 4, 256, 100, 0, 8, 64, None) == -2
     assert kp(p, p + 1, p, 4, 256, 100, 0, 8, 64, None) == -4
     bi = L.qkv_block_index_ms
-    assert bi(p, p, p, p, 16, 4, 256, 2, 1, 100, 8, 64, 2, 2, 0.5, None) == -1   # sub_n > sub_n_max
-    assert bi(p, p, p, p, 16, 4, 256, 1, 1, 100, 0, 64, 2, 2, 0.5, None) == -1   # top_k 0
-    assert bi(p, p, p, p, 16, 4, 256, 1, 1, 100, 8, 64, 3, 2, 0.5, None) == -1   # n_blocks > stride
-    assert bi(p, p, p, p, 16, 4, 256, 1, 1, 100, 8, 64, 40000, 40000, 0.5, None) == -3
-    assert bi(p, None, p, p, 16, 4, 256, 1, 1, 100, 8, 64, 2, 2, 0.5, None) == -2
+    wsb = L.qkv_block_index_ms_workspace_bytes(4, 1, 2)
+    assert wsb == 256
+    assert bi(p, p, p, p, 16, 4, 256, 2, 1, 100, 8, 64, 2, 2, 0.5, p, wsb, None) == -1   # sub_n > sub_n_max
+    assert bi(p, p, p, p, 16, 4, 256, 1, 1, 100, 0, 64, 2, 2, 0.5, p, wsb, None) == -1   # top_k 0
+    assert bi(p, p, p, p, 16, 4, 256, 1, 1, 100, 8, 64, 3, 2, 0.5, p, wsb, None) == -1   # n_blocks > stride
+    assert bi(p, None, p, p, 16, 4, 256, 1, 1, 100, 8, 64, 2, 2, 0.5, p, wsb, None) == -2
+    assert bi(p, p, p, p, 16, 4, 256, 1, 1, 100, 8, 64, 2, 2, 0.5, None, wsb, None) == -7
+    assert bi(p, p, p, p, 16, 4, 256, 1, 1, 100, 8, 64, 40000, 40000, 0.5, p, 1 << 30, None) == -3
+    assert bi(p, p, p, p, 16, 4, 256, 1, 1, 100, 8, 64, 2, 2, 0.5, p, wsb - 1, None) == -7
     sp = L.qkv_attn_block_sparse_split_tq3
     assert sp(p, p, p, p, p, p, p, 16, 4, 256, 100, 1, 1, 1.0, 8, 32, 8, None, None) == -3
     assert sp(p, p, p, p, p, p, p, 16, 4, 256, 100, 1, 1, 1.0, 600, 64, 8, None, None) == -3
