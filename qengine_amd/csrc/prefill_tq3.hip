@@ -53,13 +53,20 @@ constexpr int kHD = 256;
 constexpr int kKeys = 64;                 // keys per tile
 constexpr int kToks = 32;                 // query tokens per workgroup
 
-// LDS layout (bytes)
-constexpr int kKPitch = 528;              // key row: 256 fp16 + 16 B (conflict-free 16-B reads)
-constexpr int kKTile = 0;                 // [64 keys][kKPitch]
-constexpr int kVPitch = 144;              // dim row: 2 x 32 keys fp16 (value order) + 16 B
-constexpr int kVTile = kKTile + kKeys * kKPitch;      // [256 dims][kVPitch]
-constexpr int kLdsBytes = kVTile + kHD * kVPitch;
+// LDS layout (bytes): two tile buffers, each keys [64][512 B] then values
+// [256 dims][128 B].  Rows are stored with their 16-byte chunks XOR-swizzled
+// (key row r: chunk c at c ^ (r & 31); value row d: chunk c at c ^ (d & 7)),
+// so that the MFMA operand reads of 32 consecutive rows at one column spread
+// over the banks; the tiles arrive by direct global-to-LDS loads
+// (global_load_lds_dwordx4: lane l of an instruction writes bytes 16l ..
+// 16l+15 of a 1 KB run, and each lane fetches the chunk that belongs there).
+constexpr int kKBytes = kKeys * kHD * 2;              // 32 KB
+constexpr int kVBytes = kHD * kKeys * 2;              // 32 KB
+constexpr int kBufBytes = kKBytes + kVBytes;
+constexpr int kLdsBytes = 2 * kBufBytes;
 static_assert(kLdsBytes <= 160 * 1024, "prefill LDS must fit one CU");
+
+typedef __attribute__((address_space(3))) void lds_void_t;
 
 // Value order inside a 32-key half: key 8a + 4h + c sits at position
 // 16(a/2) + 8h + 4(a%2) + c, so the 8 keys one lane contributes to a value
@@ -176,6 +183,7 @@ __global__ __launch_bounds__(64 * WAVES, 1) void prefill_attn_kernel(PrefillArgs
     qt = (xcd % pl.span) * pl.per + j;
     if (qt >= qtiles || pair >= pairs || xcd / pl.span >= pl.pairs_per_round) return;
   }
+  (void)NT;
   const int z = pair % p.n_split;
   const int hg_all = pair / p.n_split;                 // kv head * groups + head group
   const int h = hg_all / groups, hg = hg_all - h * groups;
@@ -213,22 +221,36 @@ __global__ __launch_bounds__(64 * WAVES, 1) void prefill_attn_kernel(PrefillArgs
   float m2 = -INFINITY, lsum = 0.0f;
   const int t_abs = t0 + tok;        // this lane's token index in the chunk
 
+  // Tile ti into buffer `buf`: 64 direct loads of 1 KB (32 for the keys, two
+  // rows each; 32 for the values, eight dim rows each), spread over the waves.
+  auto issue_tile = [&](int ti, int buf) {
+    uint8_t* base = lds + buf * kBufBytes;
+    const uint16_t* ksrc = p.kx + ((long)h * rows + (long)ti * kKeys) * kHD;
+    const uint16_t* vsrc = p.vt + ((long)h * (rows / kKeys) + ti) * kHD * kKeys;
+    for (int inst = wave; inst < 64; inst += WAVES) {
+      const uint16_t* src;
+      if (inst < 32) {
+        const int row = 2 * inst + (lane >> 5), c = (lane & 31) ^ (row & 31);
+        src = ksrc + row * kHD + c * 8;
+      } else {
+        const int row = 8 * (inst - 32) + (lane >> 3), c = (lane & 7) ^ (row & 7);
+        src = vsrc + row * kKeys + c * 8;
+      }
+      __builtin_amdgcn_global_load_lds(src, (lds_void_t*)(base + inst * 1024), 16, 0, 0);
+    }
+  };
+  if (tlo < thi) issue_tile(tlo, 0);
+
   for (int ti = tlo; ti < thi; ti++) {
     const bool cached = ti < th;
-    __syncthreads();   // the previous tile's MFMAs are done with the tile buffers
-    {
-      const uint4* ksrc = reinterpret_cast<const uint4*>(p.kx + ((long)h * rows + (long)ti * kKeys) * kHD);
-      for (int i = tid; i < kKeys * 32; i += NT) {
-        const int key = i >> 5, piece = i & 31;
-        *reinterpret_cast<uint4*>(lds + kKTile + key * kKPitch + piece * 16) = ksrc[i];
-      }
-      const uint4* vsrc = reinterpret_cast<const uint4*>(p.vt + ((long)h * (rows / kKeys) + ti) * kHD * kKeys);
-      for (int i = tid; i < kHD * 8; i += NT) {
-        const int dim = i >> 3, piece = i & 7;
-        *reinterpret_cast<uint4*>(lds + kVTile + dim * kVPitch + piece * 16) = vsrc[i];
-      }
-    }
+    const int buf = (ti - tlo) & 1;
+    // tile ti has landed (every wave waits for its own loads, then the
+    // barrier), and every wave is done with the other buffer's tile
+    __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
+    if (ti + 1 < thi) issue_tile(ti + 1, buf ^ 1);
+    const uint8_t* kbuf = lds + buf * kBufBytes;
+    const uint8_t* vbuf = kbuf + kKBytes;
     __builtin_amdgcn_sched_barrier(0);
 
     // key index of tile key `key`: a history row (visible to every token when
@@ -244,10 +266,12 @@ __global__ __launch_bounds__(64 * WAVES, 1) void prefill_attn_kernel(PrefillArgs
       f16x_t sd = f16x_t{};
 #pragma unroll
       for (int b = 0; b < 2; b++) {
-        const uint8_t* arow = lds + kKTile + (kt * 32 + tok) * kKPitch + (b * 128 + 8 * hh) * 2;
+        const int krow = kt * 32 + tok;   // krow & 31 == tok
+        const uint8_t* arow = kbuf + krow * (kHD * 2);
 #pragma unroll
         for (int s = 0; s < 8; s++) {
-          const h8_t a = *reinterpret_cast<const h8_t*>(arow + 32 * s);
+          const int c = b * 16 + hh + 2 * s;   // 16-byte chunk of dims b*128 + 8hh + 16s
+          const h8_t a = *reinterpret_cast<const h8_t*>(arow + ((c ^ tok) * 16));
           sd = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, qb[b][s], sd, 0, 0, 0);
         }
       }
@@ -298,8 +322,8 @@ __global__ __launch_bounds__(64 * WAVES, 1) void prefill_attn_kernel(PrefillArgs
         for (int i = 0; i < 8; i++) pb[i] = (_Float16)sc[8 * sg + i];
 #pragma unroll
         for (int d = 0; d < 8; d++) {
-          const h8_t a = *reinterpret_cast<const h8_t*>(
-              lds + kVTile + (d * 32 + tok) * kVPitch + (kt * 32 + 16 * sg + 8 * hh) * 2);
+          const int vrow = d * 32 + tok, c = kt * 4 + 2 * sg + hh;   // keys kt*32 + 16sg + 8hh ..
+          const h8_t a = *reinterpret_cast<const h8_t*>(vbuf + vrow * (kKeys * 2) + ((c ^ (tok & 7)) * 16));
           acc[d] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, pb, acc[d], 0, 0, 0);
         }
       }
