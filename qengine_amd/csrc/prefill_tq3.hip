@@ -50,23 +50,27 @@ namespace {
 typedef float f16x_t __attribute__((ext_vector_type(16)));
 
 constexpr int kHD = 256;
-constexpr int kKeys = 64;                 // keys per tile
+constexpr int kKeys = 64;                 // row granule of the staged K / V (stage tiles)
+constexpr int kTK = 32;                   // keys per attention tile
 constexpr int kToks = 32;                 // query tokens per workgroup
 
-// LDS layout (bytes): two tile buffers, each keys [64][512 B] then values
-// [256 dims][128 B].  Rows are stored with their 16-byte chunks XOR-swizzled
-// (key row r: chunk c at c ^ (r & 31); value row d: chunk c at c ^ (d & 7)),
-// so that the MFMA operand reads of 32 consecutive rows at one column spread
-// over the banks; the tiles arrive by direct global-to-LDS loads
-// (global_load_lds_dwordx4: lane l of an instruction writes bytes 16l ..
-// 16l+15 of a 1 KB run, and each lane fetches the chunk that belongs there).
-constexpr int kKBytes = kKeys * kHD * 2;              // 32 KB
-constexpr int kVBytes = kHD * kKeys * 2;              // 32 KB
+// LDS of the attention (bytes): two tile buffers, each keys [32][512 B] then
+// values [256 dims][64 B]; 64 KB per workgroup, so two workgroups share a CU
+// and the matrix core of one overlaps the softmax of the other.  16-byte
+// chunks are XOR-swizzled so that the MFMA operand reads (16 lanes per LDS
+// cycle, 16 consecutive rows at one logical chunk) hit 16 different 16-byte
+// bank groups: key row r holds chunk c at c ^ (r & 15), value row d holds
+// chunk c at c ^ ((d >> 2) & 3).  The tiles arrive by direct global-to-LDS
+// loads (buffer_load_dwordx4 ... lds: lane l of an instruction writes bytes
+// 16l .. 16l+15 of a 1 KB run; each lane fetches the chunk that lands there).
+constexpr int kKBytes = kTK * kHD * 2;                // 16 KB
+constexpr int kVBytes = kHD * kTK * 2;                // 16 KB
 constexpr int kBufBytes = kKBytes + kVBytes;
 constexpr int kLdsBytes = 2 * kBufBytes;
-static_assert(kLdsBytes <= 160 * 1024, "prefill LDS must fit one CU");
+static_assert(2 * kLdsBytes <= 160 * 1024, "two prefill workgroups must fit one CU");
 
 typedef __attribute__((address_space(3))) void lds_void_t;
+typedef _Float16 h2_t __attribute__((ext_vector_type(2)));
 
 // Value order inside a 32-key half: key 8a + 4h + c sits at position
 // 16(a/2) + 8h + 4(a%2) + c, so the 8 keys one lane contributes to a value
@@ -101,7 +105,8 @@ __host__ __device__ inline Placement placement(int qtiles, int pairs) {
 // 128-block) of 16 lanes; lane `part` of a unit owns elements part*8 ..
 // part*8+7.  Keys go straight to their kx row; values are transposed through
 // LDS ([dim][value position], 132-byte dim pitch: 2-way banks on the 2-byte
-// stores) and leave as whole 16-byte pieces of the tile.
+// stores) and leave as whole 16-byte pieces of the two 32-key tiles
+// vt [kv head][row / 32][256 dims][32].
 // ---------------------------------------------------------------------------
 constexpr int kStVPitch = 132;   // bytes per staged value dim row (64 keys fp16 + 4)
 
@@ -144,12 +149,12 @@ __global__ __launch_bounds__(256) void prefill_stage_kernel(PrefillArgs p, const
     }
   }
   __syncthreads();
-  // the value tile: 256 dims x 128 bytes = 2048 16-byte pieces, 8 per thread
+  // the two 32-key value tiles: 2 x 256 dims x 64 bytes = 2048 16-byte pieces, 8 per thread
   uint4* dst = reinterpret_cast<uint4*>(p.vt + ((long)h * tiles + tile) * kHD * kKeys);
 #pragma unroll
   for (int i = 0; i < 8; i++) {
-    const int piece = i * 256 + tid, dim = piece >> 3, q = piece & 7;
-    const uint32_t* src = reinterpret_cast<const uint32_t*>(vt_lds + dim * kStVPitch + q * 16);
+    const int piece = i * 256 + tid, half = piece >> 10, dim = (piece >> 2) & 255, q = piece & 3;
+    const uint32_t* src = reinterpret_cast<const uint32_t*>(vt_lds + dim * kStVPitch + half * 64 + q * 16);
     dst[piece] = make_uint4(src[0], src[1], src[2], src[3]);
   }
 }
@@ -159,10 +164,9 @@ __global__ __launch_bounds__(256) void prefill_stage_kernel(PrefillArgs p, const
 // workgroup, one wave per head
 // ---------------------------------------------------------------------------
 template <int WAVES, bool FROM_CACHE>
-__global__ __launch_bounds__(64 * WAVES, 1) void prefill_attn_kernel(PrefillArgs p,
+__global__ __launch_bounds__(64 * WAVES, 2) void prefill_attn_kernel(PrefillArgs p,
                                                                      const uint16_t* q) {
   __shared__ __attribute__((aligned(16))) uint8_t lds[kLdsBytes];
-  constexpr int NT = 64 * WAVES;
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -183,7 +187,6 @@ __global__ __launch_bounds__(64 * WAVES, 1) void prefill_attn_kernel(PrefillArgs
     qt = (xcd % pl.span) * pl.per + j;
     if (qt >= qtiles || pair >= pairs || xcd / pl.span >= pl.pairs_per_round) return;
   }
-  (void)NT;
   const int z = pair % p.n_split;
   const int hg_all = pair / p.n_split;                 // kv head * groups + head group
   const int h = hg_all / groups, hg = hg_all - h * groups;
@@ -191,10 +194,10 @@ __global__ __launch_bounds__(64 * WAVES, 1) void prefill_attn_kernel(PrefillArgs
   const int n_q = min(kToks, p.n_tok - t0);
   const int qh = h * gqa + hg * WAVES + wave;
 
-  // tiles: history rows [0, h_pad) then (unless every key comes from the
-  // cache) the chunk's own keys [0, t0 + n_q)
-  const int th = p.h_pad / kKeys;
-  const int tc = FROM_CACHE ? 0 : (t0 + n_q + kKeys - 1) / kKeys;
+  // 32-key tiles: history rows [0, h_pad) then (unless every key comes from
+  // the cache) the chunk's own keys [0, t0 + n_q)
+  const int th = p.h_pad / kTK;
+  const int tc = FROM_CACHE ? 0 : (t0 + n_q + kTK - 1) / kTK;
   const int total = th + tc;
   const int tps = (total + p.n_split - 1) / p.n_split;
   const int tlo = min(total, z * tps), thi = min(total, tlo + tps);
@@ -215,117 +218,110 @@ __global__ __launch_bounds__(64 * WAVES, 1) void prefill_attn_kernel(PrefillArgs
             h8_t, __builtin_amdgcn_raw_buffer_load_b128(rq, base + (b * 128 + 16 * s + 8 * hh) * 2, 0, 0));
   }
 
+  // ---- tile loads: one buffer resource per tensor of this kv head (kx rows
+  // and vt tiles share the head stride), the tile offset in the scalar offset;
+  // 16 loads of 1 KB per tensor and tile, spread over the waves (with 3 waves
+  // the last load of wave 2 repeats load 15, which writes the same bytes).
+  const uint32_t head_bytes = (uint32_t)(rows * kHD * 2);
+  const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint16_t*>(p.kx) + (long)h * rows * kHD, 0, head_bytes, kBufferRsrcWord3);
+  const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint16_t*>(p.vt) + (long)h * rows * kHD, 0, head_bytes, kBufferRsrcWord3);
+  constexpr int kLoads = (16 + WAVES - 1) / WAVES;
+  // load j: key rows 2j, 2j+1 (lane l: row 2j + l/32, slot l%32) and value
+  // dims 16j .. 16j+15 (lane l: dim 16j + l/4, slot l%4); the value offset
+  // within the run does not depend on j
+  const int v_off = (lane >> 2) * (kTK * 2) + (((lane & 3) ^ ((lane >> 4) & 3)) * 16);
+  auto issue = [&](int ti, int buf) {
+    uint8_t* base = lds + buf * kBufBytes;
+#pragma unroll
+    for (int jj = 0; jj < kLoads; jj++) {
+      const int j = min(wave + jj * WAVES, 15);
+      const int row = 2 * j + (lane >> 5);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rk, (lds_void_t*)(base + j * 1024), 16,
+                                               (lane >> 5) * (kHD * 2) + (((lane & 31) ^ (row & 15)) * 16),
+                                               ti * kKBytes + j * 1024, 0, 0);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rv, (lds_void_t*)(base + kKBytes + j * 1024), 16, v_off,
+                                               ti * kVBytes + j * 1024, 0, 0);
+    }
+  };
+
   f16x_t acc[8];
 #pragma unroll
   for (int d = 0; d < 8; d++) acc[d] = f16x_t{};
   float m2 = -INFINITY, lsum = 0.0f;
   const int t_abs = t0 + tok;        // this lane's token index in the chunk
+  const int lim_hist = FROM_CACHE ? min(p.hist, p.start_pos + t_abs + 1) : p.hist;
+  const float sl = p.scale_log2;
+  // The weights are taken against a reference maximum m2 that is raised (and
+  // the accumulators rescaled) only when some row's maximum exceeds it by
+  // more than kSlack (log2 units): the weights stay below 2^kSlack, inside fp16.
+  constexpr float kSlack = 12.0f;
+  // operand addresses (bytes within a tile buffer) of this lane
+  const int k_row = tok * (kHD * 2);
+  const int v_row = tok * (kTK * 2);
 
-  // Tile ti into buffer `buf`: 64 direct loads of 1 KB (32 for the keys, two
-  // rows each; 32 for the values, eight dim rows each), spread over the waves.
-  auto issue_tile = [&](int ti, int buf) {
-    uint8_t* base = lds + buf * kBufBytes;
-    const uint16_t* ksrc = p.kx + ((long)h * rows + (long)ti * kKeys) * kHD;
-    const uint16_t* vsrc = p.vt + ((long)h * (rows / kKeys) + ti) * kHD * kKeys;
-    for (int inst = wave; inst < 64; inst += WAVES) {
-      const uint16_t* src;
-      if (inst < 32) {
-        const int row = 2 * inst + (lane >> 5), c = (lane & 31) ^ (row & 31);
-        src = ksrc + row * kHD + c * 8;
-      } else {
-        const int row = 8 * (inst - 32) + (lane >> 3), c = (lane & 7) ^ (row & 7);
-        src = vsrc + row * kKeys + c * 8;
-      }
-      __builtin_amdgcn_global_load_lds(src, (lds_void_t*)(base + inst * 1024), 16, 0, 0);
-    }
-  };
-  if (tlo < thi) issue_tile(tlo, 0);
-
+  if (tlo < thi) issue(tlo, 0);
   for (int ti = tlo; ti < thi; ti++) {
-    const bool cached = ti < th;
     const int buf = (ti - tlo) & 1;
-    // tile ti has landed (every wave waits for its own loads, then the
+    // visible keys of this tile for this lane: tile key index < lim
+    const int lim = ti < th ? lim_hist - ti * kTK : t_abs + 1 - (ti - th) * kTK;
+    // tile ti has landed (each wave waits for its own loads, then the
     // barrier), and every wave is done with the other buffer's tile
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
-    if (ti + 1 < thi) issue_tile(ti + 1, buf ^ 1);
+    if (ti + 1 < thi) issue(ti + 1, buf ^ 1);
     const uint8_t* kbuf = lds + buf * kBufBytes;
     const uint8_t* vbuf = kbuf + kKBytes;
-    __builtin_amdgcn_sched_barrier(0);
 
-    // key index of tile key `key`: a history row (visible to every token when
-    // below `hist`; in verify mode causal within the block), or chunk token u
-    const int k0 = cached ? ti * kKeys : (ti - th) * kKeys;
-    const bool dense = cached ? (k0 + kKeys <= p.hist &&
-                                 (!FROM_CACHE || k0 + kKeys - 1 <= p.start_pos + t0))
-                              : (k0 + kKeys - 1 <= t0);
+    // ---- scores S^T = K Q^T: row = key 8(v/4) + 4hh + v%4, column = token
+    f16x_t sd = f16x_t{};
 #pragma unroll
-    for (int kt = 0; kt < 2; kt++) {
-      __builtin_amdgcn_sched_barrier(0);
-      // ---- scores S^T = K Q^T: row = key kt*32 + 8(v/4) + 4hh + v%4, col = token
-      f16x_t sd = f16x_t{};
+    for (int b = 0; b < 2; b++)
 #pragma unroll
-      for (int b = 0; b < 2; b++) {
-        const int krow = kt * 32 + tok;   // krow & 31 == tok
-        const uint8_t* arow = kbuf + krow * (kHD * 2);
-#pragma unroll
-        for (int s = 0; s < 8; s++) {
-          const int c = b * 16 + hh + 2 * s;   // 16-byte chunk of dims b*128 + 8hh + 16s
-          const h8_t a = *reinterpret_cast<const h8_t*>(arow + ((c ^ tok) * 16));
-          sd = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, qb[b][s], sd, 0, 0, 0);
-        }
+      for (int s = 0; s < 8; s++) {
+        // logical chunk b*16 + hh + 2s (dims b*128 + 8hh + 16s) of key row tok
+        const int slot = b * 16 + ((hh + 2 * s) ^ (tok & 15));
+        const h8_t a = *reinterpret_cast<const h8_t*>(kbuf + k_row + slot * 16);
+        sd = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, qb[b][s], sd, 0, 0, 0);
       }
-      float sc[16];
+    float mt = -INFINITY;
 #pragma unroll
-      for (int a = 0; a < 4; a++) {
+    for (int v = 0; v < 16; v++) {
+      const int key = 8 * (v >> 2) + 4 * hh + (v & 3);
+      const float sv = key < lim ? sd[v] * sl : -INFINITY;
+      sd[v] = sv;
+      mt = fmaxf(mt, sv);
+    }
+    {
+      const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(mt), __float_as_uint(mt), false, false);
+      mt = fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1]));
+    }
+    if (__builtin_amdgcn_ballot_w64(mt > m2 + kSlack) != 0) {
+      const float mn = fmaxf(m2, mt);
+      const float corr = (mn == -INFINITY) ? 1.0f : __builtin_amdgcn_exp2f(m2 - mn);
+      lsum *= corr;
 #pragma unroll
-        for (int c = 0; c < 4; c++) {
-          float sv = sd[4 * a + c] * p.scale_log2;
-          if (!dense) {
-            const int key = k0 + kt * 32 + 8 * a + 4 * hh + c;
-            const bool vis = cached ? (key < p.hist) & (!FROM_CACHE || key <= p.start_pos + t_abs)
-                                    : (key <= t_abs);
-            sv = vis ? sv : -INFINITY;
-          }
-          sc[4 * a + c] = sv;
-        }
-      }
-      // ---- online softmax of this lane's row (partner lane: lane ^ 32)
-      float mt = sc[0];
+      for (int d = 0; d < 8; d++) acc[d] *= corr;
+      m2 = mn;
+    }
+    const float msafe = (m2 == -INFINITY) ? 0.0f : m2;
+    // ---- values O^T += V^T P^T.  B operand sg: the weights v = 8sg .. 8sg+7
+    // (keys 16sg + 8hh .. in value order), fp16; the row sum takes them as used.
 #pragma unroll
-      for (int v = 1; v < 16; v++) mt = fmaxf(mt, sc[v]);
-      {
-        const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(mt), __float_as_uint(mt), false, false);
-        mt = fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1]));
-      }
-      // The accumulators are rescaled only on steps where some row's maximum
-      // grows (a wave-uniform branch, rare after the first tiles).
-      if (__builtin_amdgcn_ballot_w64(mt > m2) != 0) {
-        const float mn = fmaxf(m2, mt);
-        const float corr = (mn == -INFINITY) ? 1.0f : __builtin_amdgcn_exp2f(m2 - mn);
-        lsum *= corr;
+    for (int sg = 0; sg < 2; sg++) {
+      h8_t pb;
 #pragma unroll
-        for (int d = 0; d < 8; d++) acc[d] *= corr;
-        m2 = mn;
-      }
-      const float msafe = (m2 == -INFINITY) ? 0.0f : m2;
+      for (int i = 0; i < 8; i++) pb[i] = (_Float16)__builtin_amdgcn_exp2f(sd[8 * sg + i] - msafe);
 #pragma unroll
-      for (int v = 0; v < 16; v++) {
-        sc[v] = __builtin_amdgcn_exp2f(sc[v] - msafe);
-        lsum += sc[v];
-      }
-      // ---- values O^T += V^T P^T.  B operand sg: the probabilities v = 8sg .. 8sg+7.
+      for (int i = 0; i < 4; i++)
+        lsum = __builtin_amdgcn_fdot2(h2_t{pb[2 * i], pb[2 * i + 1]}, h2_t{(_Float16)1.0f, (_Float16)1.0f},
+                                      lsum, false);
+      const int slot = (2 * sg + hh) ^ ((tok >> 2) & 3);
 #pragma unroll
-      for (int sg = 0; sg < 2; sg++) {
-        h8_t pb;
-#pragma unroll
-        for (int i = 0; i < 8; i++) pb[i] = (_Float16)sc[8 * sg + i];
-#pragma unroll
-        for (int d = 0; d < 8; d++) {
-          const int vrow = d * 32 + tok, c = kt * 4 + 2 * sg + hh;   // keys kt*32 + 16sg + 8hh ..
-          const h8_t a = *reinterpret_cast<const h8_t*>(vbuf + vrow * (kKeys * 2) + ((c ^ (tok & 7)) * 16));
-          acc[d] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, pb, acc[d], 0, 0, 0);
-        }
+      for (int d = 0; d < 8; d++) {
+        const h8_t a = *reinterpret_cast<const h8_t*>(vbuf + d * 32 * (kTK * 2) + v_row + slot * 16);
+        acc[d] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, pb, acc[d], 0, 0, 0);
       }
     }
   }
@@ -396,7 +392,7 @@ PrefillGeom prefill_geom(int num_q, int num_kv, int n_tok, int start_pos) {
   const int qtiles = (n_tok + kToks - 1) / kToks;
   const int wgs = num_kv * (num_q / num_kv == 6 ? 2 : 1) * qtiles;
   const int tiles = g.h_pad / kKeys + g.n_pad / kKeys;
-  int ns = (256 + wgs - 1) / wgs;                 // fill 256 CUs
+  int ns = (512 + wgs - 1) / wgs;                 // two workgroups on each of 256 CUs
   ns = std::min(ns, std::max(1, tiles / 8));      // at least ~8 tiles per split
   g.n_split = std::max(1, ns);
   size_t off = 0;
