@@ -274,22 +274,35 @@ __global__ __launch_bounds__(64 * WAVES, 2) void prefill_attn_kernel(PrefillArgs
     const uint8_t* kbuf = lds + buf * kBufBytes;
     const uint8_t* vbuf = kbuf + kKBytes;
 
-    // ---- scores S^T = K Q^T: row = key 8(v/4) + 4hh + v%4, column = token
+    // ---- scores S^T = K Q^T: row = key 8(v/4) + 4hh + v%4, column = token.
+    // Operand i (block i / 8, slice i % 8) is the logical chunk
+    // 16(i/8) + hh + 2(i%8) (dims 128(i/8) + 8hh + 16(i%8)) of key row tok;
+    // four reads stay in flight ahead of the MFMAs.
+    auto k_operand = [&](int i) {
+      const int slot = (i >> 3) * 16 + ((hh + 2 * (i & 7)) ^ (tok & 15));
+      return *reinterpret_cast<const h8_t*>(kbuf + k_row + slot * 16);
+    };
     f16x_t sd = f16x_t{};
+    h8_t ka[4];
 #pragma unroll
-    for (int b = 0; b < 2; b++)
+    for (int i = 0; i < 4; i++) ka[i] = k_operand(i);
 #pragma unroll
-      for (int s = 0; s < 8; s++) {
-        // logical chunk b*16 + hh + 2s (dims b*128 + 8hh + 16s) of key row tok
-        const int slot = b * 16 + ((hh + 2 * s) ^ (tok & 15));
-        const h8_t a = *reinterpret_cast<const h8_t*>(kbuf + k_row + slot * 16);
-        sd = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, qb[b][s], sd, 0, 0, 0);
-      }
+    for (int i = 0; i < 16; i++) {
+      sd = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka[i & 3], qb[i >> 3][i & 7], sd, 0, 0, 0);
+      if (i + 4 < 16) ka[i & 3] = k_operand(i + 4);
+    }
+    __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);     // four reads ahead
+#pragma unroll
+    for (int i = 0; i < 12; i++) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // MFMA i
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);   // read i + 4
+    }
+    __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
     float mt = -INFINITY;
+    const int lim_h = lim - 4 * hh;
 #pragma unroll
     for (int v = 0; v < 16; v++) {
-      const int key = 8 * (v >> 2) + 4 * hh + (v & 3);
-      const float sv = key < lim ? sd[v] * sl : -INFINITY;
+      const float sv = 8 * (v >> 2) + (v & 3) < lim_h ? sd[v] * sl : -INFINITY;
       sd[v] = sv;
       mt = fmaxf(mt, sv);
     }
