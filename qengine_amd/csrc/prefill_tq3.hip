@@ -252,7 +252,16 @@ __global__ __launch_bounds__(64 * WAVES, 2) void prefill_attn_kernel(PrefillArgs
   float m2 = -INFINITY, lsum = 0.0f;
   const int t_abs = t0 + tok;        // this lane's token index in the chunk
   const int lim_hist = FROM_CACHE ? min(p.hist, p.start_pos + t_abs + 1) : p.hist;
-  const float sl = p.scale_log2;
+  // a negative scale is carried by the query (an exact fp16 sign flip), so
+  // that the row maximum of the raw scores gives the maximum of the scaled ones
+  float sl = p.scale_log2;
+  if (sl < 0.0f) {
+#pragma unroll
+    for (int b = 0; b < 2; b++)
+#pragma unroll
+      for (int s = 0; s < 8; s++) qb[b][s] = -qb[b][s];
+    sl = -sl;
+  }
   // The weights are taken against a reference maximum m2 that is raised (and
   // the accumulators rescaled) only when some row's maximum exceeds it by
   // more than kSlack (log2 units): the weights stay below 2^kSlack, inside fp16.
@@ -298,17 +307,26 @@ __global__ __launch_bounds__(64 * WAVES, 2) void prefill_attn_kernel(PrefillArgs
       __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);   // read i + 4
     }
     __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
-    float mt = -INFINITY;
-    const int lim_h = lim - 4 * hh;
+    // Row maximum (scaled).  Tiles every row sees whole keep the raw scores
+    // (scaled inside the exponent); the others are scaled and masked here.
+    float mt = -INFINITY, sl_w;
+    if (__builtin_amdgcn_ballot_w64(lim < kTK) == 0) {
 #pragma unroll
-    for (int v = 0; v < 16; v++) {
-      const float sv = 8 * (v >> 2) + (v & 3) < lim_h ? sd[v] * sl : -INFINITY;
-      sd[v] = sv;
-      mt = fmaxf(mt, sv);
-    }
-    {
+      for (int v = 0; v < 16; v++) mt = fmaxf(mt, sd[v]);
+      const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(mt), __float_as_uint(mt), false, false);
+      mt = fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1])) * sl;
+      sl_w = sl;
+    } else {
+      const int lim_h = lim - 4 * hh;
+#pragma unroll
+      for (int v = 0; v < 16; v++) {
+        const float sv = 8 * (v >> 2) + (v & 3) < lim_h ? sd[v] * sl : -INFINITY;
+        sd[v] = sv;
+        mt = fmaxf(mt, sv);
+      }
       const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(mt), __float_as_uint(mt), false, false);
       mt = fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1]));
+      sl_w = 1.0f;
     }
     if (__builtin_amdgcn_ballot_w64(mt > m2 + kSlack) != 0) {
       const float mn = fmaxf(m2, mt);
@@ -325,7 +343,7 @@ __global__ __launch_bounds__(64 * WAVES, 2) void prefill_attn_kernel(PrefillArgs
     for (int sg = 0; sg < 2; sg++) {
       h8_t pb;
 #pragma unroll
-      for (int i = 0; i < 8; i++) pb[i] = (_Float16)__builtin_amdgcn_exp2f(sd[8 * sg + i] - msafe);
+      for (int i = 0; i < 8; i++) pb[i] = (_Float16)__builtin_amdgcn_exp2f(__builtin_fmaf(sd[8 * sg + i], sl_w, -msafe));
 #pragma unroll
       for (int i = 0; i < 4; i++)
         lsum = __builtin_amdgcn_fdot2(h2_t{pb[2 * i], pb[2 * i + 1]}, h2_t{(_Float16)1.0f, (_Float16)1.0f},
