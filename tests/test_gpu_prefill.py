@@ -94,6 +94,28 @@ def test_prefill_vs_oracle(dev, start_pos, n_tok, num_q):
     assert rel_err(got, ref) < TOL
 
 
+@pytest.mark.parametrize("scale,grow", [
+    (-1 / 16, False),   # negative scale (carried by the query's sign)
+    (0.0, False),       # uniform weights over the visible keys
+    (1.0, False),       # peaked weights: the running maximum moves by more than 2^12
+    (1 / 16, True),     # keys growing along the sequence: the maximum rises tile after tile
+])
+def test_prefill_scales_and_rescaling(dev, scale, grow):
+    num_q, num_kv, start_pos, n_tok = 16, 4, 700, 80
+    q, hk, hv, ck, cv = _inputs(29, start_pos, n_tok, num_q)
+    if grow:   # key magnitude rising 1x .. 6x over history and chunk
+        ramp = np.linspace(1.0, 6.0, start_pos + n_tok, dtype=np.float32)[:, None, None]
+        hk = (hk.astype(np.float32) * ramp[:start_pos]).astype(np.float16)
+        ck = (ck.astype(np.float32) * ramp[start_pos:]).astype(np.float16)
+    kb, vb = O.tq3_encode(hk), O.tq3_encode(hv)
+    got = _gpu(dev, q, kb, vb, ck, cv, num_q=num_q, num_kv=num_kv, start_pos=start_pos,
+               scale=scale)
+    k_all, v_all = _oracle_kv(kb, vb, ck, cv, num_kv)
+    ref = _oracle(q, k_all, v_all, num_q=num_q, num_kv=num_kv, start_pos=start_pos, scale=scale)
+    assert np.all(np.isfinite(got))
+    assert rel_err(got, ref) < TOL
+
+
 def test_prefill_vs_fp64(dev):
     """Independent fp64 softmax reference on the same fp16 key/value array."""
     num_q, num_kv, start_pos, n_tok, scale = 16, 4, 500, 24, 1 / 16
