@@ -432,6 +432,286 @@ __global__ __launch_bounds__(kAp2Threads, 3) void tq3_append2_kernel(
 }
 
 // ---------------------------------------------------------------------------
+// Append: a lane pair encodes two blocks.
+//
+// Lane l of a 64-block wave tile holds R1 = elements 0..63 of block l and
+// R2 = elements 64..127 of block l ^ 1 (16 KiB of fp16 per tile), loaded
+// straight into registers (lane l reads the 128-byte lines it needs; the 8
+// loads of a line are consecutive, so the line is fetched once).  No
+// prefetch registers: three waves per SIMD cover each other's load waits.
+// Per tile:
+//   - norm: the reference's sequential sum of block b runs over its first
+//     half in lane b (R1), then -- the partial handed over by DPP -- over its
+//     second half in lane b ^ 1 (R2).  Every chain step is useful: a lane runs
+//     128 steps for its 128 elements (a pair with one block would run 128 steps
+//     for 64 elements per lane);
+//   - scaling by the inverse norms with the random signs folded into the
+//     factors (R1: block l's factor, R2: block l ^ 1's);
+//   - WHT stages 1..32 in registers on R1 and on R2; stage 64 pairs element k
+//     of R1 in lane l with element k of R2 in lane l ^ 1 (both halves of block
+//     l): a DPP-sourced add and reverse subtract give a + b and a - b, so lane
+//     l then holds all 128 outputs of block l;
+//   - bins in the sign-folded form (kFoldQBits), codes words 0..5 from the
+//     first 64 outputs and 6..11 from the last 64; the lane writes its whole
+//     block (through LDS and coalesced dword stores when contiguous).
+// ---------------------------------------------------------------------------
+constexpr int kAp4Waves = 4;
+constexpr int kAp4Threads = 64 * kAp4Waves;
+constexpr int kAp4Tile = 64;                           // blocks per wave tile
+constexpr int kAp4WaveLdsDw = kAp4Tile * 13;           // output staging, 3328 B per wave
+
+// This lane's halves of a 64-block tile (blocks b0 .. b0+nb-1): h1 = fp16
+// elements 0..63 of block b0 + lane, h2 = elements 64..127 of block
+// b0 + (lane ^ 1).  Blocks past the last read zero (range-checked resource).
+// A DFK2 source (int8 rows, one fp16 scale per block) is dequantized here to
+// the reference's fp16 values.
+template <bool kDfk2>
+__device__ __forceinline__ void load_halves(uint32_t (&h1)[32], uint32_t (&h2)[32],
+                                            const uint4* __restrict__ in,
+                                            const uint16_t* __restrict__ sc, int b0, int nb,
+                                            int lane) {
+  if constexpr (kDfk2) {
+    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint4*>(in + (long)b0 * 8), 0, nb * 128, kBufferRsrcWord3);
+    const __amdgpu_buffer_rsrc_t rsc = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint16_t*>(sc + b0), 0, nb * 2, kBufferRsrcWord3);
+    u4_t c1[4], c2[4];
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+      c1[k] = __builtin_amdgcn_raw_buffer_load_b128(rs, lane * 128, 16 * k, 0);
+      c2[k] = __builtin_amdgcn_raw_buffer_load_b128(rs, (lane ^ 1) * 128 + 64, 16 * k, 0);
+    }
+    const float s1 = h2f(__builtin_amdgcn_raw_buffer_load_b16(rsc, lane * 2, 0, 0));
+    const float s2 = h2f(__builtin_amdgcn_raw_buffer_load_b16(rsc, (lane ^ 1) * 2, 0, 0));
+#pragma unroll
+    for (int k = 0; k < 4; k++)
+#pragma unroll
+      for (int w = 0; w < 4; w++) {
+        h1[8 * k + 2 * w] = dfk2_pair(c1[k][w], 0, s1);
+        h1[8 * k + 2 * w + 1] = dfk2_pair(c1[k][w], 2, s1);
+        h2[8 * k + 2 * w] = dfk2_pair(c2[k][w], 0, s2);
+        h2[8 * k + 2 * w + 1] = dfk2_pair(c2[k][w], 2, s2);
+      }
+  } else {
+    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint4*>(in + (long)b0 * 16), 0, nb * 256, kBufferRsrcWord3);
+#pragma unroll
+    for (int k = 0; k < 8; k++) {
+      const u4_t v = __builtin_amdgcn_raw_buffer_load_b128(rs, lane * 256, 16 * k, 0);
+      h1[4 * k] = v.x;
+      h1[4 * k + 1] = v.y;
+      h1[4 * k + 2] = v.z;
+      h1[4 * k + 3] = v.w;
+    }
+#pragma unroll
+    for (int k = 0; k < 8; k++) {
+      const u4_t v = __builtin_amdgcn_raw_buffer_load_b128(rs, (lane ^ 1) * 256 + 128, 16 * k, 0);
+      h2[4 * k] = v.x;
+      h2[4 * k + 1] = v.y;
+      h2[4 * k + 2] = v.z;
+      h2[4 * k + 3] = v.w;
+    }
+  }
+}
+
+// Stage 64 of the WHT for elements k0 .. k0+7 of a block whose first half is
+// a (this lane) and second half b (the other lane of the pair, read through
+// DPP quad_perm [1,0,3,2]): lo = a + b, hi = a - b, the reference's two
+// roundings.  A DPP read of a VGPR needs two wait states after the VALU write
+// of that VGPR: the s_nop provides them, and nothing inside the block writes
+// a register that a later instruction of it reads through DPP.
+__device__ __forceinline__ void pair_stage8(const float (&a)[64], const float (&b)[64],
+                                            float (&lo)[64], float (&hi)[64], int k0) {
+  asm volatile(
+      "s_nop 1\n\t"
+      "v_add_f32_dpp %0, %16, %24 quad_perm:[1,0,3,2] row_mask:0xf bank_mask:0xf\n\t"
+      "v_subrev_f32_dpp %8, %16, %24 quad_perm:[1,0,3,2] row_mask:0xf bank_mask:0xf\n\t"
+      "v_add_f32_dpp %1, %17, %25 quad_perm:[1,0,3,2] row_mask:0xf bank_mask:0xf\n\t"
+      "v_subrev_f32_dpp %9, %17, %25 quad_perm:[1,0,3,2] row_mask:0xf bank_mask:0xf\n\t"
+      "v_add_f32_dpp %2, %18, %26 quad_perm:[1,0,3,2] row_mask:0xf bank_mask:0xf\n\t"
+      "v_subrev_f32_dpp %10, %18, %26 quad_perm:[1,0,3,2] row_mask:0xf bank_mask:0xf\n\t"
+      "v_add_f32_dpp %3, %19, %27 quad_perm:[1,0,3,2] row_mask:0xf bank_mask:0xf\n\t"
+      "v_subrev_f32_dpp %11, %19, %27 quad_perm:[1,0,3,2] row_mask:0xf bank_mask:0xf\n\t"
+      "v_add_f32_dpp %4, %20, %28 quad_perm:[1,0,3,2] row_mask:0xf bank_mask:0xf\n\t"
+      "v_subrev_f32_dpp %12, %20, %28 quad_perm:[1,0,3,2] row_mask:0xf bank_mask:0xf\n\t"
+      "v_add_f32_dpp %5, %21, %29 quad_perm:[1,0,3,2] row_mask:0xf bank_mask:0xf\n\t"
+      "v_subrev_f32_dpp %13, %21, %29 quad_perm:[1,0,3,2] row_mask:0xf bank_mask:0xf\n\t"
+      "v_add_f32_dpp %6, %22, %30 quad_perm:[1,0,3,2] row_mask:0xf bank_mask:0xf\n\t"
+      "v_subrev_f32_dpp %14, %22, %30 quad_perm:[1,0,3,2] row_mask:0xf bank_mask:0xf\n\t"
+      "v_add_f32_dpp %7, %23, %31 quad_perm:[1,0,3,2] row_mask:0xf bank_mask:0xf\n\t"
+      "v_subrev_f32_dpp %15, %23, %31 quad_perm:[1,0,3,2] row_mask:0xf bank_mask:0xf"
+      : "=&v"(lo[k0]), "=&v"(lo[k0 + 1]), "=&v"(lo[k0 + 2]), "=&v"(lo[k0 + 3]), "=&v"(lo[k0 + 4]),
+        "=&v"(lo[k0 + 5]), "=&v"(lo[k0 + 6]), "=&v"(lo[k0 + 7]), "=&v"(hi[k0]), "=&v"(hi[k0 + 1]),
+        "=&v"(hi[k0 + 2]), "=&v"(hi[k0 + 3]), "=&v"(hi[k0 + 4]), "=&v"(hi[k0 + 5]), "=&v"(hi[k0 + 6]),
+        "=&v"(hi[k0 + 7])
+      : "v"(b[k0]), "v"(b[k0 + 1]), "v"(b[k0 + 2]), "v"(b[k0 + 3]), "v"(b[k0 + 4]), "v"(b[k0 + 5]),
+        "v"(b[k0 + 6]), "v"(b[k0 + 7]), "v"(a[k0]), "v"(a[k0 + 1]), "v"(a[k0 + 2]), "v"(a[k0 + 3]),
+        "v"(a[k0 + 4]), "v"(a[k0 + 5]), "v"(a[k0 + 6]), "v"(a[k0 + 7]));
+}
+
+// Codes of 64 consecutive transformed elements (one half of a block) into
+// the 6 words of that half's 192-bit stream: chains k = 63..32 (words 3..5)
+// and k = 31..0 (words 0..2), then the sign fix.
+__device__ __forceinline__ void bin_half(const float (&x)[64], const uint32_t (&q)[3],
+                                         uint32_t (&acc)[6]) {
+#pragma unroll
+  for (int w = 0; w < 6; w++) acc[w] = 0u;
+#pragma unroll
+  for (int i = 0; i < 32; i++) {
+    const int ka = 63 - i, kb = 31 - i;
+    const float ya = __builtin_fmaf(x[ka], -kFoldA, __builtin_fabsf(x[ka]));
+    const float yb = __builtin_fmaf(x[kb], -kFoldA, __builtin_fabsf(x[kb]));
+    uint64_t pa[2], pb[2];
+    fold_planes2(ya, yb, q, pa, pb);
+    shift_in_sign(acc[(3 * ka + 2) >> 5], ya);
+    shift_in_sign(acc[(3 * kb + 2) >> 5], yb);
+    shift_in(acc[(3 * ka + 1) >> 5], pa[0]);
+    shift_in(acc[(3 * kb + 1) >> 5], pb[0]);
+    shift_in(acc[(3 * ka) >> 5], pa[1]);
+    shift_in(acc[(3 * kb) >> 5], pb[1]);
+  }
+  sign_fix<0, 3>(acc);
+  sign_fix<3, 3>(acc + 3);
+}
+
+template <bool kDfk2>
+__global__ __launch_bounds__(kAp4Threads, 3) void tq3_append4_kernel(
+    const uint4* __restrict__ in0, uint32_t* __restrict__ out0, const uint4* __restrict__ in1,
+    uint32_t* __restrict__ out1, int n_blocks, int n_tensors, PagedRows pr,
+    const uint16_t* __restrict__ sc0, const uint16_t* __restrict__ sc1) {
+  __shared__ uint32_t lds[kAp4Waves * kAp4WaveLdsDw];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  uint32_t* wl = lds + wave * kAp4WaveLdsDw;
+  // 32-bit tile bookkeeping (n_blocks < 2^31, so tiles * n_tensors < 2^27).
+  // Work item t is tile t % tiles of tensor t / tiles; the wave's items are
+  // t0, t0 + stride, ...: the tile and tensor advance without a division.
+  const int tiles = (n_blocks + kAp4Tile - 1) / kAp4Tile;
+  const int total = tiles * n_tensors;
+  const int stride = (int)gridDim.x * kAp4Waves;
+  int t = (int)blockIdx.x * kAp4Waves + wave;
+  if (t >= total) return;
+  int tile = t, tensor = 0;
+  while (tile >= tiles) { tile -= tiles; tensor++; }
+  const int s_tiles = stride % tiles, s_tensors = stride / tiles;   // scalar, once
+
+  uint32_t q[3];
+#pragma unroll
+  for (int k = 0; k < 3; k++) q[k] = __builtin_amdgcn_readfirstlane(kFoldQBits[k]);
+
+  for (;;) {
+    uint32_t* __restrict__ out = tensor ? out1 : out0;
+    const int b0 = tile * kAp4Tile;
+    const int nb = min(kAp4Tile, n_blocks - b0);
+    int tile_n = tile + s_tiles, tensor_n = tensor + s_tensors;
+    if (tile_n >= tiles) { tile_n -= tiles; tensor_n++; }
+    const bool more = tensor_n < n_tensors;
+
+    // R1 = first half of block `lane`, R2 = second half of block lane ^ 1
+    uint32_t h1[32], h2[32];
+    load_halves<kDfk2>(h1, h2, tensor ? in1 : in0, tensor ? sc1 : sc0, b0, nb, lane);
+    // norm (reference order): block lane's chain over R1 here, handed to the
+    // other lane of the pair, which continues over its R2
+    float n1 = 0.0f;
+#pragma unroll
+    for (int k = 0; k < 32; k++) {
+      const float lo = h2f(h1[k] & 0xffffu), hi = h2f(h1[k] >> 16);
+      n1 = __builtin_fmaf(lo, lo, n1);
+      n1 = __builtin_fmaf(hi, hi, n1);
+    }
+    float n2 = lane_dpp<0xB1>(n1);   // quad_perm [1,0,3,2]: block lane ^ 1's first-half partial
+#pragma unroll
+    for (int k = 0; k < 32; k++) {
+      const float lo = h2f(h2[k] & 0xffffu), hi = h2f(h2[k] >> 16);
+      n2 = __builtin_fmaf(lo, lo, n2);
+      n2 = __builtin_fmaf(hi, hi, n2);
+    }
+    const float norm2 = __builtin_sqrtf(n2);   // block lane ^ 1
+    const float inv2 = 1.0f / norm2;
+    const float norm1 = lane_dpp<0xB1>(norm2);   // block lane
+    const float inv1 = lane_dpp<0xB1>(inv2);
+    // x * inv * sign (turboquant.cuh:141-149; the sign multiply is exact, so
+    // it folds into the factor)
+    float x1[64], x2[64];
+#pragma unroll
+    for (int e = 0; e < 64; e++) {
+      x1[e] = __builtin_fmaf(h2f((e & 1) ? h1[e >> 1] >> 16 : h1[e >> 1] & 0xffffu),
+                             sign_pos(e) ? inv1 : -inv1, 0.0f);
+      x2[e] = __builtin_fmaf(h2f((e & 1) ? h2[e >> 1] >> 16 : h2[e >> 1] & 0xffffu),
+                             sign_pos(64 + e) ? inv2 : -inv2, 0.0f);
+    }
+    // WHT stages 1 .. 32 (turboquant.cuh:50-59) on each half, then stage 64
+    // across the pair
+#pragma unroll
+    for (int step = 1; step < 64; step <<= 1) {
+#pragma unroll
+      for (int i = 0; i < 64; i += 2 * step) {
+#pragma unroll
+        for (int j = i; j < i + step; j++) {
+          const float a = x1[j], b = x1[j + step];
+          x1[j] = a + b;
+          x1[j + step] = a - b;
+          const float c = x2[j], d = x2[j + step];
+          x2[j] = c + d;
+          x2[j + step] = c - d;
+        }
+      }
+    }
+    float y1[64], y2[64];
+#pragma unroll
+    for (int k = 0; k < 64; k += 8) pair_stage8(x1, x2, y1, y2, k);
+
+    // bins of block `lane`: words 0..5 from outputs 0..63, 6..11 from 64..127
+    uint32_t acc[12];
+    {
+      uint32_t a0[6], a1[6];
+      bin_half(y1, q, a0);
+      bin_half(y2, q, a1);
+      const bool keep = norm1 >= 1e-10f && norm1 < __builtin_inff();
+#pragma unroll
+      for (int w = 0; w < 6; w++) {
+        acc[w] = keep ? a0[w] : 0u;
+        acc[6 + w] = keep ? a1[w] : 0u;
+      }
+    }
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "workgroup");
+
+    if (pr.block_tables != nullptr) {
+      // paged: each lane stores its block at the block's row
+      if (lane < nb) {
+        const long ob = paged_block(pr, (long)b0 + lane);
+        if (ob >= 0) {
+          uint32_t* dst = out + ob * 13;
+          dst[0] = __float_as_uint(norm1);
+#pragma unroll
+          for (int w = 0; w < 12; w++) dst[1 + w] = acc[w];
+        }
+      }
+    } else {
+      // 4. stage the tile's 64 x 13 dwords, then store them contiguously
+      uint32_t* ob = wl + lane * 13;
+      ob[0] = __float_as_uint(norm1);
+#pragma unroll
+      for (int w = 0; w < 12; w++) ob[1 + w] = acc[w];
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "workgroup");
+      // the resource spans the tile's nb * 52 bytes: stores past it are dropped
+      const __amdgpu_buffer_rsrc_t rd = __builtin_amdgcn_make_buffer_rsrc(
+          out + (long)b0 * 13, 0, nb * 52, kBufferRsrcWord3);
+#pragma unroll
+      for (int j = 0; j < 13; j++)
+        __builtin_amdgcn_raw_buffer_store_b32(wl[j * 64 + lane], rd, lane * 4, j * 256, 0);
+    }
+    if (!more) break;
+    tile = tile_n;
+    tensor = tensor_n;
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "workgroup");
+  }
+}
+
+// ---------------------------------------------------------------------------
 // Dequant (turboquant.cuh:169-200): half(((H*c)*rs)*sign*norm)
 // ---------------------------------------------------------------------------
 __global__ __launch_bounds__(kCodecThreads) void tq3_dequant_kernel(
@@ -510,7 +790,7 @@ __global__ __launch_bounds__(kCodecThreads) void tq3_dequant_kernel(
 hipError_t launch_tq3_append(const void* in0, void* out0, const void* in1, void* out1,
                              int n_blocks, int n_tensors, hipStream_t stream,
                              const PagedRows* paged, const uint16_t* sc0, const uint16_t* sc1) {
-  // Persistent grid: two workgroups (8 waves) per CU, fewer when the work
+  // Persistent grid: three workgroups (12 waves) per CU, fewer when the work
   // list is shorter.
   static std::atomic<int> cus[64];
   int dev = 0;
@@ -524,18 +804,18 @@ hipError_t launch_tq3_append(const void* in0, void* out0, const void* in1, void*
     n_cu = n_cu > 0 ? n_cu : 1;
     cus[dev].store(n_cu, std::memory_order_relaxed);
   }
-  const long tiles = ((long)n_blocks + kAp2Tile - 1) / kAp2Tile * n_tensors;
-  const long wgs_needed = (tiles + kAp2Waves - 1) / kAp2Waves;
+  const long tiles = ((long)n_blocks + kAp4Tile - 1) / kAp4Tile * n_tensors;
+  const long wgs_needed = (tiles + kAp4Waves - 1) / kAp4Waves;
   const int grid = (int)std::min<long>(wgs_needed, 3L * n_cu);
   if (grid == 0) return hipSuccess;
   const PagedRows pr = paged ? *paged : PagedRows{};
   if (sc0 != nullptr)
-    hipLaunchKernelGGL(tq3_append2_kernel<true>, dim3(grid), dim3(kAp2Threads), 0, stream,
+    hipLaunchKernelGGL(tq3_append4_kernel<true>, dim3(grid), dim3(kAp4Threads), 0, stream,
                        static_cast<const uint4*>(in0), static_cast<uint32_t*>(out0),
                        static_cast<const uint4*>(in1), static_cast<uint32_t*>(out1), n_blocks,
                        n_tensors, pr, sc0, sc1);
   else
-    hipLaunchKernelGGL(tq3_append2_kernel<false>, dim3(grid), dim3(kAp2Threads), 0, stream,
+    hipLaunchKernelGGL(tq3_append4_kernel<false>, dim3(grid), dim3(kAp4Threads), 0, stream,
                        static_cast<const uint4*>(in0), static_cast<uint32_t*>(out0),
                        static_cast<const uint4*>(in1), static_cast<uint32_t*>(out1), n_blocks,
                        n_tensors, pr, nullptr, nullptr);
