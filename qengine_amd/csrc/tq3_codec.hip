@@ -2,20 +2,20 @@
 //
 // Reference arithmetic: turboquant.cuh:112-165 (encode) and 169-200 (decode).
 //
-// Append layout on the GPU: two lanes own one 128-element block (64
-// elements each).  Waves are persistent: each takes 32-block tiles (8 KiB of
-// fp16) in turn, with the coalesced 16-byte buffer loads of its next tile in
-// flight into registers while it encodes the current one.  A tile passes
-// through LDS at a 272-byte pitch (bank-conflict-free 16-byte reads); each
-// lane then runs its part of the reference's sequential norm, the unit
-// scaling with the random signs, and the butterfly WHT in registers (the last
-// stage across the lane pair through DPP), bins the result in a sign-folded
-// form that reproduces binning fl(w * rs) exactly, and the wave writes its
-// 32 x 52-byte output through an LDS staging area with dword stores that
-// cover whole cache lines.  Every float operation that feeds a code or a norm
-// is the same single-rounding IEEE operation in the same order as the
-// reference, so codes and norms are bit-identical.  The dequant kernel keeps
-// one lane per block.
+// Append layout on the GPU: a lane pair encodes two 128-element blocks; lane
+// l of a 64-block wave tile holds the first half of block l and the second
+// half of block l ^ 1, loaded straight into registers.  Waves are persistent
+// (three per SIMD) and take 64-block tiles in turn.  Each lane runs the
+// reference's sequential norm over its first half, hands the partial to the
+// other lane of the pair, which continues over its second half; then the
+// unit scaling with the random signs and the butterfly WHT in registers (the
+// last stage across the lane pair through DPP, after which lane l holds all
+// of block l), bins the result in a sign-folded form that reproduces binning
+// fl(w * rs) exactly, and the wave writes its 64 x 52-byte output through an
+// LDS staging area with dword stores that cover whole cache lines.  Every
+// float operation that feeds a code or a norm is the same single-rounding
+// IEEE operation in the same order as the reference, so codes and norms are
+// bit-identical.  The dequant kernel keeps one lane per block.
 #include <algorithm>
 #include <atomic>
 
@@ -127,73 +127,6 @@ __device__ __forceinline__ long paged_block(const PagedRows& pr, long i) {
   return row * pr.blocks_per_row + j;
 }
 
-// ---------------------------------------------------------------------------
-// Append: two lanes per block.
-//
-// Lane l holds half h = l & 1 (elements 64h .. 64h+63) of block l >> 1 of a
-// 32-block wave tile (8 KiB of fp16), which halves the registers a lane needs
-// (64 floats instead of 128) and lets four waves share a SIMD.  Per tile:
-//   - the tile's prefetched pieces go to LDS; each lane reads its half back;
-//   - norm: the reference's sequential sum over all 128 squares.  Both lanes
-//     run the chain over their own 64 elements; the odd lane then runs it
-//     again starting from its even partner's partial (DPP), and the full sum
-//     goes back to the even lane;
-//   - scaling by the inverse norm with the random signs folded into the
-//     factor;
-//   - WHT stages 1..32 in registers; stage 64 pairs element k of the even
-//     lane with element k of the odd lane: a DPP-sourced FMA gives a + b in
-//     the even lane and b - a = -(a - b) in the odd lane, which carries its
-//     outputs negated;
-//   - bins in the sign-folded form (kFoldQBits); the negated lane folds with
-//     +A instead of -A, which gives the same y;
-//   - the even lane writes the norm and code words 0..5, the odd lane words
-//     6..11, through LDS and coalesced dword stores.
-// ---------------------------------------------------------------------------
-constexpr int kAp2Waves = 4;
-constexpr int kAp2Threads = 64 * kAp2Waves;
-constexpr int kAp2Tile = 32;                           // blocks per wave tile
-constexpr int kAp2WaveLdsDw = kAp2Tile * kInPitchDw;   // 8704 B per wave
-
-// 8 coalesced 16-byte loads of one 32-block tile (blocks b0 .. b0+nb-1);
-// chunk j*64+lane is piece (lane & 15) of block 4j + (lane >> 4).  Pieces
-// past the last block read zero (range-checked resource).
-__device__ __forceinline__ void load_tile32(uint32_t (&pre)[32], const uint4* __restrict__ in,
-                                            int b0, int nb, int lane) {
-  const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
-      const_cast<uint4*>(in + (long)b0 * 16), 0, nb * 256, kBufferRsrcWord3);
-#pragma unroll
-  for (int j = 0; j < 8; j++) {
-    const u4_t v = __builtin_amdgcn_raw_buffer_load_b128(rs, lane * 16, j * 1024, 0);
-    pre[4 * j] = v.x;
-    pre[4 * j + 1] = v.y;
-    pre[4 * j + 2] = v.z;
-    pre[4 * j + 3] = v.w;
-  }
-}
-
-// DFK2 source (int8 rows with one fp16 scale per 128 elements, i.e. per TQ3
-// block): 4 coalesced 16-byte loads of the tile's int8 codes -- chunk
-// j*64+lane is piece (lane & 7) (16 elements) of block 8j + (lane >> 3) --
-// and that block's scale in the high half of pre[16 + j].  Past the last
-// block the loads read zero.
-__device__ __forceinline__ void load_tile32_dfk2(uint32_t (&pre)[32], const uint4* __restrict__ in,
-                                                 const uint16_t* __restrict__ sc, int b0, int nb,
-                                                 int lane) {
-  const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
-      const_cast<uint4*>(in + (long)b0 * 8), 0, nb * 128, kBufferRsrcWord3);
-  const __amdgpu_buffer_rsrc_t rsc = __builtin_amdgcn_make_buffer_rsrc(
-      const_cast<uint16_t*>(sc + b0), 0, nb * 2, kBufferRsrcWord3);
-#pragma unroll
-  for (int j = 0; j < 4; j++) {
-    const u4_t v = __builtin_amdgcn_raw_buffer_load_b128(rs, lane * 16, j * 1024, 0);
-    pre[4 * j] = v.x;
-    pre[4 * j + 1] = v.y;
-    pre[4 * j + 2] = v.z;
-    pre[4 * j + 3] = v.w;
-    pre[16 + j] = __builtin_amdgcn_raw_buffer_load_b16(rsc, (8 * j + (lane >> 3)) * 2, 0, 0);
-  }
-}
-
 // dfki2_dequant_kernel's element (model.cuh:149-159): half(float(q) * float(s));
 // the product of an int8 and an fp16 is exact in fp32, then one rounding.
 __device__ __forceinline__ uint32_t dfk2_pair(uint32_t word, int byte, float s) {
@@ -207,228 +140,6 @@ __device__ __forceinline__ float lane_dpp(float v) {
   return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(
                                        __builtin_bit_cast(int, v), __builtin_bit_cast(int, v),
                                        CTRL, 0xf, 0xf, false));
-}
-
-// Stage 64 of the WHT for elements k0 .. k0+7: x = x + s * (partner lane's x)
-// in one DPP-sourced FMA each (quad_perm [1,0,3,2] reads the other lane of
-// the pair).  A DPP read of a VGPR needs two wait states after the VALU write
-// of that VGPR: the s_nop provides them, and no instruction inside the block
-// writes a register that a later one reads through DPP.
-template <int N>
-__device__ __forceinline__ void cross_stage8(float (&x)[N], int k0, float s) {
-  asm volatile(
-      "s_nop 1\n\t"
-      "v_fmac_f32_dpp %0, %0, %8 quad_perm:[1,0,3,2] row_mask:0xf bank_mask:0xf\n\t"
-      "v_fmac_f32_dpp %1, %1, %8 quad_perm:[1,0,3,2] row_mask:0xf bank_mask:0xf\n\t"
-      "v_fmac_f32_dpp %2, %2, %8 quad_perm:[1,0,3,2] row_mask:0xf bank_mask:0xf\n\t"
-      "v_fmac_f32_dpp %3, %3, %8 quad_perm:[1,0,3,2] row_mask:0xf bank_mask:0xf\n\t"
-      "v_fmac_f32_dpp %4, %4, %8 quad_perm:[1,0,3,2] row_mask:0xf bank_mask:0xf\n\t"
-      "v_fmac_f32_dpp %5, %5, %8 quad_perm:[1,0,3,2] row_mask:0xf bank_mask:0xf\n\t"
-      "v_fmac_f32_dpp %6, %6, %8 quad_perm:[1,0,3,2] row_mask:0xf bank_mask:0xf\n\t"
-      "v_fmac_f32_dpp %7, %7, %8 quad_perm:[1,0,3,2] row_mask:0xf bank_mask:0xf"
-      : "+v"(x[k0]), "+v"(x[k0 + 1]), "+v"(x[k0 + 2]), "+v"(x[k0 + 3]), "+v"(x[k0 + 4]),
-        "+v"(x[k0 + 5]), "+v"(x[k0 + 6]), "+v"(x[k0 + 7])
-      : "v"(s));
-}
-
-// kDfk2: the input is DFK2 int8 rows (in0/in1) with per-block fp16 scales
-// (sc0/sc1), dequantized to the reference's fp16 values on the way into LDS.
-template <bool kDfk2>
-__global__ __launch_bounds__(kAp2Threads, 3) void tq3_append2_kernel(
-    const uint4* __restrict__ in0, uint32_t* __restrict__ out0, const uint4* __restrict__ in1,
-    uint32_t* __restrict__ out1, int n_blocks, int n_tensors, PagedRows pr,
-    const uint16_t* __restrict__ sc0, const uint16_t* __restrict__ sc1) {
-  __shared__ uint32_t lds[kAp2Waves * kAp2WaveLdsDw];
-  const int lane = threadIdx.x & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  uint32_t* wl = lds + wave * kAp2WaveLdsDw;
-  // 32-bit tile bookkeeping (n_blocks < 2^31, so tiles * n_tensors < 2^28)
-  const int tiles = (n_blocks + kAp2Tile - 1) / kAp2Tile;
-  const int total = tiles * n_tensors;
-  const int stride = (int)gridDim.x * kAp2Waves;
-  int t = (int)blockIdx.x * kAp2Waves + wave;
-  if (t >= total) return;
-
-  const bool odd = lane & 1;
-  const int blk = lane >> 1;   // block of the tile this lane encodes
-  const float s_cross = odd ? -1.0f : 1.0f;   // stage 64: even a + b, odd b - a
-  const float a_fold = odd ? kFoldA : -kFoldA;
-  uint32_t q[3];
-#pragma unroll
-  for (int k = 0; k < 3; k++) q[k] = __builtin_amdgcn_readfirstlane(kFoldQBits[k]);
-
-  uint32_t pre[32];
-  {
-    const int b0 = (t % tiles) * kAp2Tile;
-    if constexpr (kDfk2)
-      load_tile32_dfk2(pre, t < tiles ? in0 : in1, t < tiles ? sc0 : sc1, b0,
-                       min(kAp2Tile, n_blocks - b0), lane);
-    else
-      load_tile32(pre, t < tiles ? in0 : in1, b0, min(kAp2Tile, n_blocks - b0), lane);
-  }
-  for (;;) {
-    const bool second = t >= tiles;
-    uint32_t* __restrict__ out = second ? out1 : out0;
-    const int b0 = (t % tiles) * kAp2Tile;
-    const int nb = min(kAp2Tile, n_blocks - b0);
-
-    // 1. prefetched tile into LDS (fp16)
-    if constexpr (kDfk2) {
-#pragma unroll
-      for (int j = 0; j < 4; j++) {
-        const int b = 8 * j + (lane >> 3), piece = lane & 7;
-        const float sc = h2f(pre[16 + j] & 0xffffu);
-        uint32_t h[8];
-#pragma unroll
-        for (int k = 0; k < 8; k++) h[k] = dfk2_pair(pre[4 * j + (k >> 1)], 2 * (k & 1), sc);
-        uint32_t* dst = wl + b * kInPitchDw + piece * 8;
-        *reinterpret_cast<uint4*>(dst) = make_uint4(h[0], h[1], h[2], h[3]);
-        *reinterpret_cast<uint4*>(dst + 4) = make_uint4(h[4], h[5], h[6], h[7]);
-      }
-    } else {
-#pragma unroll
-      for (int j = 0; j < 8; j++) {
-        const int chunk = j * 64 + lane;
-        const int b = chunk >> 4, part = chunk & 15;
-        *reinterpret_cast<uint4*>(wl + b * kInPitchDw + part * 4) =
-            make_uint4(pre[4 * j], pre[4 * j + 1], pre[4 * j + 2], pre[4 * j + 3]);
-      }
-    }
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "workgroup");
-
-    // 2. next tile's loads go out before this tile's vector work
-    const int tn = t + stride;
-    if (tn < total) {
-      const int nb0 = (tn % tiles) * kAp2Tile;
-      if constexpr (kDfk2)
-        load_tile32_dfk2(pre, tn < tiles ? in0 : in1, tn < tiles ? sc0 : sc1, nb0,
-                         min(kAp2Tile, n_blocks - nb0), lane);
-      else
-        load_tile32(pre, tn < tiles ? in0 : in1, nb0, min(kAp2Tile, n_blocks - nb0), lane);
-    }
-
-    // 3. this lane's half block
-    uint32_t hw[32];
-#pragma unroll
-    for (int k = 0; k < 8; k++) {
-      const uint4 v = *reinterpret_cast<const uint4*>(wl + blk * kInPitchDw + 32 * odd + 4 * k);
-      hw[4 * k] = v.x;
-      hw[4 * k + 1] = v.y;
-      hw[4 * k + 2] = v.z;
-      hw[4 * k + 3] = v.w;
-    }
-    // norm: sequential sum of squares in reference order
-    float n1 = 0.0f;
-#pragma unroll
-    for (int k = 0; k < 32; k++) {
-      const float lo = h2f(hw[k] & 0xffffu), hi = h2f(hw[k] >> 16);
-      n1 = __builtin_fmaf(lo, lo, n1);
-      n1 = __builtin_fmaf(hi, hi, n1);
-    }
-    float n2 = lane_dpp<0xA0>(n1);   // quad_perm [0,0,2,2]: the even lane's partial
-#pragma unroll
-    for (int k = 0; k < 32; k++) {
-      const float lo = h2f(hw[k] & 0xffffu), hi = h2f(hw[k] >> 16);
-      n2 = __builtin_fmaf(lo, lo, n2);
-      n2 = __builtin_fmaf(hi, hi, n2);
-    }
-    const float nsq = lane_dpp<0xF5>(n2);   // quad_perm [1,1,3,3]: the odd lane's full sum
-    const float norm = __builtin_sqrtf(nsq);
-    // x * inv * sign (turboquant.cuh:141-149; the sign multiply is exact, so
-    // it folds into the factor).  Element e of the lane's half is element
-    // 64h + e of the block: where the signs of e and 64 + e agree the factor
-    // is the same for both lanes, where they differ it is +-invx, which
-    // carries the odd lane's flip.
-    const float inv = 1.0f / norm;
-    const float invx = odd ? -inv : inv;
-    float x[64];
-#pragma unroll
-    for (int e = 0; e < 64; e++) {
-      const float f = sign_pos(e) == sign_pos(64 + e) ? (sign_pos(e) ? inv : -inv)
-                                                      : (sign_pos(e) ? invx : -invx);
-      x[e] = __builtin_fmaf(h2f((e & 1) ? hw[e >> 1] >> 16 : hw[e >> 1] & 0xffffu), f, 0.0f);
-    }
-    // WHT stages 1 .. 32 (turboquant.cuh:50-59), then stage 64 across the pair
-#pragma unroll
-    for (int step = 1; step < 64; step <<= 1) {
-#pragma unroll
-      for (int i = 0; i < 64; i += 2 * step) {
-#pragma unroll
-        for (int j = i; j < i + step; j++) {
-          const float a = x[j], b = x[j + step];
-          x[j] = a + b;
-          x[j + step] = a - b;
-        }
-      }
-    }
-#pragma unroll
-    for (int k = 0; k < 64; k += 8) cross_stage8(x, k, s_cross);
-
-    // bins: local bit 3k+b of this lane's 192-bit half stream; chains
-    // k = 63..32 (words 3..5) and k = 31..0 (words 0..2)
-    uint32_t acc[6];
-#pragma unroll
-    for (int w = 0; w < 6; w++) acc[w] = 0u;
-#pragma unroll
-    for (int i = 0; i < 32; i++) {
-      const int ka = 63 - i, kb = 31 - i;
-      const float ya = __builtin_fmaf(x[ka], a_fold, __builtin_fabsf(x[ka]));
-      const float yb = __builtin_fmaf(x[kb], a_fold, __builtin_fabsf(x[kb]));
-      uint64_t pa[2], pb[2];
-      fold_planes2(ya, yb, q, pa, pb);
-      shift_in_sign(acc[(3 * ka + 2) >> 5], ya);
-      shift_in_sign(acc[(3 * kb + 2) >> 5], yb);
-      shift_in(acc[(3 * ka + 1) >> 5], pa[0]);
-      shift_in(acc[(3 * kb + 1) >> 5], pb[0]);
-      shift_in(acc[(3 * ka) >> 5], pa[1]);
-      shift_in(acc[(3 * kb) >> 5], pb[1]);
-    }
-    // (words 6..11 of the block have the bit-2 layout of words 0..5)
-    sign_fix<0, 3>(acc);
-    sign_fix<3, 3>(acc + 3);
-    const bool keep = norm >= 1e-10f && norm < __builtin_inff();
-#pragma unroll
-    for (int w = 0; w < 6; w++) acc[w] = keep ? acc[w] : 0u;
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "workgroup");
-
-    if (pr.block_tables != nullptr) {
-      // paged: each lane stores its part of its block at the block's row
-      if (blk < nb) {
-        const long ob = paged_block(pr, (long)b0 + blk);
-        if (ob >= 0) {
-          uint32_t* dst = out + ob * 13;
-          if (odd) {
-#pragma unroll
-            for (int w = 0; w < 6; w++) dst[7 + w] = acc[w];
-          } else {
-            dst[0] = __float_as_uint(norm);
-#pragma unroll
-            for (int w = 0; w < 6; w++) dst[1 + w] = acc[w];
-          }
-        }
-      }
-    } else {
-      // 4. stage the tile's 32 x 13 dwords, then store them contiguously
-      uint32_t* ob = wl + blk * 13 + (odd ? 7 : 1);
-#pragma unroll
-      for (int w = 0; w < 6; w++) ob[w] = acc[w];
-      if (!odd) wl[blk * 13] = __float_as_uint(norm);
-      __builtin_amdgcn_wave_barrier();
-      __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "workgroup");
-      // the resource spans the tile's nb * 52 bytes: stores past it are dropped
-      const __amdgpu_buffer_rsrc_t rd = __builtin_amdgcn_make_buffer_rsrc(
-          out + (long)b0 * 13, 0, nb * 52, kBufferRsrcWord3);
-#pragma unroll
-      for (int j = 0; j < 7; j++)
-        __builtin_amdgcn_raw_buffer_store_b32(wl[j * 64 + lane], rd, lane * 4, j * 256, 0);
-    }
-    if (tn >= total) break;
-    t = tn;
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "workgroup");
-  }
 }
 
 // ---------------------------------------------------------------------------
@@ -574,7 +285,7 @@ __device__ __forceinline__ void bin_half(const float (&x)[64], const uint32_t (&
   sign_fix<3, 3>(acc + 3);
 }
 
-template <bool kDfk2>
+template <bool kDfk2, bool kPaged>
 __global__ __launch_bounds__(kAp4Threads, 3) void tq3_append4_kernel(
     const uint4* __restrict__ in0, uint32_t* __restrict__ out0, const uint4* __restrict__ in1,
     uint32_t* __restrict__ out1, int n_blocks, int n_tensors, PagedRows pr,
@@ -677,7 +388,7 @@ __global__ __launch_bounds__(kAp4Threads, 3) void tq3_append4_kernel(
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "workgroup");
 
-    if (pr.block_tables != nullptr) {
+    if constexpr (kPaged) {
       // paged: each lane stores its block at the block's row
       if (lane < nb) {
         const long ob = paged_block(pr, (long)b0 + lane);
@@ -809,16 +520,11 @@ hipError_t launch_tq3_append(const void* in0, void* out0, const void* in1, void*
   const int grid = (int)std::min<long>(wgs_needed, 3L * n_cu);
   if (grid == 0) return hipSuccess;
   const PagedRows pr = paged ? *paged : PagedRows{};
-  if (sc0 != nullptr)
-    hipLaunchKernelGGL(tq3_append4_kernel<true>, dim3(grid), dim3(kAp4Threads), 0, stream,
-                       static_cast<const uint4*>(in0), static_cast<uint32_t*>(out0),
-                       static_cast<const uint4*>(in1), static_cast<uint32_t*>(out1), n_blocks,
-                       n_tensors, pr, sc0, sc1);
-  else
-    hipLaunchKernelGGL(tq3_append4_kernel<false>, dim3(grid), dim3(kAp4Threads), 0, stream,
-                       static_cast<const uint4*>(in0), static_cast<uint32_t*>(out0),
-                       static_cast<const uint4*>(in1), static_cast<uint32_t*>(out1), n_blocks,
-                       n_tensors, pr, nullptr, nullptr);
+  auto kernel = sc0 != nullptr ? (paged ? tq3_append4_kernel<true, true> : tq3_append4_kernel<true, false>)
+                                : (paged ? tq3_append4_kernel<false, true> : tq3_append4_kernel<false, false>);
+  hipLaunchKernelGGL(kernel, dim3(grid), dim3(kAp4Threads), 0, stream, static_cast<const uint4*>(in0),
+                     static_cast<uint32_t*>(out0), static_cast<const uint4*>(in1),
+                     static_cast<uint32_t*>(out1), n_blocks, n_tensors, pr, sc0, sc1);
   return hipGetLastError();
 }
 
