@@ -232,14 +232,18 @@ __global__ __launch_bounds__(64 * WAVES, 2) void prefill_attn_kernel(PrefillArgs
   // dims 16j .. 16j+15 (lane l: dim 16j + l/4, slot l%4); the value offset
   // within the run does not depend on j
   const int v_off = (lane >> 2) * (kTK * 2) + (((lane & 3) ^ ((lane >> 4) & 3)) * 16);
+  // key offset of load j: row 2j + hi, slot l%32 holds chunk (l%32) ^ (row & 15);
+  // (2j + hi) & 15 = (2j & 15) ^ hi, so the offset is k_base ^ 16 * (2j & 15).
+  // Formed per load (one XOR; kept out of the registers across the tile loop).
+  const int k_base = (lane >> 5) * (kHD * 2) + (((lane & 31) ^ (lane >> 5)) * 16);
   auto issue = [&](int ti, int buf) {
     uint8_t* base = lds + buf * kBufBytes;
 #pragma unroll
     for (int jj = 0; jj < kLoads; jj++) {
       const int j = min(wave + jj * WAVES, 15);
-      const int row = 2 * j + (lane >> 5);
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rk, (lds_void_t*)(base + j * 1024), 16,
-                                               (lane >> 5) * (kHD * 2) + (((lane & 31) ^ (row & 15)) * 16),
+      int k_off;
+      asm volatile("v_xor_b32 %0, %1, %2" : "=v"(k_off) : "s"(16 * ((2 * j) & 15)), "v"(k_base));
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rk, (lds_void_t*)(base + j * 1024), 16, k_off,
                                                ti * kKBytes + j * 1024, 0, 0);
       __builtin_amdgcn_raw_ptr_buffer_load_lds(rv, (lds_void_t*)(base + kKBytes + j * 1024), 16, v_off,
                                                ti * kVBytes + j * 1024, 0, 0);
