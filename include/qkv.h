@@ -256,8 +256,7 @@ int qkv_tq3_kpool_update(const qkv_block_tq3* k_cache, uint16_t* k_pool, uint16_
  * through a caller-provided workspace of
  * qkv_block_index_ms_workspace_bytes(num_kv, sub_n, n_blocks) bytes
  * (256-byte aligned, no initialisation needed).  k_pool / k_pool_max 16-byte
- * aligned.  n_blocks <= 32768 (with top_k <= 64; a longer pick list shares
- * that 128 KiB of LDS). */
+ * aligned. */
 size_t qkv_block_index_ms_workspace_bytes(int num_kv, int sub_n, int n_blocks);
 int qkv_block_index_ms(const uint16_t* q, const uint16_t* k_pool, const uint16_t* k_pool_max,
                        int32_t* block_index, int num_q, int num_kv, int head_dim, int sub_n,

@@ -379,8 +379,6 @@ int qkv_block_index_ms(const uint16_t* q, const uint16_t* k_pool, const uint16_t
       start_pos < 0 || top_k < 1 || block_size_n < 1 || n_blocks < 1 ||
       n_blocks > n_blocks_stride)
     return QKV_ERR_INVALID;
-  // the selection keeps up to n_blocks scores and top_k picks in LDS
-  if ((long)n_blocks * 4 + (top_k > 64 ? (long)top_k * 4 : 0) > 128 * 1024) return QKV_ERR_UNSUPPORTED;
   if (!q || !k_pool || !k_pool_max || !block_index) return QKV_ERR_NULL;
   if (!aligned(q, 4) || !aligned(k_pool, 16) || !aligned(k_pool_max, 16) ||
       !aligned(block_index, 4))

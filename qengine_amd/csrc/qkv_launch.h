@@ -85,7 +85,7 @@ hipError_t launch_block_index(const BlockIndexArgs& a, float* scores, hipStream_
 // kx  keys [num_kv][h_pad + n_pad][256] fp16: the history rows dequantized
 //     exactly as the reference's bulk dequantization, padded to whole 64-row
 //     tiles, then the chunk's own keys
-// vt  values in 64-key tiles [num_kv][(h_pad + n_pad)/64][256 dims][64] fp16
+// vt  values in 32-key tiles [num_kv][(h_pad + n_pad)/32][256 dims][32] fp16
 // part_ml / part_o  key-split partials {m (log2 units), l} and o
 //                   [n_split][n_tok][num_q] (x 256 for o)
 struct PrefillArgs {

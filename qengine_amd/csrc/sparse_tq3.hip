@@ -137,125 +137,134 @@ __global__ __launch_bounds__(kSpThreads) void block_score_kernel(BlockIndexArgs 
 
 // (value, index) order of the selection: higher value first, then lower index;
 // index -1 (nothing) last
-__device__ __forceinline__ bool better(float v, int i, float bv, int bi) {
-  return i >= 0 && (bi < 0 || v > bv || (v == bv && i < bi));
+// Selection, one workgroup per (kv head, query t).  The reference's repeated
+// argmax (ties to the lower block, -inf and NaN never chosen, -1 padding)
+// picks the first top_k blocks in the order (score descending, block
+// ascending), and its list is then sorted ascending: it is that set.  It is
+// found without sorting by a radix select on an order-preserving 32-bit key
+// of the score (-0 and +0 equal):
+//   1. four 8-bit passes narrow the key T of the top_k-th pick (a 256-bin
+//      histogram of the keys that share the digits found so far, and a
+//      suffix scan over the bins);
+//   2. the picks are the blocks with key > T and the lowest-numbered `need`
+//      blocks with key == T (a block-wide scan in block order);
+//   3. a second scan gives each pick its place in the ascending list.
+// Each thread owns a contiguous run of blocks; the scores are read from the
+// workspace (L2) in every pass.
+constexpr int kTkThreads = 256;
+
+__device__ __forceinline__ uint32_t order_key(float v) {
+  const uint32_t b = __float_as_uint(v == 0.0f ? 0.0f : v);
+  return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
 }
+__device__ __forceinline__ bool pickable(float v) { return v > -INFINITY; }   // false for NaN
 
-// Selection, one wave per (kv head, query t): lane l keeps the best (score,
-// block) of blocks l, l + 64, ...; each pick is the wave's best pair, after
-// which its lane rescans its blocks; then the picks are sorted ascending (by
-// rank across the lanes, or in LDS past 64 picks) and padded with -1.  The result is the reference's repeated argmax.  Lanes hold
-// their blocks' scores in registers when there are at most 64 * kSelRegs
-// blocks, in LDS otherwise.
-constexpr int kSelRegs = 40;
-
-// One step of a wave argmax under `better`: the (score, block) pair of the
-// DPP source lane replaces the lane's own when it is better.
-template <int CTRL, int ROW_MASK = 0xf>
-__device__ __forceinline__ void argmax_step(float& v, int& i) {
-  const float ov = dpp_f<CTRL, ROW_MASK>(v);
-  const int oi = __builtin_amdgcn_update_dpp(i, i, CTRL, ROW_MASK, 0xf, false);
-  if (better(ov, oi, v, i)) {
-    v = ov;
-    i = oi;
+// Exclusive scan of v over the workgroup (block order = thread order), and the total.
+__device__ __forceinline__ int block_scan(int v, int* wtot, int& total) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  int inc = v;
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) {
+    const int u = __shfl_up(inc, d, 64);
+    if (lane >= d) inc += u;
   }
+  if (lane == 63) wtot[wave] = inc;
+  __syncthreads();
+  int off = 0, tot = 0;
+#pragma unroll
+  for (int w = 0; w < kTkThreads / 64; w++) {
+    const int x = wtot[w];
+    off += w < wave ? x : 0;
+    tot += x;
+  }
+  __syncthreads();
+  total = tot;
+  return off + inc - v;
 }
 
-// The wave's best pair, in every lane (the reduction of wave_max: quad swaps,
-// row rotations, row broadcasts, the result in lane 63).
-__device__ __forceinline__ void wave_argmax(float& v, int& i) {
-  argmax_step<0xB1>(v, i);
-  argmax_step<0x4E>(v, i);
-  argmax_step<0x124>(v, i);
-  argmax_step<0x128>(v, i);
-  argmax_step<0x142, 0xa>(v, i);
-  argmax_step<0x143, 0xc>(v, i);
-  v = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
-  i = __builtin_amdgcn_readlane(i, 63);
-}
-template <bool REGS>
-__global__ __launch_bounds__(64) void block_select_kernel(BlockIndexArgs a, const float* scores) {
-  extern __shared__ float sc_lds[];
+__global__ __launch_bounds__(kTkThreads) void block_select_kernel(BlockIndexArgs a, const float* scores) {
+  __shared__ int hist[256];
+  __shared__ int wtot[kTkThreads / 64];
+  __shared__ int found[2];
   const int h = blockIdx.x % a.num_kv, t = blockIdx.x / a.num_kv;
-  const int lane = threadIdx.x;
+  const int tid = threadIdx.x;
   const float* src = scores + ((long)h * a.sub_n + t) * a.n_blocks;
-  float r[REGS ? kSelRegs : 1];
-  if constexpr (REGS) {
-#pragma unroll
-    for (int j = 0; j < kSelRegs; j++) {
-      const int n = lane + 64 * j;
-      r[j] = n < a.n_blocks ? src[n] : -INFINITY;
-    }
-  } else {
-    for (int n = lane; n < a.n_blocks; n += 64) sc_lds[n] = src[n];
-  }
-  auto lane_best = [&](float& bv, int& bi) {
-    bv = -INFINITY;
-    bi = -1;
-    if constexpr (REGS) {
-#pragma unroll
-      for (int j = 0; j < kSelRegs; j++)
-        if (r[j] > bv) {   // strict: never -inf or NaN; ascending blocks keep the lower one
-          bv = r[j];
-          bi = lane + 64 * j;
-        }
-    } else {
-      for (int n = lane; n < a.n_blocks; n += 64) {
-        const float v = sc_lds[n];
-        if (v > bv) {
-          bv = v;
-          bi = n;
-        }
-      }
-    }
-  };
-  float lv;
-  int li;
-  lane_best(lv, li);
   int32_t* row = a.block_index + ((long)h * a.sub_n_max + t) * a.top_k;
-  // picks: lane k holds pick k when top_k <= 64, else an LDS list after the scores
-  int* picks = reinterpret_cast<int*>(sc_lds + (REGS ? 0 : a.n_blocks));
-  int mine = -1;
-  int k = 0;
-  for (; k < a.top_k; k++) {
-    float bv = lv;
-    int bi = li;
-    wave_argmax(bv, bi);
-    if (bi < 0) break;   // wave-uniform
-    if (a.top_k <= 64) {
-      if (lane == k) mine = bi;
-    } else if (lane == 0) {
-      picks[k] = bi;
-    }
-    if (lane == (bi & 63)) {
-      if constexpr (REGS) {
-#pragma unroll
-        for (int j = 0; j < kSelRegs; j++)
-          if (lane + 64 * j == bi) r[j] = -INFINITY;
-      } else {
-        sc_lds[bi] = -INFINITY;
+  const int per = (a.n_blocks + kTkThreads - 1) / kTkThreads;
+  const int i0 = min(tid * per, a.n_blocks), i1 = min(i0 + per, a.n_blocks);
+
+  int n_ok = 0;
+  for (int i = i0; i < i1; i++) n_ok += pickable(src[i]);
+  int total;
+  (void)block_scan(n_ok, wtot, total);
+  const bool all = total <= a.top_k;   // every pickable block is picked
+  uint32_t T = 0u;
+  int need = 0;
+  if (!all) {
+    uint32_t prefix = 0u, mask = 0u;
+    int kk = a.top_k;   // rank of the pick sought among the keys sharing `prefix`
+    for (int shift = 24; shift >= 0; shift -= 8) {
+      hist[tid] = 0;
+      __syncthreads();
+      for (int i = i0; i < i1; i++) {
+        const float v = src[i];
+        const uint32_t key = order_key(v);
+        if (pickable(v) && (key & mask) == prefix) atomicAdd(&hist[(key >> shift) & 255u], 1);
       }
-      lane_best(lv, li);
+      __syncthreads();
+      // suffix sums: thread tid takes bin 255 - tid
+      const int c = hist[255 - tid];
+      int tot;
+      const int above = block_scan(c, wtot, tot);   // keys in bins above 255 - tid
+      if (above < kk && above + c >= kk) {
+        found[0] = 255 - tid;
+        found[1] = kk - above;
+      }
+      __syncthreads();
+      prefix |= (uint32_t)found[0] << shift;
+      mask |= 255u << shift;
+      kk = found[1];
+      __syncthreads();
+    }
+    T = prefix;
+    need = kk;   // picks among the blocks whose key is exactly T
+  }
+  // picks, in block order
+  int n_eq = 0;
+  if (!all)
+    for (int i = i0; i < i1; i++) {
+      const float v = src[i];
+      n_eq += pickable(v) && order_key(v) == T;
+    }
+  int tot_eq;
+  int eq_rank = block_scan(n_eq, wtot, tot_eq);
+  int n_pick = 0;
+  for (int i = i0; i < i1; i++) {
+    const float v = src[i];
+    if (!pickable(v)) continue;
+    const uint32_t key = order_key(v);
+    if (all || key > T) {
+      n_pick++;
+    } else if (key == T) {
+      n_pick += eq_rank < need;
+      eq_rank++;
     }
   }
-  if (a.top_k <= 64) {
-    // ascending: each pick's rank among the k picks (block indices are distinct)
-    int rank = 0;
-    for (int j = 0; j < k; j++) rank += __builtin_amdgcn_readlane(mine, j) < mine;
-    if (lane < k) row[rank] = mine;
-    else if (lane < a.top_k) row[lane] = -1;
-  } else if (lane == 0) {
-    for (int i = 1; i < k; i++) {   // ascending, in LDS
-      const int x = picks[i];
-      int j = i;
-      while (j > 0 && picks[j - 1] > x) {
-        picks[j] = picks[j - 1];
-        j--;
-      }
-      picks[j] = x;
+  int n_total;
+  int pos = block_scan(n_pick, wtot, n_total);
+  eq_rank -= n_eq;   // back to this thread's first equal key
+  for (int i = i0; i < i1; i++) {
+    const float v = src[i];
+    if (!pickable(v)) continue;
+    const uint32_t key = order_key(v);
+    bool pick = all || key > T;
+    if (!all && key == T) {
+      pick = eq_rank < need;
+      eq_rank++;
     }
-    for (int i = 0; i < a.top_k; i++) row[i] = i < k ? picks[i] : -1;
+    if (pick) row[pos++] = i;
   }
+  for (int j = n_total + tid; j < a.top_k; j += kTkThreads) row[j] = -1;
 }
 
 hipError_t launch_tq3_kpool(const KpoolArgs& a, hipStream_t stream) {
@@ -271,13 +280,8 @@ hipError_t launch_block_index(const BlockIndexArgs& a, float* scores, hipStream_
   if (nb_wg == 0) return hipErrorInvalidValue;
   hipLaunchKernelGGL(block_score_kernel, dim3((unsigned)(a.num_kv * nb_wg)), dim3(kSpThreads), 0,
                      stream, a, scores);
-  const size_t pick_lds = a.top_k > 64 ? (size_t)a.top_k * 4 : 0;
-  if (a.n_blocks <= 64 * kSelRegs)
-    hipLaunchKernelGGL(block_select_kernel<true>, dim3((unsigned)(a.num_kv * a.sub_n)), dim3(64),
-                       pick_lds, stream, a, static_cast<const float*>(scores));
-  else
-    hipLaunchKernelGGL(block_select_kernel<false>, dim3((unsigned)(a.num_kv * a.sub_n)), dim3(64),
-                       (size_t)a.n_blocks * 4 + pick_lds, stream, a, static_cast<const float*>(scores));
+  hipLaunchKernelGGL(block_select_kernel, dim3((unsigned)(a.num_kv * a.sub_n)), dim3(kTkThreads), 0,
+                     stream, a, static_cast<const float*>(scores));
   return hipGetLastError();
 }
 

@@ -197,7 +197,8 @@ def test_block_sparse_argument_errors_without_gpu(L):
     assert bi(p, p, p, p, 16, 4, 256, 1, 1, 100, 8, 64, 3, 2, 0.5, p, wsb, None) == -1   # n_blocks > stride
     assert bi(p, None, p, p, 16, 4, 256, 1, 1, 100, 8, 64, 2, 2, 0.5, p, wsb, None) == -2
     assert bi(p, p, p, p, 16, 4, 256, 1, 1, 100, 8, 64, 2, 2, 0.5, None, wsb, None) == -7
-    assert bi(p, p, p, p, 16, 4, 256, 1, 1, 100, 8, 64, 40000, 40000, 0.5, p, 1 << 30, None) == -3
+    # no cap on n_blocks beyond the workspace (the selection keeps nothing per block in LDS)
+    assert bi(p, p, p, p, 16, 4, 256, 1, 1, 100, 8, 64, 40000, 40000, 0.5, p, wsb, None) == -7
     assert bi(p, p, p, p, 16, 4, 256, 1, 1, 100, 8, 64, 2, 2, 0.5, p, wsb - 1, None) == -7
     sp = L.qkv_attn_block_sparse_split_tq3
     assert sp(p, p, p, p, p, p, p, 16, 4, 256, 100, 1, 1, 1.0, 8, 32, 8, None, None) == -3

@@ -89,6 +89,29 @@ def test_block_index_bitexact(dev, num_q, top_k, beta):
     assert np.array_equal(got, exp)
 
 
+@pytest.mark.parametrize("nb,top_k,distinct", [(2049, 64, None), (9000, 64, 50), (9000, 300, 50),
+                                                (40000, 16, 7)])
+def test_block_index_many_blocks_bitexact(dev, nb, top_k, distinct):
+    """Long block lists (several blocks per selecting thread, past any LDS
+    budget) from synthetic signatures.  With `distinct` set, every block's
+    signature is one of that many, so the scores take few values and runs of
+    equal scores straddle the pick threshold (ties go to the lower block).
+    The last blocks lie past the first queries' reach."""
+    rng = np.random.default_rng(nb + top_k)
+    sub = 4
+    n_sig = distinct or nb
+    bp = (rng.standard_normal((NKV, n_sig, HD)) * 0.3).astype(np.float16).view(np.uint16)
+    bx = (rng.standard_normal((NKV, n_sig, HD)) * 0.6).astype(np.float16).view(np.uint16)
+    pick = rng.integers(0, n_sig, nb) if distinct else np.arange(nb)
+    kp, kx = np.ascontiguousarray(bp[:, pick]), np.ascontiguousarray(bx[:, pick])
+    start = 64 * (nb - 3) - sub
+    q = q_f16(rng, sub, 16, HD)
+    got = _gpu_index(dev, q, kp, kx, num_q=16, sub_n=sub, start=start, top_k=top_k, nb=nb)
+    exp = O.block_index_ms(q, kp, kx, num_q=16, num_kv=NKV, hd=HD, sub_n=sub, sub_n_max=sub,
+                           start_pos=start, top_k=top_k, n_blocks=nb)
+    assert np.array_equal(got, exp)
+
+
 def test_block_index_ties_bitexact(dev):
     rng = np.random.default_rng(41)
     n, sub = 64 * 30, 4
