@@ -69,25 +69,32 @@ __global__ __launch_bounds__(kSpThreads) void tq3_kpool_kernel(KpoolArgs a) {
   a.k_pool_max[ob] = (uint16_t)f2h(best_val);
 }
 
-constexpr int kScBlocks = 64;          // blocks scored per workgroup
+typedef _Float16 h2_t __attribute__((ext_vector_type(2)));
+
+constexpr int kScBlocks = 32;          // blocks scored per workgroup
+constexpr int kScQueries = 8;          // queries scored per workgroup
 constexpr int kScPitchDw = 129;        // staged pool row: 128 dwords + 1 (conflict-free lanes)
 
-// Block scores for every verify query of a kv head: one workgroup per (kv
-// head, 64 blocks).  The blocks' mean and max-abs rows are staged in LDS once
-// and scored against all sub_n GQA-mean queries (fp16-rounded, as the
-// reference forms them, sparse_index.cuh:243-252); thread (t, b) runs block
-// b's two dot products for query t over the 128 half2 pairs in the
-// reference's order.  Scores (-inf past the query's causal block) go to the
-// workspace [num_kv][sub_n][n_blocks].
+// Block scores, one workgroup per (kv head, 32 blocks, 8 queries).  The
+// blocks' mean and max-abs rows are staged in LDS; the GQA-mean queries
+// (fp16-rounded, as the reference forms them, sparse_index.cuh:243-252) sit in
+// LDS as fp16 pairs; thread (t, b) runs block b's two dot products for query
+// t over the 128 pairs in the reference's order: each pair's products are
+// exact and their sum is rounded once (one v_dot2_f32_f16 with a zero
+// addend), then added to the running fp32 sum.  Scores (-inf past the
+// query's causal block) go to the workspace [num_kv][sub_n][n_blocks].
 __global__ __launch_bounds__(kSpThreads) void block_score_kernel(BlockIndexArgs a, float* scores) {
   __shared__ uint32_t rows_mean[kScBlocks * kScPitchDw];
   __shared__ uint32_t rows_max[kScBlocks * kScPitchDw];
-  __shared__ float qa[16 * kSpHD];   // up to 16 queries per pass
+  __shared__ uint32_t qa2[kScQueries * kSpHD / 2];   // fp16 pairs
   const int nb_wg = (a.n_blocks + kScBlocks - 1) / kScBlocks;
-  const int h = blockIdx.x / nb_wg, b0 = (blockIdx.x - h * nb_wg) * kScBlocks;
+  const int nq_wg = (a.sub_n + kScQueries - 1) / kScQueries;
+  const int qg = blockIdx.x % nq_wg, r = blockIdx.x / nq_wg;
+  const int h = r / nb_wg, b0 = (r - h * nb_wg) * kScBlocks, t0 = qg * kScQueries;
+  const int nt = min(kScQueries, a.sub_n - t0);
   const int tid = threadIdx.x;
   const int gqa = a.num_q / a.num_kv;
-  // stage 64 blocks x {mean, max} x 512 B: 4096 16-byte pieces, 16 per thread
+  // stage 32 blocks x {mean, max} x 512 B: 2048 16-byte pieces, 8 per thread
   for (int piece = tid; piece < kScBlocks * 64; piece += kSpThreads) {
     const int b = piece >> 6, w = piece & 63;   // w < 32: mean, else max; 8 dims each
     uint4 v = make_uint4(0u, 0u, 0u, 0u);
@@ -101,42 +108,38 @@ __global__ __launch_bounds__(kSpThreads) void block_score_kernel(BlockIndexArgs 
     d[3] = v.w;
   }
   const float inv_g = 1.0f / (float)gqa;
-  for (int t0 = 0; t0 < a.sub_n; t0 += 16) {
-    const int nt = min(16, a.sub_n - t0);
-    __syncthreads();   // staging done / the previous pass is done with qa
-    for (int i = tid; i < nt * kSpHD; i += kSpThreads) {
-      const int tq = i / kSpHD, c = i - tq * kSpHD;
-      float s = 0.0f;
-      for (int g = 0; g < gqa; g++)
-        s += h2f(a.q[((long)(t0 + tq) * a.num_q + h * gqa + g) * kSpHD + c]);
-      qa[tq * kSpHD + c] = h2f(f2h(s * inv_g));
+  for (int i = tid; i < nt * kSpHD / 2; i += kSpThreads) {
+    const int tq = i / (kSpHD / 2), c = 2 * (i - tq * (kSpHD / 2));
+    float s0 = 0.0f, s1 = 0.0f;
+    for (int g = 0; g < gqa; g++) {
+      const uint16_t* qr = a.q + ((long)(t0 + tq) * a.num_q + h * gqa + g) * kSpHD + c;
+      s0 += h2f(qr[0]);
+      s1 += h2f(qr[1]);
     }
-    __syncthreads();
-    // thread -> (query tq, block b): a wave's 64 lanes are 64 blocks of one query
-    for (int pr = tid; pr < nt * kScBlocks; pr += kSpThreads) {
-      const int tq = pr / kScBlocks, b = pr - tq * kScBlocks;
-      const uint32_t* mn = rows_mean + b * kScPitchDw;
-      const uint32_t* mx = rows_max + b * kScPitchDw;
-      const float* q = qa + tq * kSpHD;
-      float s_mean = 0.0f, s_max = 0.0f;
-#pragma unroll 8
-      for (int c2 = 0; c2 < kSpHD / 2; c2++) {
-        const uint32_t m2 = mn[c2], x2 = mx[c2];
-        const float q0 = q[2 * c2], q1 = q[2 * c2 + 1];
-        s_mean += q0 * h2f(m2 & 0xffffu) + q1 * h2f(m2 >> 16);
-        s_max += q0 * h2f(x2 & 0xffffu) + q1 * h2f(x2 >> 16);
-      }
-      const int n = b0 + b, t = t0 + tq;
-      if (n < a.n_blocks) {
-        const float s = fmaxf(s_mean, a.beta * s_max);
-        scores[((long)h * a.sub_n + t) * a.n_blocks + n] = n > (a.start_pos + t) / a.bsn ? -INFINITY : s;
-      }
+    qa2[i] = f2h(s0 * inv_g) | (f2h(s1 * inv_g) << 16);
+  }
+  __syncthreads();
+  // thread -> (query tq, block b): 32 lanes of a wave are the 32 blocks of one query
+  const int tq = tid / kScBlocks, b = tid - tq * kScBlocks;
+  if (tq < nt) {
+    const uint32_t* mn = rows_mean + b * kScPitchDw;
+    const uint32_t* mx = rows_max + b * kScPitchDw;
+    const uint32_t* q = qa2 + tq * (kSpHD / 2);
+    float s_mean = 0.0f, s_max = 0.0f;
+#pragma unroll 16
+    for (int c2 = 0; c2 < kSpHD / 2; c2++) {
+      const h2_t qq = __builtin_bit_cast(h2_t, q[c2]);
+      s_mean += __builtin_amdgcn_fdot2(qq, __builtin_bit_cast(h2_t, mn[c2]), 0.0f, false);
+      s_max += __builtin_amdgcn_fdot2(qq, __builtin_bit_cast(h2_t, mx[c2]), 0.0f, false);
+    }
+    const int n = b0 + b, t = t0 + tq;
+    if (n < a.n_blocks) {
+      const float sc = fmaxf(s_mean, a.beta * s_max);
+      scores[((long)h * a.sub_n + t) * a.n_blocks + n] = n > (a.start_pos + t) / a.bsn ? -INFINITY : sc;
     }
   }
 }
 
-// (value, index) order of the selection: higher value first, then lower index;
-// index -1 (nothing) last
 // Selection, one workgroup per (kv head, query t).  The reference's repeated
 // argmax (ties to the lower block, -inf and NaN never chosen, -1 padding)
 // picks the first top_k blocks in the order (score descending, block
@@ -277,8 +280,9 @@ hipError_t launch_tq3_kpool(const KpoolArgs& a, hipStream_t stream) {
 
 hipError_t launch_block_index(const BlockIndexArgs& a, float* scores, hipStream_t stream) {
   const int nb_wg = (a.n_blocks + kScBlocks - 1) / kScBlocks;
-  if (nb_wg == 0) return hipErrorInvalidValue;
-  hipLaunchKernelGGL(block_score_kernel, dim3((unsigned)(a.num_kv * nb_wg)), dim3(kSpThreads), 0,
+  const int nq_wg = (a.sub_n + kScQueries - 1) / kScQueries;
+  if (nb_wg == 0 || nq_wg == 0) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(block_score_kernel, dim3((unsigned)(a.num_kv * nb_wg * nq_wg)), dim3(kSpThreads), 0,
                      stream, a, scores);
   hipLaunchKernelGGL(block_select_kernel, dim3((unsigned)(a.num_kv * a.sub_n)), dim3(kTkThreads), 0,
                      stream, a, static_cast<const float*>(scores));
