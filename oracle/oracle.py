@@ -87,6 +87,7 @@ def _declare(L):
     L.or_dfk2_dequant.argtypes = [_P, _P, _P, _I64, _I]
     L.or_tq3_kpool_update.argtypes = [_P, _P, _P, _I, _I, _I, _I, _I, _I]
     L.or_block_index_ms.argtypes = [_P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _I, _I, _I, _F]
+    L.or_block_scores_ms.argtypes = [_P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _I, _F]
     L.or_attn_block_sparse_split.argtypes = [_P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I,
                                              _F, _I, _I, _I, _P]
     L.or_legacy_decode.restype = _I
@@ -386,6 +387,18 @@ def block_index_ms(q, k_pool, k_pool_max, *, num_q, num_kv, hd, sub_n, sub_n_max
     lib().or_block_index_ms(_ptr(qq), _ptr(_u16(k_pool)), _ptr(_u16(k_pool_max)), _ptr(out),
                             num_q, num_kv, hd, sub_n, sub_n_max, start_pos, top_k, block_size_n,
                             n_blocks, k_pool.shape[1], float(beta))
+    return out
+
+
+def block_scores_ms(q, k_pool, k_pool_max, *, num_q, num_kv, hd, sub_n, start_pos, n_blocks,
+                    block_size_n=64, beta=0.5):
+    """The block scores build_block_index_ms_kern selects from
+    (sparse_attn/sparse_index.cuh:243-290): float32 [num_kv][sub_n][n_blocks],
+    -inf past each query's causal block."""
+    out = np.zeros((num_kv, sub_n, n_blocks), np.float32)
+    lib().or_block_scores_ms(_ptr(_u16(q)), _ptr(_u16(k_pool)), _ptr(_u16(k_pool_max)), _ptr(out),
+                             num_q, num_kv, hd, sub_n, start_pos, block_size_n, n_blocks,
+                             k_pool.shape[1], float(beta))
     return out
 
 

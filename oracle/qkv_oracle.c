@@ -972,36 +972,57 @@ void or_tq3_kpool_update(const or_block_tq3* k, uint16_t* k_pool, uint16_t* k_po
  * (start_pos + t_idx) / bsn; top_k picks of the highest score, the lower
  * block index on ties, never a -inf (or NaN) score; the picks sorted
  * ascending, then -1 padding. */
+/* The block scores of one (kv_head, t_idx) into sc[n_blocks] (the first
+ * half of build_block_index_ms_kern, sparse_index.cuh:243-290). */
+static void block_scores_one(const uint16_t* q, const uint16_t* k_pool, const uint16_t* k_pool_max,
+                             float* sc, int h, int t, int num_q, int num_kv, int hd, int start_pos,
+                             int bsn, int n_blocks, int n_blocks_stride, float beta) {
+    const int gqa = num_q / num_kv;
+    const float inv_g = 1.0f / (float)gqa;
+    float* qa = (float*)malloc(sizeof(float) * hd);
+    for (int c = 0; c < hd; c++) {
+        float s = 0.0f;
+        for (int g = 0; g < gqa; g++)
+            s += or_f16_to_f32(q[((int64_t)t * num_q + h * gqa + g) * hd + c]);
+        qa[c] = or_f16_to_f32(or_f32_to_f16(s * inv_g));
+    }
+    const int causal_max = (start_pos + t) / bsn;
+    for (int n = 0; n < n_blocks; n++) {
+        const uint16_t* mn = k_pool + ((int64_t)h * n_blocks_stride + n) * hd;
+        const uint16_t* mx = k_pool_max + ((int64_t)h * n_blocks_stride + n) * hd;
+        float s_mean = 0.0f, s_max = 0.0f;
+        for (int c = 0; c < hd; c += 2) {
+            s_mean += qa[c] * or_f16_to_f32(mn[c]) + qa[c + 1] * or_f16_to_f32(mn[c + 1]);
+            s_max += qa[c] * or_f16_to_f32(mx[c]) + qa[c + 1] * or_f16_to_f32(mx[c + 1]);
+        }
+        float s = fmaxf(s_mean, beta * s_max);
+        if (n > causal_max) s = -INFINITY;
+        sc[n] = s;
+    }
+    free(qa);
+}
+
+/* Block scores [num_kv][sub_n][n_blocks] as build_block_index_ms_kern forms them. */
+void or_block_scores_ms(const uint16_t* q, const uint16_t* k_pool, const uint16_t* k_pool_max,
+                        float* scores, int num_q, int num_kv, int hd, int sub_n, int start_pos,
+                        int bsn, int n_blocks, int n_blocks_stride, float beta) {
+    #pragma omp parallel for collapse(2) schedule(static)
+    for (int h = 0; h < num_kv; h++)
+        for (int t = 0; t < sub_n; t++)
+            block_scores_one(q, k_pool, k_pool_max, scores + ((int64_t)h * sub_n + t) * n_blocks, h, t,
+                             num_q, num_kv, hd, start_pos, bsn, n_blocks, n_blocks_stride, beta);
+}
+
 void or_block_index_ms(const uint16_t* q, const uint16_t* k_pool, const uint16_t* k_pool_max,
                        int32_t* block_index, int num_q, int num_kv, int hd, int sub_n,
                        int sub_n_max, int start_pos, int top_k, int bsn, int n_blocks,
                        int n_blocks_stride, float beta) {
-    const int gqa = num_q / num_kv;
-    const float inv_g = 1.0f / (float)gqa;
     #pragma omp parallel for collapse(2) schedule(static)
     for (int h = 0; h < num_kv; h++) {
         for (int t = 0; t < sub_n; t++) {
-            float* qa = (float*)malloc(sizeof(float) * hd);
             float* sc = (float*)malloc(sizeof(float) * (n_blocks > 0 ? n_blocks : 1));
-            for (int c = 0; c < hd; c++) {
-                float s = 0.0f;
-                for (int g = 0; g < gqa; g++)
-                    s += or_f16_to_f32(q[((int64_t)t * num_q + h * gqa + g) * hd + c]);
-                qa[c] = or_f16_to_f32(or_f32_to_f16(s * inv_g));
-            }
-            const int causal_max = (start_pos + t) / bsn;
-            for (int n = 0; n < n_blocks; n++) {
-                const uint16_t* mn = k_pool + ((int64_t)h * n_blocks_stride + n) * hd;
-                const uint16_t* mx = k_pool_max + ((int64_t)h * n_blocks_stride + n) * hd;
-                float s_mean = 0.0f, s_max = 0.0f;
-                for (int c = 0; c < hd; c += 2) {
-                    s_mean += qa[c] * or_f16_to_f32(mn[c]) + qa[c + 1] * or_f16_to_f32(mn[c + 1]);
-                    s_max += qa[c] * or_f16_to_f32(mx[c]) + qa[c + 1] * or_f16_to_f32(mx[c + 1]);
-                }
-                float s = fmaxf(s_mean, beta * s_max);
-                if (n > causal_max) s = -INFINITY;
-                sc[n] = s;
-            }
+            block_scores_one(q, k_pool, k_pool_max, sc, h, t, num_q, num_kv, hd, start_pos, bsn,
+                             n_blocks, n_blocks_stride, beta);
             int32_t* row = block_index + ((int64_t)h * sub_n_max + t) * top_k;
             int k = 0;
             for (; k < top_k; k++) {
@@ -1020,7 +1041,6 @@ void or_block_index_ms(const uint16_t* q, const uint16_t* k_pool, const uint16_t
                 while (j > 0 && row[j - 1] > x) { row[j] = row[j - 1]; j--; }
                 row[j] = x;
             }
-            free(qa);
             free(sc);
         }
     }

@@ -145,6 +145,11 @@ void or_dfk2_dequant(const int8_t* q, const uint16_t* s, uint16_t* out, int64_t 
 void or_tq3_kpool_update(const or_block_tq3* k, uint16_t* k_pool, uint16_t* k_pool_max,
                          int num_kv, int hd, int total_kv, int blk_lo, int n_blocks_stride,
                          int bsn);
+/* block scores [num_kv][sub_n][n_blocks] of build_block_index_ms_kern
+ * (sparse_index.cuh:243-290): the first half of or_block_index_ms. */
+void or_block_scores_ms(const uint16_t* q, const uint16_t* k_pool, const uint16_t* k_pool_max,
+                        float* scores, int num_q, int num_kv, int hd, int sub_n, int start_pos,
+                        int bsn, int n_blocks, int n_blocks_stride, float beta);
 void or_block_index_ms(const uint16_t* q, const uint16_t* k_pool, const uint16_t* k_pool_max,
                        int32_t* block_index, int num_q, int num_kv, int hd, int sub_n,
                        int sub_n_max, int start_pos, int top_k, int bsn, int n_blocks,

@@ -70,7 +70,6 @@ constexpr int kLdsBytes = 2 * kBufBytes;
 static_assert(2 * kLdsBytes <= 160 * 1024, "two prefill workgroups must fit one CU");
 
 typedef __attribute__((address_space(3))) void lds_void_t;
-typedef _Float16 h2_t __attribute__((ext_vector_type(2)));
 
 // Value order inside a 32-key half: key 8a + 4h + c sits at position
 // 16(a/2) + 8h + 4(a%2) + c, so the 8 keys one lane contributes to a value
@@ -349,9 +348,7 @@ __global__ __launch_bounds__(64 * WAVES, 2) void prefill_attn_kernel(PrefillArgs
 #pragma unroll
       for (int i = 0; i < 8; i++) pb[i] = (_Float16)__builtin_amdgcn_exp2f(__builtin_fmaf(sd[8 * sg + i], sl_w, -msafe));
 #pragma unroll
-      for (int i = 0; i < 4; i++)
-        lsum = __builtin_amdgcn_fdot2(h2_t{pb[2 * i], pb[2 * i + 1]}, h2_t{(_Float16)1.0f, (_Float16)1.0f},
-                                      lsum, false);
+      for (int i = 0; i < 8; i++) lsum += (float)pb[i];
       const int slot = (2 * sg + hh) ^ ((tok >> 2) & 3);
 #pragma unroll
       for (int d = 0; d < 8; d++) {

@@ -401,6 +401,7 @@ int qkv_block_index_ms(const uint16_t* q, const uint16_t* k_pool, const uint16_t
   a.n_blocks = n_blocks;
   a.stride = n_blocks_stride;
   a.beta = beta;
+  a.inv_gqa = 1.0f / (float)(num_q / num_kv);
   return launch_status(qkv::launch_block_index(a, static_cast<float*>(workspace), stream));
 }
 

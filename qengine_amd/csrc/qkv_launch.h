@@ -77,6 +77,7 @@ struct BlockIndexArgs {
   int32_t* block_index;      // [num_kv][sub_n_max][top_k]
   int num_q, num_kv, sub_n, sub_n_max, start_pos, top_k, bsn, n_blocks, stride;
   float beta;
+  float inv_gqa;             // 1.0f / GQA (the reference's compile-time constant)
 };
 // scores: workspace of block_index_workspace_bytes (block scores [num_kv][sub_n][n_blocks])
 hipError_t launch_block_index(const BlockIndexArgs& a, float* scores, hipStream_t stream);

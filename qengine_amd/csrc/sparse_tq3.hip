@@ -69,8 +69,6 @@ __global__ __launch_bounds__(kSpThreads) void tq3_kpool_kernel(KpoolArgs a) {
   a.k_pool_max[ob] = (uint16_t)f2h(best_val);
 }
 
-typedef _Float16 h2_t __attribute__((ext_vector_type(2)));
-
 constexpr int kScBlocks = 32;          // blocks scored per workgroup
 constexpr int kScQueries = 8;          // queries scored per workgroup
 constexpr int kScPitchDw = 129;        // staged pool row: 128 dwords + 1 (conflict-free lanes)
@@ -80,8 +78,9 @@ constexpr int kScPitchDw = 129;        // staged pool row: 128 dwords + 1 (confl
 // (fp16-rounded, as the reference forms them, sparse_index.cuh:243-252) sit in
 // LDS as fp16 pairs; thread (t, b) runs block b's two dot products for query
 // t over the 128 pairs in the reference's order: each pair's products are
-// exact and their sum is rounded once (one v_dot2_f32_f16 with a zero
-// addend), then added to the running fp32 sum.  Scores (-inf past the
+// exact and their sum is rounded once (an FMA onto the other exact product),
+// then added to the running fp32 sum.  (v_dot2_f32_f16 does not give that
+// rounding.)  Scores (-inf past the
 // query's causal block) go to the workspace [num_kv][sub_n][n_blocks].
 __global__ __launch_bounds__(kSpThreads) void block_score_kernel(BlockIndexArgs a, float* scores) {
   __shared__ uint32_t rows_mean[kScBlocks * kScPitchDw];
@@ -107,7 +106,7 @@ __global__ __launch_bounds__(kSpThreads) void block_score_kernel(BlockIndexArgs 
     d[2] = v.z;
     d[3] = v.w;
   }
-  const float inv_g = 1.0f / (float)gqa;
+  const float inv_g = a.inv_gqa;
   for (int i = tid; i < nt * kSpHD / 2; i += kSpThreads) {
     const int tq = i / (kSpHD / 2), c = 2 * (i - tq * (kSpHD / 2));
     float s0 = 0.0f, s1 = 0.0f;
@@ -116,7 +115,11 @@ __global__ __launch_bounds__(kSpThreads) void block_score_kernel(BlockIndexArgs 
       s0 += h2f(qr[0]);
       s1 += h2f(qr[1]);
     }
-    qa2[i] = f2h(s0 * inv_g) | (f2h(s1 * inv_g) << 16);
+    // the reference rounds s * (1/GQA) to fp32, then to fp16: the empty asm
+    // keeps the fp32 product (no fused fp16-rounding mixed FMA)
+    float p0 = s0 * inv_g, p1 = s1 * inv_g;
+    asm volatile("" : "+v"(p0), "+v"(p1));
+    qa2[i] = f2h(p0) | (f2h(p1) << 16);
   }
   __syncthreads();
   // thread -> (query tq, block b): 32 lanes of a wave are the 32 blocks of one query
@@ -128,9 +131,10 @@ __global__ __launch_bounds__(kSpThreads) void block_score_kernel(BlockIndexArgs 
     float s_mean = 0.0f, s_max = 0.0f;
 #pragma unroll 16
     for (int c2 = 0; c2 < kSpHD / 2; c2++) {
-      const h2_t qq = __builtin_bit_cast(h2_t, q[c2]);
-      s_mean += __builtin_amdgcn_fdot2(qq, __builtin_bit_cast(h2_t, mn[c2]), 0.0f, false);
-      s_max += __builtin_amdgcn_fdot2(qq, __builtin_bit_cast(h2_t, mx[c2]), 0.0f, false);
+      const uint32_t qw = q[c2], m2 = mn[c2], x2 = mx[c2];
+      const float q0 = h2f(qw & 0xffffu), q1 = h2f(qw >> 16);
+      s_mean += __builtin_fmaf(q0, h2f(m2 & 0xffffu), q1 * h2f(m2 >> 16));
+      s_max += __builtin_fmaf(q0, h2f(x2 & 0xffffu), q1 * h2f(x2 >> 16));
     }
     const int n = b0 + b, t = t0 + tq;
     if (n < a.n_blocks) {

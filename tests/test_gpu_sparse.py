@@ -112,6 +112,30 @@ def test_block_index_many_blocks_bitexact(dev, nb, top_k, distinct):
     assert np.array_equal(got, exp)
 
 
+def test_block_scores_bitexact(dev):
+    """The block scores the selection works from (the workspace's first
+    num_kv * sub_n * n_blocks floats) bit for bit against the oracle's."""
+    import torch
+    from qengine_amd import kvcache
+    rng = np.random.default_rng(77)
+    nb, sub = 700, 16
+    kp = (rng.standard_normal((NKV, nb, HD)) * 0.3).astype(np.float16).view(np.uint16)
+    kx = (rng.standard_normal((NKV, nb, HD)) * 0.6).astype(np.float16).view(np.uint16)
+    start = 64 * (nb - 2) - sub
+    q = q_f16(rng, sub, 24, HD)
+    wsb = int(kvcache.lib().qkv_block_index_ms_workspace_bytes(NKV, sub, nb))
+    ws = torch.empty(wsb, dtype=torch.uint8, device=dev)
+    bi = torch.full((NKV, sub, 8), 7, dtype=torch.int32, device=dev)
+    kvcache.block_index_ms(_dev(q.view(np.uint16), dev), _dev(kp, dev), _dev(kx, dev), bi,
+                           num_q=24, num_kv=NKV, sub_n=sub, start_pos=start, top_k=8,
+                           n_blocks=nb, beta=0.5, workspace=ws)
+    torch.cuda.synchronize()
+    got = ws[:NKV * sub * nb * 4].cpu().numpy().view(np.float32).reshape(NKV, sub, nb)
+    exp = O.block_scores_ms(q, kp, kx, num_q=24, num_kv=NKV, hd=HD, sub_n=sub, start_pos=start,
+                            n_blocks=nb, beta=0.5)
+    assert np.array_equal(got.view(np.uint32), exp.view(np.uint32))
+
+
 def test_block_index_ties_bitexact(dev):
     rng = np.random.default_rng(41)
     n, sub = 64 * 30, 4

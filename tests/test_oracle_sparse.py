@@ -98,6 +98,51 @@ def test_block_index_vs_f64_ranking(num_q, top_k):
             assert set(must) <= set(sel) and not (set(never) & set(sel)), (h, t)
 
 
+def test_block_scores_pairwise_order_and_selection():
+    """block_scores_ms against a numpy float32 restatement of the pair order
+    (exact fp16 x fp16 products, each pair's sum rounded once, then added to
+    the running sum), bit for bit; -inf past each query's causal block; and
+    block_index_ms is the first top_k of (score descending, block ascending)
+    over those scores, listed ascending."""
+    n, sub, start = 64 * 40 + 5, 4, 64 * 33 + 2
+    rng, kb, _ = _cache(8, n)
+    nb = (n + 63) // 64
+    kp, kx = _pools(kb, n, nb)
+    q = q_f16(rng, sub, 16, HD)
+    sc = O.block_scores_ms(q, kp, kx, num_q=16, num_kv=NKV, hd=HD, sub_n=sub, start_pos=start,
+                           n_blocks=nb, beta=0.5)
+    gqa = 16 // NKV
+    qf = O.f16_to_f32(q.view(np.uint16).reshape(-1)).reshape(q.shape)
+    for h in range(NKV):
+        mn = O.f16_to_f32(kp[h, :nb].reshape(-1)).reshape(nb, HD)
+        mx = O.f16_to_f32(kx[h, :nb].reshape(-1)).reshape(nb, HD)
+        for t in range(sub):
+            acc = np.zeros(HD, np.float32)
+            for g in range(gqa):
+                acc = acc + qf[t, h * gqa + g]
+            qa = np.float16(acc * np.float32(1.0 / gqa)).astype(np.float32)
+            s_mean = np.zeros(nb, np.float32)
+            s_max = np.zeros(nb, np.float32)
+            for c in range(0, HD, 2):
+                s_mean = s_mean + (qa[c] * mn[:, c] + qa[c + 1] * mn[:, c + 1])
+                s_max = s_max + (qa[c] * mx[:, c] + qa[c + 1] * mx[:, c + 1])
+            ref = np.maximum(s_mean, np.float32(0.5) * s_max)
+            cmax = (start + t) // 64
+            ref[cmax + 1:] = -np.inf
+            assert np.array_equal(sc[h, t].view(np.uint32), ref.view(np.uint32)), (h, t)
+    for top_k in (1, 7, 40):
+        bi = O.block_index_ms(q, kp, kx, num_q=16, num_kv=NKV, hd=HD, sub_n=sub, sub_n_max=sub,
+                              start_pos=start, top_k=top_k, n_blocks=nb)
+        for h in range(NKV):
+            for t in range(sub):
+                v = sc[h, t]
+                ok = np.nonzero(v > -np.inf)[0]
+                order = ok[np.lexsort((ok, -v[ok]))][:top_k]
+                exp = np.full(top_k, -1, np.int32)
+                exp[:len(order)] = np.sort(order)
+                assert np.array_equal(bi[h, t], exp), (top_k, h, t)
+
+
 def test_block_index_ties_and_padding():
     n = 64 * 10
     rng, kb, _ = _cache(5, n)
