@@ -518,6 +518,12 @@ __global__ __launch_bounds__(kThreads, 1) void tq3_attn_kernel(AttnArgs p, uint1
                           : q_extent;
     q_raw = __builtin_amdgcn_raw_buffer_load_b128(rq, qoff, 0, 0);
   }
+  // waves 0..3 issue their first tile's loads as soon as the query has
+  // arrived (so it does not queue behind them), ahead of the table build
+  // and the rotation; waves 4..7 issue theirs after the setup barrier.
+  __builtin_amdgcn_s_waitcnt(0);
+  TileRegs tr;
+  if (wave < 4) load_tile(p, wave_tile_row(ts0), p.num_kv, h, lane, row, col, tr);
   // centroid-pair table: entry e = (centroid[e & 7], centroid[(e >> 3) & 7])
   // as fp16, from immediates (wave-uniform values); wave w writes every lane's
   // copy of entries 32w .. 32w+31
@@ -585,9 +591,6 @@ __global__ __launch_bounds__(kThreads, 1) void tq3_attn_kernel(AttnArgs p, uint1
   // before the second (waves 4..7), so that across the chip the first waves'
   // tiles arrive in the first half of the stream and are computed while the
   // second waves' tiles are still in flight.
-  TileRegs tr;
-  if (wave < 4) load_tile(p, wave_tile_row(ts0), p.num_kv, h, lane, row, col, tr);
-  __syncthreads();
   if (wave >= 4) load_tile(p, wave_tile_row(ts0), p.num_kv, h, lane, row, col, tr);
   // qa[s], slice s = 4j+u: column `col`, element i = dim 128j + 8(4*row+u) + i
   h8_t qa[8];
