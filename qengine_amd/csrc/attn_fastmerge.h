@@ -30,6 +30,10 @@ namespace qkv {
 
 constexpr int kCoherent = 1 | 16;   // sc0 | sc1
 
+// Diagnostic build (-DQKV_PHASE_TRACE): byte offset, inside the merge area,
+// where a merger leaves the time its polls completed.
+constexpr int kTracePolledByte = 16384;
+
 // Record index of (q head, query t, chunk) in the fast-path workspace.
 __device__ __forceinline__ long rec_index(const AttnArgs& p, int qh, int t, int chunk) {
   return (long)(qh * p.sub_n + t) * p.n_slots + chunk;
@@ -136,6 +140,11 @@ __device__ bool merge_unit(float* red, f2_t* mls, const AttnArgs& p, __amdgpu_bu
     }
     __builtin_amdgcn_s_sleep(1);
   }
+#ifdef QKV_PHASE_TRACE
+  if (tid == 0)
+    *reinterpret_cast<uint64_t*>(reinterpret_cast<uint8_t*>(red) + kTracePolledByte) =
+        __builtin_amdgcn_s_memrealtime();
+#endif
   if (!complete) {
     if (tid < n && seen)   // the tags this merger saw will not be read again
       __builtin_amdgcn_raw_buffer_store_b32(0u, rml, (uint32_t)((base + tid) * kRecMlBytes + 8 + 4 * blk),

@@ -53,6 +53,33 @@ constexpr int kWaves = 8;
 constexpr int kThreads = 64 * kWaves;
 constexpr int kHD = 256;
 
+// Phase stamps of the fast path (a diagnostic build, compiled with
+// -DQKV_PHASE_TRACE; the product build has none of this).  Every wave keeps
+// s_memrealtime values (100 MHz, one clock for the whole GPU) at the phase
+// boundaries below in registers and stores them once, at the end of the
+// kernel, to qkv_phase_stamps[workgroup][wave][16]; slot 15 holds the XCD
+// the workgroup ran on.  Workgroups past kTraceMaxWgs are not recorded.
+enum TracePhase {
+  kPhEntry = 0,      // kernel entry
+  kPhQuery = 1,      // the query has arrived
+  kPhSetup = 2,      // table and rotated query ready (setup barrier passed)
+  kPhScores = 3,     // the wave's first tile: scores done
+  kPhSoftmax = 4,    // the wave's first tile: staging and softmax done
+  kPhTiles = 5,      // every tile of the wave done
+  kPhMerged = 6,     // in-workgroup merge done (records stored)
+  kPhPublished = 7,  // tags stored
+  kPhPolled = 8,     // mergers: every record of the unit seen
+  kPhEnd = 9,        // the workgroup is done (mergers: output stored)
+  kPhXcd = 15
+};
+#ifdef QKV_PHASE_TRACE
+constexpr int kTraceMaxWgs = 4096;
+__device__ uint64_t qkv_phase_stamps[kTraceMaxWgs * kWaves * 16];
+#define QKV_STAMP(k) (trace_st[k] = __builtin_amdgcn_s_memrealtime())
+#else
+#define QKV_STAMP(k) ((void)0)
+#endif
+
 // Per-wave staging of one 64-key tile, in dwords; every row holds 64 keys
 // (key = position in the tile) at a pitch of 68, so 16 lanes reading 16-byte
 // pieces of 16 different rows hit 16 disjoint bank quads.
@@ -83,6 +110,8 @@ constexpr int kLdsMergeML = kLdsMergeO + kWaves * 16 * kHD * 4;
 constexpr int kLdsMergeEnd = kLdsMergeML + 512 * 4;
 constexpr int kLdsTotal = kLdsTileEnd;
 static_assert(kLdsMergeEnd <= kLdsQ, "merge area must not reach the query scratch");
+static_assert(kTracePolledByte >= kWaves * 128 * 4 && kTracePolledByte + 8 <= kLdsMergeML - kLdsMergeO,
+              "the merger's trace slot lies in the merge area, past the reduction area");
 
 // merge-area float offsets (ML): m[w][16], l[w][16], M[16], L[16]
 constexpr int kMlW0 = 0, kMlLw0 = 16 * kWaves, kMlM = 32 * kWaves, kMlL = 32 * kWaves + 16;
@@ -365,6 +394,10 @@ template <int MODE>
 __global__ __launch_bounds__(kThreads, 1) void tq3_attn_kernel(AttnArgs p, uint16_t* out) {
   // static LDS: table and tile offsets fold into the instructions' offset field
   __shared__ __attribute__((aligned(16))) uint8_t lds[kLdsTotal];
+#ifdef QKV_PHASE_TRACE
+  uint64_t trace_st[10] = {0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
+#endif
+  QKV_STAMP(kPhEntry);
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int gqa = p.num_q / p.num_kv;
@@ -522,6 +555,7 @@ __global__ __launch_bounds__(kThreads, 1) void tq3_attn_kernel(AttnArgs p, uint1
   // arrived (so it does not queue behind them), ahead of the table build
   // and the rotation; waves 4..7 issue theirs after the setup barrier.
   __builtin_amdgcn_s_waitcnt(0);
+  QKV_STAMP(kPhQuery);
   TileRegs tr;
   if (wave < 4) load_tile(p, wave_tile_row(ts0), p.num_kv, h, lane, row, col, tr);
   // centroid-pair table: entry e = (centroid[e & 7], centroid[(e >> 3) & 7])
@@ -587,6 +621,7 @@ __global__ __launch_bounds__(kThreads, 1) void tq3_attn_kernel(AttnArgs p, uint1
     }
   }
   __syncthreads();
+  QKV_STAMP(kPhSetup);
   // ---- first tile: the first wave of each SIMD (waves 0..3) issues its loads
   // before the second (waves 4..7), so that across the chip the first waves'
   // tiles arrive in the first half of the stream and are computed while the
@@ -626,6 +661,7 @@ __global__ __launch_bounds__(kThreads, 1) void tq3_attn_kernel(AttnArgs p, uint1
                      group_operand<0>(lds, ac, kq[g][1]), sa[g][0], sa[g][1]);
     }
 
+    if constexpr (first) QKV_STAMP(kPhScores);
     // ---------------- staging: key norms, value rows (lane = key ts + lane) ----------------
     if (row == 0) {
 #pragma unroll
@@ -718,6 +754,7 @@ __global__ __launch_bounds__(kThreads, 1) void tq3_attn_kernel(AttnArgs p, uint1
         for (int r = 0; r < 4; r++) acc[t][r] *= cr[r];
     }
 
+    if constexpr (first) QKV_STAMP(kPhSoftmax);
     // ---------------- values ----------------
     // 32-key chunk c2: MFMA k index i <-> key 32*c2 + 4*row + i (i < 4) and
     // 32*c2 + 16 + 4*row + (i - 4) (i >= 4), in both operands.  A = p * value
@@ -760,6 +797,7 @@ __global__ __launch_bounds__(kThreads, 1) void tq3_attn_kernel(AttnArgs p, uint1
     for (int t = 0; t < 16; t++) acc[t] = f4_t{0.f, 0.f, 0.f, 0.f};
   }
   lsum = xrow_sum(lsum);
+  QKV_STAMP(kPhTiles);
 
   // ---------------- merge the 4 waves in LDS ----------------
   __syncthreads();
@@ -819,14 +857,50 @@ __global__ __launch_bounds__(kThreads, 1) void tq3_attn_kernel(AttnArgs p, uint1
   }
 
   // ---------------- fast path: tagged records, designated mergers ----------------
+  QKV_STAMP(kPhMerged);
   if (has_work) publish_records(p, rml, h, rec_t0, rows, rec_chunk);
+  QKV_STAMP(kPhPublished);
+#ifdef QKV_PHASE_TRACE
+  if (threadIdx.x == 0) *reinterpret_cast<uint64_t*>(lds + kLdsMergeO + kTracePolledByte) = 0;
+#endif
   using ML = MergeLayout<kThreads>;
   static_assert(kLdsMergeO + ML::kRedFloats * 4 <= kLdsMergeML, "merge reduction must fit");
   merge_phase<kThreads, true>(reinterpret_cast<float*>(lds + kLdsMergeO),
                               reinterpret_cast<f2_t*>(lds + kLdsMergeML), p, rml, ro, out);
+#ifdef QKV_PHASE_TRACE
+  __syncthreads();
+  trace_st[kPhPolled] = *reinterpret_cast<const uint64_t*>(lds + kLdsMergeO + kTracePolledByte);
+  QKV_STAMP(kPhEnd);
+  if (lane < 10 && blockIdx.x < kTraceMaxWgs) {
+    uint64_t v = 0;
+#pragma unroll
+    for (int i = 0; i < 10; i++) v = lane == i ? trace_st[i] : v;
+    qkv_phase_stamps[(blockIdx.x * kWaves + wave) * 16 + lane] = v;
+  }
+  if (lane == 0 && blockIdx.x < kTraceMaxWgs)
+    qkv_phase_stamps[(blockIdx.x * kWaves + wave) * 16 + kPhXcd] =
+        __builtin_amdgcn_s_getreg((3 << 11) | 20) & 15u;   // HW_REG_XCC_ID bits 3:0
+#endif
 }
 
 size_t tq3_attn_lds_bytes() { return kLdsTotal; }
+
+#ifdef QKV_PHASE_TRACE
+}  // namespace qkv
+// Diagnostic build only: copies the phase stamps of the last fast-path
+// launch (n <= kTraceMaxWgs * 8 * 16 values) to host memory.
+extern "C" int qkv_debug_phase_stamps(uint64_t* host, size_t n) {
+  if (host == nullptr || n > sizeof(qkv::qkv_phase_stamps) / 8) return -1;
+  return hipMemcpyFromSymbol(host, HIP_SYMBOL(qkv::qkv_phase_stamps), n * 8, 0, hipMemcpyDeviceToHost) ==
+                 hipSuccess ? 0 : -6;
+}
+extern "C" int qkv_debug_phase_clear() {
+  void* p = nullptr;
+  if (hipGetSymbolAddress(&p, HIP_SYMBOL(qkv::qkv_phase_stamps)) != hipSuccess) return -6;
+  return qkv::launch_fill_zero(p, sizeof(qkv::qkv_phase_stamps), nullptr) == hipSuccess ? 0 : -6;
+}
+namespace qkv {
+#endif
 
 // ---- the allocation-free decode's scratch ----------------------------------
 // One fixed-size array per GPU, holding the fast path's workspace layout
