@@ -16,7 +16,11 @@
 // computed while the second one streams.  Per tile:
 //   scores  v_mfma_f32_16x16x32_f16, A = key codes of 16 keys x 32 dims, B =
 //           rotated query (columns = heads, held in 32 VGPRs for the whole
-//           kernel): lane (key, octet o) reads the 12 aligned bytes holding
+//           kernel; the fp16 rounding and the remainder of the query either
+//           share the 16 columns, or, for calls with more than 8 / GQA
+//           queries, fill them with 16 / GQA queries each, the remainders
+//           read from LDS into a second product chained onto the first):
+//           lane (key, octet o) reads the 12 aligned bytes holding
 //           code groups 4o..4o+3 of each 128-block and decodes centroid pairs
 //           through a per-lane LDS table.  One accumulator per 128-block, each
 //           scaled by its block norm (which carries the softmax scale).
@@ -155,20 +159,32 @@ __device__ __forceinline__ h8_t group_operand(const uint8_t* lds, uint32_t (&ac)
 
 // Score MFMAs for one 16-key group: 4 slices per block, one accumulator per
 // block.  Slice U+1's table reads are issued before slice U's MFMAs.
-template <int U>
+// CHAIN: the query remainders (lo) have MFMA columns of their own in a second
+// product chained onto the same accumulator; slice s of this lane's lo
+// operand is at LDS byte qlo + 1024 s.
+template <int U, bool CHAIN>
 __device__ __forceinline__ void score_group(const uint8_t* lds, uint32_t (&ac)[4], const uint32_t (&k0)[3],
                                             const uint32_t (&k1)[3], const h8_t (&qa)[8],
+                                            uint32_t qlo,
                                             const h8_t& b0, const h8_t& b1, f4_t& a0, f4_t& a1) {
   if constexpr (U < 4) {
-    h8_t n0, n1;
+    h8_t n0, n1, l0, l1;
+    if constexpr (CHAIN) {
+      l0 = *reinterpret_cast<const h8_t*>(lds + qlo + 1024 * U);
+      l1 = *reinterpret_cast<const h8_t*>(lds + qlo + 1024 * (4 + U));
+    }
     if constexpr (U < 3) {
       n0 = group_operand<U + 1>(lds, ac, k0);
       n1 = group_operand<U + 1>(lds, ac, k1);
     }
     a0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(b0, qa[U], a0, 0, 0, 0);
     a1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(b1, qa[4 + U], a1, 0, 0, 0);
+    if constexpr (CHAIN) {
+      a0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(b0, l0, a0, 0, 0, 0);
+      a1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(b1, l1, a1, 0, 0, 0);
+    }
     __builtin_amdgcn_sched_barrier(0);
-    if constexpr (U < 3) score_group<U + 1>(lds, ac, k0, k1, qa, n0, n1, a0, a1);
+    if constexpr (U < 3) score_group<U + 1, CHAIN>(lds, ac, k0, k1, qa, qlo, n0, n1, a0, a1);
   }
 }
 
@@ -390,7 +406,10 @@ __device__ void finish_rows(const uint8_t* lds, const AttnArgs& p, int h, int t,
 // MODE 0: fast path (final fp16 rows).  MODE 1: reference split partials.
 // MODE 2: block-sparse split partials (attention.cuh:2193-2433): one query
 // per workgroup (qpw = 1), split z over the query's selected 64-key blocks.
-template <int MODE>
+// CHAIN (fast path, several queries): 16 / GQA queries per workgroup, every
+// MFMA column a real (query, head); the remainders ride in a chained second
+// score product (see score_group).
+template <int MODE, bool CHAIN = false>
 __global__ __launch_bounds__(kThreads, 1) void tq3_attn_kernel(AttnArgs p, uint16_t* out) {
   // static LDS: table and tile offsets fold into the instructions' offset field
   __shared__ __attribute__((aligned(16))) uint8_t lds[kLdsTotal];
@@ -575,6 +594,7 @@ __global__ __launch_bounds__(kThreads, 1) void tq3_attn_kernel(AttnArgs p, uint1
     }
   }
   uint32_t ac[4] = {lane4, lane4, lane4, lane4};   // table address chains
+  uint32_t q_lo[4] = {0u, 0u, 0u, 0u};              // CHAIN: this thread's query remainders
   {
     // rotated query: fp16 in LDS scratch (q_unit), so that each lane's A
     // operand slice is one 16-byte read
@@ -584,7 +604,37 @@ __global__ __launch_bounds__(kThreads, 1) void tq3_attn_kernel(AttnArgs p, uint1
     // in fp32, so the rotated query is carried to ~2^-22 (real columns <= 8).
     uint16_t* qs = reinterpret_cast<uint16_t*>(lds + kLdsQ);
     const int o = q_part >> 2, u = q_part & 3;   // elements part*8..+7 = code group 4*o + u
-    if (q_col >= 8) {
+    if (CHAIN) {
+      // every column is a (query, head) of its own; the remainders stay in
+      // registers until the rounded query has been read (then they replace it)
+      uint32_t pk[4] = {0u, 0u, 0u, 0u};
+      if (q_col < rows_used) {
+        float x[8];
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+          x[2 * i] = h2f(q_raw[i] & 0xffffu);
+          x[2 * i + 1] = h2f(q_raw[i] >> 16);
+        }
+        const uint32_t sbits = sign_word_sel(q_part >> 2) >> (8 * (q_part & 3));
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+          const bool pos = (sbits >> i) & 1u;
+          x[i] = pos ? x[i] : -x[i];
+        }
+        wht8_inreg(x);
+        wht_xor_lanes16(x, lane);
+        const float rs = wht_scale();
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+          const float a = x[2 * i] * rs, b = x[2 * i + 1] * rs;
+          const uint32_t ha = f2h(a), hb = f2h(b);
+          pk[i] = ha | (hb << 16);
+          q_lo[i] = f2h(a - h2f(ha)) | (f2h(b - h2f(hb)) << 16);
+        }
+      }
+      *reinterpret_cast<uint4*>(qs + q_unit(q_col, 4 * q_blk + u, o) * 8) =
+          make_uint4(pk[0], pk[1], pk[2], pk[3]);
+    } else if (q_col >= 8) {
       // columns 8..15 are written by the waves of columns 0..7
     } else if (2 * wave >= rows_used) {
       // a wave whose two columns are both dead writes zeros (hi and lo)
@@ -635,6 +685,19 @@ __global__ __launch_bounds__(kThreads, 1) void tq3_attn_kernel(AttnArgs p, uint1
     for (int s = 0; s < 8; s++)   // dead columns were written as zeros
       qa[s] = *reinterpret_cast<const h8_t*>(qs + q_unit(col, s, row) * 8);
   }
+  // CHAIN: the remainders replace the rounded query in the scratch, unswizzled
+  // (written once): 16-byte unit (s * 4 + o) * 16 + c holds elements
+  // 8(4o+u)..+7 of 128-block j of column c, s = 4j + u
+  const uint32_t qlo = (uint32_t)(kLdsQ + row * 256 + col * 16);
+  if constexpr (CHAIN) {
+    __syncthreads();
+    {
+      const int o = q_part >> 2, u = q_part & 3;
+      *reinterpret_cast<uint4*>(lds + kLdsQ + (((4 * q_blk + u) * 4 + o) * 16 + q_col) * 16) =
+          make_uint4(q_lo[0], q_lo[1], q_lo[2], q_lo[3]);
+    }
+    __syncthreads();
+  }
 
   const float scale2 = p.scale_log2 * kCenScaleInv;
   float m2 = -INFINITY;   // running max of head `col` (base-2 units)
@@ -657,8 +720,8 @@ __global__ __launch_bounds__(kThreads, 1) void tq3_attn_kernel(AttnArgs p, uint1
     for (int g = 0; g < 4; g++) {
       sa[g][0] = f4_t{0.f, 0.f, 0.f, 0.f};
       sa[g][1] = f4_t{0.f, 0.f, 0.f, 0.f};
-      score_group<0>(lds, ac, kq[g][0], kq[g][1], qa, group_operand<0>(lds, ac, kq[g][0]),
-                     group_operand<0>(lds, ac, kq[g][1]), sa[g][0], sa[g][1]);
+      score_group<0, CHAIN>(lds, ac, kq[g][0], kq[g][1], qa, qlo, group_operand<0>(lds, ac, kq[g][0]),
+                            group_operand<0>(lds, ac, kq[g][1]), sa[g][0], sa[g][1]);
     }
 
     if constexpr (first) QKV_STAMP(kPhScores);
@@ -707,7 +770,8 @@ __global__ __launch_bounds__(kThreads, 1) void tq3_attn_kernel(AttnArgs p, uint1
 #pragma unroll
       for (int r = 0; r < 4; r++) {
         s[g][r] = k0[r] * sa[g][0][r] + k1[r] * sa[g][1][r];
-        s[g][r] += dpp_f<0x128>(s[g][r]);   // + the lo half of the query (column + 8, row_ror:8)
+        if constexpr (!CHAIN)
+          s[g][r] += dpp_f<0x128>(s[g][r]);   // + the lo half of the query (column + 8, row_ror:8)
       }
     }
     if (!dense) {
@@ -935,7 +999,9 @@ hipError_t launch_tq3_attn(const AttnArgs& a, int mode, uint16_t* out, hipStream
   const int groups = (a.sub_n + a.qpw - 1) / a.qpw * a.n_chunks;
   const int n_wg = ((groups + 7) / 8) * 8 * a.num_kv;
   dim3 grid(n_wg), block(kThreads);
-  if (mode == 0)
+  if (mode == 0 && a.qpw * (a.num_q / a.num_kv) > 8)
+    hipLaunchKernelGGL((tq3_attn_kernel<0, true>), grid, block, 0, stream, a, out);
+  else if (mode == 0)
     hipLaunchKernelGGL((tq3_attn_kernel<0>), grid, block, 0, stream, a, out);
   else if (mode == 1)
     hipLaunchKernelGGL((tq3_attn_kernel<1>), grid, block, 0, stream, a, out);

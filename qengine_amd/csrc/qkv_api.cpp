@@ -503,8 +503,15 @@ struct FastGeom {
 // chunk and q head, merged by the designated merger workgroups.
 // Query groups of a contiguous TQ3 fast-path launch (16 / GQA queries share a
 // workgroup's MFMA columns).
+int tq3_fast_qpw(int num_q, int num_kv, int sub_n) {
+  const int gqa = num_q / num_kv;
+  // one query group of rounded queries + remainders in the 16 MFMA columns, or,
+  // when the call has more queries than that, 16 / GQA queries per group with
+  // the remainders in a chained product (tq3_attn_kernel<0, true>)
+  return sub_n > 8 / gqa ? 16 / gqa : 8 / gqa;
+}
 int tq3_groups(int num_q, int num_kv, int sub_n) {
-  const int qpw = 8 / (num_q / num_kv);
+  const int qpw = tq3_fast_qpw(num_q, num_kv, sub_n);
   return (sub_n + qpw - 1) / qpw;
 }
 
@@ -571,7 +578,7 @@ static int decode_tq3(const uint16_t* q, const qkv_block_tq3* k, const qkv_block
   a.start_pos = start_pos;
   a.sub_n = sub_n;
   a.sub_n_max = sub_n;
-  a.qpw = 8 / (num_q / num_kv);   // queries share MFMA columns 0..7 (8..15: query remainders)
+  a.qpw = tq3_fast_qpw(num_q, num_kv, sub_n);
   {
     const uint64_t extent = (uint64_t)n_keys * num_kv * 104;
     a.kv_bytes = extent;
