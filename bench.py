@@ -13,7 +13,9 @@ Prints one JSON line (value = microseconds per token, lower is better) with:
                 launch / its average duration (HIP events on the launch stream
                 around the timed region, which holds only these launches),
                 against 8 TB/s; traffic = HBM bytes per launch from rocprofv3
-                counters (profiles/traffic.json)
+                counters (profiles/traffic.json); launch_read_floor = one
+                launch of a plain read kernel over the same bytes (back to
+                back, rotating buffers), the single-launch floor on this box
   step_stats    per-step median / p10 / p90 over the timed steps (an event
                 pair around every step)
   hbm_read_peak measured streaming-read bandwidth (qkv_hbm_read_bench over a
@@ -339,6 +341,39 @@ def hbm_read_peak(torch, kvcache, dev, stream):
             "bytes": 1 << 30, "kernel": "stream_read_kernel (qkv_hbm_read_bench)"}
 
 
+def launch_read_floor(torch, kvcache, dev, stream, nbytes):
+    """Per-launch time of a kernel that only reads `nbytes` (qkv_hbm_read_bench)
+    once per launch: 16 launches over 16 buffers (more than the Infinity Cache
+    holds) captured in a HIP graph, so that host submission does not pace
+    them, and the graph replayed back to back: what one launch that streams a
+    decode layer's bytes costs on this device, launch included."""
+    nbytes = (nbytes + 63) // 64 * 64
+    bufs = [torch.ones(nbytes, dtype=torch.uint8, device=dev) for _ in range(16)]
+    sink = torch.zeros(1, dtype=torch.int32, device=dev)
+    for b in bufs:
+        kvcache.hbm_read_bench(b, sink)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for b in bufs:
+            kvcache.hbm_read_bench(b, sink)
+    for _ in range(3):
+        graph.replay()
+    reps = 20
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    a.record(stream)
+    for _ in range(reps):
+        graph.replay()
+    b.record(stream)
+    torch.cuda.synchronize()
+    us = a.elapsed_time(b) / (reps * len(bufs)) * 1e3
+    del graph, bufs
+    return {"us_per_launch": round(us, 3), "bytes": nbytes,
+            "gbps": round(nbytes / (us * 1e-6) / 1e9, 1),
+            "kernel": "stream_read_short_kernel (qkv_hbm_read_bench), 16 buffers, HIP graph replay"}
+
+
 def config1_report(torch, kvcache, dev):
     """BASELINE config 1 (seed 0): K and V [1024][4][256] fp16 ~ N(0,1) with 5
     fixed x8 outlier channels per head, TQ3-encoded on the GPU (append) and
@@ -546,6 +581,7 @@ def main():
             traffic = json.load(f).get("attn_tq3_32k_bytes_per_launch")
 
     read_peak = hbm_read_peak(torch, kvcache, dev, stream)
+    read_floor = launch_read_floor(torch, kvcache, dev, stream, ATTN_BYTES)
     # CPU leg (the oracle as baseline and checker): CPU baselines, and config 1
     # -- the reference's CPU-runnable roundtrip case -- checked against it
     cpu = cfg1 = None
@@ -585,7 +621,10 @@ def main():
                      "traffic": traffic, "kernel": "tq3_attn_kernel<0>",
                      "frac_of_measured_peak": round(achieved / read_peak["gbps"], 4),
                      "avg_launch_us": round(launch_ms * 1e3, 3),
-                     "isolated_launch_median_us": round(durs[len(durs) // 2] * 1e3, 3)},
+                     "isolated_launch_median_us": round(durs[len(durs) // 2] * 1e3, 3),
+                     "launch_read_floor": read_floor,
+                     "frac_of_launch_read_floor": round(read_floor["us_per_launch"]
+                                                        / (launch_ms * 1e3), 4)},
         "append": {"mtok_layers_per_s": round(append_tok_layers / append_s / 1e6, 1),
                    "gbps": round(append_tok_layers * APPEND_BYTES_PER_TOKEN / append_s / 1e9, 1),
                    "frac": round(append_tok_layers * APPEND_BYTES_PER_TOKEN / append_s / 1e9

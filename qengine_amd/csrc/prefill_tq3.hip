@@ -37,7 +37,8 @@
 //                         so every lane owns one query row (token lane % 32)
 //                         for the softmax and the accumulators.  Workgroups
 //                         that stream the same tiles run on one XCD (shared L2).
-//   prefill_merge_kernel  merges the key splits (log-sum-exp) and stores fp16.
+//   prefill_merge_kernel  merges the key splits (log-sum-exp) and stores fp16
+//                         (prefill_merge_wide_kernel when there are many splits).
 #include <algorithm>
 
 #include "qkv_device.h"
@@ -415,6 +416,73 @@ __global__ __launch_bounds__(256) void prefill_merge_kernel(PrefillArgs p, uint1
 // ---------------------------------------------------------------------------
 // host side
 // ---------------------------------------------------------------------------
+// Many key splits (verify mode: up to 512): one workgroup per (token, q head)
+// row.  The split maxima and weights are reduced across the workgroup first;
+// then 8 groups of 32 threads take every 8th split (8 dims per thread, the
+// loads of a group's splits independent of each other), and the groups' sums
+// meet in LDS.
+constexpr int kMergeMaxSplits = 512;
+__global__ __launch_bounds__(256) void prefill_merge_wide_kernel(PrefillArgs p, uint16_t* out) {
+  __shared__ float w_s[kMergeMaxSplits];
+  __shared__ float red[8][kHD];
+  __shared__ float stat[2][4];
+  const long row = blockIdx.x;   // t * num_q + qh
+  const long nrows = (long)p.n_tok * p.num_q;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  float m = -INFINITY;
+  for (int z = tid; z < p.n_split; z += 256) {
+    const f2_t ml = *reinterpret_cast<const f2_t*>(p.part_ml + 2 * (z * nrows + row));
+    if (ml[1] > 0.f) m = fmaxf(m, ml[0]);
+  }
+  m = wave_max(m);
+  if (lane == 0) stat[0][wave] = m;
+  __syncthreads();
+  const float M = fmaxf(fmaxf(stat[0][0], stat[0][1]), fmaxf(stat[0][2], stat[0][3]));
+  float l = 0.f;
+  for (int z = tid; z < p.n_split; z += 256) {
+    const f2_t ml = *reinterpret_cast<const f2_t*>(p.part_ml + 2 * (z * nrows + row));
+    const float w = ml[1] > 0.f ? __builtin_amdgcn_exp2f(ml[0] - M) : 0.f;
+    w_s[z] = w;
+    l += w * ml[1];
+  }
+  l = wave_sum(l);
+  if (lane == 0) stat[1][wave] = l;
+  __syncthreads();
+  const float L = (stat[1][0] + stat[1][1]) + (stat[1][2] + stat[1][3]);
+  const int sg = tid >> 5, d0 = (tid & 31) * 8;
+  float x[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+#pragma unroll 4
+  for (int z = sg; z < p.n_split; z += 8) {
+    const float w = w_s[z];
+    const float* po = p.part_o + (z * nrows + row) * kHD + d0;
+    const f4_t a = *reinterpret_cast<const f4_t*>(po);
+    const f4_t b = *reinterpret_cast<const f4_t*>(po + 4);
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      x[i] += w * a[i];
+      x[4 + i] += w * b[i];
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < 8; i++) red[sg][d0 + i] = x[i];
+  __syncthreads();
+  if (tid < 32) {
+    const float inv = L > 0.f ? 1.0f / L : 0.f;
+    float y[8];
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+      float v = 0.f;
+#pragma unroll
+      for (int g = 0; g < 8; g++) v += red[g][d0 + i];
+      y[i] = v * inv;
+    }
+    uint32_t pk[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) pk[i] = f2h(y[2 * i]) | (f2h(y[2 * i + 1]) << 16);
+    *reinterpret_cast<uint4*>(out + row * kHD + d0) = make_uint4(pk[0], pk[1], pk[2], pk[3]);
+  }
+}
+
 PrefillGeom prefill_geom(int num_q, int num_kv, int n_tok, int start_pos) {
   PrefillGeom g{};
   g.n_pad = (n_tok + kKeys - 1) / kKeys * kKeys;
@@ -464,8 +532,12 @@ hipError_t launch_prefill_tq3(const PrefillArgs& a, int gqa, const uint16_t* q, 
   else
     return hipErrorInvalidValue;
   const long rows = (long)a.n_tok * a.num_q;
-  hipLaunchKernelGGL(prefill_merge_kernel, dim3((unsigned)((rows + 7) / 8)), dim3(256), 0, stream, a,
-                     out);
+  if (a.n_split > kMergeMaxSplits) return hipErrorInvalidValue;
+  if (a.n_split >= 16)   // one workgroup per row, the splits spread over its threads
+    hipLaunchKernelGGL(prefill_merge_wide_kernel, dim3((unsigned)rows), dim3(256), 0, stream, a, out);
+  else
+    hipLaunchKernelGGL(prefill_merge_kernel, dim3((unsigned)((rows + 7) / 8)), dim3(256), 0, stream, a,
+                       out);
   return hipGetLastError();
 }
 

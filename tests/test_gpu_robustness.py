@@ -97,3 +97,4 @@ def test_q8_decode_merge_timeout(dev):
         torch.cuda.synchronize()
         return out.cpu().numpy().astype(np.float64)
     _timeout_cycle(dev, call, ws, ref)
+
