@@ -131,15 +131,33 @@ def secondary(torch, kvcache, dev, stream):
         kvcache.decode_attn_q8(q, kb, vb, o, ws8, num_q=NUM_Q, num_kv=NUM_KV, start_pos=ctx,
                                sub_n=1, scale=scale)
     ms_split = _time(torch, stream, q8_layer_split, 200)
-    ms = _time(torch, stream, q8_layer, 200)
+    ms_eager = _time(torch, stream, q8_layer, 200)
+    # the same layers launched from HIP graphs (one graph per cache set: 8
+    # layers x 2 launches), replayed back to back: two kernels of ~2 and ~13 us
+    # per layer are launch-bound when each call also pays the Python host path
+    graphs = []
+    for s_ in range(sets):
+        for l_ in range(layers):
+            q8_layer(s_ * layers + l_)
+        torch.cuda.synchronize()
+        gr = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(gr):
+            for l_ in range(layers):
+                q8_layer(s_ * layers + l_)
+        graphs.append(gr)
+    ms = _time(torch, stream, lambda i=0: graphs[i % sets].replay(), 50) / layers
+    del graphs
     q8_bytes = 2 * (ctx + 1) * blocks_tok * 36 + NUM_Q * HD * 2 * 2
     out["config2_q8_decode"] = {
         "us_per_layer": round(ms * 1e3, 3),
         "bytes_per_layer": q8_bytes, "gbps": round(q8_bytes / (ms * 1e-3) / 1e9, 1),
         "frac": round(q8_bytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+        "eager_us_per_layer": round(ms_eager * 1e3, 3),
         "split_api_us_per_layer": round(ms_split * 1e3, 3),
         "note": "per layer: Q8 append of the new token's K and V and single-launch decode over "
-                "4097 keys (2 launches); split_api_us_per_layer: the same through the reference "
+                "4097 keys (2 launches), launched from HIP graphs (8 layers per graph, 4 cache "
+                "sets); eager_us_per_layer: the same calls launched one by one from Python; "
+                "split_api_us_per_layer: the same through the reference "
                 "split layout (2 appends, split-K decode K_SPLITS 8, merge: 4 launches); 8 layers "
                 "x 4 cache sets rotated"}
     del caches
