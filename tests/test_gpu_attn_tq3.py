@@ -103,7 +103,8 @@ def test_split_verify_masks(dev, sink, window, tree):
 
 
 @pytest.mark.parametrize("n,num_q,sub_n", [(4097, 16, 1), (32768, 16, 1), (1, 16, 1),
-                                           (300, 24, 1), (2064, 16, 16)])
+                                           (300, 24, 1), (2064, 16, 16), (2000, 20, 1), (1000, 28, 1),
+                                           (1500, 12, 1)])
 def test_fast_decode_vs_oracle(dev, n, num_q, sub_n):
     from qengine_amd import kvcache
     torch = _torch()
@@ -130,11 +131,12 @@ def test_fast_decode_vs_oracle(dev, n, num_q, sub_n):
     (2000, 16, 5, 0, 0, False), (1500, 16, 7, 0, 0, True), (1200, 24, 3, 0, 0, False),
     (900, 8, 11, 0, 0, True), (700, 4, 17, 0, 0, False), (20016, 16, 16, 0, 0, False),
     (800, 32, 3, 0, 0, True), (2500, 24, 2, 16, 512, False), (600, 16, 3, 0, 0, False),
+    (900, 12, 7, 0, 0, True), (700, 20, 4, 0, 0, False), (650, 28, 3, 0, 0, True),
     # chunks grown to keep one round of workgroups: 2 and 3 tiles per wave
     (40000, 16, 1, 0, 0, False), (70000, 24, 1, 0, 0, False), (40000, 16, 2, 128, 2048, True)])
 def test_fast_decode_multi_query(dev, n, num_q, sub_n, sink, window, tree):
     """Several queries per workgroup (they share the MFMA columns): partial
-    last groups, GQA 1, 2, 4, 6, 8, causal, tree and sink/window masks; calls
+    last groups, GQA 1 to 8, causal, tree and sink/window masks; calls
     with at most 8 / GQA queries carry rounded query and remainder in one
     product, larger ones take 16 / GQA queries per workgroup with the
     remainders in a chained product."""
