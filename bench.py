@@ -433,9 +433,45 @@ def config1_report(torch, kvcache, dev):
             "code_hist": [int(c) for c in hist],
             "code_frac": [round(float(c) / hist.sum(), 4) for c in hist],
             "codes_equal_oracle": equal, "near_boundary_1ulp": near,
+            "literal_wht256_fp16_scale": config1_literal(planes),
             "note": "K and V of config 1 (2 x 8192 blocks of 128), GPU append + dequant; "
                     "near_boundary_1ulp: rotated values whose one-ulp neighbourhood holds a "
                     "decision bound (oracle rotation)"}
+
+
+def config1_literal(planes):
+    """Config 1's wording taken literally, on the same K and V: one 256-point
+    orthonormal WHT per head vector (random signs: the TQ3 128-entry sign
+    vector repeated), the 8 Lloyd-Max levels for coordinates of a unit vector
+    in 256 dimensions (the TQ3 levels, which are for 128, times sqrt(1/2)),
+    one fp16 scale (the vector's norm) per 256-element block.  No reference
+    kernel uses this format (the reference packs two 128-blocks with fp32
+    norms, as above); numpy on the host, reported for the config's wording."""
+    import numpy as np
+    from scipy.linalg import hadamard
+    from oracle import oracle as O
+    h = hadamard(256).astype(np.float64) / 16.0
+    sign = np.tile(np.where(O.tq3_signs() > 0, 1.0, -1.0), 2)
+    cen = O.tq3_centroids().astype(np.float64) * np.sqrt(0.5)
+    bnd = (cen[1:] + cen[:-1]) / 2
+    sq = ref = 0.0
+    n_el = 0
+    codes = []
+    for x in planes:
+        v = x.astype(np.float64).reshape(-1, 256)
+        norm = np.sqrt((v * v).sum(1))
+        scale = norm.astype(np.float16).astype(np.float64)
+        safe = np.where(norm > 0, norm, 1.0)
+        y = (v / safe[:, None] * sign) @ h.T
+        idx = np.searchsorted(bnd, y)
+        rec = ((cen[idx] @ h) * sign) * scale[:, None]
+        sq += float(((rec - v) ** 2).sum())
+        ref += float((v * v).sum())
+        n_el += v.size
+        codes.append(idx.reshape(-1))
+    hist = np.bincount(np.concatenate(codes), minlength=8)
+    return {"mse": sq / n_el, "rel_mse": sq / ref, "code_hist": [int(c) for c in hist],
+            "bytes_per_vector": 256 * 3 // 8 + 2}
 
 
 def cpu_baselines(torch, caches, q, scale):
