@@ -93,13 +93,39 @@ __global__ __launch_bounds__(kSpThreads) void block_score_kernel(BlockIndexArgs 
   const int nt = min(kScQueries, a.sub_n - t0);
   const int tid = threadIdx.x;
   const int gqa = a.num_q / a.num_kv;
-  // stage 32 blocks x {mean, max} x 512 B: 2048 16-byte pieces, 8 per thread
-  for (int piece = tid; piece < kScBlocks * 64; piece += kSpThreads) {
+  // Every load of the staging and of the query is issued before the first
+  // one is used (one memory round trip for the workgroup's inputs).
+  // 32 blocks x {mean, max} x 512 B: 2048 16-byte pieces, 8 per thread
+  // (blocks past the pool's end are read at its last block and zeroed)
+  static_assert(kScBlocks * 64 == 8 * kSpThreads, "8 staging pieces per thread");
+  uint4 pv[8];
+#pragma unroll
+  for (int k = 0; k < 8; k++) {
+    const int piece = tid + k * kSpThreads;
     const int b = piece >> 6, w = piece & 63;   // w < 32: mean, else max; 8 dims each
-    uint4 v = make_uint4(0u, 0u, 0u, 0u);
-    if (b0 + b < a.n_blocks)
-      v = *reinterpret_cast<const uint4*>((w < 32 ? a.k_pool : a.k_pool_max) +
-                                          ((long)h * a.stride + b0 + b) * kSpHD + (w & 31) * 8);
+    const int nbk = min(b0 + b, a.n_blocks - 1);
+    pv[k] = *reinterpret_cast<const uint4*>((w < 32 ? a.k_pool : a.k_pool_max) +
+                                            ((long)h * a.stride + nbk) * kSpHD + (w & 31) * 8);
+  }
+  // GQA-mean query pairs: thread i < nt * 128 forms pair c of query tq from
+  // the 8 (or gqa) heads' fp16 pairs, loaded together (heads past gqa re-read
+  // the last head and are not added)
+  static_assert(kScQueries * kSpHD / 2 == 4 * kSpThreads, "4 query pairs per thread");
+  uint32_t qv[4][8];
+#pragma unroll
+  for (int k = 0; k < 4; k++) {
+    const int i = min(tid + k * kSpThreads, nt * kSpHD / 2 - 1);
+    const int tq = i / (kSpHD / 2), c = 2 * (i - tq * (kSpHD / 2));
+#pragma unroll
+    for (int g = 0; g < 8; g++)
+      qv[k][g] = *reinterpret_cast<const uint32_t*>(
+          a.q + ((long)(t0 + tq) * a.num_q + h * gqa + min(g, gqa - 1)) * kSpHD + c);
+  }
+#pragma unroll
+  for (int k = 0; k < 8; k++) {
+    const int piece = tid + k * kSpThreads;
+    const int b = piece >> 6, w = piece & 63;
+    const uint4 v = b0 + b < a.n_blocks ? pv[k] : make_uint4(0u, 0u, 0u, 0u);
     uint32_t* d = (w < 32 ? rows_mean : rows_max) + b * kScPitchDw + (w & 31) * 4;
     d[0] = v.x;
     d[1] = v.y;
@@ -107,19 +133,23 @@ __global__ __launch_bounds__(kSpThreads) void block_score_kernel(BlockIndexArgs 
     d[3] = v.w;
   }
   const float inv_g = a.inv_gqa;
-  for (int i = tid; i < nt * kSpHD / 2; i += kSpThreads) {
-    const int tq = i / (kSpHD / 2), c = 2 * (i - tq * (kSpHD / 2));
-    float s0 = 0.0f, s1 = 0.0f;
-    for (int g = 0; g < gqa; g++) {
-      const uint16_t* qr = a.q + ((long)(t0 + tq) * a.num_q + h * gqa + g) * kSpHD + c;
-      s0 += h2f(qr[0]);
-      s1 += h2f(qr[1]);
+#pragma unroll
+  for (int k = 0; k < 4; k++) {
+    const int i = tid + k * kSpThreads;
+    if (i < nt * kSpHD / 2) {
+      float s0 = 0.0f, s1 = 0.0f;   // heads in order (the reference's sum)
+#pragma unroll
+      for (int g = 0; g < 8; g++)
+        if (g < gqa) {
+          s0 += h2f(qv[k][g] & 0xffffu);
+          s1 += h2f(qv[k][g] >> 16);
+        }
+      // the reference rounds s * (1/GQA) to fp32, then to fp16: the empty asm
+      // keeps the fp32 product (no fused fp16-rounding mixed FMA)
+      float p0 = s0 * inv_g, p1 = s1 * inv_g;
+      asm volatile("" : "+v"(p0), "+v"(p1));
+      qa2[i] = f2h(p0) | (f2h(p1) << 16);
     }
-    // the reference rounds s * (1/GQA) to fp32, then to fp16: the empty asm
-    // keeps the fp32 product (no fused fp16-rounding mixed FMA)
-    float p0 = s0 * inv_g, p1 = s1 * inv_g;
-    asm volatile("" : "+v"(p0), "+v"(p1));
-    qa2[i] = f2h(p0) | (f2h(p1) << 16);
   }
   __syncthreads();
   // thread -> (query tq, block b): 32 lanes of a wave are the 32 blocks of one query
@@ -156,8 +186,7 @@ __global__ __launch_bounds__(kSpThreads) void block_score_kernel(BlockIndexArgs 
 //   2. the picks are the blocks with key > T and the lowest-numbered `need`
 //      blocks with key == T (a block-wide scan in block order);
 //   3. a second scan gives each pick its place in the ascending list.
-// Each thread owns a contiguous run of blocks; the scores are read from the
-// workspace (L2) in every pass.
+// Each thread owns a contiguous run of blocks.
 constexpr int kTkThreads = 256;
 
 __device__ __forceinline__ uint32_t order_key(float v) {
@@ -189,7 +218,11 @@ __device__ __forceinline__ int block_scan(int v, int* wtot, int& total) {
   return off + inc - v;
 }
 
+// Rows of up to kSelLdsKeys blocks are read once and keep their keys in LDS
+// for all passes; longer rows read the scores from the workspace in every pass.
+constexpr int kSelLdsKeys = 8192;
 __global__ __launch_bounds__(kTkThreads) void block_select_kernel(BlockIndexArgs a, const float* scores) {
+  __shared__ uint32_t keys_s[kSelLdsKeys];
   __shared__ int hist[256];
   __shared__ int wtot[kTkThreads / 64];
   __shared__ int found[2];
@@ -199,9 +232,18 @@ __global__ __launch_bounds__(kTkThreads) void block_select_kernel(BlockIndexArgs
   int32_t* row = a.block_index + ((long)h * a.sub_n_max + t) * a.top_k;
   const int per = (a.n_blocks + kTkThreads - 1) / kTkThreads;
   const int i0 = min(tid * per, a.n_blocks), i1 = min(i0 + per, a.n_blocks);
+  // key of block i: the order key of a pickable score, 0 otherwise (every
+  // pickable score, > -inf and not NaN, has a key above 0x007FFFFF)
+  const bool staged = a.n_blocks <= kSelLdsKeys;
+  auto key_from = [](float v) -> uint32_t { return pickable(v) ? order_key(v) : 0u; };
+  if (staged) {
+    for (int i = tid; i < a.n_blocks; i += kTkThreads) keys_s[i] = key_from(src[i]);
+    __syncthreads();
+  }
+  auto key_at = [&](int i) -> uint32_t { return staged ? keys_s[i] : key_from(src[i]); };
 
   int n_ok = 0;
-  for (int i = i0; i < i1; i++) n_ok += pickable(src[i]);
+  for (int i = i0; i < i1; i++) n_ok += key_at(i) != 0u;
   int total;
   (void)block_scan(n_ok, wtot, total);
   const bool all = total <= a.top_k;   // every pickable block is picked
@@ -214,9 +256,8 @@ __global__ __launch_bounds__(kTkThreads) void block_select_kernel(BlockIndexArgs
       hist[tid] = 0;
       __syncthreads();
       for (int i = i0; i < i1; i++) {
-        const float v = src[i];
-        const uint32_t key = order_key(v);
-        if (pickable(v) && (key & mask) == prefix) atomicAdd(&hist[(key >> shift) & 255u], 1);
+        const uint32_t key = key_at(i);
+        if (key != 0u && (key & mask) == prefix) atomicAdd(&hist[(key >> shift) & 255u], 1);
       }
       __syncthreads();
       // suffix sums: thread tid takes bin 255 - tid
@@ -239,17 +280,13 @@ __global__ __launch_bounds__(kTkThreads) void block_select_kernel(BlockIndexArgs
   // picks, in block order
   int n_eq = 0;
   if (!all)
-    for (int i = i0; i < i1; i++) {
-      const float v = src[i];
-      n_eq += pickable(v) && order_key(v) == T;
-    }
+    for (int i = i0; i < i1; i++) n_eq += key_at(i) == T;
   int tot_eq;
   int eq_rank = block_scan(n_eq, wtot, tot_eq);
   int n_pick = 0;
   for (int i = i0; i < i1; i++) {
-    const float v = src[i];
-    if (!pickable(v)) continue;
-    const uint32_t key = order_key(v);
+    const uint32_t key = key_at(i);
+    if (key == 0u) continue;
     if (all || key > T) {
       n_pick++;
     } else if (key == T) {
@@ -261,9 +298,8 @@ __global__ __launch_bounds__(kTkThreads) void block_select_kernel(BlockIndexArgs
   int pos = block_scan(n_pick, wtot, n_total);
   eq_rank -= n_eq;   // back to this thread's first equal key
   for (int i = i0; i < i1; i++) {
-    const float v = src[i];
-    if (!pickable(v)) continue;
-    const uint32_t key = order_key(v);
+    const uint32_t key = key_at(i);
+    if (key == 0u) continue;
     bool pick = all || key > T;
     if (!all && key == T) {
       pick = eq_rank < need;
