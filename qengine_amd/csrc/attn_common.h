@@ -215,14 +215,23 @@ __device__ __forceinline__ float centroid_f32(uint32_t i) {
 // group gets elements part*8 .. part*8+7 as four fp16 pairs.  fp32 centroids,
 // the seven butterfly stages in the reference's pairing (three in registers,
 // four across the lanes), * rs, sign, * norm kept an fp32 product, fp16.
-__device__ __forceinline__ void tq3_dequant_exact8(const uint8_t* blk, int part, int lane,
-                                                   uint32_t (&pk)[4]) {
-  const float norm = *reinterpret_cast<const float*>(blk);
+// The three dwords a lane needs (norm and the two code words holding its
+// group), loaded apart from the arithmetic so that a caller can issue the
+// loads of several blocks before the first is used.
+struct Tq3Group {
+  float norm;
+  uint32_t lo, hi;
+};
+__device__ __forceinline__ Tq3Group tq3_group_load(const uint8_t* blk, int part) {
   // code group `part`: bytes 3*part .. 3*part+2 of the 48 code bytes
-  const int b0 = 3 * part, w0 = b0 >> 2;
+  const int w0 = (3 * part) >> 2;
   const uint32_t* cw = reinterpret_cast<const uint32_t*>(blk + 4);
-  const uint32_t lo = cw[w0], hi = cw[min(w0 + 1, 11)];
-  const uint32_t g = __builtin_amdgcn_alignbyte(hi, lo, b0 & 3);
+  return Tq3Group{*reinterpret_cast<const float*>(blk), cw[w0], cw[min(w0 + 1, 11)]};
+}
+__device__ __forceinline__ void tq3_group_dequant(const Tq3Group& gr, int part, int lane,
+                                                  uint32_t (&pk)[4]) {
+  const float norm = gr.norm;
+  const uint32_t g = __builtin_amdgcn_alignbyte(gr.hi, gr.lo, (3 * part) & 3);
   float x[8];
 #pragma unroll
   for (int i = 0; i < 8; i++) x[i] = centroid_f32((g >> (3 * i)) & 7u);
@@ -241,6 +250,10 @@ __device__ __forceinline__ void tq3_dequant_exact8(const uint8_t* blk, int part,
     asm volatile("" : "+v"(pa), "+v"(pb));
     pk[i] = f2h(pa) | (f2h(pb) << 16);
   }
+}
+__device__ __forceinline__ void tq3_dequant_exact8(const uint8_t* blk, int part, int lane,
+                                                   uint32_t (&pk)[4]) {
+  tq3_group_dequant(tq3_group_load(blk, part), part, lane, pk);
 }
 
 hipError_t launch_tq3_attn(const AttnArgs& a, int mode, uint16_t* out, hipStream_t stream);

@@ -41,16 +41,29 @@ __global__ __launch_bounds__(kSpThreads) void tq3_kpool_kernel(KpoolArgs a) {
   const int n_pos = t_hi - t_lo;   // >= 1: n < cur_blocks
   const int tid = threadIdx.x;
   const int part = tid & 15, lane = tid & 63;
-  // units (position, 128-block): 16 per pass of the workgroup
-  for (int u = tid >> 4; u < 2 * n_pos; u += kSpThreads / 16) {
-    const int pos = u >> 1, blk = u & 1;
+  // units (position, 128-block): 16 per pass of the workgroup, at most 8
+  // passes (64 rows); every pass's loads are issued before the first is used
+  constexpr int kPasses = 2 * 64 / (kSpThreads / 16);
+  Tq3Group gr[kPasses];
+#pragma unroll
+  for (int p = 0; p < kPasses; p++) {
+    const int u0 = (tid >> 4) + p * (kSpThreads / 16);
+    const int u = u0 < 2 * n_pos ? u0 : 0;   // a unit past the block's rows re-reads unit 0
     const uint8_t* src = reinterpret_cast<const uint8_t*>(a.k) +
-                         ((uint64_t)(uint32_t)(t_lo + pos) * (uint32_t)a.num_kv + h) * 104u +
-                         blk * 52u;
-    uint32_t pk[4];
-    tq3_dequant_exact8(src, part, lane, pk);
-    *reinterpret_cast<uint4*>(rows + pos * kPoolPitch + (blk * 128 + part * 8) * 2) =
-        make_uint4(pk[0], pk[1], pk[2], pk[3]);
+                         ((uint64_t)(uint32_t)(t_lo + (u >> 1)) * (uint32_t)a.num_kv + h) * 104u +
+                         (u & 1) * 52u;
+    gr[p] = tq3_group_load(src, part);
+  }
+#pragma unroll
+  for (int p = 0; p < kPasses; p++) {
+    const int u = (tid >> 4) + p * (kSpThreads / 16);
+    if (u < 2 * n_pos) {   // uniform over the unit's 16 lanes (lane exchange inside)
+      const int pos = u >> 1, blk = u & 1;
+      uint32_t pk[4];
+      tq3_group_dequant(gr[p], part, lane, pk);
+      *reinterpret_cast<uint4*>(rows + pos * kPoolPitch + (blk * 128 + part * 8) * 2) =
+          make_uint4(pk[0], pk[1], pk[2], pk[3]);
+    }
   }
   __syncthreads();
   const int c = tid;   // 256 threads: one dimension each
