@@ -423,6 +423,146 @@ __global__ __launch_bounds__(kAp4Threads, 3) void tq3_append4_kernel(
 }
 
 // ---------------------------------------------------------------------------
+// Append of a few blocks (a decode step's new tokens): latency first.
+//
+// The lane-pair kernel gives each lane 128 elements, so a small append is one
+// wave running ~2,000 dependent instructions.  Here a block is spread over a
+// 16-lane DPP row, lane t holding elements 8t..8t+7 (one 16-byte load):
+//   - norm: the reference's sequential sum runs through the row, each lane
+//     adding its 8 squares to its left neighbour's partial (row_shr:1), 16
+//     steps; lane 15 ends with the block's sum;
+//   - scaling with the sign folded into the factor, as the lane-pair kernel;
+//   - WHT stages 1..4 in registers, stages 8..64 across lanes t ^ 1, t ^ 2,
+//     t ^ 4 and t ^ 8 of the row (DPP quad_perm, half_mirror, mirror): the
+//     lower element of a pair becomes own + other, the upper other - own,
+//     the reference's roundings;
+//   - bins in the sign-folded form, 8 codes = 24 bits per lane (bits
+//     24t..24t+23 of the code stream), gathered into the 12 code dwords by
+//     lanes 0..11 (ds_bpermute), lane 12 storing the norm.
+// Four blocks per wave, sixteen per workgroup; no persistent loop.
+// ---------------------------------------------------------------------------
+constexpr int kSmallThreads = 256;
+// At most this many blocks (all tensors) take this kernel: measured K+V
+// appends of n tokens (16 blocks each), small / lane-pair kernel: 1 token
+// 2.6 / 6.6 us, 256 tokens 3.8 / 9.0, 1024 tokens 6.3 / 9.1, 2048 tokens
+// 10.2 / 9.2.
+constexpr long kSmallAppendBlocks = 16384;
+constexpr int kSmallBlocksPerWg = kSmallThreads / 16;
+
+template <int CTRL>
+__device__ __forceinline__ float row_dpp(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), CTRL, 0xf, 0xf,
+                                                            false));
+}
+
+// One cross-lane WHT stage on the lane's 8 elements: partner values through
+// the DPP path P (1: t ^ 1, 2: t ^ 2, 4: t ^ 4, 8: t ^ 8 within the row).
+template <int P>
+__device__ __forceinline__ void row_stage(float (&x)[8], bool upper) {
+  const uint32_t flip = upper ? 0x80000000u : 0u;
+#pragma unroll
+  for (int i = 0; i < 8; i++) {
+    float o;
+    if constexpr (P == 1) o = row_dpp<0xB1>(x[i]);                   // quad_perm [1,0,3,2]
+    else if constexpr (P == 2) o = row_dpp<0x4E>(x[i]);              // quad_perm [2,3,0,1]
+    else if constexpr (P == 4) o = row_dpp<0x1B>(row_dpp<0x141>(x[i]));   // i^7, then i^3
+    else o = row_dpp<0x141>(row_dpp<0x140>(x[i]));                   // i^15, then i^7
+    // lower: own + other; upper: other - own (= other + (-own), one rounding)
+    x[i] = o + __uint_as_float(__float_as_uint(x[i]) ^ flip);
+  }
+}
+
+template <bool kPaged>
+__global__ __launch_bounds__(kSmallThreads) void tq3_append_small_kernel(
+    const uint4* __restrict__ in0, uint32_t* __restrict__ out0, const uint4* __restrict__ in1,
+    uint32_t* __restrict__ out1, int n_blocks, int n_tensors, PagedRows pr) {
+  const int lane = threadIdx.x & 63;
+  const int t = lane & 15;
+  const long item = (long)blockIdx.x * kSmallBlocksPerWg + (threadIdx.x >> 4);
+  const bool valid = item < (long)n_blocks * n_tensors;
+  const int tensor = valid && item >= n_blocks ? 1 : 0;
+  const long b = item - (long)tensor * n_blocks;
+  const uint4* __restrict__ in = tensor ? in1 : in0;
+  uint32_t* __restrict__ out = tensor ? out1 : out0;
+
+  uint4 raw = make_uint4(0u, 0u, 0u, 0u);
+  if (valid) raw = in[b * 16 + t];
+  const uint32_t rw[4] = {raw.x, raw.y, raw.z, raw.w};
+  float h[8];
+#pragma unroll
+  for (int k = 0; k < 4; k++) {
+    h[2 * k] = h2f(rw[k] & 0xffffu);
+    h[2 * k + 1] = h2f(rw[k] >> 16);
+  }
+  // norm (reference order): lane t continues lane t - 1's partial
+  float part = 0.0f;
+#pragma unroll
+  for (int r = 0; r < 16; r++) {
+    float s = part;
+#pragma unroll
+    for (int i = 0; i < 8; i++) s = __builtin_fmaf(h[i], h[i], s);
+    part = r < 15 ? __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(
+                                                  0, __builtin_bit_cast(int, s), 0x111, 0xf, 0xf, false))
+                  : s;   // row_shr:1
+  }
+  const float norm_sq =
+      __builtin_bit_cast(float, __builtin_amdgcn_ds_bpermute((lane | 15) << 2, __builtin_bit_cast(int, part)));
+  const float norm = __builtin_sqrtf(norm_sq);
+  const float inv = 1.0f / norm;
+  // x * inv * sign (turboquant.cuh:141-149)
+  const uint32_t sbits = sign_word_sel(t >> 2) >> (8 * (t & 3));   // elements 8t..8t+7
+  float x[8];
+#pragma unroll
+  for (int i = 0; i < 8; i++) x[i] = __builtin_fmaf(h[i], ((sbits >> i) & 1u) ? inv : -inv, 0.0f);
+  // WHT stages 1, 2, 4 in registers, 8 .. 64 across the row (turboquant.cuh:50-59)
+#pragma unroll
+  for (int step = 1; step < 8; step <<= 1) {
+#pragma unroll
+    for (int i = 0; i < 8; i += 2 * step) {
+#pragma unroll
+      for (int j = i; j < i + step; j++) {
+        const float a = x[j], c = x[j + step];
+        x[j] = a + c;
+        x[j + step] = a - c;
+      }
+    }
+  }
+  row_stage<1>(x, (t & 1) != 0);
+  row_stage<2>(x, (t & 2) != 0);
+  row_stage<4>(x, (t & 4) != 0);
+  row_stage<8>(x, (t & 8) != 0);
+  // bins, sign-folded: bit 2 = [w > 0] (sign of y), bits 1..0 = the
+  // thermometer count m of |y| against the fold thresholds, inverted for w <= 0
+  const float q0 = __uint_as_float(kFoldQBits[0]), q1 = __uint_as_float(kFoldQBits[1]),
+              q2 = __uint_as_float(kFoldQBits[2]);
+  uint32_t v = 0u;
+#pragma unroll
+  for (int i = 0; i < 8; i++) {
+    const float y = __builtin_fmaf(x[i], -kFoldA, __builtin_fabsf(x[i]));
+    const float ay = __builtin_fabsf(y);
+    const uint32_t m = (uint32_t)(ay > q0) + (uint32_t)(ay > q1) + (uint32_t)(ay > q2);
+    const uint32_t code = (__float_as_uint(y) >> 31) ? 4u + m : 3u - m;
+    v |= code << (3 * i);
+  }
+  const bool keep = norm >= 1e-10f && norm < __builtin_inff();
+  // code dword k (k = t < 12): bytes 4k..4k+3 of the stream, from lanes a and
+  // a + 1 of the row, a = 4k / 3
+  const int a = (4 * t) / 3, off = 4 * t - 3 * a;
+  const int row0 = lane & ~15;
+  const uint32_t va = (uint32_t)__builtin_amdgcn_ds_bpermute((row0 + a) << 2, (int)v);
+  const uint32_t vb = (uint32_t)__builtin_amdgcn_ds_bpermute((row0 + min(a + 1, 15)) << 2, (int)v);
+  const uint64_t pair = (uint64_t)va | ((uint64_t)vb << 24);
+  const uint32_t word = keep ? (uint32_t)(pair >> (8 * off)) : 0u;
+  if (!valid || t > 12) return;
+  long ob = b;
+  if constexpr (kPaged) ob = paged_block(pr, b);
+  if (ob < 0) return;
+  uint32_t* dst = out + ob * 13;
+  if (t == 12) dst[0] = __float_as_uint(norm);
+  else dst[1 + t] = word;
+}
+
+// ---------------------------------------------------------------------------
 // Dequant (turboquant.cuh:169-200): half(((H*c)*rs)*sign*norm)
 // ---------------------------------------------------------------------------
 __global__ __launch_bounds__(kCodecThreads) void tq3_dequant_kernel(
@@ -515,11 +655,20 @@ hipError_t launch_tq3_append(const void* in0, void* out0, const void* in1, void*
     n_cu = n_cu > 0 ? n_cu : 1;
     cus[dev].store(n_cu, std::memory_order_relaxed);
   }
+  const PagedRows pr = paged ? *paged : PagedRows{};
+  const long items = (long)n_blocks * n_tensors;
+  if (sc0 == nullptr && items > 0 && items <= kSmallAppendBlocks) {
+    const int grid = (int)((items + kSmallBlocksPerWg - 1) / kSmallBlocksPerWg);
+    auto kernel = paged ? tq3_append_small_kernel<true> : tq3_append_small_kernel<false>;
+    hipLaunchKernelGGL(kernel, dim3(grid), dim3(kSmallThreads), 0, stream, static_cast<const uint4*>(in0),
+                       static_cast<uint32_t*>(out0), static_cast<const uint4*>(in1),
+                       static_cast<uint32_t*>(out1), n_blocks, n_tensors, pr);
+    return hipGetLastError();
+  }
   const long tiles = ((long)n_blocks + kAp4Tile - 1) / kAp4Tile * n_tensors;
   const long wgs_needed = (tiles + kAp4Waves - 1) / kAp4Waves;
   const int grid = (int)std::min<long>(wgs_needed, 3L * n_cu);
   if (grid == 0) return hipSuccess;
-  const PagedRows pr = paged ? *paged : PagedRows{};
   auto kernel = sc0 != nullptr ? (paged ? tq3_append4_kernel<true, true> : tq3_append4_kernel<true, false>)
                                 : (paged ? tq3_append4_kernel<false, true> : tq3_append4_kernel<false, false>);
   hipLaunchKernelGGL(kernel, dim3(grid), dim3(kAp4Threads), 0, stream, static_cast<const uint4*>(in0),

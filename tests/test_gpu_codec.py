@@ -49,7 +49,10 @@ def _diff_report(got, exp):
     return bad
 
 
-@pytest.mark.parametrize("n_blocks", [1, 7, 63, 64, 65, 257, 1000])
+# Appends of at most 16384 blocks (all tensors together) take the small-append
+# kernel (a block per 16-lane row), larger ones the lane-pair kernel: sizes on
+# both sides of that limit.
+@pytest.mark.parametrize("n_blocks", [1, 7, 63, 64, 65, 257, 1000, 16383, 16384, 16385, 20000])
 def test_tq3_append_bitexact_odd_sizes(dev, n_blocks):
     rng = np.random.default_rng(n_blocks)
     x = kv_f16(rng, n_blocks, 1, 128)
@@ -59,10 +62,14 @@ def test_tq3_append_bitexact_odd_sizes(dev, n_blocks):
     assert bad.size == 0, f"{bad.size} blocks differ, first {bad[:5]}"
 
 
-def test_tq3_append_config1_and_specials(dev):
+@pytest.mark.parametrize("n_tok,reps", [(1024, 1), (100, 1), (1024, 2)])
+def test_tq3_append_config1_and_specials(dev, n_tok, reps):
     # config 1: 1024 tokens x 4 heads x 256 (K), 2% x8 outlier channels, seed 0
+    # (8200 blocks) and its first 100 tokens: small kernel; the 8200 blocks
+    # twice over (16400): lane-pair kernel
     rng = np.random.default_rng(0)
-    x = np.concatenate([kv_f16(rng, 1024, 4, 256).reshape(-1, 128), _special_blocks(rng)])
+    x = np.concatenate([kv_f16(rng, 1024, 4, 256).reshape(-1, 128)[: n_tok * 8], _special_blocks(rng)])
+    x = np.tile(x, (reps, 1))
     got = _tq3_gpu(x, dev)
     exp = O.tq3_encode(x)
     assert np.array_equal(got["norm"].view(np.uint32), exp["norm"].view(np.uint32))
@@ -70,7 +77,8 @@ def test_tq3_append_config1_and_specials(dev):
     assert bad.size == 0, f"{bad.size} of {len(exp)} blocks differ, first {bad[:5]}"
 
 
-def test_tq3_append_nonfinite_and_extreme_blocks(dev):
+@pytest.mark.parametrize("reps", [1, 1026])
+def test_tq3_append_nonfinite_and_extreme_blocks(dev, reps):
     """Blocks with inf / NaN elements: the reference bins the NaN WHT outputs
     to 0, so the codes are zero and the norm is inf or NaN.  Blocks mixing
     the largest and the smallest fp16 magnitudes reach the smallest nonzero
@@ -90,6 +98,7 @@ def test_tq3_append_nonfinite_and_extreme_blocks(dev):
     x[10, ::2] = np.float16(6e-8)
     x[10, 1::2] = np.float16(-6e-8)
     x[10, 64] = np.float16(65504.0)
+    x = np.tile(x, (reps, 1))   # 16 blocks: small kernel; 16416: lane-pair kernel
     got = _tq3_gpu(x, dev)
     exp = O.tq3_encode(x)
     gn, en = got["norm"], exp["norm"]
@@ -129,6 +138,24 @@ def test_tq3_append_kv_matches_two_appends(dev):
     kvcache.tq3_append(v, v1)
     torch.cuda.synchronize()
     assert torch.equal(ko, k1) and torch.equal(vo, v1)
+
+
+@pytest.mark.parametrize("n_tok", [1024, 1025, 1])
+def test_tq3_append_kv_bitexact(dev, n_tok):
+    """K and V in one launch against the oracle: 1024 tokens (2 x 8192
+    blocks, the small kernel's limit), 1025 (the lane-pair kernel) and one
+    token (a decode step)."""
+    from qengine_amd import kvcache
+    torch = _torch()
+    rng = np.random.default_rng(22 + n_tok)
+    k16, v16 = kv_f16(rng, n_tok, 4, 256), kv_f16(rng, n_tok, 4, 256)
+    n = n_tok * 8
+    ko, vo = kvcache.tq3_blocks(n, dev), kvcache.tq3_blocks(n, dev)
+    kvcache.tq3_append_kv(_to_dev(k16.reshape(-1), dev), _to_dev(v16.reshape(-1), dev), ko, vo)
+    torch.cuda.synchronize()
+    for got, x in ((ko, k16), (vo, v16)):
+        bad = _diff_report(got.cpu().numpy().view(O.BLOCK_TQ3).reshape(-1), O.tq3_encode(x))
+        assert bad.size == 0, f"{bad.size} blocks differ, first {bad[:5]}"
 
 
 def test_tq3_append_writes_only_its_blocks(dev):
