@@ -29,7 +29,9 @@
 //           probabilities), B = codes of 32 keys x 16 dims.  The wave's value
 //           rows are loaded with aligned 16-byte loads (lane = key) and staged
 //           in LDS; lane (n, o) gathers dim group n of both blocks for 8 keys
-//           and pairs keys with v_perm; the table reads run two steps ahead.
+//           and interleaves the codes of key pairs (bit select), so that each
+//           table entry read is a B dword (two keys, one dim); the table
+//           reads run two steps ahead.
 // Merging: the 8 waves merge in LDS and each merged piece goes straight to
 // its record {m, l, tags} + o[256] (rotated); the tags are set once the
 // workgroup's data stores are complete.  The last workgroups of the grid are
@@ -188,13 +190,21 @@ __device__ __forceinline__ void score_group(const uint8_t* lds, uint32_t (&ac)[4
   }
 }
 
-// One value pass: a (32-key chunk c2, 128-block j) pair.  x[i]: code group
-// `col` (8 dims) of key 32*c2 + 4*row + i (i < 4) or 32*c2 + 16 + 4*row + i - 4;
+// One value pass: a (32-key chunk c2, 128-block j) pair.  MFMA k index i of
+// the pass is key 32*c2 + 4*row + i (i < 4) or 32*c2 + 16 + 4*row + i - 4.
+// x: the code group `col` (8 dims, 24 bits) of keys i = 2k and 2k + 1
+// interleaved per dim, so that one 6-bit field is a table index whose entry is
+// already the B dword (key 2k in the low half, key 2k + 1 in the high half):
+// x[k] holds dims 0, 2, 4, 6 (field 6d: codes of dim 2d), x[4 + k] dims 1, 3,
+// 5, 7 (field 6d + 3: codes of dim 2d + 1).
 // a: A operand (p * value norm of those keys, head `col`).
 struct ValuePass {
   uint32_t x[8];
   h8_t a;
 };
+
+// Dims 0, 2, 4, 6 of a 24-bit code group (bits 6d .. 6d + 2).
+constexpr uint32_t kEvenDims = 0x1C71C7u;
 
 // Codes and A operand of pass c = 2*c2 + j from the tile's staging area.
 __device__ __forceinline__ void value_pass_load(const float* st, const uint32_t* stu, int c, int row,
@@ -209,19 +219,32 @@ __device__ __forceinline__ void value_pass_load(const float* st, const uint32_t*
   for (int r = 0; r < 4; r++) {
     vp.a[r] = (_Float16)(s[2 * c2][r] * va[r]);
     vp.a[4 + r] = (_Float16)(s[2 * c2 + 1][r] * vb[r]);
-    vp.x[r] = xa[r];
-    vp.x[4 + r] = xb[r];
+  }
+  // key pairs (i, i + 1) = (2k, 2k + 1): the second key's codes moved up by
+  // one code, merged with the first key's by bit select
+#pragma unroll
+  for (int k = 0; k < 4; k++) {
+    const uint32_t lo = k < 2 ? xa[2 * k] : xb[2 * k - 4];
+    const uint32_t hi = (k < 2 ? xa[2 * k + 1] : xb[2 * k - 3]) << 3;
+    vp.x[k] = (lo & kEvenDims) | (hi & ~kEvenDims);
+    vp.x[4 + k] = (lo & (kEvenDims << 3)) | (hi & ~(kEvenDims << 3));
   }
 }
 
-// Table reads of centroid pair PP (dims 2PP, 2PP+1 of the group) of the 8 keys.
+// Table reads of dims 2PP (cp[0..3]) and 2PP+1 (cp[4..7]) of the 4 key pairs:
+// each entry is a B dword (two keys, one dim).
 template <int PP>
 __device__ __forceinline__ void value_pairs(const uint8_t* lds, uint32_t (&ac)[4], const uint32_t (&x)[8],
                                             uint32_t (&cp)[8]) {
 #pragma unroll
-  for (int i = 0; i < 8; i++) {
-    ac[i & 3] = sdwa_index<6 * PP>(ac[i & 3], x[i]);
-    cp[i] = lut_read(lds, ac[i & 3]);
+  for (int k = 0; k < 4; k++) {
+    ac[k] = sdwa_index<6 * PP>(ac[k], x[k]);
+    cp[k] = lut_read(lds, ac[k]);
+  }
+#pragma unroll
+  for (int k = 0; k < 4; k++) {
+    ac[k] = sdwa_index<6 * PP + 3>(ac[k], x[4 + k]);
+    cp[4 + k] = lut_read(lds, ac[k]);
   }
 }
 
@@ -246,8 +269,7 @@ __device__ __forceinline__ void value_steps(const uint8_t* lds, uint32_t (&ac)[4
     for (int e = 0; e < 2; e++) {
       u4_t bv;
 #pragma unroll
-      for (int k2 = 0; k2 < 4; k2++)
-        bv[k2] = __builtin_amdgcn_perm(cp[2 * k2 + 1], cp[2 * k2], e ? 0x07060302u : 0x05040100u);
+      for (int k2 = 0; k2 < 4; k2++) bv[k2] = cp[4 * e + k2];
       constexpr int t0 = 8 * (c & 1) + 2 * PP;
       const f4_t cin = (FIRST && c < 2) ? f4_t{0.f, 0.f, 0.f, 0.f} : acc[t0 + e];
       acc[t0 + e] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vp[c & 1].a, __builtin_bit_cast(h8_t, bv),
