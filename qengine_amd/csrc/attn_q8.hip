@@ -339,19 +339,26 @@ __global__ __launch_bounds__(kThreads, 2) void q8_attn_kernel(AttnArgs p, uint16
         const u4_t xb =
             *reinterpret_cast<const u4_t*>(stu + kMxStCodes + (16 * a + col) * kPitch + 16 + 4 * row);
         const uint32_t x[8] = {xa[0], xa[1], xa[2], xa[3], xb[0], xb[1], xb[2], xb[3]};
+        // keys (2k, 2k + 1) interleaved per dim: field 6d of z[k] holds the two
+        // codes of dim 2d, field 6d + 3 of z[4 + k] those of dim 2d + 1, so a
+        // table entry is a B dword (key 2k low half, key 2k + 1 high half)
+        constexpr uint32_t kEven = 0x1C71C7u;   // dims 0, 2, 4, 6 of a code group
+        uint32_t z[8];
 #pragma unroll
-        for (int pp = 0; pp < 4; pp++) {   // centroid pair pp: dims 2pp (low half), 2pp+1
-          uint32_t cp[8];
+        for (int k = 0; k < 4; k++) {
+          const uint32_t hi = x[2 * k + 1] << 3;
+          z[k] = (x[2 * k] & kEven) | (hi & ~kEven);
+          z[4 + k] = (x[2 * k] & (kEven << 3)) | (hi & ~(kEven << 3));
+        }
 #pragma unroll
-          for (int i = 0; i < 8; i++)
-            cp[i] = *reinterpret_cast<const uint32_t*>(lds + kMxLdsLut +
-                                                       ((((x[i] >> (6 * pp)) & 63u) << 8) | lane4));
+        for (int pp = 0; pp < 4; pp++) {   // dims 2pp (e = 0) and 2pp + 1 (e = 1)
 #pragma unroll
           for (int e = 0; e < 2; e++) {
             u4_t bv;
 #pragma unroll
             for (int k2 = 0; k2 < 4; k2++)
-              bv[k2] = __builtin_amdgcn_perm(cp[2 * k2 + 1], cp[2 * k2], e ? 0x07060302u : 0x05040100u);
+              bv[k2] = *reinterpret_cast<const uint32_t*>(
+                  lds + kMxLdsLut + ((((z[4 * e + k2] >> (6 * pp + 3 * e)) & 63u) << 8) | lane4));
             acc[8 * a + 2 * pp + e] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
                 pv, __builtin_bit_cast(h8_t, bv), acc[8 * a + 2 * pp + e], 0, 0, 0);
           }
