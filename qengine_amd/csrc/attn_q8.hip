@@ -347,8 +347,11 @@ __global__ __launch_bounds__(kThreads, 2) void q8_attn_kernel(AttnArgs p, uint16
 #pragma unroll
         for (int k = 0; k < 4; k++) {
           const uint32_t hi = x[2 * k + 1] << 3;
-          z[k] = (x[2 * k] & kEven) | (hi & ~kEven);
-          z[4 + k] = (x[2 * k] & (kEven << 3)) | (hi & ~(kEven << 3));
+          uint32_t e0, e1;
+          asm("v_bfi_b32 %0, %1, %2, %3" : "=v"(e0) : "s"(kEven), "v"(x[2 * k]), "v"(hi));
+          asm("v_bfi_b32 %0, %1, %2, %3" : "=v"(e1) : "s"(kEven << 3), "v"(x[2 * k]), "v"(hi));
+          z[k] = e0;
+          z[4 + k] = e1;
         }
 #pragma unroll
         for (int pp = 0; pp < 4; pp++) {   // dims 2pp (e = 0) and 2pp + 1 (e = 1)

@@ -206,6 +206,14 @@ struct ValuePass {
 // Dims 0, 2, 4, 6 of a 24-bit code group (bits 6d .. 6d + 2).
 constexpr uint32_t kEvenDims = 0x1C71C7u;
 
+// (a & m) | (b & ~m) in one v_bfi_b32 (the compiler splits some constant
+// masks into an and plus an and-or)
+__device__ __forceinline__ uint32_t bit_select(uint32_t m, uint32_t a, uint32_t b) {
+  uint32_t d;
+  asm("v_bfi_b32 %0, %1, %2, %3" : "=v"(d) : "s"(m), "v"(a), "v"(b));
+  return d;
+}
+
 // Codes and A operand of pass c = 2*c2 + j from the tile's staging area.
 __device__ __forceinline__ void value_pass_load(const float* st, const uint32_t* stu, int c, int row,
                                                 int col, const float (&s)[4][4], ValuePass& vp) {
@@ -226,8 +234,8 @@ __device__ __forceinline__ void value_pass_load(const float* st, const uint32_t*
   for (int k = 0; k < 4; k++) {
     const uint32_t lo = k < 2 ? xa[2 * k] : xb[2 * k - 4];
     const uint32_t hi = (k < 2 ? xa[2 * k + 1] : xb[2 * k - 3]) << 3;
-    vp.x[k] = (lo & kEvenDims) | (hi & ~kEvenDims);
-    vp.x[4 + k] = (lo & (kEvenDims << 3)) | (hi & ~(kEvenDims << 3));
+    vp.x[k] = bit_select(kEvenDims, lo, hi);
+    vp.x[4 + k] = bit_select(kEvenDims << 3, lo, hi);
   }
 }
 
