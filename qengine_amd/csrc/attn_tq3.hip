@@ -192,11 +192,12 @@ __device__ __forceinline__ void score_group(const uint8_t* lds, uint32_t (&ac)[4
 
 // One value pass: a (32-key chunk c2, 128-block j) pair.  MFMA k index i of
 // the pass is key 32*c2 + 4*row + i (i < 4) or 32*c2 + 16 + 4*row + i - 4.
-// x: the code group `col` (8 dims, 24 bits) of keys i = 2k and 2k + 1
-// interleaved per dim, so that one 6-bit field is a table index whose entry is
-// already the B dword (key 2k in the low half, key 2k + 1 in the high half):
-// x[k] holds dims 0, 2, 4, 6 (field 6d: codes of dim 2d), x[4 + k] dims 1, 3,
-// 5, 7 (field 6d + 3: codes of dim 2d + 1).
+// x: the code group `col` (8 dims, 24 bits) of key i as loaded; from the
+// pass's first table reads on (interleave_pairs), the codes of keys 2k and
+// 2k + 1 interleaved per dim, so that one 6-bit field is a table index whose
+// entry is already the B dword (key 2k in the low half, key 2k + 1 in the
+// high half): x[k] holds dims 0, 2, 4, 6 (field 6d: codes of dim 2d),
+// x[4 + k] dims 1, 3, 5, 7 (field 6d + 3: codes of dim 2d + 1).
 // a: A operand (p * value norm of those keys, head `col`).
 struct ValuePass {
   uint32_t x[8];
@@ -227,23 +228,33 @@ __device__ __forceinline__ void value_pass_load(const float* st, const uint32_t*
   for (int r = 0; r < 4; r++) {
     vp.a[r] = (_Float16)(s[2 * c2][r] * va[r]);
     vp.a[4 + r] = (_Float16)(s[2 * c2 + 1][r] * vb[r]);
+    vp.x[r] = xa[r];
+    vp.x[4 + r] = xb[r];
   }
-  // key pairs (i, i + 1) = (2k, 2k + 1): the second key's codes moved up by
-  // one code, merged with the first key's by bit select
+}
+
+// Key pairs (i, i + 1) = (2k, 2k + 1) of a pass's codes as loaded (x[i]: key
+// i's code group): the second key's codes moved up by one code, merged with
+// the first key's by bit select.  Done in place at the pass's first table
+// reads, two steps after its staging loads were issued.
+__device__ __forceinline__ void interleave_pairs(uint32_t (&x)[8]) {
+  uint32_t z[8];
 #pragma unroll
   for (int k = 0; k < 4; k++) {
-    const uint32_t lo = k < 2 ? xa[2 * k] : xb[2 * k - 4];
-    const uint32_t hi = (k < 2 ? xa[2 * k + 1] : xb[2 * k - 3]) << 3;
-    vp.x[k] = bit_select(kEvenDims, lo, hi);
-    vp.x[4 + k] = bit_select(kEvenDims << 3, lo, hi);
+    const uint32_t hi = x[2 * k + 1] << 3;
+    z[k] = bit_select(kEvenDims, x[2 * k], hi);
+    z[4 + k] = bit_select(kEvenDims << 3, x[2 * k], hi);
   }
+#pragma unroll
+  for (int i = 0; i < 8; i++) x[i] = z[i];
 }
 
 // Table reads of dims 2PP (cp[0..3]) and 2PP+1 (cp[4..7]) of the 4 key pairs:
 // each entry is a B dword (two keys, one dim).
 template <int PP>
-__device__ __forceinline__ void value_pairs(const uint8_t* lds, uint32_t (&ac)[4], const uint32_t (&x)[8],
+__device__ __forceinline__ void value_pairs(const uint8_t* lds, uint32_t (&ac)[4], uint32_t (&x)[8],
                                             uint32_t (&cp)[8]) {
+  if constexpr (PP == 0) interleave_pairs(x);
 #pragma unroll
   for (int k = 0; k < 4; k++) {
     ac[k] = sdwa_index<6 * PP>(ac[k], x[k]);
