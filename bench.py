@@ -147,6 +147,24 @@ def secondary(torch, kvcache, dev, stream):
         graphs.append(gr)
     ms = _time(torch, stream, lambda i=0: graphs[i % sets].replay(), 50) / layers
     del graphs
+
+    # the same step as one fused launch per layer (append inside the decode)
+    def q8_layer_fused(i=0):
+        kb, vb = caches[i % len(caches)]
+        kvcache.decode_attn_q8_append(q, knew, vnew, kb, vb, o, ws8, num_q=NUM_Q, num_kv=NUM_KV,
+                                      start_pos=ctx, scale=scale)
+    graphs = []
+    for s_ in range(sets):
+        for l_ in range(layers):
+            q8_layer_fused(s_ * layers + l_)
+        torch.cuda.synchronize()
+        gr = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(gr):
+            for l_ in range(layers):
+                q8_layer_fused(s_ * layers + l_)
+        graphs.append(gr)
+    ms_fused = _time(torch, stream, lambda i=0: graphs[i % sets].replay(), 50) / layers
+    del graphs
     q8_bytes = 2 * (ctx + 1) * blocks_tok * 36 + NUM_Q * HD * 2 * 2
     out["config2_q8_decode"] = {
         "us_per_layer": round(ms * 1e3, 3),
@@ -154,7 +172,11 @@ def secondary(torch, kvcache, dev, stream):
         "frac": round(q8_bytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
         "eager_us_per_layer": round(ms_eager * 1e3, 3),
         "split_api_us_per_layer": round(ms_split * 1e3, 3),
-        "note": "per layer: Q8 append of the new token's K and V and single-launch decode over "
+        "fused_us_per_layer": round(ms_fused * 1e3, 3),
+        "fused_frac": round(q8_bytes / (ms_fused * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+        "note": "fused_us_per_layer: the same step through qkv_decode_attn_q8_append (the "
+                "append inside the decode launch: 1 launch per layer), HIP graphs as above; "
+                "per layer: Q8 append of the new token's K and V and single-launch decode over "
                 "4097 keys (2 launches), launched from HIP graphs (8 layers per graph, 4 cache "
                 "sets); eager_us_per_layer: the same calls launched one by one from Python; "
                 "split_api_us_per_layer: the same through the reference "

@@ -358,6 +358,22 @@ int qkv_decode_attn_q8(const uint16_t* q, const qkv_block_q8* k, const qkv_block
                        int sub_n, float scale, void* workspace, size_t workspace_bytes,
                        hipStream_t stream);
 
+/* Q8_0 append and decode of one new token in one launch.  Replaces the
+ * reference's decode-step pair quantize_kv_q8_0_kern (K, then V; append,
+ * model.cuh:2316-2333, attention.cuh:2587-2609) followed by the decode
+ * attention (model.cuh:2430-2463): k_new, v_new are the token's fp16 K and V
+ * rows [num_kv][256] (16-byte aligned); the kernel quantizes them exactly as
+ * qkv_q8_append does, writes them to row start_pos of k and v (pad fields
+ * untouched) and uses them as key start_pos of the attention of the one query
+ * q over keys 0..start_pos.  The result and the caches equal those of
+ * qkv_q8_append (K and V) followed by qkv_decode_attn_q8 with sub_n 1; same
+ * workspace (qkv_decode_attn_q8_workspace_bytes(num_q, num_kv, 1,
+ * start_pos + 1)) and errors. */
+int qkv_decode_attn_q8_append(const uint16_t* q, const uint16_t* k_new, const uint16_t* v_new,
+                              qkv_block_q8* k, qkv_block_q8* v, uint16_t* out, int num_q,
+                              int num_kv, int head_dim, int start_pos, float scale,
+                              void* workspace, size_t workspace_bytes, hipStream_t stream);
+
 /* V-only TurboQuant (TQ_KEYS_Q8=1): keys in Q8_0 (k, 8 blocks per kv head and
  * token), values in TQ3 (v, 2 blocks per kv head and token).  Replaces the
  * reference's unfused sequence for that mode (model.cuh:2574-2588:

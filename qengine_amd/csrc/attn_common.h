@@ -69,6 +69,13 @@ struct AttnArgs {
   int* ws_header;           // kWsHeaderBytes; word kWsErrorWord: sticky merge error
   uint32_t ws_ml_bytes, ws_o_bytes;
   int spin_limit;           // merger poll limit (kMergeSpinLimit unless a test lowers it)
+  // fused Q8 append (q8_attn_kernel APPEND, sub_n == 1): the new token's fp16
+  // K and V rows [num_kv][256], quantized in the kernel, used for key
+  // start_pos and written to that row of the caches (k_w, v_w = k, v)
+  const uint16_t* k_new;
+  const uint16_t* v_new;
+  uint8_t* k_w;
+  uint8_t* v_w;
 };
 
 // Buffer resource over bytes [off, extent) of a cache, rebased at the 64-bit
@@ -266,6 +273,7 @@ hipError_t noalloc_scratch(int device, bool clear, hipStream_t stream, void** pt
 hipError_t launch_q8_attn_split(const AttnArgs& a, hipStream_t stream);
 hipError_t launch_q8_attn_fast(const AttnArgs& a, uint16_t* out, hipStream_t stream);
 hipError_t launch_q8k_tq3v_attn_fast(const AttnArgs& a, uint16_t* out, hipStream_t stream);
+hipError_t launch_q8_attn_fast_append(const AttnArgs& a, uint16_t* out, hipStream_t stream);
 hipError_t launch_split_merge(const float* m, const float* l, const float* o, uint16_t* out,
                               int num_q, int sub_n, int sub_n_max, int k_splits,
                               hipStream_t stream);

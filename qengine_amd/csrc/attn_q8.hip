@@ -160,12 +160,91 @@ __device__ __forceinline__ void wave_sync() {
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
-template <int MODE, bool VTQ3 = false>
+// Fused append (q8_attn_kernel APPEND): the wave whose tile holds key
+// P = start_pos quantizes the new K and V rows of its kv head with the
+// arithmetic of q8_append_kernel (attention.cuh:2587-2609): lane l takes
+// elements 4l..4l+3 (block l / 8), the block absmax is an xor reduction over
+// its 8 lanes, amax / 127 and 1 / scale are IEEE single roundings, codes are
+// rint (half to even) clamped to [-128, 127].  Every lane stores its code
+// dword to the cache row (lanes 8b also the fp16 scale, with a 16-bit store
+// so that pad keeps what the cache held) and to the wave's row image in LDS
+// (9 dwords per block: codes, then pad|d with pad 0).  The key registers of
+// key P (lane (row, col = P % 16), blocks 2row and 2row + 1 of group
+// (P - ts) / 16), loaded from the not yet written row, are replaced from the
+// image, and so are key P's staged values.
+constexpr int kNewRowDw = 2 * 72;   // K then V image, 8 blocks x 9 dwords each
+
+__device__ __forceinline__ uint32_t q8_new_dword(uint2 hv, int lane, uint8_t* cache,
+                                                 uint64_t row_off, uint32_t* img) {
+  const float v[4] = {h2f(hv.x & 0xffffu), h2f(hv.x >> 16), h2f(hv.y & 0xffffu), h2f(hv.y >> 16)};
+  float amax = fmaxf(fmaxf(__builtin_fabsf(v[0]), __builtin_fabsf(v[1])),
+                     fmaxf(__builtin_fabsf(v[2]), __builtin_fabsf(v[3])));
+  amax = fmaxf(amax, __shfl_xor(amax, 1));
+  amax = fmaxf(amax, __shfl_xor(amax, 2));
+  amax = fmaxf(amax, __shfl_xor(amax, 4));
+  const float scale = amax / 127.0f;
+  const float inv = scale > 0.0f ? 1.0f / scale : 0.0f;
+  uint32_t word = 0u;
+#pragma unroll
+  for (int e = 0; e < 4; e++) {
+    int q = (int)__builtin_rintf(v[e] * inv);
+    q = q > 127 ? 127 : (q < -128 ? -128 : q);
+    word |= ((uint32_t)q & 0xffu) << (8 * e);
+  }
+  const int b = lane >> 3, i = lane & 7;
+  const uint32_t d = f2h(scale);
+  *reinterpret_cast<uint32_t*>(cache + row_off + 36 * b + 4 * i) = word;
+  img[9 * b + i] = word;
+  if (i == 0) {
+    *reinterpret_cast<uint16_t*>(cache + row_off + 36 * b + 34) = (uint16_t)d;
+    img[9 * b + 8] = d << 16;
+  }
+  return word;
+}
+
+// kn, vn: elements 4 lane .. 4 lane + 3 of the new K and V rows of kv head h
+// (loaded at kernel start).
+__device__ __forceinline__ void append_new_row(const AttnArgs& p, int kp, int h, int lane, int row,
+                                               int col, uint2 kn, uint2 vn, uint32_t* img,
+                                               TileQ8& t) {
+  const uint64_t row_off = ((uint64_t)(uint32_t)p.start_pos * (uint32_t)p.num_kv + h) * kRowBytes;
+  q8_new_dword(kn, lane, p.k_w, row_off, img);
+  q8_new_dword(vn, lane, p.v_w, row_off, img + 72);
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  // keys: selects with constant register indices (the group is wave-uniform,
+  // the lane is not), so that the tile registers stay registers
+  const bool mine = col == (kp & 15), g0 = (kp >> 4) == 0;
+  const uint32_t* src = img + 18 * row;
+#pragma unroll
+  for (int i = 0; i < 18; i++) {
+    const uint32_t nv = src[i];
+    t.k[0][i] = (mine && g0) ? nv : t.k[0][i];
+    t.k[1][i] = (mine && !g0) ? nv : t.k[1][i];
+  }
+}
+
+// Values of the new key in the staging area ([8 blk + q][key] code dwords,
+// [blk][key] scales), over what the lanes of key kp staged from the cache.
+__device__ __forceinline__ void stage_new_values(const uint32_t* img, int kp, int lane, float* st,
+                                                 uint32_t* stu) {
+  const int b = lane >> 3, i = lane & 7;
+  stu[kStCodes + (8 * b + i) * kPitch + kp] = img[72 + 9 * b + i];
+  if (i == 0) st[kStScale + b * kPitch + kp] = scale_of(img[72 + 9 * b + 8]);
+}
+
+template <int MODE, bool VTQ3 = false, bool APPEND = false>
 __global__ __launch_bounds__(kThreads, 2) void q8_attn_kernel(AttnArgs p, uint16_t* out) {
   static_assert(!VTQ3 || MODE == 0, "mixed formats: fast path only");
-  __shared__ __attribute__((aligned(16))) uint8_t lds[VTQ3 ? kMxLdsTotal : kLdsTotal];
+  static_assert(!APPEND || (MODE == 0 && !VTQ3), "fused append: Q8 fast path only");
+  // APPEND: each wave's new-row image follows the tile staging areas
+  constexpr int kLdsNewRow = kLdsTotalTile;
+  constexpr int kLdsAppend = kLdsNewRow + kWaves * kNewRowDw * 4;
+  __shared__ __attribute__((aligned(16)))
+  uint8_t lds[VTQ3 ? kMxLdsTotal : (APPEND && kLdsAppend > kLdsTotal ? kLdsAppend : kLdsTotal)];
   const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int row = lane >> 4, col = lane & 15;
   const int gqa = p.num_q / p.num_kv;
 
@@ -228,10 +307,29 @@ __global__ __launch_bounds__(kThreads, 2) void q8_attn_kernel(AttnArgs p, uint16
                                                    : kLdsStage + wave * kStageBytes));
   uint32_t* stu = reinterpret_cast<uint32_t*>(st);
 
+  // fused append: the new rows' elements of this lane, loaded up front by the
+  // wave whose tiles include key start_pos
+  uint2 new_k = make_uint2(0u, 0u), new_v = make_uint2(0u, 0u);
+  if constexpr (APPEND) {
+    if (p.start_pos >= lo + wave * kTile && p.start_pos < hi &&
+        ((p.start_pos - lo) / kTile) % kWaves == wave) {
+      new_k = *reinterpret_cast<const uint2*>(p.k_new + (long)h * kHD + 4 * lane);
+      new_v = *reinterpret_cast<const uint2*>(p.v_new + (long)h * kHD + 4 * lane);
+    }
+  }
   bool first = true;
   for (int ts = lo + wave * kTile; ts < hi; ts += kWaves * kTile) {
     TileQ8 tr;
     load_tile_q8<VTQ3>(p, ts, p.num_kv, h, lane, row, col, tr);
+    if constexpr (APPEND) {
+      // the new token (sub_n == 1: key start_pos) lies in at most one tile
+      // of the kv head; ts is wave-uniform
+      if (p.start_pos >= ts && p.start_pos < ts + kTile)
+        append_new_row(p, p.start_pos - ts, h, lane, row, col, new_k, new_v,
+                       reinterpret_cast<uint32_t*>(lds + kLdsNewRow) + wave * kNewRowDw, tr);
+      // (the new key's value registers stay stale: its staged values are
+      // replaced from the image below)
+    }
 
     // ---- scores: D rows = keys 16g + 4*row + r, D col = head `col`
     f4_t sa[2];
@@ -279,6 +377,11 @@ __global__ __launch_bounds__(kThreads, 2) void q8_attn_kernel(AttnArgs p, uint16
 #pragma unroll
         for (int q = 0; q < 8; q++) stu[kStCodes + (8 * blk + q) * kPitch + kl] = w[q];
         st[kStScale + blk * kPitch + kl] = scale_of(w[8]);
+      }
+      if constexpr (APPEND) {
+        if (p.start_pos >= ts && p.start_pos < ts + kTile)
+          stage_new_values(reinterpret_cast<const uint32_t*>(lds + kLdsNewRow) + wave * kNewRowDw,
+                           p.start_pos - ts, lane, st, stu);
       }
     }
     wave_sync();
@@ -488,6 +591,13 @@ hipError_t launch_q8_attn_fast(const AttnArgs& a, uint16_t* out, hipStream_t str
   const int groups = a.sub_n * a.n_chunks;
   const int n_wg = ((groups + 7) / 8) * 8 * a.num_kv;
   hipLaunchKernelGGL((q8_attn_kernel<0>), dim3(n_wg), dim3(kThreads), 0, stream, a, out);
+  return hipGetLastError();
+}
+
+hipError_t launch_q8_attn_fast_append(const AttnArgs& a, uint16_t* out, hipStream_t stream) {
+  const int groups = a.sub_n * a.n_chunks;
+  const int n_wg = ((groups + 7) / 8) * 8 * a.num_kv;
+  hipLaunchKernelGGL((q8_attn_kernel<0, false, true>), dim3(n_wg), dim3(kThreads), 0, stream, a, out);
   return hipGetLastError();
 }
 

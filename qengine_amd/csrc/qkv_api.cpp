@@ -628,7 +628,8 @@ size_t qkv_decode_attn_q8_workspace_bytes(int num_q, int num_kv, int sub_n, int 
 static int decode_q8_keys(const uint16_t* q, const void* k, const void* v, uint16_t* out,
                           int num_q, int num_kv, int head_dim, int start_pos, int sub_n,
                           float scale, void* workspace, size_t workspace_bytes, bool v_tq3,
-                          hipStream_t stream) {
+                          hipStream_t stream, const uint16_t* k_new = nullptr,
+                          const uint16_t* v_new = nullptr) {
   int st = check_attn_shape(num_q, num_kv, head_dim, start_pos, sub_n, nullptr);
   if (st) return st;
   if (!q || !k || !v || !out) return QKV_ERR_NULL;
@@ -667,8 +668,25 @@ static int decode_q8_keys(const uint16_t* q, const void* k, const void* v, uint1
   if (g.total > 0xffffffffULL) return QKV_ERR_UNSUPPORTED;   // 32-bit buffer offsets
   a.ws_ml_bytes = (uint32_t)(g.o_off - g.ml_off);
   a.ws_o_bytes = (uint32_t)(g.total - g.o_off);
+  if (k_new) {
+    a.k_new = k_new;
+    a.v_new = v_new;
+    a.k_w = static_cast<uint8_t*>(const_cast<void*>(k));
+    a.v_w = static_cast<uint8_t*>(const_cast<void*>(v));
+    return launch_status(qkv::launch_q8_attn_fast_append(a, out, stream));
+  }
   return launch_status(v_tq3 ? qkv::launch_q8k_tq3v_attn_fast(a, out, stream)
                              : qkv::launch_q8_attn_fast(a, out, stream));
+}
+
+int qkv_decode_attn_q8_append(const uint16_t* q, const uint16_t* k_new, const uint16_t* v_new,
+                              qkv_block_q8* k, qkv_block_q8* v, uint16_t* out, int num_q,
+                              int num_kv, int head_dim, int start_pos, float scale,
+                              void* workspace, size_t workspace_bytes, hipStream_t stream) {
+  if (!k_new || !v_new) return QKV_ERR_NULL;
+  if (!aligned(k_new, 16) || !aligned(v_new, 16)) return QKV_ERR_ALIGN;
+  return decode_q8_keys(q, k, v, out, num_q, num_kv, head_dim, start_pos, 1, scale, workspace,
+                        workspace_bytes, false, stream, k_new, v_new);
 }
 
 int qkv_decode_attn_q8(const uint16_t* q, const qkv_block_q8* k, const qkv_block_q8* v,

@@ -307,6 +307,18 @@ def decode_attn_q8(q, k, v, out, workspace, *, num_q, num_kv, start_pos, sub_n, 
         workspace.numel() * workspace.element_size(), _stream(stream)), "qkv_decode_attn_q8")
 
 
+def decode_attn_q8_append(q, k_new, v_new, k, v, out, workspace, *, num_q, num_kv, start_pos,
+                          scale, head_dim=256, stream=None) -> None:
+    """One launch for a decode step over the Q8_0 cache: k_new / v_new (fp16
+    [num_kv][256]) are quantized into row start_pos of k / v and attended as
+    key start_pos by the one query q (keys 0..start_pos)."""
+    check(lib().qkv_decode_attn_q8_append(
+        _dev_ptr(q, "q"), _dev_ptr(k_new, "k_new"), _dev_ptr(v_new, "v_new"), _dev_ptr(k, "k"),
+        _dev_ptr(v, "v"), _dev_ptr(out, "out"), num_q, num_kv, head_dim, start_pos, float(scale),
+        _dev_ptr(workspace, "workspace"), workspace.numel() * workspace.element_size(),
+        _stream(stream)), "qkv_decode_attn_q8_append")
+
+
 def decode_attn_q8k_tq3v_workspace(num_q, num_kv, sub_n, n_keys, device) -> torch.Tensor:
     """Zero-filled workspace for decode_attn_q8k_tq3v."""
     n = int(lib().qkv_decode_attn_q8k_tq3v_workspace_bytes(num_q, num_kv, sub_n, n_keys))

@@ -149,3 +149,47 @@ def test_q8_append_kv_matches_two_appends(dev):
     kvcache.q8_append(v, b2)
     torch.cuda.synchronize()
     assert torch.equal(a1, b1) and torch.equal(a2, b2)
+
+
+@pytest.mark.parametrize("n_old,num_q", [
+    (4096, 16),    # config 2: 4096 cached keys + the new one
+    (0, 16), (31, 16), (32, 16), (127, 16), (128, 16), (5000, 16),
+    (700, 24),     # GQA 6
+])
+def test_q8_fused_append_decode_matches_two_calls(dev, n_old, num_q):
+    """qkv_decode_attn_q8_append (quantize the new token into row n_old and
+    attend keys 0..n_old in one launch) against qkv_q8_append_kv followed by
+    qkv_decode_attn_q8: identical cache bytes (pad fields untouched) and
+    identical output bits; the output also against the oracle."""
+    from qengine_amd import kvcache
+    torch = _torch()
+    n = n_old + 1
+    rng, kb, vb = _cache(900 + n_old + num_q, n)
+    kn = _torch().from_numpy(kv_f16(rng, 1, 4, 256).reshape(-1).view(np.uint16).copy())
+    vn = _torch().from_numpy(kv_f16(rng, 1, 4, 256).reshape(-1).view(np.uint16).copy())
+    q = q_f16(rng, 1, num_q, 256)
+    k_new, v_new = kn.view(torch.float16).to(dev), vn.view(torch.float16).to(dev)
+    # cache rows past n_old hold a marker pattern: the fused call must write row
+    # n_old exactly as the append does and leave the pad half-words alone
+    kc = _dev(kb.view(np.uint8), dev).reshape(n, -1)
+    vc = _dev(vb.view(np.uint8), dev).reshape(n, -1)
+    kc[n_old:] = 0x5A
+    vc[n_old:] = 0xA5
+    k1, v1, k2, v2 = kc.clone(), vc.clone(), kc.clone(), vc.clone()
+    qd = _dev(q.view(np.uint16), dev)
+    ws1 = kvcache.decode_attn_q8_workspace(num_q, 4, 1, n, dev)
+    ws2 = kvcache.decode_attn_q8_workspace(num_q, 4, 1, n, dev)
+    o1 = torch.zeros((1, num_q, 256), dtype=torch.float16, device=dev)
+    o2 = torch.zeros((1, num_q, 256), dtype=torch.float16, device=dev)
+    row = 4 * 8 * 36
+    kvcache.q8_append_kv(k_new, v_new, k1.view(-1)[n_old * row:], v1.view(-1)[n_old * row:])
+    kvcache.decode_attn_q8(qd, k1, v1, o1, ws1, num_q=num_q, num_kv=4, start_pos=n_old,
+                           sub_n=1, scale=1 / 16)
+    kvcache.decode_attn_q8_append(qd, k_new, v_new, k2, v2, o2, ws2, num_q=num_q, num_kv=4,
+                                  start_pos=n_old, scale=1 / 16)
+    torch.cuda.synchronize()
+    assert torch.equal(k1, k2) and torch.equal(v1, v2)
+    assert torch.equal(o1, o2)
+    kb2 = k2.cpu().numpy().reshape(-1).view(kb.dtype)
+    vb2 = v2.cpu().numpy().reshape(-1).view(vb.dtype)
+    assert rel_err(o2.cpu().numpy(), _expected(q, kb2, vb2, n, num_q, 1)) < TOL
