@@ -78,6 +78,48 @@ struct AttnArgs {
   uint8_t* v_w;
 };
 
+// ---- leading (preloaded) kernel arguments -------------------------------
+// The library is compiled with -mllvm -amdgpu-kernarg-preload-count=16: on
+// gfx950 the command processor writes the leading kernel arguments straight
+// into SGPRs at wave launch (14 SGPRs, after the kernarg segment pointer).
+// The attention kernels therefore take the fields their first loads depend on
+// as leading scalar arguments ahead of the AttnArgs block (whose remaining
+// fields are read through the kernarg segment as before), so that the query
+// and tile loads issue without waiting for a kernel-argument round trip.
+// (Firmware without preload support runs the compiler's compatibility
+// prologue, which loads the same SGPRs.)
+//   lead_heads: num_q | num_kv << 16;  lead_flags: qpw | paged << 8 | ragged << 9
+#define QKV_ATTN_LEAD_PARAMS                                                                    \
+  const uint16_t *lead_q, const uint32_t *lead_k, const uint32_t *lead_v, uint64_t lead_kv_bytes, \
+      uint32_t lead_heads, uint32_t lead_flags, int lead_start_pos, int lead_sub_n,              \
+      int lead_n_chunks, int lead_chunk_keys
+#define QKV_ATTN_LEAD_ARGS(a)                                                                    \
+  (a).q, (a).k, (a).v, (a).kv_bytes, ::qkv::attn_lead_heads(a), ::qkv::attn_lead_flags(a),      \
+      (a).start_pos, (a).sub_n, (a).n_chunks, (a).chunk_keys
+// Local AttnArgs `p`: the block `pin` with the leading arguments written over
+// it (the compiler then takes those fields from the preloaded SGPRs).
+#define QKV_ATTN_LEAD_APPLY(p, pin)                                                   \
+  AttnArgs p = (pin);                                                                 \
+  p.q = lead_q;                                                                       \
+  p.k = lead_k;                                                                       \
+  p.v = lead_v;                                                                       \
+  p.kv_bytes = lead_kv_bytes;                                                         \
+  p.num_q = (int)(lead_heads & 0xffffu);                                              \
+  p.num_kv = (int)(lead_heads >> 16);                                                 \
+  p.qpw = (int)(lead_flags & 0xffu);                                                  \
+  p.start_pos = lead_start_pos;                                                       \
+  p.sub_n = lead_sub_n;                                                               \
+  p.n_chunks = lead_n_chunks;                                                         \
+  p.chunk_keys = lead_chunk_keys
+inline uint32_t attn_lead_heads(const AttnArgs& a) {
+  return (uint32_t)a.num_q | ((uint32_t)a.num_kv << 16);
+}
+inline uint32_t attn_lead_flags(const AttnArgs& a) {
+  return (uint32_t)a.qpw | (a.block_tables ? 1u << 8 : 0u) | (a.ctx_lens ? 1u << 9 : 0u);
+}
+// Head counts that fit the 16-bit fields of lead_heads.
+constexpr int kLeadMaxHeads = 0xffff;
+
 // Buffer resource over bytes [off, extent) of a cache, rebased at the 64-bit
 // byte offset `off` (wave-uniform) so that the in-tile offsets of a load stay
 // small: caches past 4 GiB are addressed exactly.  Bytes at or past `extent`

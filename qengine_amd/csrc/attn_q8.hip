@@ -235,7 +235,9 @@ __device__ __forceinline__ void stage_new_values(const uint32_t* img, int kp, in
 }
 
 template <int MODE, bool VTQ3 = false, bool APPEND = false>
-__global__ __launch_bounds__(kThreads, 2) void q8_attn_kernel(AttnArgs p, uint16_t* out) {
+__global__ __launch_bounds__(kThreads, 2) void q8_attn_kernel(QKV_ATTN_LEAD_PARAMS, AttnArgs pin,
+                                                              uint16_t* out) {
+  QKV_ATTN_LEAD_APPLY(p, pin);
   static_assert(!VTQ3 || MODE == 0, "mixed formats: fast path only");
   static_assert(!APPEND || (MODE == 0 && !VTQ3), "fused append: Q8 fast path only");
   // APPEND: each wave's new-row image follows the tile staging areas
@@ -583,28 +585,28 @@ __global__ __launch_bounds__(kThreads, 2) void q8_attn_kernel(AttnArgs p, uint16
 
 hipError_t launch_q8_attn_split(const AttnArgs& a, hipStream_t stream) {
   const int n_wg = a.num_kv * a.sub_n * a.k_splits;
-  hipLaunchKernelGGL((q8_attn_kernel<1>), dim3(n_wg), dim3(kThreads), 0, stream, a, nullptr);
+  hipLaunchKernelGGL((q8_attn_kernel<1>), dim3(n_wg), dim3(kThreads), 0, stream, QKV_ATTN_LEAD_ARGS(a), a, nullptr);
   return hipGetLastError();
 }
 
 hipError_t launch_q8_attn_fast(const AttnArgs& a, uint16_t* out, hipStream_t stream) {
   const int groups = a.sub_n * a.n_chunks;
   const int n_wg = ((groups + 7) / 8) * 8 * a.num_kv;
-  hipLaunchKernelGGL((q8_attn_kernel<0>), dim3(n_wg), dim3(kThreads), 0, stream, a, out);
+  hipLaunchKernelGGL((q8_attn_kernel<0>), dim3(n_wg), dim3(kThreads), 0, stream, QKV_ATTN_LEAD_ARGS(a), a, out);
   return hipGetLastError();
 }
 
 hipError_t launch_q8_attn_fast_append(const AttnArgs& a, uint16_t* out, hipStream_t stream) {
   const int groups = a.sub_n * a.n_chunks;
   const int n_wg = ((groups + 7) / 8) * 8 * a.num_kv;
-  hipLaunchKernelGGL((q8_attn_kernel<0, false, true>), dim3(n_wg), dim3(kThreads), 0, stream, a, out);
+  hipLaunchKernelGGL((q8_attn_kernel<0, false, true>), dim3(n_wg), dim3(kThreads), 0, stream, QKV_ATTN_LEAD_ARGS(a), a, out);
   return hipGetLastError();
 }
 
 hipError_t launch_q8k_tq3v_attn_fast(const AttnArgs& a, uint16_t* out, hipStream_t stream) {
   const int groups = a.sub_n * a.n_chunks;
   const int n_wg = ((groups + 7) / 8) * 8 * a.num_kv;
-  hipLaunchKernelGGL((q8_attn_kernel<0, true>), dim3(n_wg), dim3(kThreads), 0, stream, a, out);
+  hipLaunchKernelGGL((q8_attn_kernel<0, true>), dim3(n_wg), dim3(kThreads), 0, stream, QKV_ATTN_LEAD_ARGS(a), a, out);
   return hipGetLastError();
 }
 

@@ -451,7 +451,10 @@ __device__ void finish_rows(const uint8_t* lds, const AttnArgs& p, int h, int t,
 // MFMA column a real (query, head); the remainders ride in a chained second
 // score product (see score_group).
 template <int MODE, bool CHAIN = false>
-__global__ __launch_bounds__(kThreads, 1) void tq3_attn_kernel(AttnArgs p, uint16_t* out) {
+__global__ __launch_bounds__(kThreads, 1) void tq3_attn_kernel(QKV_ATTN_LEAD_PARAMS, AttnArgs pin,
+                                                                uint16_t* out) {
+  QKV_ATTN_LEAD_APPLY(p, pin);
+  const bool paged = (lead_flags & (1u << 8)) != 0, ragged = (lead_flags & (1u << 9)) != 0;
   // static LDS: table and tile offsets fold into the instructions' offset field
   __shared__ __attribute__((aligned(16))) uint8_t lds[kLdsTotal];
 #ifdef QKV_PHASE_TRACE
@@ -477,7 +480,7 @@ __global__ __launch_bounds__(kThreads, 1) void tq3_attn_kernel(AttnArgs p, uint1
     const int g = (r / p.num_kv) * 8 + xcd;
     const int groups = (p.sub_n + p.qpw - 1) / p.qpw;
     has_work = g < groups * p.n_chunks;
-    if (MODE == 0 && p.ctx_lens) {
+    if (MODE == 0 && ragged) {
       // ragged slots (one query each): share g of the length-proportional split
       int first, count;
       const int s = has_work ? share_slot(p, g, first, count) : -1;
@@ -504,12 +507,32 @@ __global__ __launch_bounds__(kThreads, 1) void tq3_attn_kernel(AttnArgs p, uint1
   const int row = lane >> 4;        // 16-lane row of the MFMA D layout
   const int col = lane & 15;
   const int t_col = t0 + min(col / gqa, nq - 1);   // this lane's query (clamped for dead columns)
+  // ---- the query load goes out first: its address depends only on the
+  // preloaded arguments
+  // 32 WHTs of 128 (16 columns x 2 blocks), 16 lanes each
+  const int q_wht = threadIdx.x >> 4;
+  const int q_part = threadIdx.x & 15;
+  const int q_col = q_wht >> 1, q_blk = q_wht & 1;   // column, 128-block
+  u4_t q_raw;
+  {
+    // unconditional (rows past the buffer's extent read as zero): a load
+    // under a branch makes the compiler wait for every load at the join
+    const uint32_t q_extent = (uint32_t)(p.sub_n * p.num_q * kHD * 2);
+    const __amdgpu_buffer_rsrc_t rq =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(p.q), 0, q_extent, kBufferRsrcWord3);
+    const uint32_t qoff =
+        q_col < rows_used ? (uint32_t)((((t0 + q_col / gqa) * p.num_q + h * gqa + q_col % gqa) * kHD +
+                                        q_blk * 128 + q_part * 8) * 2)
+                          : q_extent;
+    q_raw = __builtin_amdgcn_raw_buffer_load_b128(rq, qoff, 0, 0);
+  }
+  __builtin_amdgcn_sched_barrier(0);
   // key counts: the lane's own query, and the first / last query of the group
   // (a paged group has one query)
-  const int active_end = p.ctx_lens ? min(max(p.ctx_lens[t_col], 0), p.ctx_max)
+  const int active_end = ragged ? min(max(p.ctx_lens[t_col], 0), p.ctx_max)
                                     : p.start_pos + t_col + 1;
-  const int active_first = p.ctx_lens ? active_end : p.start_pos + t0 + 1;
-  const int active_last = p.ctx_lens ? active_end : p.start_pos + t0 + nq;
+  const int active_first = ragged ? active_end : p.start_pos + t0 + 1;
+  const int active_last = ragged ? active_end : p.start_pos + t0 + nq;
   int lo = 0, hi = 0, hi_col = 0, hi_first = 0;
   if (MODE == 0) {
     if (has_work) {
@@ -538,16 +561,11 @@ __global__ __launch_bounds__(kThreads, 1) void tq3_attn_kernel(AttnArgs p, uint1
   hi_first = __builtin_amdgcn_readfirstlane(hi_first);
   // A dead column has a zero query: its scores are 0 and its accumulator rows
   // are never stored, so it needs no mask of its own.
-  const KeyRule rule(p.start_pos, t_col, p.sink_tok, p.window_tok, p.tree_mask);
 
-  // ---- setup: query load, centroid-pair table, rotated query --------------
+  // ---- setup: centroid-pair table, rotated query --------------------------
   // The query is loaded and rotated before any tile load is issued: a query
   // load issued after the tile loads of the whole chip would wait behind
   // them in the memory queues.
-  // 32 WHTs of 128 (16 columns x 2 blocks), 16 lanes each
-  const int q_wht = threadIdx.x >> 4;
-  const int q_part = threadIdx.x & 15;
-  const int q_col = q_wht >> 1, q_blk = q_wht & 1;   // column, 128-block
   // paged caches: the block-table entries of this wave's first 64 tiles (lane
   // k: tile k, key lo + wave*64 + k*kStep), loaded now so that no tile load
   // waits for a table read (rows past the table's extent read as 0)
@@ -581,13 +599,13 @@ __global__ __launch_bounds__(kThreads, 1) void tq3_attn_kernel(AttnArgs p, uint1
                                  : 0xffffffffu;
     return (int)__builtin_amdgcn_raw_buffer_load_b32(rbt, off, 0, 0);
   };
-  int bt_entry = bt_batch(0), bt_k0 = 0;
+  int bt_entry = paged ? bt_batch(0) : 0, bt_k0 = 0;
   // cache row of this wave's tile starting at key ts: ts itself for a
   // contiguous cache; through the query's block table for a paged one (block
   // sizes are multiples of 64, so a 64-key tile never straddles two blocks);
   // rows outside the cache extent read as zero (buffer range checks)
   auto wave_tile_row = [&](int ts) -> int {
-    if (p.block_tables == nullptr) return ts;
+    if (!paged) return ts;
     if (ts >= hi) return 0;
     const int k = (ts - ts0) / kStep;
     if (k - bt_k0 >= 64) {
@@ -598,19 +616,6 @@ __global__ __launch_bounds__(kThreads, 1) void tq3_attn_kernel(AttnArgs p, uint1
     const int b = ts / p.block_tokens;
     return e * p.block_tokens + (ts - b * p.block_tokens);
   };
-  u4_t q_raw;
-  {
-    // unconditional (rows past the buffer's extent read as zero): a load
-    // under a branch makes the compiler wait for every load at the join
-    const uint32_t q_extent = (uint32_t)(p.sub_n * p.num_q * kHD * 2);
-    const __amdgpu_buffer_rsrc_t rq =
-        __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(p.q), 0, q_extent, kBufferRsrcWord3);
-    const uint32_t qoff =
-        q_col < rows_used ? (uint32_t)((((t0 + q_col / gqa) * p.num_q + h * gqa + q_col % gqa) * kHD +
-                                        q_blk * 128 + q_part * 8) * 2)
-                          : q_extent;
-    q_raw = __builtin_amdgcn_raw_buffer_load_b128(rq, qoff, 0, 0);
-  }
   // waves 0..3 issue their first tile's loads as soon as the query has
   // arrived (so it does not queue behind them), ahead of the table build
   // and the rotation; waves 4..7 issue theirs after the setup barrier.
@@ -713,6 +718,8 @@ __global__ __launch_bounds__(kThreads, 1) void tq3_attn_kernel(AttnArgs p, uint1
   }
   __syncthreads();
   QKV_STAMP(kPhSetup);
+  // (built after the setup: its tree word is a load the first loads must not wait for)
+  const KeyRule rule(p.start_pos, t_col, p.sink_tok, p.window_tok, p.tree_mask);
   // ---- first tile: the first wave of each SIMD (waves 0..3) issues its loads
   // before the second (waves 4..7), so that across the chip the first waves'
   // tiles arrive in the first half of the stream and are computed while the
@@ -1041,13 +1048,13 @@ hipError_t launch_tq3_attn(const AttnArgs& a, int mode, uint16_t* out, hipStream
   const int n_wg = ((groups + 7) / 8) * 8 * a.num_kv;
   dim3 grid(n_wg), block(kThreads);
   if (mode == 0 && a.qpw * (a.num_q / a.num_kv) > 8)
-    hipLaunchKernelGGL((tq3_attn_kernel<0, true>), grid, block, 0, stream, a, out);
+    hipLaunchKernelGGL((tq3_attn_kernel<0, true>), grid, block, 0, stream, QKV_ATTN_LEAD_ARGS(a), a, out);
   else if (mode == 0)
-    hipLaunchKernelGGL((tq3_attn_kernel<0>), grid, block, 0, stream, a, out);
+    hipLaunchKernelGGL((tq3_attn_kernel<0>), grid, block, 0, stream, QKV_ATTN_LEAD_ARGS(a), a, out);
   else if (mode == 1)
-    hipLaunchKernelGGL((tq3_attn_kernel<1>), grid, block, 0, stream, a, out);
+    hipLaunchKernelGGL((tq3_attn_kernel<1>), grid, block, 0, stream, QKV_ATTN_LEAD_ARGS(a), a, out);
   else
-    hipLaunchKernelGGL((tq3_attn_kernel<2>), grid, block, 0, stream, a, out);
+    hipLaunchKernelGGL((tq3_attn_kernel<2>), grid, block, 0, stream, QKV_ATTN_LEAD_ARGS(a), a, out);
   return hipGetLastError();
 }
 

@@ -288,7 +288,7 @@ int check_attn_shape(int num_q, int num_kv, int head_dim, int start_pos, int sub
                      const uint32_t* tree_mask) {
   if (head_dim != 256) return QKV_ERR_UNSUPPORTED;
   if (num_kv <= 0 || num_q <= 0 || num_q % num_kv != 0) return QKV_ERR_INVALID;
-  if (num_q / num_kv > 8) return QKV_ERR_UNSUPPORTED;
+  if (num_q / num_kv > 8 || num_q > qkv::kLeadMaxHeads) return QKV_ERR_UNSUPPORTED;
   if (start_pos < 0 || sub_n < 1) return QKV_ERR_INVALID;
   if (tree_mask && sub_n > 32) return QKV_ERR_INVALID;
   return QKV_OK;

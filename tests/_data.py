@@ -44,6 +44,38 @@ def rel_err_global(out, ref):
     return float(np.max(np.abs(out - ref)) / (den if den > 0 else 1.0))
 
 
+# Fixed cap of the reference-order leg of assert_tq3_attn, used only where the
+# reference order itself lies further than `tol` from the exact attention
+# (the largest such distance measured here: 2.35e-3, 16 verify queries over
+# 32768 keys).  It does not move with the error being checked.
+REF_CAP = 3.5e-3
+
+
+def record_margin(kind, **values):
+    """Append one JSON line {test, kind, values...} to the file named by the
+    QKV_MARGINS environment variable (no-op when it is unset), so that a GPU
+    run can tabulate the measured error of every parity check next to its
+    bar.  The test is pytest's current node id."""
+    import json
+    import os
+    path = os.environ.get("QKV_MARGINS")
+    if not path:
+        return
+    rec = {"test": os.environ.get("PYTEST_CURRENT_TEST", "").split(" ")[0], "kind": kind}
+    for k, v in values.items():
+        rec[k] = v if isinstance(v, (int, float, str, type(None))) else repr(v)
+    with open(path, "a") as f:
+        f.write(json.dumps(rec) + "\n")
+
+
+def check_rel(got, ref, tol, what=""):
+    """rel_err(got, ref) < tol, recorded with record_margin; returns the error."""
+    e = rel_err(got, ref)
+    record_margin("rel_row", err=e, bar=tol, what=what)
+    assert e < tol, (what, e, tol)
+    return e
+
+
 def assert_tq3_attn(got, ref, exact, tol=2e-3, what=""):
     """Bar of the TQ3 decode consumers (rotated-domain arithmetic, fp32
     accumulation):
@@ -51,20 +83,26 @@ def assert_tq3_attn(got, ref, exact, tol=2e-3, what=""):
         attention over the exactly dequantized cache (rel_err, per row);
       - the whole output within `tol` of the reference-order oracle
         (fp16-rounded dequantization, the reference's split order;
-        rel_err_global), or, where the reference itself lies further than
-        that from the exact attention, no further from the reference than
-        `tol` plus the reference's own distance d_ref from the exact result.
+        rel_err_global) whenever that reference lies within `tol` of the
+        exact attention (d_ref <= tol); where it lies further, within the
+        fixed cap REF_CAP instead.  The bar of this leg never grows with the
+        error it checks.
     The reference's numerics round every dequantized element to fp16 before
     its fp32 dot products (attention.cuh:2036-2072 in the split decode,
     turboquant.cuh:199 in the bulk dequantization), which puts its rows up to
     2.4e-3 (per row, 20 seeds at 4097 keys) and its whole output up to ~2.3e-3
-    (32768 keys, 16 verify queries) from the exact attention; the rotated-domain kernels never form those fp16 elements and
-    are held to the exact values instead.  The second part guards the exact
-    oracle path itself (a mistake shared by the kernel and attn_exact_tq3
-    would show up against the independently computed reference order).
+    (32768 keys, 16 verify queries) from the exact attention; the
+    rotated-domain kernels never form those fp16 elements and are held per
+    row to the exact values instead.  The second leg checks the kernel
+    against the independently computed reference order: a mistake shared by
+    the kernel and attn_exact_tq3 that moves the output by more than the bar
+    fails it.  The three errors are recorded (record_margin).
     Returns (per-row vs exact, global vs reference, d_ref)."""
     e_row = rel_err(got, exact)
     e_ref = rel_err_global(got, ref)
     d_ref = rel_err_global(ref, exact)
-    assert e_row < tol and e_ref < max(tol, tol + d_ref), (what, e_row, e_ref, d_ref)
+    bar_ref = tol if d_ref <= tol else REF_CAP
+    record_margin("tq3_attn", e_row=e_row, bar_row=tol, e_ref=e_ref, bar_ref=bar_ref, d_ref=d_ref,
+                  what=what)
+    assert e_row < tol and e_ref < bar_ref, (what, e_row, e_ref, d_ref, bar_ref)
     return e_row, e_ref, d_ref
