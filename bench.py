@@ -21,6 +21,7 @@ Prints one JSON line (value = microseconds per token, lower is better) with:
   hbm_read_peak measured streaming-read bandwidth (qkv_hbm_read_bench over a
                 1 GiB buffer); every fraction is also given against it
   append        TQ3 append (K+V) throughput of the cache build
+  append_q8     Q8_0 append (K+V) throughput over the same inputs
   config1       (CPU leg) the CPU-plumbing config: TQ3 roundtrip MSE, code
                 histogram, codes checked against the oracle, and the elements
                 within one fp32 ulp of a decision boundary
@@ -46,6 +47,8 @@ BLOCKS_PER_TOKEN = NUM_KV * HD // 128              # 8 TQ3 blocks per token for 
 # algorithmic bytes per layer and query token: K+V blocks + Q + O
 ATTN_BYTES = CTX * 2 * BLOCKS_PER_TOKEN * 52 + NUM_Q * HD * 2 * 2
 APPEND_BYTES_PER_TOKEN = 2 * NUM_KV * HD * 2 + 2 * BLOCKS_PER_TOKEN * 52   # 4928
+Q8_BLOCKS_PER_TOKEN = NUM_KV * HD // 32                                      # 32 Q8_0 blocks (K or V)
+APPEND_Q8_BYTES_PER_TOKEN = 2 * NUM_KV * HD * 2 + 2 * Q8_BLOCKS_PER_TOKEN * 36   # 6400
 CPU_REPS = 5
 APPEND_REPS = 5
 
@@ -599,7 +602,22 @@ def main():
     torch.cuda.synchronize()
     append_s = e0.elapsed_time(e1) * 1e-3
     append_tok_layers = APPEND_REPS * LAYERS * CTX
-    del keep_src
+    # ---- Q8_0 append throughput: the same fp16 K/V of set 0's 8 layers
+    # encoded into a Q8_0 cache pair (K+V in one launch per layer; 6400 B per
+    # token-layer: 4096 read, 2304 written) ----
+    q8k = kvcache.q8_blocks(CTX * Q8_BLOCKS_PER_TOKEN, dev)
+    q8v = kvcache.q8_blocks(CTX * Q8_BLOCKS_PER_TOKEN, dev)
+    for k16, v16 in keep_src:
+        kvcache.q8_append_kv(k16, v16, q8k, q8v)
+    torch.cuda.synchronize()
+    e0.record(stream)
+    for _ in range(APPEND_REPS):
+        for k16, v16 in keep_src:
+            kvcache.q8_append_kv(k16, v16, q8k, q8v)
+    e1.record(stream)
+    torch.cuda.synchronize()
+    append_q8_s = e0.elapsed_time(e1) * 1e-3
+    del keep_src, q8k, q8v
     q = [torch.randn(1, NUM_Q, HD, generator=gen, device=dev).to(torch.float16)
          for _ in range(LAYERS)]
     out = torch.empty(1, NUM_Q, HD, dtype=torch.float16, device=dev)
@@ -707,6 +725,16 @@ def main():
                                  / HBM_PEAK_GBS, 4),
                    "frac_of_measured_peak": round(append_tok_layers * APPEND_BYTES_PER_TOKEN
                                                   / append_s / 1e9 / read_peak["gbps"], 4)},
+        "append_q8": {"mtok_layers_per_s": round(append_tok_layers / append_q8_s / 1e6, 1),
+                      "gbps": round(append_tok_layers * APPEND_Q8_BYTES_PER_TOKEN / append_q8_s / 1e9, 1),
+                      "frac": round(append_tok_layers * APPEND_Q8_BYTES_PER_TOKEN / append_q8_s / 1e9
+                                    / HBM_PEAK_GBS, 4),
+                      "frac_of_measured_peak": round(append_tok_layers * APPEND_Q8_BYTES_PER_TOKEN
+                                                     / append_q8_s / 1e9 / read_peak["gbps"], 4),
+                      "us_per_launch": round(append_q8_s * 1e6 / (APPEND_REPS * LAYERS), 2),
+                      "note": "qkv_q8_append_kv over 32768 tokens x 4 kv heads (K+V, one launch "
+                              "per layer), 8 layers x %d passes; 6400 B per token-layer "
+                              "(4096 fp16 read, 2304 Q8_0 written)" % APPEND_REPS},
         "config1": cfg1,
         "cpu_baseline": cpu,
         "secondary": sec,

@@ -307,8 +307,9 @@ int qkv_decode_attn_tq3(const uint16_t* q, const qkv_block_tq3* k, const qkv_blo
                         const uint32_t* tree_mask, void* workspace, size_t workspace_bytes,
                         hipStream_t stream);
 
-/* Health of a fast-path decode workspace (qkv_decode_attn_tq3, _q8, _q8k_tq3v,
- * _tq3_paged).  The in-kernel merge waits for the records of its launch with
+/* Health of a fast-path decode workspace (qkv_decode_attn_tq3, _q8, _q8_append,
+ * _q8k_tq3v, _tq3_paged; for _tq3_noalloc see qkv_decode_noalloc_status
+ * below).  The in-kernel merge waits for the records of its launch with
  * a bounded poll; if the bound runs out (a launch starved of GPU time for
  * seconds), the affected output rows are written as NaN and the workspace
  * header keeps an error word, after which every later call on that workspace
@@ -344,6 +345,16 @@ int qkv_decode_attn_tq3_noalloc(const uint16_t* q, const qkv_block_tq3* k,
                                 const qkv_block_tq3* v, uint16_t* out, int num_q, int num_kv,
                                 int head_dim, int start_pos, int sub_n, float scale, int sink_tok,
                                 int window_tok, const uint32_t* tree_mask, hipStream_t stream);
+
+/* Health and reset of the allocation-free decode's scratch on `device` (the
+ * same error word as qkv_decode_workspace_status, for callers that never see
+ * the scratch's address).  No counterpart in the reference.
+ * qkv_decode_noalloc_status synchronises `stream` (a stream of `device`),
+ * then returns QKV_OK or QKV_ERR_TIMEOUT; qkv_decode_noalloc_reset zero-fills
+ * the scratch on `stream` (a fill kernel), clearing a sticky merge error.
+ * Both make `device` current for the call and restore the caller's device. */
+int qkv_decode_noalloc_status(int device, hipStream_t stream);
+int qkv_decode_noalloc_reset(int device, hipStream_t stream);
 
 /* Fast path for qkv_attn_split_q8 + qkv_attn_split_merge over the Q8_0 cache
  * (decode launch model.cuh:2430-2463; attention.cuh:2633-2801 and 1837-1891) in ONE launch:

@@ -787,6 +787,32 @@ int qkv_decode_workspace_reset(void* workspace, size_t bytes, hipStream_t stream
   return launch_status(qkv::launch_fill_zero(workspace, bytes, stream));
 }
 
+// The allocation-free scratch of `device` (made current for the lookup; the
+// caller's device is restored): looked up, and zero-filled on `stream` when
+// `clear` or on the device's first use.
+static int noalloc_scratch_on(int device, bool clear, hipStream_t stream, void** ptr) {
+  if (device < 0 || device >= 64) return QKV_ERR_INVALID;
+  int n = 0, cur = 0;
+  if (hipGetDeviceCount(&n) != hipSuccess || device >= n) return QKV_ERR_DEVICE;
+  if (hipGetDevice(&cur) != hipSuccess) return QKV_ERR_DEVICE;
+  if (hipSetDevice(device) != hipSuccess) return QKV_ERR_DEVICE;
+  const bool ok = qkv::noalloc_scratch(device, clear, stream, ptr) == hipSuccess;
+  if (hipSetDevice(cur) != hipSuccess || !ok) return QKV_ERR_DEVICE;
+  return QKV_OK;
+}
+
+int qkv_decode_noalloc_status(int device, hipStream_t stream) {
+  void* ptr = nullptr;
+  const int st = noalloc_scratch_on(device, false, stream, &ptr);
+  if (st) return st;
+  return qkv_decode_workspace_status(ptr, stream);
+}
+
+int qkv_decode_noalloc_reset(int device, hipStream_t stream) {
+  void* ptr = nullptr;
+  return noalloc_scratch_on(device, true, stream, &ptr);
+}
+
 int qkv_debug_set_merge_spin_limit(int limit) {
   g_spin_limit.store(limit < 0 ? qkv::kMergeSpinLimit : limit, std::memory_order_relaxed);
   return QKV_OK;

@@ -23,6 +23,26 @@ def _stream(stream=None) -> int:
     return s.cuda_stream
 
 
+# fp16 arguments: torch.float16, or 16-bit integer tensors holding fp16 bit
+# patterns (the C ABI takes uint16_t)
+FP16 = (torch.float16, torch.uint16, torch.int16)
+
+
+def _need(t, nbytes: int, what: str, dtype=None) -> None:
+    """Raise ValueError (before any launch) when `t` is not of `dtype` or
+    holds fewer than `nbytes` bytes: the kernels trust the sizes implied by
+    the shape arguments, so an undersized buffer would be read or written
+    out of bounds on the device."""
+    if t is None:
+        raise ValueError(f"{what} is required")
+    allowed = dtype if isinstance(dtype, tuple) else (dtype,)
+    if dtype is not None and t.dtype not in allowed:
+        raise ValueError(f"{what} must be {' or '.join(str(d) for d in allowed)}, got {t.dtype}")
+    have = t.numel() * t.element_size()
+    if have < nbytes:
+        raise ValueError(f"{what} holds {have} bytes, the call needs {int(nbytes)}")
+
+
 def _dev_ptr(t: torch.Tensor, what: str) -> int:
     if not t.is_cuda:
         raise ValueError(f"{what} must be a device tensor")
@@ -130,12 +150,23 @@ def _pool_rows(k_pool, v_pool, k_row_bytes, v_row_bytes):
     return rows
 
 
+def _flat_sizes(k_flat, v_flat, v_pool, n_rows, k_row_bytes, v_row_bytes, block_table,
+                block_tokens) -> None:
+    """The flat buffers hold n_rows rows and the table covers them."""
+    _need(k_flat, n_rows * k_row_bytes, "k_flat")
+    if v_pool is not None or v_flat is not None:
+        _need(v_flat, n_rows * v_row_bytes, "v_flat")
+    if block_tokens > 0:
+        _need(block_table, -(-n_rows // block_tokens) * 4, "block_table", torch.int32)
+
+
 def kv_gather_rows(k_pool, v_pool, k_flat, v_flat, block_table, *, n_rows, block_tokens,
                    k_row_bytes, v_row_bytes=0, stream=None) -> None:
     """Slot snapshot over a paged pool: logical rows 0 .. n_rows-1 of the slot
     whose block-table row is `block_table` (int32 device tensor) into the flat
     buffers [n_rows][row_bytes] (model.cuh:3394-3417 for the contiguous
     layout).  v_pool / v_flat may be None (keys only)."""
+    _flat_sizes(k_flat, v_flat, v_pool, n_rows, k_row_bytes, v_row_bytes, block_table, block_tokens)
     pool_rows = _pool_rows(k_pool, v_pool, k_row_bytes, v_row_bytes)
     check(lib().qkv_kv_gather_rows(
         _dev_ptr(k_pool, "k_pool"), _opt_ptr(v_pool), _dev_ptr(k_flat, "k_flat"),
@@ -148,6 +179,7 @@ def kv_scatter_rows(k_pool, v_pool, k_flat, v_flat, block_table, *, n_rows, bloc
                     k_row_bytes, v_row_bytes=0, stream=None) -> None:
     """Slot restore over a paged pool: the inverse of kv_gather_rows
     (model.cuh:3314-3335 for the contiguous layout)."""
+    _flat_sizes(k_flat, v_flat, v_pool, n_rows, k_row_bytes, v_row_bytes, block_table, block_tokens)
     pool_rows = _pool_rows(k_pool, v_pool, k_row_bytes, v_row_bytes)
     check(lib().qkv_kv_scatter_rows(
         _dev_ptr(k_pool, "k_pool"), _opt_ptr(v_pool), _dev_ptr(k_flat, "k_flat"),
@@ -260,6 +292,20 @@ def attn_block_sparse_split_tq3(q, k, v, block_index, part_m, part_l, part_o, *,
         k_splits, _opt_ptr(tree_mask), _stream(stream)), "qkv_attn_block_sparse_split_tq3")
 
 
+# bytes per token row and kv head of one cache (head_dim 256): TQ3 two 52-byte
+# blocks, Q8_0 eight 36-byte blocks
+TQ3_ROW = 2 * TQ3_BLOCK_BYTES
+Q8_ROW = 8 * Q8_BLOCK_BYTES
+
+
+def _attn_sizes(q, k, v, out, num_q, num_kv, n_keys, sub_n, head_dim, k_row, v_row) -> None:
+    """q / out hold sub_n x num_q fp16 rows; k / v hold n_keys token rows."""
+    _need(q, sub_n * num_q * head_dim * 2, "q", FP16)
+    _need(out, sub_n * num_q * head_dim * 2, "out", FP16)
+    _need(k, n_keys * num_kv * k_row, "k")
+    _need(v, n_keys * num_kv * v_row, "v")
+
+
 def decode_attn_tq3_workspace_bytes(num_q, num_kv, sub_n, n_keys) -> int:
     return int(lib().qkv_decode_attn_tq3_workspace_bytes(num_q, num_kv, sub_n, n_keys))
 
@@ -273,6 +319,7 @@ def decode_attn_tq3_workspace(num_q, num_kv, sub_n, n_keys, device) -> torch.Ten
 def decode_attn_tq3(q, k, v, out, workspace, *, num_q, num_kv, start_pos, sub_n, scale,
                     sink_tok=0, window_tok=0, tree_mask=None, head_dim=256, stream=None) -> None:
     """Fast path: split-K decode with the merge inside the same launch."""
+    _attn_sizes(q, k, v, out, num_q, num_kv, start_pos + sub_n, sub_n, head_dim, TQ3_ROW, TQ3_ROW)
     check(lib().qkv_decode_attn_tq3(
         _dev_ptr(q, "q"), _dev_ptr(k, "k"), _dev_ptr(v, "v"), _dev_ptr(out, "out"), num_q,
         num_kv, head_dim, start_pos, sub_n, float(scale), sink_tok, window_tok,
@@ -285,6 +332,7 @@ def decode_attn_tq3_noalloc(q, k, v, out, *, num_q, num_kv, start_pos, sub_n, sc
                             stream=None) -> None:
     """decode_attn_tq3 without a workspace argument: the library's fixed
     per-GPU scratch serves as the workspace (no allocation in the call)."""
+    _attn_sizes(q, k, v, out, num_q, num_kv, start_pos + sub_n, sub_n, head_dim, TQ3_ROW, TQ3_ROW)
     check(lib().qkv_decode_attn_tq3_noalloc(
         _dev_ptr(q, "q"), _dev_ptr(k, "k"), _dev_ptr(v, "v"), _dev_ptr(out, "out"), num_q,
         num_kv, head_dim, start_pos, sub_n, float(scale), sink_tok, window_tok,
@@ -301,6 +349,7 @@ def decode_attn_q8(q, k, v, out, workspace, *, num_q, num_kv, start_pos, sub_n, 
                    head_dim=256, stream=None) -> None:
     """Fast path over the Q8_0 cache: split-K decode with the merge inside the
     same launch."""
+    _attn_sizes(q, k, v, out, num_q, num_kv, start_pos + sub_n, sub_n, head_dim, Q8_ROW, Q8_ROW)
     check(lib().qkv_decode_attn_q8(
         _dev_ptr(q, "q"), _dev_ptr(k, "k"), _dev_ptr(v, "v"), _dev_ptr(out, "out"), num_q,
         num_kv, head_dim, start_pos, sub_n, float(scale), _dev_ptr(workspace, "workspace"),
@@ -311,7 +360,11 @@ def decode_attn_q8_append(q, k_new, v_new, k, v, out, workspace, *, num_q, num_k
                           scale, head_dim=256, stream=None) -> None:
     """One launch for a decode step over the Q8_0 cache: k_new / v_new (fp16
     [num_kv][256]) are quantized into row start_pos of k / v and attended as
-    key start_pos by the one query q (keys 0..start_pos)."""
+    key start_pos by the one query q (keys 0..start_pos).  k and v must hold
+    row start_pos (the kernel writes it)."""
+    _attn_sizes(q, k, v, out, num_q, num_kv, start_pos + 1, 1, head_dim, Q8_ROW, Q8_ROW)
+    _need(k_new, num_kv * head_dim * 2, "k_new", FP16)
+    _need(v_new, num_kv * head_dim * 2, "v_new", FP16)
     check(lib().qkv_decode_attn_q8_append(
         _dev_ptr(q, "q"), _dev_ptr(k_new, "k_new"), _dev_ptr(v_new, "v_new"), _dev_ptr(k, "k"),
         _dev_ptr(v, "v"), _dev_ptr(out, "out"), num_q, num_kv, head_dim, start_pos, float(scale),
@@ -329,6 +382,7 @@ def decode_attn_q8k_tq3v(q, k, v, out, workspace, *, num_q, num_kv, start_pos, s
                          head_dim=256, stream=None) -> None:
     """V-only TurboQuant (reference TQ_KEYS_Q8 mode): keys in Q8_0 blocks, values
     in TQ3 blocks; one fused decode launch with the merge inside it."""
+    _attn_sizes(q, k, v, out, num_q, num_kv, start_pos + sub_n, sub_n, head_dim, Q8_ROW, TQ3_ROW)
     check(lib().qkv_decode_attn_q8k_tq3v(
         _dev_ptr(q, "q"), _dev_ptr(k, "k"), _dev_ptr(v, "v"), _dev_ptr(out, "out"), num_q,
         num_kv, head_dim, start_pos, sub_n, float(scale), _dev_ptr(workspace, "workspace"),
@@ -347,6 +401,18 @@ def decode_workspace_reset(workspace, stream=None) -> None:
     check(lib().qkv_decode_workspace_reset(_dev_ptr(workspace, "workspace"),
                                            workspace.numel() * workspace.element_size(),
                                            _stream(stream)), "qkv_decode_workspace_reset")
+
+
+def decode_noalloc_status(device: int = 0, stream=None) -> int:
+    """decode_workspace_status for the allocation-free decode's scratch of
+    `device`: synchronises the stream, returns QKV_OK (0) or QKV_ERR_TIMEOUT (-8)."""
+    return int(lib().qkv_decode_noalloc_status(int(device), _stream(stream)))
+
+
+def decode_noalloc_reset(device: int = 0, stream=None) -> None:
+    """Zero-fill the allocation-free decode's scratch of `device` (clears a
+    sticky merge error)."""
+    check(lib().qkv_decode_noalloc_reset(int(device), _stream(stream)), "qkv_decode_noalloc_reset")
 
 
 def debug_set_merge_spin_limit(limit: int) -> None:

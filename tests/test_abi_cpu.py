@@ -206,3 +206,30 @@ def test_block_sparse_argument_errors_without_gpu(L):
     assert sp(p, p, p, p, p, p, p, 16, 4, 256, 100, 1, 1, 1.0, 0, 64, 8, None, None) == -1
     assert sp(p, p, p, None, p, p, p, 16, 4, 256, 100, 1, 1, 1.0, 8, 64, 8, None, None) == -2
     assert sp(p + 8, p, p, p, p, p, p, 16, 4, 256, 100, 1, 1, 1.0, 8, 64, 8, None, None) == -4
+
+
+def test_noalloc_health_argument_errors(L):
+    # device numbers outside 0..63 are rejected before any HIP call
+    for dev in (-1, 64):
+        assert L.qkv_decode_noalloc_status(dev, None) == -1
+        assert L.qkv_decode_noalloc_reset(dev, None) == -1
+
+
+@pytest.mark.parametrize("lang,compiler,std", [("c", "gcc", "-std=c11"), ("c++", "g++", "-std=c++17")])
+def test_header_compiles_as_c_and_cxx(lang, compiler, std):
+    """include/qkv.h (through the compiled caller tests/c_caller/qkv_caller.c)
+    is valid C11 and C++17 with warnings as errors."""
+    import os
+    import shutil
+    import subprocess
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    rocm_inc = "/opt/rocm/include"
+    if shutil.which(compiler) is None or not os.path.isdir(rocm_inc):
+        pytest.skip(f"{compiler} or the HIP headers are not installed")
+    cmd = [compiler, std, "-fsyntax-only", "-Wall", "-Wextra", "-Werror",
+           "-I", os.path.join(root, "include"), "-isystem", rocm_inc, "-D__HIP_PLATFORM_AMD__",
+           "-x", lang, os.path.join(root, "tests", "c_caller", "qkv_caller.c")]
+    if lang == "c":
+        cmd.insert(2, "-pedantic")
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    assert r.returncode == 0, r.stderr

@@ -98,3 +98,44 @@ def test_q8_decode_merge_timeout(dev):
         return out.cpu().numpy().astype(np.float64)
     _timeout_cycle(dev, call, ws, ref)
 
+
+
+def test_noalloc_decode_merge_timeout(dev):
+    """The allocation-free decode's scratch through its device-keyed status and
+    reset (the caller never sees the scratch's address)."""
+    import torch
+    from qengine_amd import kvcache
+    rng = np.random.default_rng(73)
+    n, nq, nkv = 2500, 16, 4
+    k16, v16 = kv_f16(rng, n, nkv, 256), kv_f16(rng, n, nkv, 256)
+    kb, vb = O.tq3_encode(k16), O.tq3_encode(v16)
+    q = q_f16(rng, 1, nq, 256)
+    ref = _oracle(O.KV_TQ3, q, kb, vb, nq, nkv, n)
+    exact = O.attn_exact_tq3(q, kb, vb, num_q=nq, num_kv=nkv, hd=256, start_pos=n - 1, sub_n=1,
+                             scale=1 / 16)
+    qd, kd, vd = _dev(q.view(np.uint16), dev), _dev(kb.view(np.uint8), dev), _dev(vb.view(np.uint8), dev)
+    device = dev.index or 0
+
+    def call():
+        out = torch.zeros((1, nq, 256), dtype=torch.float16, device=dev)
+        kvcache.decode_attn_tq3_noalloc(qd, kd, vd, out, num_q=nq, num_kv=nkv, start_pos=n - 1,
+                                        sub_n=1, scale=1 / 16)
+        torch.cuda.synchronize()
+        return out.cpu().numpy().astype(np.float64)
+
+    kvcache.decode_noalloc_reset(device)
+    assert kvcache.decode_noalloc_status(device) == 0
+    try:
+        kvcache.debug_set_merge_spin_limit(0)
+        assert np.all(np.isnan(call())), "timed-out merge must write NaN rows"
+        assert kvcache.decode_noalloc_status(device) == -8
+        kvcache.debug_set_merge_spin_limit(-1)
+        assert np.all(np.isnan(call())), "the error is sticky until the scratch is reset"
+        assert kvcache.decode_noalloc_status(device) == -8
+    finally:
+        kvcache.debug_set_merge_spin_limit(-1)
+        kvcache.decode_noalloc_reset(device)
+    assert kvcache.decode_noalloc_status(device) == 0
+    out = call()
+    assert_tq3_attn(out, ref, exact)
+    assert kvcache.decode_noalloc_status(device) == 0
