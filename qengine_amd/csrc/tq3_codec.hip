@@ -260,15 +260,16 @@ __device__ __forceinline__ void pair_stage8(const float (&a)[64], const float (&
         "v"(a[k0 + 4]), "v"(a[k0 + 5]), "v"(a[k0 + 6]), "v"(a[k0 + 7]));
 }
 
-// Codes of 64 consecutive transformed elements (one half of a block) into
-// the 6 words of that half's 192-bit stream: chains k = 63..32 (words 3..5)
-// and k = 31..0 (words 0..2), then the sign fix.
-__device__ __forceinline__ void bin_half(const float (&x)[64], const uint32_t (&q)[3],
-                                         uint32_t (&acc)[6]) {
+// Codes of 64 consecutive transformed elements (one half of a block) go to
+// the 6 words of that half's 192-bit stream in two chains, k = 63..32 (words
+// 3..5) and k = 31..0 (words 0..2); bin_steps runs chain steps I0 .. I0+N-1
+// (elements 63-i and 31-i), so that each group of outputs is binned as soon
+// as it exists, and the sign fix follows the last step.
+template <int I0, int N>
+__device__ __forceinline__ void bin_steps(const float (&x)[64], const uint32_t (&q)[3],
+                                          uint32_t (&acc)[6]) {
 #pragma unroll
-  for (int w = 0; w < 6; w++) acc[w] = 0u;
-#pragma unroll
-  for (int i = 0; i < 32; i++) {
+  for (int i = I0; i < I0 + N; i++) {
     const int ka = 63 - i, kb = 31 - i;
     const float ya = __builtin_fmaf(x[ka], -kFoldA, __builtin_fabsf(x[ka]));
     const float yb = __builtin_fmaf(x[kb], -kFoldA, __builtin_fabsf(x[kb]));
@@ -281,8 +282,6 @@ __device__ __forceinline__ void bin_half(const float (&x)[64], const uint32_t (&
     shift_in(acc[(3 * ka) >> 5], pa[1]);
     shift_in(acc[(3 * kb) >> 5], pb[1]);
   }
-  sign_fix<0, 3>(acc);
-  sign_fix<3, 3>(acc + 3);
 }
 
 template <bool kDfk2, bool kPaged>
@@ -318,9 +317,14 @@ __global__ __launch_bounds__(kAp4Threads, 3) void tq3_append4_kernel(
     if (tile_n >= tiles) { tile_n -= tiles; tensor_n++; }
     const bool more = tensor_n < n_tensors;
 
+    // DFK2 and paged tiles: the per-lane offsets and the paged divisors are
+    // re-formed every tile (a few instructions) instead of living in
+    // registers across the loop, where the tile leaves no room for them.
+    int lane_t = lane;
+    if constexpr (kDfk2 || kPaged) asm volatile("" : "+v"(lane_t));
     // R1 = first half of block `lane`, R2 = second half of block lane ^ 1
     uint32_t h1[32], h2[32];
-    load_halves<kDfk2>(h1, h2, tensor ? in1 : in0, tensor ? sc1 : sc0, b0, nb, lane);
+    load_halves<kDfk2>(h1, h2, tensor ? in1 : in0, tensor ? sc1 : sc0, b0, nb, lane_t);
     // norm (reference order): block lane's chain over R1 here, handed to the
     // other lane of the pair, which continues over its R2
     float n1 = 0.0f;
@@ -368,16 +372,33 @@ __global__ __launch_bounds__(kAp4Threads, 3) void tq3_append4_kernel(
         }
       }
     }
+    // stage 64 and the bins of block `lane`, eight chain steps at a time (a
+    // group's outputs are binned as soon as they exist, which keeps the live
+    // outputs to 32): words 0..5 from outputs 0..63, 6..11 from 64..127
     float y1[64], y2[64];
-#pragma unroll
-    for (int k = 0; k < 64; k += 8) pair_stage8(x1, x2, y1, y2, k);
-
-    // bins of block `lane`: words 0..5 from outputs 0..63, 6..11 from 64..127
     uint32_t acc[12];
     {
-      uint32_t a0[6], a1[6];
-      bin_half(y1, q, a0);
-      bin_half(y2, q, a1);
+      uint32_t a0[6] = {0u, 0u, 0u, 0u, 0u, 0u}, a1[6] = {0u, 0u, 0u, 0u, 0u, 0u};
+      pair_stage8(x1, x2, y1, y2, 56);
+      pair_stage8(x1, x2, y1, y2, 24);
+      bin_steps<0, 8>(y1, q, a0);
+      bin_steps<0, 8>(y2, q, a1);
+      pair_stage8(x1, x2, y1, y2, 48);
+      pair_stage8(x1, x2, y1, y2, 16);
+      bin_steps<8, 8>(y1, q, a0);
+      bin_steps<8, 8>(y2, q, a1);
+      pair_stage8(x1, x2, y1, y2, 40);
+      pair_stage8(x1, x2, y1, y2, 8);
+      bin_steps<16, 8>(y1, q, a0);
+      bin_steps<16, 8>(y2, q, a1);
+      pair_stage8(x1, x2, y1, y2, 32);
+      pair_stage8(x1, x2, y1, y2, 0);
+      bin_steps<24, 8>(y1, q, a0);
+      bin_steps<24, 8>(y2, q, a1);
+      sign_fix<0, 3>(a0);
+      sign_fix<3, 3>(a0 + 3);
+      sign_fix<0, 3>(a1);
+      sign_fix<3, 3>(a1 + 3);
       const bool keep = norm1 >= 1e-10f && norm1 < __builtin_inff();
 #pragma unroll
       for (int w = 0; w < 6; w++) {
@@ -390,8 +411,10 @@ __global__ __launch_bounds__(kAp4Threads, 3) void tq3_append4_kernel(
 
     if constexpr (kPaged) {
       // paged: each lane stores its block at the block's row
-      if (lane < nb) {
-        const long ob = paged_block(pr, (long)b0 + lane);
+      PagedRows prt = pr;
+      asm volatile("" : "+s"(prt.block_tokens), "+s"(prt.blocks_per_row), "+s"(prt.n_tok));
+      if (lane_t < nb) {
+        const long ob = paged_block(prt, (long)b0 + lane_t);
         if (ob >= 0) {
           uint32_t* dst = out + ob * 13;
           dst[0] = __float_as_uint(norm1);
@@ -401,7 +424,7 @@ __global__ __launch_bounds__(kAp4Threads, 3) void tq3_append4_kernel(
       }
     } else {
       // 4. stage the tile's 64 x 13 dwords, then store them contiguously
-      uint32_t* ob = wl + lane * 13;
+      uint32_t* ob = wl + lane_t * 13;
       ob[0] = __float_as_uint(norm1);
 #pragma unroll
       for (int w = 0; w < 12; w++) ob[1 + w] = acc[w];
@@ -412,7 +435,7 @@ __global__ __launch_bounds__(kAp4Threads, 3) void tq3_append4_kernel(
           out + (long)b0 * 13, 0, nb * 52, kBufferRsrcWord3);
 #pragma unroll
       for (int j = 0; j < 13; j++)
-        __builtin_amdgcn_raw_buffer_store_b32(wl[j * 64 + lane], rd, lane * 4, j * 256, 0);
+        __builtin_amdgcn_raw_buffer_store_b32(wl[j * 64 + lane_t], rd, lane_t * 4, j * 256, 0);
     }
     if (!more) break;
     tile = tile_n;
