@@ -7,7 +7,7 @@ import numpy as np
 import pytest
 
 from oracle import oracle as O
-from tests._data import kv_f16, q_f16, rel_err
+from tests._data import check_rel, kv_f16, q_f16
 
 pytestmark = pytest.mark.gpu
 TOL = 2e-3
@@ -60,7 +60,7 @@ def test_mixed_decode_vs_oracle(dev, n, num_q, sub_n):
     from qengine_amd import kvcache
     q, kq, vt, ref = _case(900 + n + num_q + sub_n, n, num_q, sub_n)
     ws = kvcache.decode_attn_q8k_tq3v_workspace(num_q, 4, sub_n, n, dev)
-    assert rel_err(_decode(dev, q, kq, vt, ws, n, num_q, sub_n), ref) < TOL
+    check_rel(_decode(dev, q, kq, vt, ws, n, num_q, sub_n), ref, TOL)
 
 
 def test_mixed_and_q8_share_a_workspace(dev):
@@ -71,7 +71,7 @@ def test_mixed_and_q8_share_a_workspace(dev):
     ws = kvcache.decode_attn_q8k_tq3v_workspace(16, 4, 4, 8192, dev)
     for i, (n, sub_n) in enumerate([(8192, 1), (4097, 1), (1000, 4), (8192, 1), (300, 4)]):
         q, kq, vt, ref = _case(950 + i, n, 16, sub_n)
-        assert rel_err(_decode(dev, q, kq, vt, ws, n, 16, sub_n), ref) < TOL, (n, sub_n)
+        check_rel(_decode(dev, q, kq, vt, ws, n, 16, sub_n), ref, TOL, what=(n, sub_n))
         rng = np.random.default_rng(960 + i)
         k16, v16 = kv_f16(rng, n, 4, 256), kv_f16(rng, n, 4, 256)
         kb, vb = O.q8_encode(k16), O.q8_encode(v16)
@@ -82,4 +82,4 @@ def test_mixed_and_q8_share_a_workspace(dev):
         torch.cuda.synchronize()
         ref8 = O.attn_ref_f64(q, O.q8_decode(kb), O.q8_decode(vb), num_q=16, num_kv=4, hd=256,
                               start_pos=n - sub_n, sub_n=sub_n, scale=1 / 16)
-        assert rel_err(out.cpu().numpy(), ref8) < TOL, ("q8", n, sub_n)
+        check_rel(out.cpu().numpy(), ref8, TOL, what=("q8", n, sub_n))

@@ -6,7 +6,7 @@ import numpy as np
 import pytest
 
 from oracle import oracle as O
-from tests._data import kv_f16, q_f16, rel_err
+from tests._data import check_rel, kv_f16, q_f16
 
 pytestmark = pytest.mark.gpu
 TOL = 2e-3
@@ -70,8 +70,8 @@ def test_q8_split_decode_vs_oracle(dev, n, k_splits, num_q, sub_n):
     assert np.max(np.abs(pm[live] - em[live])) < 1e-2
     w = np.exp(pm[live] - em[live])
     assert np.max(np.abs(pl[live] * w - el[live]) / el[live]) < TOL
-    assert rel_err(po[live] * w[:, None], eo[live]) < TOL
-    assert rel_err(out, exp.view(np.float16)) < TOL
+    check_rel(po[live] * w[:, None], eo[live], TOL)
+    check_rel(out, exp.view(np.float16), TOL)
 
 
 def test_q8_split_rejects_bad_shapes(dev):
@@ -117,7 +117,7 @@ def test_q8_fast_decode_vs_oracle(dev, n, num_q, sub_n):
                            _dev(vb.view(np.uint8), dev), out, ws, num_q=num_q, num_kv=4,
                            start_pos=n - sub_n, sub_n=sub_n, scale=1 / 16)
     torch.cuda.synchronize()
-    assert rel_err(out.cpu().numpy(), _expected(q, kb, vb, n, num_q, sub_n)) < TOL
+    check_rel(out.cpu().numpy(), _expected(q, kb, vb, n, num_q, sub_n), TOL)
 
 
 def test_q8_fast_decode_workspace_reuse(dev):
@@ -133,7 +133,7 @@ def test_q8_fast_decode_workspace_reuse(dev):
                                _dev(vb.view(np.uint8), dev), out, ws, num_q=16, num_kv=4,
                                start_pos=n - sub_n, sub_n=sub_n, scale=1 / 16)
         torch.cuda.synchronize()
-        assert rel_err(out.cpu().numpy(), _expected(q, kb, vb, n, 16, sub_n)) < TOL, (n, sub_n)
+        check_rel(out.cpu().numpy(), _expected(q, kb, vb, n, 16, sub_n), TOL, what=(n, sub_n))
 
 
 def test_q8_append_kv_matches_two_appends(dev):
@@ -192,4 +192,4 @@ def test_q8_fused_append_decode_matches_two_calls(dev, n_old, num_q):
     assert torch.equal(o1, o2)
     kb2 = k2.cpu().numpy().reshape(-1).view(kb.dtype)
     vb2 = v2.cpu().numpy().reshape(-1).view(vb.dtype)
-    assert rel_err(o2.cpu().numpy(), _expected(q, kb2, vb2, n, num_q, 1)) < TOL
+    check_rel(o2.cpu().numpy(), _expected(q, kb2, vb2, n, num_q, 1), TOL)

@@ -18,7 +18,7 @@ import numpy as np
 import pytest
 
 from oracle import oracle as O
-from tests._data import assert_tq3_attn, kv_f16, q_f16, rel_err
+from tests._data import assert_tq3_attn, check_rel, kv_f16, q_f16
 
 pytestmark = pytest.mark.gpu
 TOL = 2e-3
@@ -67,7 +67,7 @@ def test_tq3_decode_vs_legacy(dev, n, num_q):
     for got in (out.cpu().numpy(), out2.cpu().numpy()):
         assert np.all(np.isfinite(got))
         assert_tq3_attn(got, legacy, exact, what=n)
-        assert rel_err(got, fused) < TOL
+        check_rel(got, fused, TOL)
 
 
 @pytest.mark.parametrize("n", LENS)
@@ -84,7 +84,7 @@ def test_q8_decode_vs_legacy(dev, n):
                            _dev(vb.view(np.uint8), dev), out, ws, num_q=16, num_kv=NKV,
                            start_pos=n - 1, sub_n=1, scale=1 / 16)
     torch.cuda.synchronize()
-    assert rel_err(out.cpu().numpy(), _legacy(O.KV_Q8, O.KV_Q8, q, kb, vb, 16, n)) < TOL
+    check_rel(out.cpu().numpy(), _legacy(O.KV_Q8, O.KV_Q8, q, kb, vb, 16, n), TOL)
 
 
 @pytest.mark.parametrize("n", LENS)
@@ -106,5 +106,5 @@ def test_q8k_tq3v_decode_vs_legacy(dev, n):
     legacy = _legacy(O.KV_Q8, O.KV_TQ3, q, kq, vt, 16, n)
     exact = O.attn_q8k_tq3v_f64(q, kq, vt, num_q=16, num_kv=NKV, hd=HD, start_pos=n - 1, sub_n=1,
                                 scale=1 / 16)
-    assert rel_err(got, fused) < TOL
+    check_rel(got, fused, TOL)
     assert_tq3_attn(got, legacy, exact, what=n)

@@ -14,7 +14,7 @@ import numpy as np
 import pytest
 
 from oracle import oracle as O
-from tests._data import kv_f16, q_f16, rel_err
+from tests._data import check_rel, kv_f16, q_f16, record_margin
 
 pytestmark = pytest.mark.gpu
 TOL = 2e-3
@@ -91,7 +91,7 @@ def test_prefill_vs_oracle(dev, start_pos, n_tok, num_q):
     k_all, v_all = _oracle_kv(kb, vb, ck, cv, num_kv)
     ref = _oracle(q, k_all, v_all, num_q=num_q, num_kv=num_kv, start_pos=start_pos, scale=scale)
     assert np.all(np.isfinite(got))
-    assert rel_err(got, ref) < TOL
+    check_rel(got, ref, TOL)
 
 
 @pytest.mark.parametrize("scale,grow", [
@@ -113,7 +113,7 @@ def test_prefill_scales_and_rescaling(dev, scale, grow):
     k_all, v_all = _oracle_kv(kb, vb, ck, cv, num_kv)
     ref = _oracle(q, k_all, v_all, num_q=num_q, num_kv=num_kv, start_pos=start_pos, scale=scale)
     assert np.all(np.isfinite(got))
-    assert rel_err(got, ref) < TOL
+    check_rel(got, ref, TOL)
 
 
 def test_prefill_vs_fp64(dev):
@@ -126,7 +126,7 @@ def test_prefill_vs_fp64(dev):
     k_all, v_all = _oracle_kv(kb, vb, ck, cv, num_kv)
     ref = O.attn_ref_f64(q, k_all, v_all, num_q=num_q, num_kv=num_kv, hd=256,
                          start_pos=start_pos, sub_n=n_tok, scale=scale)
-    assert rel_err(got, ref) < TOL
+    check_rel(got, ref, TOL)
 
 
 def test_prefill_causal_rows_ignore_later_tokens(dev):
@@ -178,9 +178,9 @@ def test_prefill_config5_full_size(dev):
         end = start_pos + t0 + 8
         ref = _oracle(q[t0:t0 + 8], k_all[:end], v_all[:end], num_q=num_q, num_kv=num_kv,
                       start_pos=start_pos + t0, scale=scale, k_splits=32)
-        e = rel_err(got[t0:t0 + 8], ref)
+        e = check_rel(got[t0:t0 + 8], ref, TOL, what=("config 5(i) rows", t0))
         worst = max(worst, e)
-        assert e < TOL, (t0, e)
+    record_margin("prefill_fullsize_worst_row", err=worst, bar=TOL)
     print(f"config 5(i): worst per-row rel err over 64 rows {worst:.3e}")
 
 
@@ -219,7 +219,7 @@ def test_verify_from_cache_vs_oracle(dev, start_pos, n_tok, num_q):
     ref = O.attn_split_merge(pm, pl, po, num_q=num_q, num_kv=num_kv, hd=256, sub_n=n_tok,
                              sub_n_max=n_tok, k_splits=8).view(np.float16)
     assert np.all(np.isfinite(got))
-    assert rel_err(got, ref) < TOL
+    check_rel(got, ref, TOL)
 
 
 def test_verify_matches_decode_path(dev):
@@ -257,6 +257,6 @@ def test_verify_matches_decode_path(dev):
                              sub_n_max=n_tok, k_splits=8).view(np.float16)
     exact = O.attn_exact_tq3(q, kb, vb, num_q=num_q, num_kv=num_kv, hd=256, start_pos=start_pos,
                              sub_n=n_tok, scale=scale)
-    assert rel_err(a, ref) < TOL
+    check_rel(a, ref, TOL)
     assert_tq3_attn(b, ref, exact)
-    assert rel_err(a, b) < 2 * TOL
+    check_rel(a, b, 2 * TOL)
