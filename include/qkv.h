@@ -321,6 +321,15 @@ int qkv_decode_attn_tq3(const uint16_t* q, const qkv_block_tq3* k, const qkv_blo
 int qkv_decode_workspace_status(const void* workspace, hipStream_t stream);
 int qkv_decode_workspace_reset(void* workspace, size_t bytes, hipStream_t stream);
 
+/* The same health check without synchronising (serving loops, HIP graph
+ * capture): enqueues on `stream` one single-thread kernel that writes QKV_OK or
+ * QKV_ERR_TIMEOUT to *status -- device memory, or host memory the device can
+ * write (hipHostMalloc) -- once every earlier call on the stream is done.
+ * Read *status after the stream has passed that point.  Returns the launch
+ * status (QKV_OK when the check was enqueued).  No counterpart in the
+ * reference. */
+int qkv_decode_workspace_status_async(const void* workspace, int* status, hipStream_t stream);
+
 /* Test hook, no counterpart in the reference: the merger poll limit of every
  * later fast-path decode launch in this process (limit >= 0; a negative value
  * restores the default of 2^22 polls).  A limit of 0 makes every merger time
@@ -354,6 +363,9 @@ int qkv_decode_attn_tq3_noalloc(const uint16_t* q, const qkv_block_tq3* k,
  * the scratch on `stream` (a fill kernel), clearing a sticky merge error.
  * Both make `device` current for the call and restore the caller's device. */
 int qkv_decode_noalloc_status(int device, hipStream_t stream);
+/* qkv_decode_workspace_status_async for the scratch of `device` (`stream` a
+ * stream of `device`); no counterpart in the reference. */
+int qkv_decode_noalloc_status_async(int device, int* status, hipStream_t stream);
 int qkv_decode_noalloc_reset(int device, hipStream_t stream);
 
 /* Fast path for qkv_attn_split_q8 + qkv_attn_split_merge over the Q8_0 cache

@@ -77,8 +77,10 @@ SIGNATURES = {
                                       _F, _P, _SZ, _P]),
     "qkv_decode_workspace_status": (_I, [_P, _P]),
     "qkv_decode_workspace_reset": (_I, [_P, _SZ, _P]),
+    "qkv_decode_workspace_status_async": (_I, [_P, _P, _P]),
     "qkv_decode_noalloc_status": (_I, [_I, _P]),
     "qkv_decode_noalloc_reset": (_I, [_I, _P]),
+    "qkv_decode_noalloc_status_async": (_I, [_I, _P, _P]),
     "qkv_debug_set_merge_spin_limit": (_I, [_I]),
     "qkv_prefill_attn_tq3_workspace_bytes": (_SZ, [_I, _I, _I, _I]),
     "qkv_prefill_attn_tq3": (_I, [_P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _F, _P, _SZ, _P]),

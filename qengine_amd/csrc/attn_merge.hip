@@ -57,6 +57,25 @@ hipError_t launch_fill_zero(void* p, size_t bytes, hipStream_t stream) {
   return hipGetLastError();
 }
 
+// The health word of a fast-path workspace (header word kWsErrorWord) turned
+// into a status and stored to `status` (device memory, or host memory the
+// device can write) by one thread: ok_value while the word is 0, else
+// timeout_value.  Stream-ordered, no host synchronization.
+__global__ __launch_bounds__(64) void ws_status_kernel(const int* __restrict__ header, int* status,
+                                                       int ok_value, int timeout_value) {
+  if (threadIdx.x == 0) {
+    const int w = __hip_atomic_load(header + kWsErrorWord, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    *status = w == 0 ? ok_value : timeout_value;
+  }
+}
+
+hipError_t launch_ws_status(const void* workspace, int* status, int ok_value, int timeout_value,
+                            hipStream_t stream) {
+  hipLaunchKernelGGL(ws_status_kernel, dim3(1), dim3(64), 0, stream, static_cast<const int*>(workspace),
+                     status, ok_value, timeout_value);
+  return hipGetLastError();
+}
+
 // Streaming read of `bytes` (a multiple of 64): every 16-byte piece loaded
 // once by a grid-stride loop; the xor of the data is written only if it
 // equals a value no test buffer produces, so no store traffic is added and

@@ -780,6 +780,12 @@ int qkv_decode_workspace_status(const void* workspace, hipStream_t stream) {
   return word == 0 ? QKV_OK : QKV_ERR_TIMEOUT;
 }
 
+int qkv_decode_workspace_status_async(const void* workspace, int* status, hipStream_t stream) {
+  if (!workspace || !status) return QKV_ERR_NULL;
+  if (!aligned(workspace, 256) || !aligned(status, 4)) return QKV_ERR_ALIGN;
+  return launch_status(qkv::launch_ws_status(workspace, status, QKV_OK, QKV_ERR_TIMEOUT, stream));
+}
+
 int qkv_decode_workspace_reset(void* workspace, size_t bytes, hipStream_t stream) {
   if (!workspace) return QKV_ERR_NULL;
   if (!aligned(workspace, 256) || bytes % 4) return QKV_ERR_ALIGN;
@@ -806,6 +812,20 @@ int qkv_decode_noalloc_status(int device, hipStream_t stream) {
   const int st = noalloc_scratch_on(device, false, stream, &ptr);
   if (st) return st;
   return qkv_decode_workspace_status(ptr, stream);
+}
+
+int qkv_decode_noalloc_status_async(int device, int* status, hipStream_t stream) {
+  if (!status) return QKV_ERR_NULL;
+  if (!aligned(status, 4)) return QKV_ERR_ALIGN;
+  void* ptr = nullptr;
+  const int st = noalloc_scratch_on(device, false, stream, &ptr);
+  if (st) return st;
+  // launched with `device` current (the stream is one of its streams)
+  int cur = 0;
+  if (hipGetDevice(&cur) != hipSuccess || hipSetDevice(device) != hipSuccess) return QKV_ERR_DEVICE;
+  const int rc = launch_status(qkv::launch_ws_status(ptr, status, QKV_OK, QKV_ERR_TIMEOUT, stream));
+  if (hipSetDevice(cur) != hipSuccess) return QKV_ERR_DEVICE;
+  return rc;
 }
 
 int qkv_decode_noalloc_reset(int device, hipStream_t stream) {

@@ -33,6 +33,8 @@ hipError_t launch_dfk2_dequant(const void* q, const uint16_t* sc, void* out, lon
 hipError_t launch_q8_dequant(const void* in, void* out, int n_blocks, hipStream_t stream);
 // Zero-fill of `bytes` (a multiple of 4) bytes by a kernel (graph-capture safe).
 hipError_t launch_fill_zero(void* p, size_t bytes, hipStream_t stream);
+hipError_t launch_ws_status(const void* workspace, int* status, int ok_value, int timeout_value,
+                            hipStream_t stream);
 
 // Token-row moves inside one slot of one layer's cache (kv_move.hip): row
 // slot_row0 + to[i] := row slot_row0 + from[i] for i = 0..n-1, K and V.

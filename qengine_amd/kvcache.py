@@ -396,6 +396,16 @@ def decode_workspace_status(workspace, stream=None) -> int:
                                                  _stream(stream)))
 
 
+def decode_workspace_status_async(workspace, status, stream=None) -> None:
+    """Enqueue the health check without synchronising: once the stream gets
+    there, status[0] (an int32 device tensor) holds QKV_OK (0) or
+    QKV_ERR_TIMEOUT (-8).  Capturable in a HIP graph."""
+    _need(status, 4, "status", dtype=(torch.int32,))
+    check(lib().qkv_decode_workspace_status_async(_dev_ptr(workspace, "workspace"),
+                                                  _dev_ptr(status, "status"), _stream(stream)),
+          "qkv_decode_workspace_status_async")
+
+
 def decode_workspace_reset(workspace, stream=None) -> None:
     """Zero-fill a fast-path decode workspace (clears a sticky merge error)."""
     check(lib().qkv_decode_workspace_reset(_dev_ptr(workspace, "workspace"),
@@ -407,6 +417,14 @@ def decode_noalloc_status(device: int = 0, stream=None) -> int:
     """decode_workspace_status for the allocation-free decode's scratch of
     `device`: synchronises the stream, returns QKV_OK (0) or QKV_ERR_TIMEOUT (-8)."""
     return int(lib().qkv_decode_noalloc_status(int(device), _stream(stream)))
+
+
+def decode_noalloc_status_async(status, device: int = 0, stream=None) -> None:
+    """decode_workspace_status_async for the allocation-free decode's scratch
+    of `device`."""
+    _need(status, 4, "status", dtype=(torch.int32,))
+    check(lib().qkv_decode_noalloc_status_async(int(device), _dev_ptr(status, "status"),
+                                                _stream(stream)), "qkv_decode_noalloc_status_async")
 
 
 def decode_noalloc_reset(device: int = 0, stream=None) -> None:

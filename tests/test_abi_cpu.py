@@ -145,6 +145,10 @@ def test_workspace_health_argument_errors(L):
     assert L.qkv_decode_workspace_reset(p + 4, 256, None) == -4
     assert L.qkv_decode_workspace_reset(p, 6, None) == -4      # whole words only
     assert L.qkv_decode_workspace_reset(p, 0, None) == 0       # nothing to clear
+    assert L.qkv_decode_workspace_status_async(None, p, None) == -2
+    assert L.qkv_decode_workspace_status_async(p, None, None) == -2
+    assert L.qkv_decode_workspace_status_async(p + 4, p, None) == -4
+    assert L.qkv_decode_workspace_status_async(p, p + 2, None) == -4
     assert L.qkv_debug_set_merge_spin_limit(-1) == 0
     assert L.qkv_status_string(-8) == b"in-kernel merge timed out; reset the workspace"
 
@@ -210,9 +214,14 @@ def test_block_sparse_argument_errors_without_gpu(L):
 
 def test_noalloc_health_argument_errors(L):
     # device numbers outside 0..63 are rejected before any HIP call
+    buf = ctypes.create_string_buffer(64)
+    st = (ctypes.addressof(buf) + 15) & ~15
     for dev in (-1, 64):
         assert L.qkv_decode_noalloc_status(dev, None) == -1
         assert L.qkv_decode_noalloc_reset(dev, None) == -1
+        assert L.qkv_decode_noalloc_status_async(dev, st, None) == -1
+    assert L.qkv_decode_noalloc_status_async(0, None, None) == -2
+    assert L.qkv_decode_noalloc_status_async(0, st + 2, None) == -4
 
 
 @pytest.mark.parametrize("lang,compiler,std", [("c", "gcc", "-std=c11"), ("c++", "g++", "-std=c++17")])

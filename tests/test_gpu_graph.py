@@ -41,18 +41,24 @@ def test_tq3_decode_graph_replays(dev):
     out = torch.zeros((1, nq, 256), dtype=torch.float16, device=dev)
     out2 = torch.zeros((3, nq, 256), dtype=torch.float16, device=dev)
 
+    status = torch.full((1,), 12345, dtype=torch.int32, device=dev)
+
     def call():
         kvcache.decode_attn_tq3(q, kb, vb, out, ws, num_q=nq, num_kv=nkv, start_pos=n - 1, sub_n=1,
                                 scale=1 / 16)
+        kvcache.decode_workspace_status_async(ws, status)   # the health check rides in the graph
     call()
     torch.cuda.synchronize()
     ref = out.clone()
     g = _capture(call)
     for i in range(4):
         out.zero_()
+        status.fill_(12345)
+        torch.cuda.synchronize()
         g.replay()
         torch.cuda.synchronize()
         assert torch.equal(out, ref), f"replay {i}"
+        assert int(status.item()) == 0, f"replay {i}: workspace status"
         # eager work on the same workspace between replays (three queries)
         kvcache.decode_attn_tq3(q2, kb, vb, out2, ws, num_q=nq, num_kv=nkv, start_pos=n - 3,
                                 sub_n=3, scale=1 / 16)

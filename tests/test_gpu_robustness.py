@@ -28,14 +28,26 @@ def _oracle(kind, q, kb, vb, nq, nkv, n):
                               k_splits=8).view(np.float16).astype(np.float64)
 
 
+def _async_status(ws):
+    """qkv_decode_workspace_status_async into a device int, read after a sync."""
+    import torch
+    from qengine_amd import kvcache
+    st = torch.full((1,), 12345, dtype=torch.int32, device=ws.device)
+    kvcache.decode_workspace_status_async(ws, st)
+    torch.cuda.synchronize()
+    return int(st.item())
+
+
 def _timeout_cycle(dev, call, ws, ref, exact=None):
     from qengine_amd import kvcache
     import torch
     assert kvcache.decode_workspace_status(ws) == 0
+    assert _async_status(ws) == 0
     try:
         kvcache.debug_set_merge_spin_limit(0)
         out = call()
         assert kvcache.decode_workspace_status(ws) == -8
+        assert _async_status(ws) == -8
         assert np.all(np.isnan(out)), "timed-out merge must write NaN rows"
         kvcache.debug_set_merge_spin_limit(-1)
         out = call()   # the error is sticky until the workspace is reset
@@ -45,6 +57,7 @@ def _timeout_cycle(dev, call, ws, ref, exact=None):
         kvcache.debug_set_merge_spin_limit(-1)
     kvcache.decode_workspace_reset(ws)
     assert kvcache.decode_workspace_status(ws) == 0
+    assert _async_status(ws) == 0
     out = call()
     torch.cuda.synchronize()
     assert not np.any(np.isnan(out))
@@ -123,12 +136,20 @@ def test_noalloc_decode_merge_timeout(dev):
         torch.cuda.synchronize()
         return out.cpu().numpy().astype(np.float64)
 
+    def async_status():
+        st = torch.full((1,), 12345, dtype=torch.int32, device=dev)
+        kvcache.decode_noalloc_status_async(st, device)
+        torch.cuda.synchronize()
+        return int(st.item())
+
     kvcache.decode_noalloc_reset(device)
     assert kvcache.decode_noalloc_status(device) == 0
+    assert async_status() == 0
     try:
         kvcache.debug_set_merge_spin_limit(0)
         assert np.all(np.isnan(call())), "timed-out merge must write NaN rows"
         assert kvcache.decode_noalloc_status(device) == -8
+        assert async_status() == -8
         kvcache.debug_set_merge_spin_limit(-1)
         assert np.all(np.isnan(call())), "the error is sticky until the scratch is reset"
         assert kvcache.decode_noalloc_status(device) == -8
@@ -136,6 +157,7 @@ def test_noalloc_decode_merge_timeout(dev):
         kvcache.debug_set_merge_spin_limit(-1)
         kvcache.decode_noalloc_reset(device)
     assert kvcache.decode_noalloc_status(device) == 0
+    assert async_status() == 0
     out = call()
     assert_tq3_attn(out, ref, exact)
     assert kvcache.decode_noalloc_status(device) == 0
