@@ -163,15 +163,6 @@ int qkv_kv_scatter_rows(void* k_pool, void* v_pool, const void* k_flat, const vo
                         const int32_t* block_table, int max_blocks, int block_tokens, int n_rows,
                         hipStream_t stream);
 
-/* Measurement helper, not a cache operation: one streaming read of `bytes`
- * (a multiple of 64) from device memory, each byte once, nothing stored
- * (sink, one dword, is written only for a data pattern no caller produces).
- * Timed around a buffer larger than the 256 MB Infinity Cache it gives the
- * sustained read bandwidth the decode's HBM fraction is also quoted against;
- * the reference measures the same with tools/bench_hbm_bandwidth.cu
- * (k_read_f4, lines 45-57). */
-int qkv_hbm_read_bench(const void* buf, size_t bytes, uint32_t* sink, hipStream_t stream);
-
 /* Token-row moves inside one slot of one layer's cache: replaces the per-token
  * device copies of kv_move_token (model.cuh:7430-7471; its tree-verify
  * acceptance calls it once per accepted token and layer).  For i = 0..n-1 in

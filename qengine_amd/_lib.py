@@ -13,6 +13,9 @@ import re
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "libqkv.so")
 HEADER_PATH = os.path.join(os.path.dirname(_HERE), "include", "qkv.h")
+# the benchmark's measurement helper lives in a library of its own
+BENCH_LIB_PATH = os.path.join(_HERE, "libqkv_bench.so")
+BENCH_HEADER_PATH = os.path.join(os.path.dirname(_HERE), "include", "qkv_bench.h")
 
 QKV_OK = 0
 STATUS_NAMES = {
@@ -48,7 +51,6 @@ SIGNATURES = {
     "qkv_kv_gather_rows": (_I, [_P, _P, _P, _P, _SZ, _SZ, ctypes.c_long, _P, _I, _I, _I, _P]),
     "qkv_kv_scatter_rows": (_I, [_P, _P, _P, _P, _SZ, _SZ, ctypes.c_long, _P, _I, _I, _I, _P]),
     "qkv_dfk2_dequant": (_I, [_P, _P, _P, ctypes.c_longlong, _I, _P]),
-    "qkv_hbm_read_bench": (_I, [_P, _SZ, _P, _P]),
     "qkv_tq3_append_dfk2": (_I, [_P, _P, _P, _I, _P]),
     "qkv_q8_append_dfk2": (_I, [_P, _P, _P, _I, _P]),
     "qkv_attn_split_tq3": (_I, [_P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _F, _I, _I,
@@ -86,12 +88,17 @@ SIGNATURES = {
     "qkv_prefill_attn_tq3": (_I, [_P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _F, _P, _SZ, _P]),
 }
 
+BENCH_SIGNATURES = {
+    "qkv_hbm_read_bench": (_I, [_P, _SZ, _P, _P]),
+}
+
 _lib = None
+_bench_lib = None
 
 
-def header_functions() -> list[str]:
-    """Names of the functions declared in include/qkv.h."""
-    text = open(HEADER_PATH).read()
+def header_functions(path: str = HEADER_PATH) -> list[str]:
+    """Names of the functions declared in a header (include/qkv.h by default)."""
+    text = open(path).read()
     text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
     return sorted(set(re.findall(r"\b(qkv_[a-z0-9_]+)\s*\(", text)))
 
@@ -108,6 +115,21 @@ def lib() -> ctypes.CDLL:
             fn.argtypes = args
         _lib = L
     return _lib
+
+
+def bench_lib() -> ctypes.CDLL:
+    """libqkv_bench.so (include/qkv_bench.h): the benchmark's streaming read."""
+    global _bench_lib
+    if _bench_lib is None:
+        if not os.path.exists(BENCH_LIB_PATH):
+            raise QKVError(-5, f"{BENCH_LIB_PATH} is not built (run __graft_entry__.build())")
+        L = ctypes.CDLL(BENCH_LIB_PATH)
+        for name, (res, args) in BENCH_SIGNATURES.items():
+            fn = getattr(L, name)
+            fn.restype = res
+            fn.argtypes = args
+        _bench_lib = L
+    return _bench_lib
 
 
 def check(status: int, where: str) -> None:

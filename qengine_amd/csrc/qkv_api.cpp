@@ -170,14 +170,6 @@ int qkv_q8_append_dfk2(const int8_t* q, const uint16_t* scales, qkv_block_q8* ou
   return launch_status(qkv::launch_q8_append(q, out, q, out, n_blocks, 1, stream, scales, scales));
 }
 
-int qkv_hbm_read_bench(const void* buf, size_t bytes, uint32_t* sink, hipStream_t stream) {
-  if (bytes == 0) return QKV_OK;
-  if (bytes % 64) return QKV_ERR_INVALID;
-  if (!buf || !sink) return QKV_ERR_NULL;
-  if (!aligned(buf, 16) || !aligned(sink, 4)) return QKV_ERR_ALIGN;
-  return launch_status(qkv::launch_stream_read(buf, bytes, sink, stream));
-}
-
 int qkv_kv_move_tokens(void* k, void* v, size_t k_row_bytes, size_t v_row_bytes, long slot_row0,
                        long slot_rows, const int32_t* from_to, int n, hipStream_t stream) {
   if (n < 0 || n > qkv::kMoveMax) return QKV_ERR_INVALID;

@@ -48,7 +48,6 @@ struct MoveArgs {
   int from[kMoveMax], to[kMoveMax];
 };
 hipError_t launch_kv_move(const MoveArgs& a, bool ordered, hipStream_t stream);
-hipError_t launch_stream_read(const void* p, size_t bytes, uint32_t* sink, hipStream_t stream);
 
 // Paged slot snapshot (gather) / restore (scatter), kv_move.hip.  Tensor t
 // (0: K, 1: V) has rows of row_bytes[t] (a multiple of 4).

@@ -12,7 +12,7 @@ from __future__ import annotations
 
 import torch
 
-from ._lib import check, lib
+from ._lib import bench_lib, check, lib
 
 TQ3_BLOCK_BYTES = 52
 Q8_BLOCK_BYTES = 36
@@ -213,8 +213,9 @@ def q8_append_dfk2(q, scales, out, stream=None) -> None:
 
 
 def hbm_read_bench(buf, sink, stream=None) -> None:
-    """One streaming read of the whole tensor `buf` (bandwidth measurement)."""
-    check(lib().qkv_hbm_read_bench(_dev_ptr(buf, "buf"), buf.numel() * buf.element_size(),
+    """One streaming read of the whole tensor `buf` (bandwidth measurement;
+    libqkv_bench.so, not the product library)."""
+    check(bench_lib().qkv_hbm_read_bench(_dev_ptr(buf, "buf"), buf.numel() * buf.element_size(),
                                    _dev_ptr(sink, "sink"), _stream(stream)), "qkv_hbm_read_bench")
 
 

@@ -20,6 +20,23 @@ def test_exports_every_declared_function(L):
         assert n in _lib.SIGNATURES, f"ctypes binding lacks {n}"
 
 
+def test_bench_library_exports_its_header():
+    """The benchmark's streaming read lives in libqkv_bench.so (include/qkv_bench.h),
+    not in the product library."""
+    B = _lib.bench_lib()
+    names = _lib.header_functions(_lib.BENCH_HEADER_PATH)
+    assert names == ["qkv_hbm_read_bench"]
+    for n in names:
+        assert hasattr(B, n) and n in _lib.BENCH_SIGNATURES
+        assert not hasattr(_lib.lib(), n), f"libqkv.so still exports {n}"
+    buf = ctypes.create_string_buffer(256)
+    p = (ctypes.addressof(buf) + 63) & ~63
+    assert B.qkv_hbm_read_bench(p, 0, p, None) == 0          # nothing to read
+    assert B.qkv_hbm_read_bench(p, 48, p, None) == -1        # multiples of 64 bytes
+    assert B.qkv_hbm_read_bench(None, 64, p, None) == -2
+    assert B.qkv_hbm_read_bench(p + 4, 64, p, None) == -4
+
+
 def test_version_and_status_strings(L):
     assert L.qkv_version() >= 100
     for code in _lib.STATUS_NAMES:
