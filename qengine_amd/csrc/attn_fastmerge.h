@@ -91,6 +91,22 @@ struct MergeLayout {
   static constexpr int kRedFloats = kWaves * 128;
 };
 
+// Workgroup-wide AND of `pred` over a 1-D workgroup of THREADS threads: one
+// LDS word per wave (`slots`, free while the call runs), no work-item id
+// beyond threadIdx.x (the device library's __syncthreads_and forms a linear
+// id from all three, which keeps them live across a whole kernel).
+template <int THREADS>
+__device__ __forceinline__ bool block_and(bool pred, int* slots) {
+  const bool wave_all = __builtin_amdgcn_ballot_w64(!pred) == 0;
+  __syncthreads();   // the previous use of the slots is over
+  if ((threadIdx.x & 63) == 0) slots[threadIdx.x >> 6] = wave_all ? 1 : 0;
+  __syncthreads();
+  bool all = true;
+#pragma unroll
+  for (int w = 0; w < THREADS / 64; w++) all = all && slots[w] != 0;
+  return all;
+}
+
 // NaN rows for unit (query t, q head qh, 128-block blk): threads 0..15 store 8 halves each.
 __device__ __forceinline__ void write_nan_unit(const AttnArgs& p, int t, int qh, int blk, uint16_t* out) {
   if (threadIdx.x < 16)
@@ -134,7 +150,8 @@ __device__ bool merge_unit(float* red, f2_t* mls, const AttnArgs& p, __amdgpu_bu
         mls[tid] = f2_t{r[0], r[1]};
       }
     }
-    if (__syncthreads_and(seen)) {
+    // (red is free until the rows are folded: it holds the vote)
+    if (block_and<THREADS>(seen, reinterpret_cast<int*>(red))) {
       complete = true;
       break;
     }
@@ -282,9 +299,9 @@ __device__ __forceinline__ void store_record_piece(const AttnArgs& p, __amdgpu_b
 
 // Tag this workgroup's records (rows 0..rows-1 as in store_records) once every
 // thread's data stores are complete; every thread of the workgroup calls it.
+// gqa = num_q / num_kv, passed in uniform (scalar register).
 __device__ __forceinline__ void publish_records(const AttnArgs& p, __amdgpu_buffer_rsrc_t rml, int h,
-                                                int t0, int rows, int chunk) {
-  const int gqa = p.num_q / p.num_kv;
+                                                int gqa, int t0, int rows, int chunk) {
   __builtin_amdgcn_s_waitcnt(0);  // this thread's data stores are complete
   __syncthreads();
   if ((int)threadIdx.x < rows) {
@@ -307,8 +324,12 @@ __device__ void merge_phase(float* red, f2_t* mls, const AttnArgs& p, __amdgpu_b
   // a workspace left inconsistent by an earlier timeout yields NaN rows until it is reset
   const bool poisoned = __hip_atomic_load(p.ws_header + kWsErrorWord, __ATOMIC_RELAXED,
                                           __HIP_MEMORY_SCOPE_AGENT) != 0;
+  // (num_q re-read here: a divisor the compiler would otherwise prepare at
+  // kernel entry and hold in a register through the whole tile loop)
+  int num_q = p.num_q;
+  asm volatile("" : "+s"(num_q));
   for (int u = mid; u < n_units; u += n_mergers) {
-    const int blk = u & 1, qh = (u >> 1) % p.num_q, t = (u >> 1) / p.num_q;
+    const int blk = u & 1, qh = (u >> 1) % num_q, t = (u >> 1) / num_q;
     long base = rec_index(p, qh, t, 0);
     int n = p.n_chunks;
     if (p.ctx_lens) {   // ragged slots: the slot's shares of the kv head's records

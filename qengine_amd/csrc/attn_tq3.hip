@@ -463,7 +463,7 @@ __global__ __launch_bounds__(kThreads, 1) void tq3_attn_kernel(QKV_ATTN_LEAD_PAR
   QKV_STAMP(kPhEntry);
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int gqa = p.num_q / p.num_kv;
+  const int gqa = __builtin_amdgcn_readfirstlane(p.num_q / p.num_kv);   // scalar register
 
   // ---- work id (XCD-aware: the num_kv workgroups of one (query group, chunk)
   // share an XCD).  A workgroup serves queries t0 .. t0+nq-1 (nq <= qpw) of
@@ -503,7 +503,8 @@ __global__ __launch_bounds__(kThreads, 1) void tq3_attn_kernel(QKV_ATTN_LEAD_PAR
   }
   if (MODE >= 1 && !has_work) return;
   const int nq = min(p.qpw, p.sub_n - t0);
-  const int rows_used = nq * gqa;   // accumulator rows (columns) that hold heads
+  // accumulator rows (columns) that hold heads (uniform: kept in a scalar register)
+  const int rows_used = __builtin_amdgcn_readfirstlane(nq * gqa);
   const int row = lane >> 4;        // 16-lane row of the MFMA D layout
   const int col = lane & 15;
   const int t_col = t0 + min(col / gqa, nq - 1);   // this lane's query (clamped for dead columns)
@@ -595,8 +596,9 @@ __global__ __launch_bounds__(kThreads, 1) void tq3_attn_kernel(QKV_ATTN_LEAD_PAR
       p.block_tables ? (uint32_t)(p.sub_n * p.bt_stride * 4) : 0u, kBufferRsrcWord3);
   auto bt_batch = [&](int k0) -> int {   // entries of tiles k0 .. k0+63 (one per lane)
     const int ts = ts0 + (k0 + lane) * kStep;
-    const uint32_t off = ts < hi ? (uint32_t)((t0 * p.bt_stride + ts / max(p.block_tokens, 1)) * 4)
-                                 : 0xffffffffu;
+    int bt = __builtin_amdgcn_readfirstlane(max(p.block_tokens, 1));
+    asm volatile("" : "+s"(bt));   // (divisor re-read per batch, not held through the loop)
+    const uint32_t off = ts < hi ? (uint32_t)((t0 * p.bt_stride + ts / bt) * 4) : 0xffffffffu;
     return (int)__builtin_amdgcn_raw_buffer_load_b32(rbt, off, 0, 0);
   };
   int bt_entry = paged ? bt_batch(0) : 0, bt_k0 = 0;
@@ -613,8 +615,11 @@ __global__ __launch_bounds__(kThreads, 1) void tq3_attn_kernel(QKV_ATTN_LEAD_PAR
       bt_entry = bt_batch(bt_k0);
     }
     const int e = __builtin_amdgcn_readlane(bt_entry, k - bt_k0);
-    const int b = ts / p.block_tokens;
-    return e * p.block_tokens + (ts - b * p.block_tokens);
+    // (the divisor re-read per tile instead of held through the loop)
+    int bt = __builtin_amdgcn_readfirstlane(p.block_tokens);
+    asm volatile("" : "+s"(bt));
+    const int b = ts / bt;
+    return e * bt + (ts - b * bt);
   };
   // waves 0..3 issue their first tile's loads as soon as the query has
   // arrived (so it does not queue behind them), ahead of the table build
@@ -915,14 +920,17 @@ __global__ __launch_bounds__(kThreads, 1) void tq3_attn_kernel(QKV_ATTN_LEAD_PAR
   __syncthreads();
   float* mo = reinterpret_cast<float*>(lds + kLdsMergeO);    // [wave][8][256]
   float* ml = reinterpret_cast<float*>(lds + kLdsMergeML);
-  if (4 * row < rows_used) {   // accumulator rows 4*row + r; rows >= rows_used are unused
+  // (row offset recomputed from the thread index rather than held through the loop)
+  int row4 = ((int)threadIdx.x & 63) >> 4 << 2;
+  asm volatile("" : "+v"(row4));
+  if (row4 < rows_used) {   // accumulator rows 4*row + r; rows >= rows_used are unused
     // acc tile t: rows 4*row+r, dim 128*(t>>3) + 8*col + (t&7): 16-byte stores
 #pragma unroll
     for (int r = 0; r < 4; r++)
 #pragma unroll
       for (int q4 = 0; q4 < 4; q4++) {
         const int t = 4 * q4;   // tiles t..t+3: dims 128*(q4>>1) + 8*col + 4*(q4&1) + 0..3
-        *reinterpret_cast<f4_t*>(mo + (wave * 16 + 4 * row + r) * kHD + 128 * (q4 >> 1) + 8 * col +
+        *reinterpret_cast<f4_t*>(mo + (wave * 16 + row4 + r) * kHD + 128 * (q4 >> 1) + 8 * col +
                                  4 * (q4 & 1)) = f4_t{acc[t][r], acc[t + 1][r], acc[t + 2][r], acc[t + 3][r]};
       }
   }
@@ -937,6 +945,10 @@ __global__ __launch_bounds__(kThreads, 1) void tq3_attn_kernel(QKV_ATTN_LEAD_PAR
       __builtin_amdgcn_make_buffer_rsrc(p.ws_ml, 0, MODE == 0 ? p.ws_ml_bytes : 0u, kBufferRsrcWord3);
   const __amdgpu_buffer_rsrc_t ro =
       __builtin_amdgcn_make_buffer_rsrc(p.ws_o, 0, MODE == 0 ? p.ws_o_bytes : 0u, kBufferRsrcWord3);
+  // (an opaque copy of gqa: its division reciprocal is formed here, not held
+  // in a register through the tile loop)
+  int gqa_m = gqa;
+  asm volatile("" : "+s"(gqa_m));
   for (int idx = threadIdx.x; idx < rows * 64; idx += kThreads) {
     const int r = idx >> 6, d4 = (idx & 63) * 4;
     float M = -INFINITY;
@@ -958,7 +970,7 @@ __global__ __launch_bounds__(kThreads, 1) void tq3_attn_kernel(QKV_ATTN_LEAD_PAR
         ml[kMlL + r] = L;
       }
     } else if (has_work) {
-      store_record_piece(p, rml, ro, h * gqa + r % gqa, rec_t0 + r / gqa, rec_chunk, d4, o, M, L);
+      store_record_piece(p, rml, ro, h * gqa_m + r % gqa_m, rec_t0 + r / gqa_m, rec_chunk, d4, o, M, L);
     }
   }
 
@@ -970,7 +982,7 @@ __global__ __launch_bounds__(kThreads, 1) void tq3_attn_kernel(QKV_ATTN_LEAD_PAR
 
   // ---------------- fast path: tagged records, designated mergers ----------------
   QKV_STAMP(kPhMerged);
-  if (has_work) publish_records(p, rml, h, rec_t0, rows, rec_chunk);
+  if (has_work) publish_records(p, rml, h, gqa_m, rec_t0, rows, rec_chunk);
   QKV_STAMP(kPhPublished);
 #ifdef QKV_PHASE_TRACE
   if (threadIdx.x == 0) *reinterpret_cast<uint64_t*>(lds + kLdsMergeO + kTracePolledByte) = 0;
