@@ -31,7 +31,9 @@ namespace qkv {
 constexpr int kCoherent = 1 | 16;   // sc0 | sc1
 
 // Diagnostic build (-DQKV_PHASE_TRACE): byte offset, inside the merge area,
-// where a merger leaves the time its polls completed.
+// where a merger leaves the time its polls completed; the next two words hold
+// the time its record rows had arrived and the time the waves' partials were
+// folded (before the normalise / rotate / store of the output rows).
 constexpr int kTracePolledByte = 16384;
 
 // Record index of (q head, query t, chunk) in the fast-path workspace.
@@ -184,6 +186,12 @@ __device__ bool merge_unit(float* red, f2_t* mls, const AttnArgs& p, __amdgpu_bu
                        ro, (uint32_t)(((base + c) * kHD + blk * 128 + 4 * dq) * 4), 0, kCoherent)
                  : f4_t{0.f, 0.f, 0.f, 0.f};
   }
+#ifdef QKV_PHASE_TRACE
+  __builtin_amdgcn_s_waitcnt(0);   // (trace build only: the rows' arrival, thread 0's view)
+  if (tid == 0)
+    *reinterpret_cast<uint64_t*>(reinterpret_cast<uint8_t*>(red) + kTracePolledByte + 8) =
+        __builtin_amdgcn_s_memrealtime();
+#endif
   // common max M and weight sum L over the records (empty chunks, l = 0,
   // carry no weight), in every wave
   const f2_t r0 = lane < n ? mls[lane] : f2_t{-INFINITY, 0.f};
@@ -210,6 +218,11 @@ __device__ bool merge_unit(float* red, f2_t* mls, const AttnArgs& p, __amdgpu_bu
   }
   if (lane < 32) *reinterpret_cast<f4_t*>(&red[wave * 128 + 4 * dq]) = acc;
   __syncthreads();
+#ifdef QKV_PHASE_TRACE
+  if (tid == 0)
+    *reinterpret_cast<uint64_t*>(reinterpret_cast<uint8_t*>(red) + kTracePolledByte + 16) =
+        __builtin_amdgcn_s_memrealtime();
+#endif
   // 16 lanes x 8 elements (threads 0..15): sum the waves' partials, normalise,
   // rotate back, store fp16
   if (tid < 16) {

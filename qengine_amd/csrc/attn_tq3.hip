@@ -76,6 +76,11 @@ enum TracePhase {
   kPhPublished = 7,  // tags stored
   kPhPolled = 8,     // mergers: every record of the unit seen
   kPhEnd = 9,        // the workgroup is done (mergers: output stored)
+  kPhMergeBar = 10,  // in-workgroup merge: every wave's rows are in LDS (barrier passed)
+  kPhRowsIn = 11,    // mergers: the unit's record rows have arrived
+  kPhFolded = 12,    // mergers: the waves' partials are folded (before normalise/rotate/store)
+  kPhSetupWork = 13, // the wave's setup work done (before the setup barrier)
+  kPhTileBar = 14,   // every wave's tiles done (the barrier before the in-workgroup merge)
   kPhXcd = 15
 };
 #ifdef QKV_PHASE_TRACE
@@ -116,7 +121,7 @@ constexpr int kLdsMergeML = kLdsMergeO + kWaves * 16 * kHD * 4;
 constexpr int kLdsMergeEnd = kLdsMergeML + 512 * 4;
 constexpr int kLdsTotal = kLdsTileEnd;
 static_assert(kLdsMergeEnd <= kLdsQ, "merge area must not reach the query scratch");
-static_assert(kTracePolledByte >= kWaves * 128 * 4 && kTracePolledByte + 8 <= kLdsMergeML - kLdsMergeO,
+static_assert(kTracePolledByte >= kWaves * 128 * 4 && kTracePolledByte + 24 <= kLdsMergeML - kLdsMergeO,
               "the merger's trace slot lies in the merge area, past the reduction area");
 
 // merge-area float offsets (ML): m[w][16], l[w][16], M[16], L[16]
@@ -458,7 +463,7 @@ __global__ __launch_bounds__(kThreads, 1) void tq3_attn_kernel(QKV_ATTN_LEAD_PAR
   // static LDS: table and tile offsets fold into the instructions' offset field
   __shared__ __attribute__((aligned(16))) uint8_t lds[kLdsTotal];
 #ifdef QKV_PHASE_TRACE
-  uint64_t trace_st[10] = {0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
+  uint64_t trace_st[15] = {0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
 #endif
   QKV_STAMP(kPhEntry);
   const int lane = threadIdx.x & 63;
@@ -721,6 +726,7 @@ __global__ __launch_bounds__(kThreads, 1) void tq3_attn_kernel(QKV_ATTN_LEAD_PAR
           make_uint4(pl[0], pl[1], pl[2], pl[3]);
     }
   }
+  QKV_STAMP(kPhSetupWork);
   __syncthreads();
   QKV_STAMP(kPhSetup);
   // (built after the setup: its tree word is a load the first loads must not wait for)
@@ -918,6 +924,7 @@ __global__ __launch_bounds__(kThreads, 1) void tq3_attn_kernel(QKV_ATTN_LEAD_PAR
 
   // ---------------- merge the 4 waves in LDS ----------------
   __syncthreads();
+  QKV_STAMP(kPhTileBar);
   float* mo = reinterpret_cast<float*>(lds + kLdsMergeO);    // [wave][8][256]
   float* ml = reinterpret_cast<float*>(lds + kLdsMergeML);
   // (row offset recomputed from the thread index rather than held through the loop)
@@ -939,6 +946,7 @@ __global__ __launch_bounds__(kThreads, 1) void tq3_attn_kernel(QKV_ATTN_LEAD_PAR
     ml[kMlLw0 + wave * 16 + col] = lsum;
   }
   __syncthreads();
+  QKV_STAMP(kPhMergeBar);
   const int rows = rows_used;
   // fast path: every merged piece goes straight to its record
   const __amdgpu_buffer_rsrc_t rml =
@@ -985,7 +993,7 @@ __global__ __launch_bounds__(kThreads, 1) void tq3_attn_kernel(QKV_ATTN_LEAD_PAR
   if (has_work) publish_records(p, rml, h, gqa_m, rec_t0, rows, rec_chunk);
   QKV_STAMP(kPhPublished);
 #ifdef QKV_PHASE_TRACE
-  if (threadIdx.x == 0) *reinterpret_cast<uint64_t*>(lds + kLdsMergeO + kTracePolledByte) = 0;
+  if (threadIdx.x < 3) *reinterpret_cast<uint64_t*>(lds + kLdsMergeO + kTracePolledByte + 8 * threadIdx.x) = 0;
 #endif
   using ML = MergeLayout<kThreads>;
   static_assert(kLdsMergeO + ML::kRedFloats * 4 <= kLdsMergeML, "merge reduction must fit");
@@ -994,11 +1002,13 @@ __global__ __launch_bounds__(kThreads, 1) void tq3_attn_kernel(QKV_ATTN_LEAD_PAR
 #ifdef QKV_PHASE_TRACE
   __syncthreads();
   trace_st[kPhPolled] = *reinterpret_cast<const uint64_t*>(lds + kLdsMergeO + kTracePolledByte);
+  trace_st[kPhRowsIn] = *reinterpret_cast<const uint64_t*>(lds + kLdsMergeO + kTracePolledByte + 8);
+  trace_st[kPhFolded] = *reinterpret_cast<const uint64_t*>(lds + kLdsMergeO + kTracePolledByte + 16);
   QKV_STAMP(kPhEnd);
-  if (lane < 10 && blockIdx.x < kTraceMaxWgs) {
+  if (lane < 15 && blockIdx.x < kTraceMaxWgs) {
     uint64_t v = 0;
 #pragma unroll
-    for (int i = 0; i < 10; i++) v = lane == i ? trace_st[i] : v;
+    for (int i = 0; i < 15; i++) v = lane == i ? trace_st[i] : v;
     qkv_phase_stamps[(blockIdx.x * kWaves + wave) * 16 + lane] = v;
   }
   if (lane == 0 && blockIdx.x < kTraceMaxWgs)

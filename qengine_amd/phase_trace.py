@@ -23,7 +23,7 @@ _HERE = os.path.dirname(os.path.abspath(__file__))
 WAVES = 8
 SLOTS = 16
 PHASES = ["entry", "query", "setup", "scores", "softmax", "tiles", "merged", "published",
-          "polled", "end"]
+          "polled", "end", "merge barrier", "rows in", "folded", "setup work", "tile barrier"]
 TICK_US = 0.01   # s_memrealtime runs at 100 MHz
 
 
@@ -37,23 +37,29 @@ def _stamps(L, n_wg):
 
 def _launch_sample(st):
     """One launch's stamps -> dict of per-workgroup phase times (us from its first wave)."""
-    t = st[:, :, :10].astype(np.int64)
+    t = st[:, :, :len(PHASES)].astype(np.int64)
     live = t[:, :, 0] > 0
     t0 = t[:, :, 0][live].min()
     rel = np.where(t > 0, (t - t0) * TICK_US, np.nan)
     out = {}
     out["entry"] = np.nanmin(rel[:, :, 0], axis=1)                       # first wave of the workgroup
     out["query"] = np.nanmax(rel[:, :, 1], axis=1)
+    out["setup work w0-3"] = np.nanmax(rel[:, :4, 13], axis=1)
+    out["setup work w4-7"] = np.nanmax(rel[:, 4:, 13], axis=1)
     out["setup"] = np.nanmax(rel[:, :, 2], axis=1)
     for name, k in (("scores", 3), ("softmax", 4), ("tiles", 5)):
         out[name + " w0-3"] = np.nanmax(rel[:, :4, k], axis=1)
         out[name + " w4-7"] = np.nanmax(rel[:, 4:, k], axis=1)
+    out["tile barrier"] = np.nanmax(rel[:, :, 14], axis=1)
+    out["merge barrier"] = np.nanmax(rel[:, :, 10], axis=1)
     out["merged"] = np.nanmax(rel[:, :, 6], axis=1)
     out["published"] = np.nanmax(rel[:, :, 7], axis=1)
     pol = rel[:, 0, 8]
-    out["polled (mergers)"] = pol[~np.isnan(pol)]
-    end = np.nanmax(rel[:, :, 9], axis=1)
     merger = ~np.isnan(pol)
+    out["polled (mergers)"] = pol[merger]
+    out["rows in (mergers)"] = rel[:, 0, 11][merger]
+    out["folded (mergers)"] = rel[:, 0, 12][merger]
+    end = np.nanmax(rel[:, :, 9], axis=1)
     out["end (mergers)"] = end[merger]
     out["end (others)"] = end[~merger]
     xcd = st[:, 0, 15].astype(np.int64)
