@@ -111,15 +111,27 @@ __device__ __forceinline__ void shift_in(uint32_t& acc, uint64_t plane) {
       : [a] "+v"(acc), [cy] "=&s"(cy) : [p] "s"(plane));
 }
 
+// This lane's index (0..63) from mbcnt of a mask the compiler cannot see as
+// constant, so that it is formed where it is used instead of being hoisted
+// and kept (or spilled) across a loop.
+__device__ __forceinline__ int opaque_lane() {
+  uint32_t all = ~0u;
+  asm volatile("" : "+s"(all));
+  return (int)__builtin_amdgcn_mbcnt_hi(all, __builtin_amdgcn_mbcnt_lo(all, 0u));
+}
+
 // Output block of input block i for a paged append (PagedRows), or -1 when
-// the row it maps to lies outside the pool (then nothing is written).
+// the row it maps to lies outside the pool (then nothing is written).  The
+// divisions run in 32 bits: i < n_blocks < 2^31, and a position past INT_MAX
+// (int32 positions, as in the reference) maps to no row.
 __device__ __forceinline__ long paged_block(const PagedRows& pr, long i) {
-  const long tok = i / pr.blocks_per_row;
-  const int j = (int)(i - tok * pr.blocks_per_row);
-  const int s = (int)(tok / pr.n_tok), t = (int)(tok - (long)s * pr.n_tok);
+  const int ii = (int)i;
+  const int tok = ii / pr.blocks_per_row;
+  const int j = ii - tok * pr.blocks_per_row;
+  const int s = tok / pr.n_tok, t = tok - s * pr.n_tok;
   const long pos = (long)pr.positions[s] + t;
-  if (pos < 0) return -1;
-  const long b = pos / pr.block_tokens;
+  if (pos < 0 || pos > 0x7fffffffL) return -1;
+  const int b = (int)pos / pr.block_tokens;
   if (b >= pr.max_blocks) return -1;
   const long row = (long)pr.block_tables[(long)s * pr.max_blocks + b] * pr.block_tokens +
                    (pos - b * pr.block_tokens);
@@ -320,8 +332,10 @@ __global__ __launch_bounds__(kAp4Threads, 3) void tq3_append4_kernel(
     // DFK2 and paged tiles: the per-lane offsets and the paged divisors are
     // re-formed every tile (a few instructions) instead of living in
     // registers across the loop, where the tile leaves no room for them.
-    int lane_t = lane;
-    if constexpr (kDfk2 || kPaged) asm volatile("" : "+v"(lane_t));
+    // DFK2 and paged tiles form the lane index where they use it (for the
+    // loads here, again for the stores), not from a register held across
+    // the tile
+    const int lane_t = (kDfk2 || kPaged) ? opaque_lane() : lane;
     // R1 = first half of block `lane`, R2 = second half of block lane ^ 1
     uint32_t h1[32], h2[32];
     load_halves<kDfk2>(h1, h2, tensor ? in1 : in0, tensor ? sc1 : sc0, b0, nb, lane_t);
@@ -408,13 +422,14 @@ __global__ __launch_bounds__(kAp4Threads, 3) void tq3_append4_kernel(
     }
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "workgroup");
+    const int lane_s = (kDfk2 || kPaged) ? opaque_lane() : lane;
 
     if constexpr (kPaged) {
       // paged: each lane stores its block at the block's row
       PagedRows prt = pr;
       asm volatile("" : "+s"(prt.block_tokens), "+s"(prt.blocks_per_row), "+s"(prt.n_tok));
-      if (lane_t < nb) {
-        const long ob = paged_block(prt, (long)b0 + lane_t);
+      if (lane_s < nb) {
+        const long ob = paged_block(prt, (long)b0 + lane_s);
         if (ob >= 0) {
           uint32_t* dst = out + ob * 13;
           dst[0] = __float_as_uint(norm1);
@@ -424,7 +439,7 @@ __global__ __launch_bounds__(kAp4Threads, 3) void tq3_append4_kernel(
       }
     } else {
       // 4. stage the tile's 64 x 13 dwords, then store them contiguously
-      uint32_t* ob = wl + lane_t * 13;
+      uint32_t* ob = wl + lane_s * 13;
       ob[0] = __float_as_uint(norm1);
 #pragma unroll
       for (int w = 0; w < 12; w++) ob[1 + w] = acc[w];
@@ -435,7 +450,7 @@ __global__ __launch_bounds__(kAp4Threads, 3) void tq3_append4_kernel(
           out + (long)b0 * 13, 0, nb * 52, kBufferRsrcWord3);
 #pragma unroll
       for (int j = 0; j < 13; j++)
-        __builtin_amdgcn_raw_buffer_store_b32(wl[j * 64 + lane_t], rd, lane_t * 4, j * 256, 0);
+        __builtin_amdgcn_raw_buffer_store_b32(wl[j * 64 + lane_s], rd, lane_s * 4, j * 256, 0);
     }
     if (!more) break;
     tile = tile_n;
