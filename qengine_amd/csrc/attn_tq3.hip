@@ -543,9 +543,12 @@ __global__ __launch_bounds__(kThreads, 1) void tq3_attn_kernel(QKV_ATTN_LEAD_PAR
   if (MODE == 0) {
     if (has_work) {
       lo = chunk * chunk_keys;
-      hi = min(lo + chunk_keys, active_last);
-      hi_col = min(lo + chunk_keys, active_end);
-      hi_first = min(lo + chunk_keys, active_first);
+      // the last chunk of a contiguous launch runs to the end of the keys: the
+      // host may have joined a remainder of at most one tile to it
+      const int c_end = (!ragged && chunk == p.n_chunks - 1) ? active_last : lo + chunk_keys;
+      hi = min(c_end, active_last);
+      hi_col = min(c_end, active_end);
+      hi_first = min(c_end, active_first);
     }
   } else if (MODE == 2) {
     // the selected blocks bound the keys; the query's causal end masks them

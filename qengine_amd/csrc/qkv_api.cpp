@@ -508,17 +508,29 @@ int tq3_groups(int num_q, int num_kv, int sub_n) {
 }
 
 FastGeom fast_geom(int num_q, int num_kv, int sub_n, int n_keys, int base = kChunkKeys,
-                   int groups = 0) {
+                   int groups = 0, bool join_tail = false) {
   FastGeom g{};
   const int cb = (n_keys + base - 1) / base;
   int tpw = (cb + 127) / 128;
+  // chunks of base * t keys; with join_tail (a contiguous TQ3 launch, whose
+  // kernel runs its last chunk to the end of the keys) a last chunk of at most
+  // one 64-key tile joins the previous one when the chunks hold >= 4 tiles per
+  // wave: one wave then takes one more tile instead of every wave one more
+  // round (a 16-token verify over 131,072 + 16 keys: 16 chunks of 16 tiles per
+  // wave and one 16-key tile, not 16 chunks of 17)
+  auto chunks = [&](int t) {
+    const long ck = (long)base * t;
+    int n = (int)((n_keys + ck - 1) / ck);
+    if (join_tail && n > 1 && t >= 4 && n_keys - (n - 1) * ck <= 64) n--;
+    return n;
+  };
   // Long contexts and many queries: grow the chunks until the launch fits one
   // round of the GPU (kMaxFastWgs workgroups, one per CU), so that each
   // workgroup pays its setup and merge once for several tiles (config 4:
   // 189 -> 119 us per step; a 16-token verify over 131K keys: 148 -> 108 us).
-  while (groups > 0 && (long)groups * ((cb + tpw - 1) / tpw) * num_kv > kMaxFastWgs && tpw < cb) tpw++;
+  while (groups > 0 && (long)groups * chunks(tpw) * num_kv > kMaxFastWgs && tpw < cb) tpw++;
   g.chunk_keys = base * tpw;
-  g.n_chunks = (n_keys + g.chunk_keys - 1) / g.chunk_keys;
+  g.n_chunks = chunks(tpw);
   g.n_slots = g.n_chunks;
   const size_t rows = (size_t)num_q * sub_n * g.n_slots;
   g.header_off = 0;
@@ -532,7 +544,7 @@ FastGeom fast_geom(int num_q, int num_kv, int sub_n, int n_keys, int base = kChu
 
 size_t qkv_decode_attn_tq3_workspace_bytes(int num_q, int num_kv, int sub_n, int n_keys) {
   if (num_q <= 0 || num_kv <= 0 || sub_n <= 0 || n_keys <= 0) return 0;
-  return fast_geom(num_q, num_kv, sub_n, n_keys, kChunkKeys, tq3_groups(num_q, num_kv, sub_n)).total;
+  return fast_geom(num_q, num_kv, sub_n, n_keys, kChunkKeys, tq3_groups(num_q, num_kv, sub_n), true).total;
 }
 
 // The TQ3 fast path with its workspace at `workspace` (caller-owned, or the
@@ -548,7 +560,7 @@ static int decode_tq3(const uint16_t* q, const qkv_block_tq3* k, const qkv_block
   if (!aligned(q, 16) || !aligned(k, 4) || !aligned(v, 4) || !aligned(out, 16))
     return QKV_ERR_ALIGN;
   const int n_keys = start_pos + sub_n;
-  const FastGeom g = fast_geom(num_q, num_kv, sub_n, n_keys, kChunkKeys, tq3_groups(num_q, num_kv, sub_n));
+  const FastGeom g = fast_geom(num_q, num_kv, sub_n, n_keys, kChunkKeys, tq3_groups(num_q, num_kv, sub_n), true);
   if (noalloc) {
     // no allocation: this device's scratch (looked up, and zero-filled on
     // `stream`, by the device's first qkv_tq3_init or first call here)
