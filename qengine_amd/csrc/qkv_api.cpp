@@ -540,11 +540,30 @@ FastGeom fast_geom(int num_q, int num_kv, int sub_n, int n_keys, int base = kChu
   g.total = g.o_off + rows * 256 * sizeof(float);
   return g;
 }
+
+// Workspace for every call over at most n_keys keys.  The record area is not
+// monotone in the key count: a longer context takes longer chunks, hence fewer
+// of them (16,384 Q8 keys: 128 chunks, 16,385: 65; a 16-query TQ3 verify over
+// 32,768 keys: 16, over 32,833: 13), so the size for n_keys alone can be less
+// than a shorter call needs.  The chunk count depends on the key count only
+// through whole 64-key tiles (base, every chunk and the joined tail are whole
+// tiles), so one evaluation per tile covers every count.
+size_t fast_ws_upto(int num_q, int num_kv, int sub_n, int n_keys, int base, int groups,
+                    bool join_tail) {
+  size_t best = 0;
+  for (long n = 64;; n += 64) {
+    const int nk = (int)std::min<long>(n, n_keys);
+    best = std::max(best, fast_geom(num_q, num_kv, sub_n, nk, base, groups, join_tail).total);
+    if (nk == n_keys) break;
+  }
+  return best;
+}
 }  // namespace
 
 size_t qkv_decode_attn_tq3_workspace_bytes(int num_q, int num_kv, int sub_n, int n_keys) {
   if (num_q <= 0 || num_kv <= 0 || sub_n <= 0 || n_keys <= 0) return 0;
-  return fast_geom(num_q, num_kv, sub_n, n_keys, kChunkKeys, tq3_groups(num_q, num_kv, sub_n), true).total;
+  return fast_ws_upto(num_q, num_kv, sub_n, n_keys, kChunkKeys, tq3_groups(num_q, num_kv, sub_n),
+                      true);
 }
 
 // The TQ3 fast path with its workspace at `workspace` (caller-owned, or the
@@ -625,7 +644,7 @@ int qkv_decode_attn_tq3_noalloc(const uint16_t* q, const qkv_block_tq3* k,
 
 size_t qkv_decode_attn_q8_workspace_bytes(int num_q, int num_kv, int sub_n, int n_keys) {
   if (num_q <= 0 || num_kv <= 0 || sub_n <= 0 || n_keys <= 0) return 0;
-  return fast_geom(num_q, num_kv, sub_n, n_keys, kChunkKeysQ8).total;
+  return fast_ws_upto(num_q, num_kv, sub_n, n_keys, kChunkKeysQ8, 0, false);
 }
 
 // Fast path over Q8_0 keys; values Q8_0 (v_tq3 false) or TQ3 (v_tq3 true).

@@ -122,17 +122,34 @@ def test_kv_move_tokens_argument_errors_without_gpu(L):
 
 def test_decode_workspace_for_the_longest_call_covers_shorter_ones(L):
     """The fast path's chunk size grows with the key count (one round of
-    workgroups), so its record area is not proportional to the length; a
-    workspace sized for the longest call must still cover every shorter one."""
-    for num_q, num_kv in [(16, 4), (24, 4), (16, 16), (8, 4), (32, 4)]:
-        for sub_n in (1, 4, 16):
-            for n_max in (4096, 40000, 131088, 262144):
-                top = L.qkv_decode_attn_tq3_workspace_bytes(num_q, num_kv, sub_n, n_max)
-                assert top > 0
-                for n in sorted({sub_n, 513, 4097, n_max // 3, n_max - 1, n_max}):
-                    if sub_n <= n <= n_max:
-                        assert L.qkv_decode_attn_tq3_workspace_bytes(num_q, num_kv, sub_n, n) <= top, \
-                            (num_q, num_kv, sub_n, n, n_max)
+    workgroups), so its record area is not monotone in the length (16,384 Q8
+    keys take 128 chunks, 16,385 take 65; a 16-query TQ3 verify over 32,768
+    keys takes 16, over 32,833 keys 13); a workspace sized for the longest call
+    must still cover every shorter one.  The chunk count moves only at whole
+    64-key tiles, so every tile boundary and the key after it are checked."""
+    queries = [L.qkv_decode_attn_tq3_workspace_bytes, L.qkv_decode_attn_q8_workspace_bytes]
+    for num_q, num_kv in [(16, 4), (24, 4), (16, 16), (8, 4)]:
+        for sub_n in (1, 16):
+            for query in queries:
+                for n_max in (16385, 32833, 40000):
+                    top = query(num_q, num_kv, sub_n, n_max)
+                    assert top > 0
+                    for n in range(64, n_max, 64):
+                        for m in (n, n + 1):
+                            if sub_n <= m <= n_max:
+                                assert query(num_q, num_kv, sub_n, m) <= top, \
+                                    (query.__name__, num_q, num_kv, sub_n, m, n_max)
+    # the sizes themselves: header 256 B, 16 B per record row rounded to
+    # 256 B, 1 KiB of fp32 output per record row; rows = queries x slots
+    def size(num_q, sub_n, slots):
+        rows = num_q * sub_n * slots
+        return 256 + ((rows * 16 + 255) & ~255) + rows * 1024
+    # 16 x 16-token verify over 32,768 keys: 16 chunks (of 4 tiles per wave);
+    # 32,833 keys take 13 chunks of 5, but a workspace for them still holds 16
+    assert L.qkv_decode_attn_tq3_workspace_bytes(16, 4, 16, 32768) == size(16, 16, 16)
+    assert L.qkv_decode_attn_tq3_workspace_bytes(16, 4, 16, 32833) == size(16, 16, 16)
+    assert L.qkv_decode_attn_q8_workspace_bytes(16, 4, 1, 16384) == size(16, 1, 128)
+    assert L.qkv_decode_attn_q8_workspace_bytes(16, 4, 1, 16385) == size(16, 1, 128)
 
 
 def test_mixed_decode_argument_errors_without_gpu(L):
