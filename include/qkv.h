@@ -283,13 +283,13 @@ size_t qkv_decode_attn_tq3_workspace_bytes(int num_q, int num_kv, int sub_n, int
 
 /* Fast path for the same computation as qkv_attn_split_tq3 + qkv_attn_split_merge
  * (model.cuh:2472-2491) in ONE launch: the key range is cut into chunks of
- * 512*k keys (the last one also takes a remainder of at most 64 keys when the
- * chunks are long), partials stay in rotated coordinates and are merged
- * inside the kernel (the last workgroups of the grid do the merge), and each
- * output row is rotated back once.  The queries of a multi-token call
- * (verify, sub_n > 1) share passes over the cache: 8/GQA per pass, or 16/GQA
- * when the call has more than 8/GQA.  out [sub_n][num_q][256] fp16
- * (16-byte aligned).
+ * 512*k keys (the last one may also take a remainder of at most 64 keys),
+ * partials stay in rotated coordinates and are merged inside the kernel (the
+ * last workgroups of the grid do the merge), and each output row is rotated
+ * back once.  The queries of a multi-token call (verify, sub_n > 1) share
+ * passes over the cache: up to 16 (query, head) columns per pass, and calls
+ * with more columns decode each tile once for up to 64 of them.
+ * out [sub_n][num_q][256] fp16 (16-byte aligned).
  * workspace: caller-owned device memory of at least
  * qkv_decode_attn_tq3_workspace_bytes() bytes, 256-byte aligned, ZERO-FILLED
  * before its first use; every completed call leaves it ready for the next

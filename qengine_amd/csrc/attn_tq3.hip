@@ -1020,6 +1020,464 @@ __global__ __launch_bounds__(kThreads, 1) void tq3_attn_kernel(QKV_ATTN_LEAD_PAR
 #endif
 }
 
+// ---- shared-decode multi-query fast path ----------------------------------
+// Calls with more than 16 (query, head) columns (a verify block, a tree
+// verify): tq3_attn_kernel<0, true> decodes every tile once per 16 columns,
+// and that decode (table-index shifts, code interleaves, table reads) is what
+// bounds it.  Here every 64-key tile is decoded ONCE per workgroup, by all 8
+// waves, into LDS as fp16 scaled centroids -- keys as rows [key][dim], values
+// as rows [dim][key] in the value MFMA's key order -- and four groups of two
+// waves run the MFMAs of up to 64 columns from there: wave w serves columns
+// 16 (w & 3) .. +15 over keys 32 (w >> 2) .. +31 of the tile.
+//   scores  v_mfma_f32_16x16x32_f16, A = 16 decoded keys x 32 dims (one
+//           16-byte LDS read per lane), B = the rotated query of the wave's
+//           16 columns as an fp16 rounding and its fp16 remainder (64 VGPRs),
+//           two products chained onto one accumulator per 128-block, each
+//           scaled by its key block norm.
+//   softmax online, per column, base 2 (the wave's 32 keys sit in 4 rows).
+//   values  v_mfma_f32_16x16x32_f16, A = p * value norm (the lane's own
+//           probabilities), B = 32 keys x 16 dims of decoded values.
+// The two waves of a column group merge in LDS and the merged rows become
+// records, merged across workgroups as in tq3_attn_kernel (attn_fastmerge.h).
+namespace mq {
+// Decoded tiles, XOR-swizzled in 16-byte chunks so that the MFMA operand reads
+// (16 lanes per LDS cycle: 16 rows at one logical chunk) and the decode's
+// stores hit 16 different bank groups (padded rows do not on this LDS):
+// key r's chunk c at c ^ (r & 15), dim d's chunk c at c ^ (d & 7).
+constexpr int kKRow = 512;      // decoded key row: 256 fp16
+constexpr int kVRow = 128;      // decoded value row (one dim): 64 fp16
+constexpr int kLdsK = kLdsLut + kLdsLutBytes;          // [64 keys][kKRow]
+constexpr int kLdsV = kLdsK + 64 * kKRow;              // [256 dims][kVRow]
+constexpr int kLdsNorm = kLdsV + 256 * kVRow;          // kn[2][64] (x softmax scale), vn[2][64] f32
+constexpr int kLdsCorr = kLdsNorm + 4 * 64 * 4;        // per wave: 16 rescale factors
+// the tile as loaded: key rows at 112 r, value rows at 112 r + 16 ((r >> 2) & 15)
+// (value rows 4 apart start in different bank groups: the value decode reads
+// rows 4kq + i for 16 kq at once)
+constexpr int kRawPitch = 112;
+constexpr int kLdsRawK = kLdsCorr + kWaves * 16 * 4;
+constexpr int kLdsRawV = kLdsRawK + 64 * kRawPitch;
+constexpr int kLdsEnd = kLdsRawV + 64 * kRawPitch + 16 * 16;
+// setup: the rotated query's fp16 rounding and remainder, [64 columns][kKRow]
+// each (swizzled as the keys), over the decoded tile areas (read into
+// registers before tile 0)
+constexpr int kLdsQhi = kLdsK;
+constexpr int kLdsQlo = kLdsK + 64 * kKRow;
+// after the tile loop: [8 waves][16 rows][kMoPitch floats], then m, l [8][16]
+constexpr int kMoPitch = 260;
+constexpr int kLdsMo = 0;
+constexpr int kLdsMl = kWaves * 16 * kMoPitch * 4;
+static_assert(kLdsQlo + 64 * kKRow <= kLdsNorm, "query scratch must fit the decoded tile areas");
+static_assert(kLdsMl + 2 * kWaves * 16 * 4 <= kLdsEnd, "merge area must fit");
+static_assert(kLdsMl >= kWaves * 128 * 4, "merger reduction area must not reach the merger scalars");
+static_assert(kLdsEnd <= 160 * 1024, "LDS");
+__device__ __forceinline__ int raw_v_row(int r) { return kLdsRawV + r * kRawPitch + 16 * ((r >> 2) & 15); }
+}  // namespace mq
+
+// One tile's rows as loaded: thread (row r = tid / 8, piece pc = tid % 8)
+// holds bytes 16 pc .. 16 pc + 15 of key row r and of value row r (piece 6:
+// bytes 96..103 used; piece 7 repeats piece 6 and is not stored).  Two wide
+// loads per thread and tile.
+struct MqRaw {
+  u4_t k, v;
+};
+
+__device__ __forceinline__ void mq_load(const AttnArgs& p, int ts, int nkv, int h, int tid, MqRaw& r) {
+  const uint64_t off0 = (uint64_t)(uint32_t)ts * (uint32_t)nkv * 104u;
+  const __amdgpu_buffer_rsrc_t rk = cache_rsrc(p.k, off0, p.kv_bytes);
+  const __amdgpu_buffer_rsrc_t rv = cache_rsrc(p.v, off0, p.kv_bytes);
+  const int row = tid >> 3, pc = min(tid & 7, 6);
+  const uint32_t off = (uint32_t)(row * nkv + h) * 104u + 16u * (uint32_t)pc;
+  r.k = __builtin_amdgcn_raw_buffer_load_b128(rk, off, 0, 0);
+  r.v = __builtin_amdgcn_raw_buffer_load_b128(rv, off, 0, 0);
+}
+
+__device__ __forceinline__ void mq_store_raw(uint8_t* lds, const MqRaw& r, int tid) {
+  const int row = tid >> 3, pc = tid & 7;
+  uint8_t* dk = lds + mq::kLdsRawK + row * mq::kRawPitch + 16 * pc;
+  uint8_t* dv = lds + mq::raw_v_row(row) + 16 * pc;
+  if (pc < 6) {
+    *reinterpret_cast<u4_t*>(dk) = r.k;
+    *reinterpret_cast<u4_t*>(dv) = r.v;
+  } else if (pc == 6) {
+    *reinterpret_cast<u2_t*>(dk) = u2_t{r.k[0], r.k[1]};
+    *reinterpret_cast<u2_t*>(dv) = u2_t{r.v[0], r.v[1]};
+  }
+}
+
+// Decode the staged tile into the LDS tile areas (every thread of the
+// workgroup; the caller orders it against the MFMA phase with barriers).
+// Key role: lane = key, wave = (block j = wave & 1, octet o = wave >> 1): code
+// groups 4o..4o+3 of block j.  Value role: keys 4kq..4kq+3 (kq = lane & 15),
+// code group g = 4 (wave >> 1) + (lane >> 4) of block j.
+__device__ __forceinline__ void mq_decode(uint8_t* lds, uint32_t lane4, int lane, int j, int o, int kq,
+                                          int g, float scale2) {
+  uint32_t ac[4] = {lane4, lane4, lane4, lane4};
+  // keys: row `lane`, dims 128j + 32o + 8U + 0..7 from code group 4o + U
+  {
+    const uint32_t* rk = reinterpret_cast<const uint32_t*>(lds + mq::kLdsRawK + lane * mq::kRawPitch + 52 * j);
+    const uint32_t q[3] = {rk[1 + 3 * o], rk[2 + 3 * o], rk[3 + 3 * o]};
+    const int kd = mq::kLdsK + lane * mq::kKRow + 256 * j + 16 * ((4 * o) ^ (lane & 15));   // chunk 4o + U at (4o + U) ^ (lane & 15)
+    const h8_t k0 = group_operand<0>(lds, ac, q);
+    const h8_t k1 = group_operand<1>(lds, ac, q);
+    const h8_t k2 = group_operand<2>(lds, ac, q);
+    const h8_t k3 = group_operand<3>(lds, ac, q);
+    *reinterpret_cast<h8_t*>(lds + (kd ^ 0)) = k0;
+    *reinterpret_cast<h8_t*>(lds + (kd ^ 16)) = k1;
+    *reinterpret_cast<h8_t*>(lds + (kd ^ 32)) = k2;
+    *reinterpret_cast<h8_t*>(lds + (kd ^ 48)) = k3;
+    if (o == 0) {   // waves 0 and 1: the block norms of key `lane`
+      const float* rv = reinterpret_cast<const float*>(lds + mq::raw_v_row(lane) + 52 * j);
+      float* nm = reinterpret_cast<float*>(lds + mq::kLdsNorm);
+      nm[64 * j + lane] = __uint_as_float(rk[0]) * scale2;
+      nm[128 + 64 * j + lane] = rv[0];
+    }
+  }
+  // values: keys 4kq..4kq+3 in dims 128j + 8g + 0..7; the codes of key pairs
+  // (4kq, 4kq+1) and (4kq+2, 4kq+3) interleaved per dim, so that each table
+  // entry is two keys at one dim
+  {
+    const int gb = 52 * j + 4 * ((4 + 3 * g) >> 2);   // dword holding the group's first byte
+    const uint32_t sh = (uint32_t)((4 + 3 * g) & 3);
+    uint32_t x[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      const uint32_t* rv = reinterpret_cast<const uint32_t*>(lds + mq::raw_v_row(4 * kq + i) + gb);
+      x[i] = __builtin_amdgcn_alignbyte(rv[1], rv[0], sh);
+    }
+    const uint32_t h0 = x[1] << 3, h1 = x[3] << 3;
+    const uint32_t ze0 = bit_select(kEvenDims, x[0], h0), zo0 = bit_select(kEvenDims << 3, x[0], h0);
+    const uint32_t ze1 = bit_select(kEvenDims, x[2], h1), zo1 = bit_select(kEvenDims << 3, x[2], h1);
+    // row (dim) e: keys of half H = kq >> 3 at bytes 64H + 16kb (+8 for the
+    // half's keys 16.. of unit kb), the order of the value MFMA's k index
+    const int kq7 = kq & 7;
+  // (dim 128j + 8g + e: chunk c at c ^ e)
+  const int vd = mq::kLdsV + (128 * j + 8 * g) * mq::kVRow + 16 * (4 * (kq >> 3) + (kq7 & 3)) + 8 * (kq7 >> 2);
+    uint32_t w[16];
+    w[0] = lut_read(lds, ac[0] = sdwa_index<0>(ac[0], ze0));
+    w[1] = lut_read(lds, ac[1] = sdwa_index<0>(ac[1], ze1));
+    w[2] = lut_read(lds, ac[2] = sdwa_index<3>(ac[2], zo0));
+    w[3] = lut_read(lds, ac[3] = sdwa_index<3>(ac[3], zo1));
+    w[4] = lut_read(lds, ac[0] = sdwa_index<6>(ac[0], ze0));
+    w[5] = lut_read(lds, ac[1] = sdwa_index<6>(ac[1], ze1));
+    w[6] = lut_read(lds, ac[2] = sdwa_index<9>(ac[2], zo0));
+    w[7] = lut_read(lds, ac[3] = sdwa_index<9>(ac[3], zo1));
+    w[8] = lut_read(lds, ac[0] = sdwa_index<12>(ac[0], ze0));
+    w[9] = lut_read(lds, ac[1] = sdwa_index<12>(ac[1], ze1));
+    w[10] = lut_read(lds, ac[2] = sdwa_index<15>(ac[2], zo0));
+    w[11] = lut_read(lds, ac[3] = sdwa_index<15>(ac[3], zo1));
+    w[12] = lut_read(lds, ac[0] = sdwa_index<18>(ac[0], ze0));
+    w[13] = lut_read(lds, ac[1] = sdwa_index<18>(ac[1], ze1));
+    w[14] = lut_read(lds, ac[2] = sdwa_index<21>(ac[2], zo0));
+    w[15] = lut_read(lds, ac[3] = sdwa_index<21>(ac[3], zo1));
+#pragma unroll
+    for (int e = 0; e < 8; e++)
+      *reinterpret_cast<u2_t*>(lds + (vd ^ (16 * e)) + mq::kVRow * e) = u2_t{w[2 * e], w[2 * e + 1]};
+  }
+}
+
+__global__ __launch_bounds__(kThreads, 1) void tq3_mq_kernel(QKV_ATTN_LEAD_PARAMS, AttnArgs pin,
+                                                              uint16_t* out) {
+  QKV_ATTN_LEAD_APPLY(p, pin);
+  __shared__ __attribute__((aligned(16))) uint8_t lds[mq::kLdsEnd];
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int gqa = __builtin_amdgcn_readfirstlane(p.num_q / p.num_kv);
+  // work id, XCD-aware as in tq3_attn_kernel: the num_kv workgroups of one
+  // (query block, chunk) share an XCD
+  int h, t0, chunk;
+  bool has_work;
+  {
+    const int L = blockIdx.x;
+    const int xcd = L & 7, r = L >> 3;
+    h = r % p.num_kv;
+    const int g = (r / p.num_kv) * 8 + xcd;
+    const int groups = (p.sub_n + p.qpw - 1) / p.qpw;
+    has_work = g < groups * p.n_chunks;
+    const int tq = has_work ? g / p.n_chunks : 0;
+    chunk = has_work ? g - tq * p.n_chunks : 0;
+    t0 = tq * p.qpw;
+  }
+  const int nq = min(p.qpw, p.sub_n - t0);
+  const int cols = __builtin_amdgcn_readfirstlane(nq * gqa);   // <= 64
+  // ---- query loads first: 128 WHTs of 128 (64 columns x 2 blocks), 16 lanes
+  // each, four per thread
+  const int q_part = tid & 15;
+  u4_t q_raw[4];
+  {
+    const uint32_t q_extent = (uint32_t)(p.sub_n * p.num_q * kHD * 2);
+    const __amdgpu_buffer_rsrc_t rq =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(p.q), 0, q_extent, kBufferRsrcWord3);
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      const int wi = (tid >> 4) + 32 * i, c = wi >> 1, jb = wi & 1;
+      const uint32_t qoff = c < cols ? (uint32_t)((((t0 + c / gqa) * p.num_q + h * gqa + c % gqa) * kHD +
+                                                   jb * 128 + q_part * 8) * 2)
+                                     : q_extent;
+      q_raw[i] = __builtin_amdgcn_raw_buffer_load_b128(rq, qoff, 0, 0);
+    }
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  // ---- key range of the workgroup and of this lane's column
+  const int grp = wave & 3, half = wave >> 2;   // MFMA role: columns 16 grp.., keys 32 half.. of a tile
+  const int n = lane & 15, kb = lane >> 4;
+  const int col = 16 * grp + n;
+  const int t_col = t0 + min(col / gqa, nq - 1);
+  const int active_end = p.start_pos + t_col + 1;
+  const int active_first = p.start_pos + t0 + 1;
+  const int active_last = p.start_pos + t0 + nq;
+  int lo = 0, hi = 0, hi_col = 0, hi_first = 0;
+  if (has_work) {
+    lo = chunk * p.chunk_keys;
+    // the last chunk runs to the end of the keys (the host may have joined a
+    // remainder of at most one tile to it)
+    const int c_end = chunk == p.n_chunks - 1 ? active_last : lo + p.chunk_keys;
+    hi = min(c_end, active_last);
+    hi_col = min(c_end, active_end);
+    hi_first = min(c_end, active_first);
+  }
+  lo = __builtin_amdgcn_readfirstlane(lo);
+  hi = __builtin_amdgcn_readfirstlane(hi);
+  hi_first = __builtin_amdgcn_readfirstlane(hi_first);
+  // decode roles
+  const int dj = wave & 1, dof = wave >> 1;              // keys: block, octet
+  const int kq = lane & 15, vg = 4 * (wave >> 1) + (lane >> 4);   // values: key quad, code group
+  // tiles of the chunk; rows loaded two tiles ahead of their decode
+  const int n_tiles = hi > lo ? (hi - lo + kTile - 1) / kTile : 0;
+  MqRaw ra, rb;
+  if (n_tiles > 0) mq_load(p, lo, p.num_kv, h, tid, ra);
+  if (n_tiles > 1) mq_load(p, lo + kTile, p.num_kv, h, tid, rb);
+  // ---- setup: centroid-pair table (as tq3_attn_kernel), rotated query
+  const uint32_t lane4 = 4u * (uint32_t)lane;
+  {
+    const uint32_t w = (uint32_t)wave;
+#pragma unroll
+    for (int hk = 0; hk < 4; hk++) {
+      const uint32_t hv = centroid_scaled_h((4u * w + hk) & 7u) << 16;
+#pragma unroll
+      for (int k = 0; k < 8; k++)
+        *reinterpret_cast<uint32_t*>(lds + kLdsLut + (w * 32 + hk * 8 + k) * 256 + lane4) =
+            centroid_scaled_h(k) | hv;
+    }
+  }
+  {
+    const uint32_t sbits = sign_word_sel(q_part >> 2) >> (8 * (q_part & 3));   // elements part*8..+7
+    const float rs = wht_scale();
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      const int wi = (tid >> 4) + 32 * i, c = wi >> 1, jb = wi & 1;
+      float x[8];
+#pragma unroll
+      for (int e = 0; e < 4; e++) {
+        x[2 * e] = h2f(q_raw[i][e] & 0xffffu);
+        x[2 * e + 1] = h2f(q_raw[i][e] >> 16);
+      }
+#pragma unroll
+      for (int e = 0; e < 8; e++) x[e] = ((sbits >> e) & 1u) ? x[e] : -x[e];
+      wht8_inreg(x);
+      wht_xor_lanes16(x, lane);
+      uint32_t pk[4], pl[4];
+#pragma unroll
+      for (int e = 0; e < 4; e++) {
+        const float a = x[2 * e] * rs, b = x[2 * e + 1] * rs;
+        const uint32_t ha = f2h(a), hb = f2h(b);
+        pk[e] = ha | (hb << 16);
+        pl[e] = f2h(a - h2f(ha)) | (f2h(b - h2f(hb)) << 16);
+      }
+      const int qb = c * mq::kKRow + 256 * jb + 16 * (q_part ^ (c & 15));
+      *reinterpret_cast<uint4*>(lds + mq::kLdsQhi + qb) = make_uint4(pk[0], pk[1], pk[2], pk[3]);
+      *reinterpret_cast<uint4*>(lds + mq::kLdsQlo + qb) = make_uint4(pl[0], pl[1], pl[2], pl[3]);
+    }
+  }
+  if (n_tiles > 0) {   // tile 0 staged; its registers take tile 2
+    mq_store_raw(lds, ra, tid);
+    if (n_tiles > 2) mq_load(p, lo + 2 * kTile, p.num_kv, h, tid, ra);
+  }
+  __syncthreads();
+  // qa[s] / ql[s]: column `col`, dims 32s + 8kb .. +7 (B operand of slice s)
+  h8_t qa[8], ql[8];
+#pragma unroll
+  for (int s = 0; s < 8; s++) {
+    qa[s] = *reinterpret_cast<const h8_t*>(lds + ((mq::kLdsQhi + col * mq::kKRow + 16 * (kb ^ n)) ^ (64 * s)));
+    ql[s] = *reinterpret_cast<const h8_t*>(lds + ((mq::kLdsQlo + col * mq::kKRow + 16 * (kb ^ n)) ^ (64 * s)));
+  }
+  const KeyRule rule(p.start_pos, t_col, p.sink_tok, p.window_tok, p.tree_mask);
+  const bool live = 16 * grp < cols;   // wave-uniform: the group holds columns
+  const float scale2 = p.scale_log2 * kCenScaleInv;
+  float m2 = -INFINITY, lsum = 0.0f;
+  f4_t acc[16];
+#pragma unroll
+  for (int t = 0; t < 16; t++) acc[t] = f4_t{0.f, 0.f, 0.f, 0.f};
+  const float* nm = reinterpret_cast<const float*>(lds + mq::kLdsNorm);
+  float* corr_w = reinterpret_cast<float*>(lds + mq::kLdsCorr) + 16 * wave;
+  __syncthreads();   // the query scratch is read: the tile areas are free
+
+  // Tile t: decode the staged rows; then stage tile t + 1 (its registers take
+  // tile t + 3) while the MFMAs of tile t run.  The loop is unrolled by two so
+  // that the two register sets stay fixed registers.
+  auto tile_step = [&](int t, MqRaw& nxt) {
+    const int ts = lo + t * kTile;
+    mq_decode(lds, lane4, lane, dj, dof, kq, vg, scale2);
+    __syncthreads();
+    if (t + 1 < n_tiles) {
+      mq_store_raw(lds, nxt, tid);
+      if (t + 3 < n_tiles) mq_load(p, ts + 3 * kTile, p.num_kv, h, tid, nxt);
+    }
+    if (live) {
+      // ---- scores: D rows = keys 32 half + 16 mb + 4 kb + r, column `col`
+      f4_t sa[2][2];
+#pragma unroll
+      for (int mb = 0; mb < 2; mb++) sa[mb][0] = sa[mb][1] = f4_t{0.f, 0.f, 0.f, 0.f};
+      const int kbase = mq::kLdsK + (32 * half + n) * mq::kKRow + 16 * (kb ^ n);   // key 32 half + 16 mb + n, chunk (4s + kb) ^ n
+      // operand reads two slices ahead of their MFMAs (three rotating buffers)
+      h8_t ka[3][2];
+#pragma unroll
+      for (int s = 0; s < 2; s++)
+#pragma unroll
+        for (int mb = 0; mb < 2; mb++)
+          ka[s][mb] = *reinterpret_cast<const h8_t*>(lds + (kbase ^ (64 * s)) + 16 * mb * mq::kKRow);
+#pragma unroll
+      for (int s = 0; s < 8; s++) {
+        if (s + 2 < 8) {
+#pragma unroll
+          for (int mb = 0; mb < 2; mb++)
+            ka[(s + 2) % 3][mb] = *reinterpret_cast<const h8_t*>(lds + (kbase ^ (64 * (s + 2))) + 16 * mb * mq::kKRow);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int mb = 0; mb < 2; mb++) {
+          sa[mb][s >> 2] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka[s % 3][mb], qa[s], sa[mb][s >> 2], 0, 0, 0);
+          sa[mb][s >> 2] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka[s % 3][mb], ql[s], sa[mb][s >> 2], 0, 0, 0);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+      }
+      const bool dense = ts + kTile <= hi_first && rule.all_visible(ts + kTile);
+      float sc[2][4];
+#pragma unroll
+      for (int mb = 0; mb < 2; mb++) {
+        const int k0 = 32 * half + 16 * mb + 4 * kb;
+        const f4_t n0 = *reinterpret_cast<const f4_t*>(nm + k0);
+        const f4_t n1 = *reinterpret_cast<const f4_t*>(nm + 64 + k0);
+#pragma unroll
+        for (int r = 0; r < 4; r++) sc[mb][r] = n0[r] * sa[mb][0][r] + n1[r] * sa[mb][1][r];
+      }
+      if (!dense) {
+#pragma unroll
+        for (int mb = 0; mb < 2; mb++)
+#pragma unroll
+          for (int r = 0; r < 4; r++) {
+            const int key = ts + 32 * half + 16 * mb + 4 * kb + r;
+            const bool vis = (key < hi_col) & rule.visible(key, active_end);
+            sc[mb][r] = vis ? sc[mb][r] : -INFINITY;
+          }
+      }
+      // ---- online softmax of column `col` (its 32 keys sit in the 4 rows)
+      float mt = sc[0][0];
+#pragma unroll
+      for (int mb = 0; mb < 2; mb++)
+#pragma unroll
+        for (int r = 0; r < 4; r++) mt = fmaxf(mt, sc[mb][r]);
+      mt = xrow_max(mt);
+      const float mn = fmaxf(m2, mt);
+      const float msafe = (mn == -INFINITY) ? 0.0f : mn;
+      const float corr = __builtin_amdgcn_exp2f(m2 - msafe);
+      float ps = 0.0f;
+#pragma unroll
+      for (int mb = 0; mb < 2; mb++)
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+          sc[mb][r] = __builtin_amdgcn_exp2f(sc[mb][r] - msafe);
+          ps += sc[mb][r];
+        }
+      lsum = lsum * corr + ps;
+      m2 = mn;
+      // accumulator rows are columns 16 grp + 4 kb + r: their factors come
+      // from the lanes of those columns
+      if (__builtin_amdgcn_ballot_w64(corr != 1.0f) != 0) {
+      if (kb == 0) corr_w[n] = corr;
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+      const f4_t cr = *reinterpret_cast<const f4_t*>(corr_w + 4 * kb);
+#pragma unroll
+      for (int t = 0; t < 16; t++)
+#pragma unroll
+        for (int r = 0; r < 4; r++) acc[t][r] *= cr[r];
+      }
+      // ---- values: A = p * value norm per 128-block, B = 32 keys x 16 dims
+      h8_t pa[2];
+#pragma unroll
+      for (int mb = 0; mb < 2; mb++) {
+        const int k0 = 32 * half + 16 * mb + 4 * kb;
+        const f4_t v0 = *reinterpret_cast<const f4_t*>(nm + 128 + k0);
+        const f4_t v1 = *reinterpret_cast<const f4_t*>(nm + 192 + k0);
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+          pa[0][4 * mb + r] = (_Float16)(sc[mb][r] * v0[r]);
+          pa[1][4 * mb + r] = (_Float16)(sc[mb][r] * v1[r]);
+        }
+      }
+      const uint8_t* vbase = lds + mq::kLdsV + n * mq::kVRow + 16 * ((4 * half + kb) ^ (n & 7));   // dim 16t + n
+      // operand reads four MFMAs ahead (five rotating buffers)
+      h8_t vb[5];
+#pragma unroll
+      for (int t = 0; t < 4; t++) vb[t] = *reinterpret_cast<const h8_t*>(vbase + 16 * t * mq::kVRow);
+#pragma unroll
+      for (int t = 0; t < 16; t++) {
+        if (t + 4 < 16) vb[(t + 4) % 5] = *reinterpret_cast<const h8_t*>(vbase + 16 * (t + 4) * mq::kVRow);
+        __builtin_amdgcn_sched_barrier(0);
+        acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pa[t >> 3], vb[t % 5], acc[t], 0, 0, 0);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    }
+    __syncthreads();   // the tile areas are read and tile t + 1 is staged
+  };
+  for (int t = 0; t < n_tiles; t += 2) {
+    tile_step(t, rb);
+    if (t + 1 < n_tiles) tile_step(t + 1, ra);
+  }
+  lsum = xrow_sum(lsum);
+
+  // ---- merge the two waves of each column group in LDS ----------------
+  float* mo = reinterpret_cast<float*>(lds + mq::kLdsMo);
+  float* ml = reinterpret_cast<float*>(lds + mq::kLdsMl);
+  if (live) {
+    // acc tile t: rows (columns) 4 kb + r of the group, dims 16t + n
+#pragma unroll
+    for (int r = 0; r < 4; r++)
+#pragma unroll
+      for (int t = 0; t < 16; t++) mo[(wave * 16 + 4 * kb + r) * mq::kMoPitch + 16 * t + n] = acc[t][r];
+    if (kb == 0) {
+      ml[wave * 16 + n] = m2;
+      ml[kWaves * 16 + wave * 16 + n] = lsum;
+    }
+  }
+  __syncthreads();
+  const __amdgpu_buffer_rsrc_t rml = __builtin_amdgcn_make_buffer_rsrc(p.ws_ml, 0, p.ws_ml_bytes, kBufferRsrcWord3);
+  const __amdgpu_buffer_rsrc_t ro = __builtin_amdgcn_make_buffer_rsrc(p.ws_o, 0, p.ws_o_bytes, kBufferRsrcWord3);
+  int gqa_m = gqa;
+  asm volatile("" : "+s"(gqa_m));
+  if (has_work) {
+    for (int idx = tid; idx < cols * 64; idx += kThreads) {
+      const int R = idx >> 6, d4 = (idx & 63) * 4;
+      const int wa = R >> 4, wb = wa + 4, rr = R & 15;
+      const float ma = ml[wa * 16 + rr], mb2 = ml[wb * 16 + rr];
+      const float M = fmaxf(ma, mb2);
+      const float fa = (ma == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(ma - M);
+      const float fb = (mb2 == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(mb2 - M);
+      const float Lr = fa * ml[kWaves * 16 + wa * 16 + rr] + fb * ml[kWaves * 16 + wb * 16 + rr];
+      const f4_t oa = *reinterpret_cast<const f4_t*>(mo + (wa * 16 + rr) * mq::kMoPitch + d4);
+      const f4_t ob = *reinterpret_cast<const f4_t*>(mo + (wb * 16 + rr) * mq::kMoPitch + d4);
+      store_record_piece(p, rml, ro, h * gqa_m + R % gqa_m, t0 + R / gqa_m, chunk, d4, fa * oa + fb * ob, M, Lr);
+    }
+    publish_records(p, rml, h, gqa_m, t0, cols, chunk);
+  } else {
+    __syncthreads();   // (the barrier publish_records passes, so that mo is free for the mergers)
+  }
+  merge_phase<kThreads, true>(reinterpret_cast<float*>(lds + mq::kLdsMo),
+                              reinterpret_cast<f2_t*>(lds + mq::kLdsMl), p, rml, ro, out);
+}
+
 size_t tq3_attn_lds_bytes() { return kLdsTotal; }
 
 #ifdef QKV_PHASE_TRACE
@@ -1072,7 +1530,9 @@ hipError_t launch_tq3_attn(const AttnArgs& a, int mode, uint16_t* out, hipStream
   const int groups = (a.sub_n + a.qpw - 1) / a.qpw * a.n_chunks;
   const int n_wg = ((groups + 7) / 8) * 8 * a.num_kv;
   dim3 grid(n_wg), block(kThreads);
-  if (mode == 0 && a.qpw * (a.num_q / a.num_kv) > 8)
+  if (mode == 0 && a.qpw * (a.num_q / a.num_kv) > 16)
+    hipLaunchKernelGGL(tq3_mq_kernel, grid, block, 0, stream, QKV_ATTN_LEAD_ARGS(a), a, out);
+  else if (mode == 0 && a.qpw * (a.num_q / a.num_kv) > 8)
     hipLaunchKernelGGL((tq3_attn_kernel<0, true>), grid, block, 0, stream, QKV_ATTN_LEAD_ARGS(a), a, out);
   else if (mode == 0)
     hipLaunchKernelGGL((tq3_attn_kernel<0>), grid, block, 0, stream, QKV_ATTN_LEAD_ARGS(a), a, out);

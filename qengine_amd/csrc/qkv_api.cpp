@@ -497,6 +497,9 @@ struct FastGeom {
 // workgroup's MFMA columns).
 int tq3_fast_qpw(int num_q, int num_kv, int sub_n) {
   const int gqa = num_q / num_kv;
+  // more than 16 (query, head) columns: up to 64 columns per workgroup, every
+  // tile decoded once for all of them (tq3_mq_kernel)
+  if (sub_n * gqa > 16) return std::min(sub_n, 64 / gqa);
   // one query group of rounded queries + remainders in the 16 MFMA columns, or,
   // when the call has more queries than that, 16 / GQA queries per group with
   // the remainders in a chained product (tq3_attn_kernel<0, true>)
@@ -506,22 +509,30 @@ int tq3_groups(int num_q, int num_kv, int sub_n) {
   const int qpw = tq3_fast_qpw(num_q, num_kv, sub_n);
   return (sub_n + qpw - 1) / qpw;
 }
+// Chunk size (in 512-key steps) from which a contiguous TQ3 launch joins a
+// last chunk of at most one 64-key tile to the previous chunk (its kernel runs
+// the last chunk to the end of the keys).  tq3_attn_kernel spreads a chunk
+// over its 8 waves, so the join pays from 4 tiles per wave on (one wave takes
+// one more tile instead of every wave one more round: a 16-token verify over
+// 131,072 + 16 keys, 16 chunks of 16 tiles per wave and a 16-key tile, not 16
+// chunks of 17); tq3_mq_kernel runs a chunk's tiles one after another with all
+// of its waves, so one more tile never costs a round (32,768 + 16 keys: 64
+// chunks of 8 tiles, one with a ninth, not 33 chunks on half of the GPU).
+int tq3_join_min(int num_q, int num_kv, int sub_n) {
+  return sub_n * (num_q / num_kv) > 16 ? 1 : 4;
+}
 
 FastGeom fast_geom(int num_q, int num_kv, int sub_n, int n_keys, int base = kChunkKeys,
-                   int groups = 0, bool join_tail = false) {
+                   int groups = 0, int join_min = 0) {
   FastGeom g{};
   const int cb = (n_keys + base - 1) / base;
   int tpw = (cb + 127) / 128;
-  // chunks of base * t keys; with join_tail (a contiguous TQ3 launch, whose
-  // kernel runs its last chunk to the end of the keys) a last chunk of at most
-  // one 64-key tile joins the previous one when the chunks hold >= 4 tiles per
-  // wave: one wave then takes one more tile instead of every wave one more
-  // round (a 16-token verify over 131,072 + 16 keys: 16 chunks of 16 tiles per
-  // wave and one 16-key tile, not 16 chunks of 17)
+  // chunks of base * t keys; from t = join_min on (0: never) a last chunk of
+  // at most one 64-key tile joins the previous one (tq3_join_min)
   auto chunks = [&](int t) {
     const long ck = (long)base * t;
     int n = (int)((n_keys + ck - 1) / ck);
-    if (join_tail && n > 1 && t >= 4 && n_keys - (n - 1) * ck <= 64) n--;
+    if (join_min > 0 && n > 1 && t >= join_min && n_keys - (n - 1) * ck <= 64) n--;
     return n;
   };
   // Long contexts and many queries: grow the chunks until the launch fits one
@@ -549,11 +560,11 @@ FastGeom fast_geom(int num_q, int num_kv, int sub_n, int n_keys, int base = kChu
 // through whole 64-key tiles (base, every chunk and the joined tail are whole
 // tiles), so one evaluation per tile covers every count.
 size_t fast_ws_upto(int num_q, int num_kv, int sub_n, int n_keys, int base, int groups,
-                    bool join_tail) {
+                    int join_min) {
   size_t best = 0;
   for (long n = 64;; n += 64) {
     const int nk = (int)std::min<long>(n, n_keys);
-    best = std::max(best, fast_geom(num_q, num_kv, sub_n, nk, base, groups, join_tail).total);
+    best = std::max(best, fast_geom(num_q, num_kv, sub_n, nk, base, groups, join_min).total);
     if (nk == n_keys) break;
   }
   return best;
@@ -563,7 +574,7 @@ size_t fast_ws_upto(int num_q, int num_kv, int sub_n, int n_keys, int base, int 
 size_t qkv_decode_attn_tq3_workspace_bytes(int num_q, int num_kv, int sub_n, int n_keys) {
   if (num_q <= 0 || num_kv <= 0 || sub_n <= 0 || n_keys <= 0) return 0;
   return fast_ws_upto(num_q, num_kv, sub_n, n_keys, kChunkKeys, tq3_groups(num_q, num_kv, sub_n),
-                      true);
+                      tq3_join_min(num_q, num_kv, sub_n));
 }
 
 // The TQ3 fast path with its workspace at `workspace` (caller-owned, or the
@@ -579,7 +590,8 @@ static int decode_tq3(const uint16_t* q, const qkv_block_tq3* k, const qkv_block
   if (!aligned(q, 16) || !aligned(k, 4) || !aligned(v, 4) || !aligned(out, 16))
     return QKV_ERR_ALIGN;
   const int n_keys = start_pos + sub_n;
-  const FastGeom g = fast_geom(num_q, num_kv, sub_n, n_keys, kChunkKeys, tq3_groups(num_q, num_kv, sub_n), true);
+  const FastGeom g = fast_geom(num_q, num_kv, sub_n, n_keys, kChunkKeys, tq3_groups(num_q, num_kv, sub_n),
+                               tq3_join_min(num_q, num_kv, sub_n));
   if (noalloc) {
     // no allocation: this device's scratch (looked up, and zero-filled on
     // `stream`, by the device's first qkv_tq3_init or first call here)
@@ -644,7 +656,7 @@ int qkv_decode_attn_tq3_noalloc(const uint16_t* q, const qkv_block_tq3* k,
 
 size_t qkv_decode_attn_q8_workspace_bytes(int num_q, int num_kv, int sub_n, int n_keys) {
   if (num_q <= 0 || num_kv <= 0 || sub_n <= 0 || n_keys <= 0) return 0;
-  return fast_ws_upto(num_q, num_kv, sub_n, n_keys, kChunkKeysQ8, 0, false);
+  return fast_ws_upto(num_q, num_kv, sub_n, n_keys, kChunkKeysQ8, 0, 0);
 }
 
 // Fast path over Q8_0 keys; values Q8_0 (v_tq3 false) or TQ3 (v_tq3 true).

@@ -123,15 +123,16 @@ def test_kv_move_tokens_argument_errors_without_gpu(L):
 def test_decode_workspace_for_the_longest_call_covers_shorter_ones(L):
     """The fast path's chunk size grows with the key count (one round of
     workgroups), so its record area is not monotone in the length (16,384 Q8
-    keys take 128 chunks, 16,385 take 65; a 16-query TQ3 verify over 32,768
-    keys takes 16, over 32,833 keys 13); a workspace sized for the longest call
-    must still cover every shorter one.  The chunk count moves only at whole
-    64-key tiles, so every tile boundary and the key after it are checked."""
+    keys take 128 chunks, 16,385 take 65; one TQ3 query over 65,536 keys takes
+    64, over 65,537 keys 43; a 16-query TQ3 verify over 32,768 keys 64, over
+    32,833 keys 33); a workspace sized for the longest call must still cover
+    every shorter one.  The chunk count moves only at whole 64-key tiles, so
+    every tile boundary and the key after it are checked."""
     queries = [L.qkv_decode_attn_tq3_workspace_bytes, L.qkv_decode_attn_q8_workspace_bytes]
     for num_q, num_kv in [(16, 4), (24, 4), (16, 16), (8, 4)]:
         for sub_n in (1, 16):
             for query in queries:
-                for n_max in (16385, 32833, 40000):
+                for n_max in (16385, 32833, 40000, 65537):
                     top = query(num_q, num_kv, sub_n, n_max)
                     assert top > 0
                     for n in range(64, n_max, 64):
@@ -144,10 +145,15 @@ def test_decode_workspace_for_the_longest_call_covers_shorter_ones(L):
     def size(num_q, sub_n, slots):
         rows = num_q * sub_n * slots
         return 256 + ((rows * 16 + 255) & ~255) + rows * 1024
-    # 16 x 16-token verify over 32,768 keys: 16 chunks (of 4 tiles per wave);
-    # 32,833 keys take 13 chunks of 5, but a workspace for them still holds 16
-    assert L.qkv_decode_attn_tq3_workspace_bytes(16, 4, 16, 32768) == size(16, 16, 16)
-    assert L.qkv_decode_attn_tq3_workspace_bytes(16, 4, 16, 32833) == size(16, 16, 16)
+    # one query over 65,536 keys: 64 chunks of 1,024; 65,537 keys take 43
+    # chunks of 1,536, but a workspace for them still holds 64
+    assert L.qkv_decode_attn_tq3_workspace_bytes(16, 4, 1, 65536) == size(16, 1, 64)
+    assert L.qkv_decode_attn_tq3_workspace_bytes(16, 4, 1, 65537) == size(16, 1, 64)
+    # 16-token verify (64 query-head columns, one workgroup per chunk): 32,768
+    # keys and 32,784 (a last 16-key tile joined) take 64 chunks of 512 keys;
+    # 32,833 keys take 33 chunks of 1,024, and a workspace for them holds 64
+    for n in (32768, 32784, 32833):
+        assert L.qkv_decode_attn_tq3_workspace_bytes(16, 4, 16, n) == size(16, 16, 64)
     assert L.qkv_decode_attn_q8_workspace_bytes(16, 4, 1, 16384) == size(16, 1, 128)
     assert L.qkv_decode_attn_q8_workspace_bytes(16, 4, 1, 16385) == size(16, 1, 128)
 

@@ -132,21 +132,23 @@ def test_fast_decode_vs_oracle(dev, n, num_q, sub_n):
     (900, 8, 11, 0, 0, True), (700, 4, 17, 0, 0, False), (20016, 16, 16, 0, 0, False),
     (800, 32, 3, 0, 0, True), (2500, 24, 2, 16, 512, False), (600, 16, 3, 0, 0, False),
     (900, 12, 7, 0, 0, True), (700, 20, 4, 0, 0, False), (650, 28, 3, 0, 0, True),
+    # more than 64 columns: several query blocks per call (64 + 16, 60 + 36, 64 + 2)
+    (3000, 16, 20, 0, 0, False), (2500, 24, 16, 0, 0, True), (1800, 8, 33, 0, 0, False),
     # chunks grown to keep one round of workgroups: 2 and 3 tiles per wave
     (40000, 16, 1, 0, 0, False), (70000, 24, 1, 0, 0, False), (40000, 16, 2, 128, 2048, True),
-    # 16 chunks of 4 tiles per wave, the last also taking the remainder past
-    # 32768 keys (16, 32 and 64 keys: joined; 65 keys: its own chunk, 13 chunks)
-    pytest.param(32784, 16, 16, 0, 0, False, marks=pytest.mark.xfail(strict=True, reason=(
-        "reference-order leg: on this draw the reference's split-K order lies 1.73e-3 from exact "
-        "attention and the kernel 1.01e-3 (per-row bar met), the two 2.10e-3 apart (bar 2e-3); "
-        "the same before the tail join"))),
+    # 16 queries x GQA 4 = 64 columns, every tile decoded once (tq3_mq_kernel):
+    # 64 chunks of 512 keys, the last also taking the remainder past 32768
+    # keys (16, 32 and 64 keys: joined; 65 keys: 33 chunks of 1024)
+    (32784, 16, 16, 0, 0, False),
     (32800, 16, 16, 0, 0, False), (32832, 16, 16, 0, 0, True), (32833, 16, 16, 0, 0, False)])
 def test_fast_decode_multi_query(dev, n, num_q, sub_n, sink, window, tree):
     """Several queries per workgroup (they share the MFMA columns): partial
     last groups, GQA 1 to 8, causal, tree and sink/window masks; calls
     with at most 8 / GQA queries carry rounded query and remainder in one
-    product, larger ones take 16 / GQA queries per workgroup with the
-    remainders in a chained product."""
+    product, up to 16 / GQA queries the remainders ride in a chained product,
+    and calls with more than 16 (query, head) columns decode each tile once
+    for up to 64 of them (tq3_mq_kernel; GQA 4 x 16 queries, GQA 2 x 11,
+    GQA 1 x 17, GQA 8 x 3, partial column groups, several query blocks)."""
     from qengine_amd import kvcache
     torch = _torch()
     num_kv = 4
