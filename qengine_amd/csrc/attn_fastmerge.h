@@ -357,4 +357,188 @@ __device__ void merge_phase(float* red, f2_t* mls, const AttnArgs& p, __amdgpu_b
   }
 }
 
+// ---- two units at once --------------------------------------------------
+// Mergers with two or more units (a multi-query call: 512 units of the
+// 16-token verify over 256 mergers) take them two at a time, one per half of
+// the workgroup: each half polls, loads and folds its own unit with reduction
+// and scalar areas of its own, and both halves pass the same barriers.
+struct MergeUnit {
+  long base;
+  int n, qh, t, blk;
+  bool valid;
+};
+
+template <int THREADS, bool ROTATE>
+__device__ void merge_unit_pair(float* red_all, f2_t* mls_all, const AttnArgs& p, __amdgpu_buffer_rsrc_t rml,
+                                __amdgpu_buffer_rsrc_t ro, const MergeUnit& u0, const MergeUnit& u1,
+                                uint16_t* out) {
+  constexpr int kTU = THREADS / 2;   // threads per unit (whole waves)
+  using ML = MergeLayout<kTU>;
+  constexpr int kSlices = ML::kSlices, kRecPerThread = ML::kRecPerThread, kWaves = ML::kWaves;
+  constexpr int kHD = 256;
+  const bool second = (int)threadIdx.x >= kTU;
+  // (selects, not an indexed pair: an indexed array of two units goes to scratch)
+  const bool valid = second ? u1.valid : u0.valid;
+  const long base = second ? u1.base : u0.base;
+  const int n = valid ? (second ? u1.n : u0.n) : 0;
+  const int qh = second ? u1.qh : u0.qh, t = second ? u1.t : u0.t, blk = second ? u1.blk : u0.blk;
+  float* red = red_all + (second ? ML::kRedFloats : 0);
+  f2_t* mls = mls_all + (second ? 128 : 0);
+  const int tid = (int)threadIdx.x - (second ? kTU : 0);
+  const int lane = tid & 63, wave = tid >> 6;
+  const int sl = tid >> 5, dq = tid & 31;
+  bool seen = tid >= n;
+  bool all0 = false, all1 = false;
+  int* slots = reinterpret_cast<int*>(red_all);   // (free until the rows are folded: it holds the vote)
+  for (int spins = 0; spins < p.spin_limit; spins++) {
+    if (!seen) {
+      const f4_t r = __builtin_amdgcn_raw_buffer_load_b128(
+          rml, (uint32_t)((base + tid) * kRecMlBytes), 0, kCoherent);
+      if (__float_as_uint(blk ? r[3] : r[2]) == kTagValid) {
+        seen = true;
+        mls[tid] = f2_t{r[0], r[1]};
+      }
+    }
+    const bool wave_all = __builtin_amdgcn_ballot_w64(!seen) == 0;
+    __syncthreads();   // the previous use of the slots is over
+    if ((threadIdx.x & 63) == 0) slots[threadIdx.x >> 6] = wave_all ? 1 : 0;
+    __syncthreads();
+    all0 = all1 = true;
+#pragma unroll
+    for (int w = 0; w < kWaves; w++) {
+      all0 = all0 && slots[w] != 0;
+      all1 = all1 && slots[kWaves + w] != 0;
+    }
+    if (all0 && all1) break;
+    __builtin_amdgcn_s_sleep(1);
+  }
+  const bool complete = second ? all1 : all0;
+  if (!complete) {
+    if (tid < n && seen)   // the tags this merger saw will not be read again
+      __builtin_amdgcn_raw_buffer_store_b32(0u, rml, (uint32_t)((base + tid) * kRecMlBytes + 8 + 4 * blk),
+                                            0, kCoherent);
+    if (valid && tid < 16)
+      *reinterpret_cast<uint4*>(out + ((long)t * p.num_q + qh) * 256 + blk * 128 + tid * 8) =
+          make_uint4(0x7e007e00u, 0x7e007e00u, 0x7e007e00u, 0x7e007e00u);
+    if (tid == 0)
+      __hip_atomic_store(p.ws_header + kWsErrorWord, kWsErrorTimeout, __ATOMIC_RELAXED,
+                         __HIP_MEMORY_SCOPE_AGENT);
+  } else if (tid < n) {   // this unit has seen its records: clear their tags for the next launch
+    __builtin_amdgcn_raw_buffer_store_b32(0u, rml, (uint32_t)((base + tid) * kRecMlBytes + 8 + 4 * blk), 0,
+                                          kCoherent);
+  }
+  const int nr = complete ? n : 0;   // a timed-out half folds nothing (it passes the barrier below)
+  f4_t v[kRecPerThread];
+#pragma unroll
+  for (int i = 0; i < kRecPerThread; i++) {
+    const int c = sl + kSlices * i;
+    v[i] = c < nr ? __builtin_amdgcn_raw_buffer_load_b128(
+                        ro, (uint32_t)(((base + c) * kHD + blk * 128 + 4 * dq) * 4), 0, kCoherent)
+                  : f4_t{0.f, 0.f, 0.f, 0.f};
+  }
+  const f2_t r0 = lane < nr ? mls[lane] : f2_t{-INFINITY, 0.f};
+  const f2_t r1 = lane + 64 < nr ? mls[lane + 64] : f2_t{-INFINITY, 0.f};
+  const bool a0 = r0[1] > 0.f, a1 = r1[1] > 0.f;
+  const float M = wave_max(fmaxf(a0 ? r0[0] : -INFINITY, a1 ? r1[0] : -INFINITY));
+  const float L = wave_sum((a0 ? __builtin_amdgcn_exp2f(r0[0] - M) * r0[1] : 0.f) +
+                           (a1 ? __builtin_amdgcn_exp2f(r1[0] - M) * r1[1] : 0.f));
+  f4_t acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int i = 0; i < kRecPerThread; i++) {
+    const int c = sl + kSlices * i;
+    if (c < nr) {
+      const f2_t r = mls[c];
+      if (r[1] > 0.f) acc += __builtin_amdgcn_exp2f(r[0] - M) * v[i];
+    }
+  }
+#pragma unroll
+  for (int e = 0; e < 4; e++) {
+    const auto s2 = __builtin_amdgcn_permlane32_swap(__float_as_uint(acc[e]), __float_as_uint(acc[e]),
+                                                     false, false);
+    acc[e] = __uint_as_float(s2[0]) + __uint_as_float(s2[1]);
+  }
+  __syncthreads();   // every wave has left the vote: red may take the partials
+  if (lane < 32) *reinterpret_cast<f4_t*>(&red[wave * 128 + 4 * dq]) = acc;
+  __syncthreads();
+  if (complete && tid < 16) {
+    const float inv = (L > 0.f ? 1.0f / L : 0.f) * (ROTATE ? kCenScaleInv : 1.0f);
+    float x[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int w = 0; w < kWaves; w++) {
+      const f4_t lo = *reinterpret_cast<const f4_t*>(&red[w * 128 + tid * 8]);
+      const f4_t hi = *reinterpret_cast<const f4_t*>(&red[w * 128 + tid * 8 + 4]);
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        x[i] += lo[i];
+        x[4 + i] += hi[i];
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < 8; i++) x[i] *= inv;
+    uint32_t pk[4];
+    if constexpr (ROTATE) {
+      wht8_inreg(x);
+      wht_xor_lanes16(x, tid);
+      const float rs = wht_scale();
+      const uint32_t sbits = sign_word_sel(tid >> 2) >> (8 * (tid & 3));   // signs of elements tid*8..+7
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        float y[2];
+#pragma unroll
+        for (int e2 = 0; e2 < 2; e2++) {
+          const bool pos = (sbits >> (2 * i + e2)) & 1u;
+          const float vv = x[2 * i + e2] * rs;
+          y[e2] = pos ? vv : -vv;
+        }
+        pk[i] = f2h(y[0]) | (f2h(y[1]) << 16);
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < 4; i++) pk[i] = f2h(x[2 * i]) | (f2h(x[2 * i + 1]) << 16);
+    }
+    *reinterpret_cast<uint4*>(out + ((long)t * p.num_q + qh) * kHD + blk * 128 + tid * 8) =
+        make_uint4(pk[0], pk[1], pk[2], pk[3]);
+  }
+  __syncthreads();   // red and mls are reused by the next units
+}
+
+// merge_phase with the units taken two at a time while at least two remain
+// for this merger (mergers: 2 * ML<THREADS / 2>::kRedFloats floats at `red`,
+// 256 record scalars at `mls`).
+template <int THREADS, bool ROTATE>
+__device__ void merge_phase_paired(float* red, f2_t* mls, const AttnArgs& p, __amdgpu_buffer_rsrc_t rml,
+                                   __amdgpu_buffer_rsrc_t ro, uint16_t* out) {
+  static_assert(THREADS % 128 == 0, "two halves of whole waves");
+  const int n_units = p.num_q * p.sub_n * 2;
+  const int n_mergers = min(n_units, (int)gridDim.x);
+  const int mid = (int)blockIdx.x - ((int)gridDim.x - n_mergers);
+  if (mid < 0) return;
+  const bool poisoned = __hip_atomic_load(p.ws_header + kWsErrorWord, __ATOMIC_RELAXED,
+                                          __HIP_MEMORY_SCOPE_AGENT) != 0;
+  int num_q = p.num_q;
+  asm volatile("" : "+s"(num_q));
+  auto unit = [&](int u) {   // a contiguous (not ragged) launch
+    MergeUnit m{};
+    m.valid = u < n_units;
+    const int uu = m.valid ? u : 0;
+    m.blk = uu & 1;
+    m.qh = (uu >> 1) % num_q;
+    m.t = (uu >> 1) / num_q;
+    m.base = rec_index(p, m.qh, m.t, 0);
+    m.n = p.n_chunks;
+    return m;
+  };
+  for (int u = mid; u < n_units; u += 2 * n_mergers) {
+    const MergeUnit a = unit(u), b = unit(u + n_mergers);
+    if (poisoned) {
+      write_nan_unit(p, a.t, a.qh, a.blk, out);
+      if (b.valid) write_nan_unit(p, b.t, b.qh, b.blk, out);
+    } else if (b.valid) {
+      merge_unit_pair<THREADS, ROTATE>(red, mls, p, rml, ro, a, b, out);
+    } else {
+      merge_unit<THREADS, ROTATE>(red, mls, p, rml, ro, a.base, a.n, a.qh, a.t, a.blk, out);
+    }
+  }
+}
+
 }  // namespace qkv

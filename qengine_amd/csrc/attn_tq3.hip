@@ -1067,7 +1067,7 @@ constexpr int kMoPitch = 260;
 constexpr int kLdsMo = 0;
 constexpr int kLdsMl = kWaves * 16 * kMoPitch * 4;
 static_assert(kLdsQlo + 64 * kKRow <= kLdsNorm, "query scratch must fit the decoded tile areas");
-static_assert(kLdsMl + 2 * kWaves * 16 * 4 <= kLdsEnd, "merge area must fit");
+static_assert(kLdsMl + 2 * kWaves * 16 * 4 <= kLdsEnd && kLdsMl + 256 * 8 <= kLdsEnd, "merge area must fit");
 static_assert(kLdsMl >= kWaves * 128 * 4, "merger reduction area must not reach the merger scalars");
 static_assert(kLdsEnd <= 160 * 1024, "LDS");
 __device__ __forceinline__ int raw_v_row(int r) { return kLdsRawV + r * kRawPitch + 16 * ((r >> 2) & 15); }
@@ -1474,8 +1474,10 @@ __global__ __launch_bounds__(kThreads, 1) void tq3_mq_kernel(QKV_ATTN_LEAD_PARAM
   } else {
     __syncthreads();   // (the barrier publish_records passes, so that mo is free for the mergers)
   }
-  merge_phase<kThreads, true>(reinterpret_cast<float*>(lds + mq::kLdsMo),
-                              reinterpret_cast<f2_t*>(lds + mq::kLdsMl), p, rml, ro, out);
+  // (a multi-query call has at least two units per merger: 512 for the
+  // 16-token verify at 16 q heads over 256 workgroups)
+  merge_phase_paired<kThreads, true>(reinterpret_cast<float*>(lds + mq::kLdsMo),
+                                     reinterpret_cast<f2_t*>(lds + mq::kLdsMl), p, rml, ro, out);
 }
 
 size_t tq3_attn_lds_bytes() { return kLdsTotal; }

@@ -91,6 +91,39 @@ def test_tq3_decode_merge_timeout(dev):
     _timeout_cycle(dev, call, ws, ref, exact)
 
 
+@pytest.mark.parametrize("sub_n", [16, 5])
+def test_tq3_multi_query_merge_timeout(dev, sub_n):
+    """The shared-decode multi-query path (more than 16 query-head columns):
+    its mergers take their units two at a time (16 queries: 16 units per
+    merger, all in pairs; 5 queries: 5 per merger, two pairs and a single),
+    and a timed-out pair writes NaN rows like a single unit."""
+    import torch
+    from qengine_amd import kvcache
+    rng = np.random.default_rng(73 + sub_n)
+    n, nq, nkv = 3000, 16, 4
+    k16, v16 = kv_f16(rng, n, nkv, 256), kv_f16(rng, n, nkv, 256)
+    kb, vb = O.tq3_encode(k16), O.tq3_encode(v16)
+    q = q_f16(rng, sub_n, nq, 256)
+    start = n - sub_n
+    pm, pl, po = O.attn_split(O.KV_TQ3, q, kb, vb, num_q=nq, num_kv=nkv, hd=256, start_pos=start,
+                              sub_n=sub_n, sub_n_max=sub_n, active_end_max=n, scale=1 / 16,
+                              k_splits=8)
+    ref = O.attn_split_merge(pm, pl, po, num_q=nq, num_kv=nkv, hd=256, sub_n=sub_n,
+                             sub_n_max=sub_n, k_splits=8).view(np.float16)
+    exact = O.attn_exact_tq3(q, kb, vb, num_q=nq, num_kv=nkv, hd=256, start_pos=start,
+                             sub_n=sub_n, scale=1 / 16)
+    ws = kvcache.decode_attn_tq3_workspace(nq, nkv, sub_n, n, dev)
+    qd, kd, vd = _dev(q.view(np.uint16), dev), _dev(kb.view(np.uint8), dev), _dev(vb.view(np.uint8), dev)
+
+    def call():
+        out = torch.zeros((sub_n, nq, 256), dtype=torch.float16, device=dev)
+        kvcache.decode_attn_tq3(qd, kd, vd, out, ws, num_q=nq, num_kv=nkv, start_pos=start,
+                                sub_n=sub_n, scale=1 / 16)
+        torch.cuda.synchronize()
+        return out.cpu().numpy()
+    _timeout_cycle(dev, call, ws, ref, exact)
+
+
 def test_q8_decode_merge_timeout(dev):
     import torch
     from qengine_amd import kvcache
