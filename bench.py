@@ -294,7 +294,7 @@ def secondary(torch, kvcache, dev, stream):
         "prefill_path_us": round(ms_pf * 1e3, 3),
         "note": "append of the 16 verify tokens, then causal attention of the 16 queries over "
                 "the TQ3 cache (131088 keys, the block's own keys read back quantized) through "
-                "qkv_decode_attn_tq3 with sub_n 16 (4 queries per workgroup pass); "
+                "qkv_decode_attn_tq3 with sub_n 16 (one pass over the cache: each tile decoded once for all 64 query-head columns); "
                 "prefill_path_us: the same through qkv_prefill_attn_tq3 in verify mode"}
 
     # ---- f2: block-sparse verify of the same 16 queries (DFLASH_VERIFY_BLOCKSPARSE
