@@ -27,11 +27,13 @@
 //                         the value MFMA consumes.  The history is padded to a
 //                         multiple of 64 rows, the chunk follows; pad rows are
 //                         zero.
-//   prefill_attn_kernel   one workgroup per (kv head, 32 query tokens, key
+//   prefill_attn_kernel   one workgroup per (kv head, 64 query tokens, key
 //                         split) -- two per kv head for GQA 6, three heads
-//                         each -- and one wave per query head.  Per 64-key
-//                         tile (keys [key][dim], values [dim][key] in LDS,
-//                         shared by the 32 x GQA query rows):
+//                         each -- and one wave per (query head, 32 tokens);
+//                         chunks of at most 32 tokens take 32-token
+//                         workgroups, two per CU.  Per 32-key tile (keys
+//                         [key][dim], values [dim][key] in LDS, shared by the
+//                         64 x GQA query rows of the workgroup):
 //                           S^T  = K Q^T       v_mfma_f32_32x32x16_f16, M = keys
 //                           O^T += V^T P^T     M = dims, N = query tokens
 //                         so every lane owns one query row (token lane % 32)
@@ -53,11 +55,18 @@ typedef float f16x_t __attribute__((ext_vector_type(16)));
 constexpr int kHD = 256;
 constexpr int kKeys = 64;                 // row granule of the staged K / V (stage tiles)
 constexpr int kTK = 32;                   // keys per attention tile
-constexpr int kToks = 32;                 // query tokens per workgroup
+constexpr int kWaveToks = 32;             // query tokens per wave (the MFMA N dimension)
+
+// Token groups of a workgroup: two (64 tokens, 8 waves at GQA 4, one
+// workgroup per CU) when the chunk has more than 32 tokens, else one (two
+// workgroups per CU).  Every tile a workgroup loads serves all its query rows,
+// so 64-token workgroups move half the L2 -> LDS bytes per MFMA of 32-token
+// ones (config 5(i): 3.94 against 4.23-4.41 ms per chunk, bit-identical).
+__host__ __device__ inline int prefill_token_groups(int n_tok) { return n_tok > kWaveToks ? 2 : 1; }
 
 // LDS of the attention (bytes): two tile buffers, each keys [32][512 B] then
-// values [256 dims][64 B]; 64 KB per workgroup, so two workgroups share a CU
-// and the matrix core of one overlaps the softmax of the other.  16-byte
+// values [256 dims][64 B]; 64 KB per workgroup, so two one-group workgroups
+// share a CU and the matrix core of one overlaps the softmax of the other.  16-byte
 // chunks are XOR-swizzled so that the MFMA operand reads (16 lanes per LDS
 // cycle, 16 consecutive rows at one logical chunk) hit 16 different 16-byte
 // bank groups: key row r holds chunk c at c ^ (r & 15), value row d holds
@@ -68,7 +77,7 @@ constexpr int kKBytes = kTK * kHD * 2;                // 16 KB
 constexpr int kVBytes = kHD * kTK * 2;                // 16 KB
 constexpr int kBufBytes = kKBytes + kVBytes;
 constexpr int kLdsBytes = 2 * kBufBytes;
-static_assert(2 * kLdsBytes <= 160 * 1024, "two prefill workgroups must fit one CU");
+static_assert(2 * kLdsBytes <= 160 * 1024, "two one-group prefill workgroups must fit one CU");
 
 typedef __attribute__((address_space(3))) void lds_void_t;
 
@@ -160,16 +169,18 @@ __global__ __launch_bounds__(256) void prefill_stage_kernel(PrefillArgs p, const
 }
 
 // ---------------------------------------------------------------------------
-// attention: 1-D grid (placement above); WAVES query heads of one kv head per
-// workgroup, one wave per head
+// attention: 1-D grid (placement above); WAVES query heads of one kv head and
+// TG groups of 32 query tokens per workgroup, one wave per (head, group)
 // ---------------------------------------------------------------------------
-template <int WAVES, bool FROM_CACHE>
-__global__ __launch_bounds__(64 * WAVES, 2) void prefill_attn_kernel(PrefillArgs p,
-                                                                     const uint16_t* q) {
+template <int WAVES, int TG, bool FROM_CACHE>
+__global__ __launch_bounds__(64 * WAVES * TG, TG == 1 ? 2 : 1) void prefill_attn_kernel(
+    PrefillArgs p, const uint16_t* q) {
+  constexpr int kToks = kWaveToks * TG;   // query tokens per workgroup
   __shared__ __attribute__((aligned(16))) uint8_t lds[kLdsBytes];
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wave = wv % WAVES, tg = wv / WAVES;   // query head, token group
   const int hh = lane >> 5;          // k-group of the MFMA operands / row group of D
   const int tok = lane & 31;         // query token (MFMA N index) of this lane
   const int gqa = p.num_q / p.num_kv;
@@ -192,6 +203,8 @@ __global__ __launch_bounds__(64 * WAVES, 2) void prefill_attn_kernel(PrefillArgs
   const int h = hg_all / groups, hg = hg_all - h * groups;
   const int t0 = qt * kToks;
   const int n_q = min(kToks, p.n_tok - t0);
+  const int t0w = t0 + kWaveToks * tg;              // this wave's first token
+  const int n_qw = min(kWaveToks, p.n_tok - t0w);   // <= 0: a group past the last token
   const int qh = h * gqa + hg * WAVES + wave;
 
   // 32-key tiles: history rows [0, h_pad) then (unless every key comes from
@@ -209,7 +222,7 @@ __global__ __launch_bounds__(64 * WAVES, 2) void prefill_attn_kernel(PrefillArgs
     const uint32_t qbytes = (uint32_t)((long)p.n_tok * p.num_q * kHD * 2);
     const __amdgpu_buffer_rsrc_t rq = __builtin_amdgcn_make_buffer_rsrc(
         const_cast<uint16_t*>(q), 0, qbytes, kBufferRsrcWord3);
-    const uint32_t base = tok < n_q ? (uint32_t)((((long)(t0 + tok) * p.num_q + qh) * kHD) * 2) : qbytes;
+    const uint32_t base = tok < n_qw ? (uint32_t)((((long)(t0w + tok) * p.num_q + qh) * kHD) * 2) : qbytes;
 #pragma unroll
     for (int b = 0; b < 2; b++)
 #pragma unroll
@@ -220,14 +233,14 @@ __global__ __launch_bounds__(64 * WAVES, 2) void prefill_attn_kernel(PrefillArgs
 
   // ---- tile loads: one buffer resource per tensor of this kv head (kx rows
   // and vt tiles share the head stride), the tile offset in the scalar offset;
-  // 16 loads of 1 KB per tensor and tile, spread over the waves (with 3 waves
-  // the last load of wave 2 repeats load 15, which writes the same bytes).
+  // 16 loads of 1 KB per tensor and tile, spread over the waves (with 3 or 6
+  // waves the last wave repeats load 15, which writes the same bytes).
   const uint32_t head_bytes = (uint32_t)(rows * kHD * 2);
   const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc(
       const_cast<uint16_t*>(p.kx) + (long)h * rows * kHD, 0, head_bytes, kBufferRsrcWord3);
   const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(
       const_cast<uint16_t*>(p.vt) + (long)h * rows * kHD, 0, head_bytes, kBufferRsrcWord3);
-  constexpr int kLoads = (16 + WAVES - 1) / WAVES;
+  constexpr int kLoads = (16 + WAVES * TG - 1) / (WAVES * TG);
   // load j: key rows 2j, 2j+1 (lane l: row 2j + l/32, slot l%32) and value
   // dims 16j .. 16j+15 (lane l: dim 16j + l/4, slot l%4); the value offset
   // within the run does not depend on j
@@ -240,7 +253,7 @@ __global__ __launch_bounds__(64 * WAVES, 2) void prefill_attn_kernel(PrefillArgs
     uint8_t* base = lds + buf * kBufBytes;
 #pragma unroll
     for (int jj = 0; jj < kLoads; jj++) {
-      const int j = min(wave + jj * WAVES, 15);
+      const int j = min(wv + jj * WAVES * TG, 15);
       int k_off;
       asm volatile("v_xor_b32 %0, %1, %2" : "=v"(k_off) : "s"(16 * ((2 * j) & 15)), "v"(k_base));
       __builtin_amdgcn_raw_ptr_buffer_load_lds(rk, (lds_void_t*)(base + j * 1024), 16, k_off,
@@ -254,7 +267,7 @@ __global__ __launch_bounds__(64 * WAVES, 2) void prefill_attn_kernel(PrefillArgs
 #pragma unroll
   for (int d = 0; d < 8; d++) acc[d] = f16x_t{};
   float m2 = -INFINITY, lsum = 0.0f;
-  const int t_abs = t0 + tok;        // this lane's token index in the chunk
+  const int t_abs = t0w + tok;       // this lane's token index in the chunk
   const int lim_hist = FROM_CACHE ? min(p.hist, p.start_pos + t_abs + 1) : p.hist;
   // a negative scale is carried by the query (an exact fp16 sign flip), so
   // that the row maximum of the raw scores gives the maximum of the scaled ones
@@ -364,8 +377,8 @@ __global__ __launch_bounds__(64 * WAVES, 2) void prefill_attn_kernel(PrefillArgs
     const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(lsum), __float_as_uint(lsum), false, false);
     lsum = __uint_as_float(sw[0]) + __uint_as_float(sw[1]);
   }
-  if (tok < n_q) {
-    const long row = ((long)z * p.n_tok + t0 + tok) * p.num_q + qh;
+  if (tok < n_qw) {
+    const long row = ((long)z * p.n_tok + t0w + tok) * p.num_q + qh;
     float* po = p.part_o + row * kHD;
 #pragma unroll
     for (int d = 0; d < 8; d++)
@@ -489,10 +502,12 @@ PrefillGeom prefill_geom(int num_q, int num_kv, int n_tok, int start_pos) {
   // history rows: start_pos (prefill) or start_pos + n_tok (verify), padded to
   // whole tiles; the workspace covers the larger of the two
   g.h_pad = (start_pos + n_tok + kKeys - 1) / kKeys * kKeys;
-  const int qtiles = (n_tok + kToks - 1) / kToks;
+  const int tg = prefill_token_groups(n_tok);
+  const int qtiles = (n_tok + kWaveToks * tg - 1) / (kWaveToks * tg);
   const int wgs = num_kv * (num_q / num_kv == 6 ? 2 : 1) * qtiles;
   const int tiles = g.h_pad / kKeys + g.n_pad / kKeys;
-  int ns = (512 + wgs - 1) / wgs;                 // two workgroups on each of 256 CUs
+  const int slots = tg == 2 ? 256 : 512;          // workgroups of one round: 256 CUs
+  int ns = (slots + wgs - 1) / wgs;
   ns = std::min(ns, std::max(1, tiles / 8));      // at least ~8 tiles per split
   g.n_split = std::max(1, ns);
   size_t off = 0;
@@ -517,20 +532,34 @@ hipError_t launch_prefill_tq3(const PrefillArgs& a, int gqa, const uint16_t* q, 
     hipLaunchKernelGGL(prefill_stage_kernel, dim3((unsigned)(a.num_kv * tiles)), dim3(256), 0,
                        stream, a, k, v);
   }
-  const int qtiles = (a.n_tok + kToks - 1) / kToks;
+  const int tg = prefill_token_groups(a.n_tok);
+  const int qtiles = (a.n_tok + kWaveToks * tg - 1) / (kWaveToks * tg);
   const int groups = gqa == 6 ? 2 : 1;
   const Placement pl = placement(qtiles, a.num_kv * groups * a.n_split);
   const dim3 grid((unsigned)(8 * pl.subs * pl.per));
-  if (gqa == 4 && !a.from_cache)
-    hipLaunchKernelGGL((prefill_attn_kernel<4, false>), grid, dim3(256), 0, stream, a, q);
-  else if (gqa == 4)
-    hipLaunchKernelGGL((prefill_attn_kernel<4, true>), grid, dim3(256), 0, stream, a, q);
-  else if (gqa == 6 && !a.from_cache)   // two workgroups of three heads per kv head
-    hipLaunchKernelGGL((prefill_attn_kernel<3, false>), grid, dim3(192), 0, stream, a, q);
-  else if (gqa == 6)
-    hipLaunchKernelGGL((prefill_attn_kernel<3, true>), grid, dim3(192), 0, stream, a, q);
-  else
-    return hipErrorInvalidValue;
+  if (gqa != 4 && gqa != 6) return hipErrorInvalidValue;
+  // GQA 6: two workgroups of three heads per kv head
+  const int heads = gqa == 6 ? 3 : 4;
+  const dim3 block((unsigned)(64 * heads * tg));
+  if (tg == 2) {
+    if (gqa == 4 && !a.from_cache)
+      hipLaunchKernelGGL((prefill_attn_kernel<4, 2, false>), grid, block, 0, stream, a, q);
+    else if (gqa == 4)
+      hipLaunchKernelGGL((prefill_attn_kernel<4, 2, true>), grid, block, 0, stream, a, q);
+    else if (!a.from_cache)
+      hipLaunchKernelGGL((prefill_attn_kernel<3, 2, false>), grid, block, 0, stream, a, q);
+    else
+      hipLaunchKernelGGL((prefill_attn_kernel<3, 2, true>), grid, block, 0, stream, a, q);
+  } else {
+    if (gqa == 4 && !a.from_cache)
+      hipLaunchKernelGGL((prefill_attn_kernel<4, 1, false>), grid, block, 0, stream, a, q);
+    else if (gqa == 4)
+      hipLaunchKernelGGL((prefill_attn_kernel<4, 1, true>), grid, block, 0, stream, a, q);
+    else if (!a.from_cache)
+      hipLaunchKernelGGL((prefill_attn_kernel<3, 1, false>), grid, block, 0, stream, a, q);
+    else
+      hipLaunchKernelGGL((prefill_attn_kernel<3, 1, true>), grid, block, 0, stream, a, q);
+  }
   const long rows = (long)a.n_tok * a.num_q;
   if (a.n_split > kMergeMaxSplits) return hipErrorInvalidValue;
   if (a.n_split >= 16)   // one workgroup per row, the splits spread over its threads
