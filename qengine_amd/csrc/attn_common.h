@@ -277,32 +277,76 @@ __device__ __forceinline__ Tq3Group tq3_group_load(const uint8_t* blk, int part)
   const uint32_t* cw = reinterpret_cast<const uint32_t*>(blk + 4);
   return Tq3Group{*reinterpret_cast<const float*>(blk), cw[w0], cw[min(w0 + 1, 11)]};
 }
-__device__ __forceinline__ void tq3_group_dequant(const Tq3Group& gr, int part, int lane,
-                                                  uint32_t (&pk)[4]) {
-  const float norm = gr.norm;
-  const uint32_t g = __builtin_amdgcn_alignbyte(gr.hi, gr.lo, (3 * part) & 3);
-  float x[8];
-#pragma unroll
-  for (int i = 0; i < 8; i++) x[i] = centroid_f32((g >> (3 * i)) & 7u);
-  wht8_inreg(x);
-  wht_xor_lanes16(x, lane);
+
+// What a lane of the group dequantization keeps for the whole kernel: the
+// factors rs * sign of its elements (negating the fp32 product x * rs is
+// exact, so the sign folds into the factor) and the sign-bit flips of its
+// four cross-lane butterfly stages (set where the lane is the upper one of a
+// pair).
+struct Tq3LaneConst {
+  float rsi[8];
+  uint32_t flip[4];
+};
+__device__ __forceinline__ Tq3LaneConst tq3_lane_const(int part) {
+  Tq3LaneConst c;
   const float rs = wht_scale();
   const uint32_t sbits = sign_word_sel(part >> 2) >> (8 * (part & 3));   // elements part*8..+7
 #pragma unroll
+  for (int i = 0; i < 8; i++) c.rsi[i] = ((sbits >> i) & 1u) ? rs : -rs;
+#pragma unroll
+  for (int k = 0; k < 4; k++) c.flip[k] = ((part >> k) & 1) ? 0x80000000u : 0u;
+  return c;
+}
+// The eight fp32 levels in LDS (threads 0..7 write them; a barrier follows
+// before the first tq3_group_dequant): a lane's level is one LDS read, where
+// a select chain would cost several four-cycle selects per element.
+__device__ __forceinline__ void tq3_centroid_table(float* cent, int tid) {
+  if (tid < 8) cent[tid] = centroid_f32((uint32_t)tid);
+}
+
+// One cross-lane butterfly stage (partner lane ^ M inside the 16-lane group):
+// the lower lane of a pair takes own + partner, the upper partner - own,
+// formed as partner + (own with its sign bit flipped) -- IEEE a - b is
+// a + (-b), so the values are those of the two-operation form -- in one
+// DPP-sourced add.
+template <int CTRL>
+__device__ __forceinline__ float dpp_mov_bc(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), CTRL, 0xf, 0xf, true));
+}
+template <int M>
+__device__ __forceinline__ void tq3_xor_stage(float (&x)[8], uint32_t flip) {
+#pragma unroll
+  for (int i = 0; i < 8; i++) {
+    float o;
+    if constexpr (M == 1) o = dpp_mov_bc<0xB1>(x[i]);                       // quad_perm [1,0,3,2]
+    else if constexpr (M == 2) o = dpp_mov_bc<0x4E>(x[i]);                  // quad_perm [2,3,0,1]
+    else if constexpr (M == 4) o = dpp_mov_bc<0x1B>(dpp_mov_bc<0x141>(x[i]));   // i ^ 7, then ^ 3
+    else o = dpp_mov_bc<0x128>(x[i]);                                       // row_ror:8
+    x[i] = o + __uint_as_float(__float_as_uint(x[i]) ^ flip);
+  }
+}
+
+// Every lane of the 16-lane group must be active (the stages read the other
+// lanes of the group).
+__device__ __forceinline__ void tq3_group_dequant(const Tq3Group& gr, int part, const float* cent,
+                                                  const Tq3LaneConst& lc, uint32_t (&pk)[4]) {
+  const uint32_t g = __builtin_amdgcn_alignbyte(gr.hi, gr.lo, (3 * part) & 3);
+  float x[8];
+#pragma unroll
+  for (int i = 0; i < 8; i++) x[i] = cent[(g >> (3 * i)) & 7u];
+  wht8_inreg(x);
+  tq3_xor_stage<1>(x, lc.flip[0]);
+  tq3_xor_stage<2>(x, lc.flip[1]);
+  tq3_xor_stage<4>(x, lc.flip[2]);
+  tq3_xor_stage<8>(x, lc.flip[3]);
+#pragma unroll
   for (int i = 0; i < 4; i++) {
-    float a = x[2 * i] * rs, b = x[2 * i + 1] * rs;
-    a = ((sbits >> (2 * i)) & 1u) ? a : -a;
-    b = ((sbits >> (2 * i + 1)) & 1u) ? b : -b;
     // the reference rounds v*norm to fp32, then to fp16: the empty asm keeps
     // the fp32 product (no fused fp16-rounding mixed FMA)
-    float pa = a * norm, pb = b * norm;
+    float pa = (x[2 * i] * lc.rsi[2 * i]) * gr.norm, pb = (x[2 * i + 1] * lc.rsi[2 * i + 1]) * gr.norm;
     asm volatile("" : "+v"(pa), "+v"(pb));
     pk[i] = f2h(pa) | (f2h(pb) << 16);
   }
-}
-__device__ __forceinline__ void tq3_dequant_exact8(const uint8_t* blk, int part, int lane,
-                                                   uint32_t (&pk)[4]) {
-  tq3_group_dequant(tq3_group_load(blk, part), part, lane, pk);
 }
 
 hipError_t launch_tq3_attn(const AttnArgs& a, int mode, uint16_t* out, hipStream_t stream);

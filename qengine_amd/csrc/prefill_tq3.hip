@@ -122,7 +122,11 @@ constexpr int kStVPitch = 132;   // bytes per staged value dim row (64 keys fp16
 __global__ __launch_bounds__(256) void prefill_stage_kernel(PrefillArgs p, const uint16_t* k,
                                                             const uint16_t* v) {
   __shared__ __attribute__((aligned(16))) uint8_t vt_lds[kHD * kStVPitch];
-  const int tid = threadIdx.x, lane = tid & 63, part = tid & 15;
+  __shared__ float cent[8];
+  const int tid = threadIdx.x, part = tid & 15;
+  tq3_centroid_table(cent, tid);
+  const Tq3LaneConst lc = tq3_lane_const(part);
+  __syncthreads();
   const long rows = (long)p.h_pad + p.n_pad;
   const int tiles = (int)(rows / kKeys);
   const int h = blockIdx.x / tiles, tile = blockIdx.x - h * tiles;
@@ -134,9 +138,10 @@ __global__ __launch_bounds__(256) void prefill_stage_kernel(PrefillArgs p, const
     uint32_t pk[4] = {0u, 0u, 0u, 0u};   // pad rows stay zero
     if (row < p.hist) {
       // history: the reference's dequantization (turboquant.cuh:169-200)
-      tq3_dequant_exact8(reinterpret_cast<const uint8_t*>(tv ? p.v_cache : p.k_cache) +
-                             ((uint64_t)(uint32_t)row * (uint32_t)p.num_kv + h) * 104u + blk * 52u,
-                         part, lane, pk);
+      tq3_group_dequant(tq3_group_load(reinterpret_cast<const uint8_t*>(tv ? p.v_cache : p.k_cache) +
+                                           ((uint64_t)(uint32_t)row * (uint32_t)p.num_kv + h) * 104u +
+                                           blk * 52u, part),
+                        part, cent, lc, pk);
     } else if (row >= p.h_pad && row - p.h_pad < p.n_tok) {
       // the chunk's own keys / values, as given
       const uint16_t* src = (tv ? v : k) + ((long)(row - p.h_pad) * p.num_kv + h) * kHD + dim0;

@@ -9,7 +9,7 @@
 // 214-330).  The attention over the selected blocks is tq3_attn_kernel<2>.
 //
 // The kernels here reproduce the reference's values exactly: the keys are
-// dequantized bit for bit (tq3_dequant_exact8), the signature sums run in the
+// dequantized bit for bit (tq3_group_dequant), the signature sums run in the
 // reference's order, the block scores sum exact fp16 x fp16 products pairwise
 // in the reference's order, and the selection is the reference's repeated
 // argmax (highest score, lower block index on ties), sorted ascending.
@@ -33,6 +33,7 @@ constexpr int kPoolPitch = kSpHD * 2 + 16;   // bytes per staged key row (fp16)
 // block), then thread c reduces dimension c over the rows in position order.
 __global__ __launch_bounds__(kSpThreads) void tq3_kpool_kernel(KpoolArgs a) {
   __shared__ __attribute__((aligned(16))) uint8_t rows[64 * kPoolPitch];
+  __shared__ float cent[8];
   const int n_upd = a.cur_blocks - a.blk_lo;
   const int h = blockIdx.x / n_upd;
   const int n = a.blk_lo + (int)(blockIdx.x - h * n_upd);
@@ -40,7 +41,9 @@ __global__ __launch_bounds__(kSpThreads) void tq3_kpool_kernel(KpoolArgs a) {
   const int t_hi = min(t_lo + a.bsn, a.total_kv);
   const int n_pos = t_hi - t_lo;   // >= 1: n < cur_blocks
   const int tid = threadIdx.x;
-  const int part = tid & 15, lane = tid & 63;
+  const int part = tid & 15;
+  tq3_centroid_table(cent, tid);
+  const Tq3LaneConst lc = tq3_lane_const(part);
   // units (position, 128-block): 16 per pass of the workgroup, at most 8
   // passes (64 rows); every pass's loads are issued before the first is used
   constexpr int kPasses = 2 * 64 / (kSpThreads / 16);
@@ -54,13 +57,14 @@ __global__ __launch_bounds__(kSpThreads) void tq3_kpool_kernel(KpoolArgs a) {
                          (u & 1) * 52u;
     gr[p] = tq3_group_load(src, part);
   }
+  __syncthreads();   // the centroid table
 #pragma unroll
   for (int p = 0; p < kPasses; p++) {
     const int u = (tid >> 4) + p * (kSpThreads / 16);
     if (u < 2 * n_pos) {   // uniform over the unit's 16 lanes (lane exchange inside)
       const int pos = u >> 1, blk = u & 1;
       uint32_t pk[4];
-      tq3_group_dequant(gr[p], part, lane, pk);
+      tq3_group_dequant(gr[p], part, cent, lc, pk);
       *reinterpret_cast<uint4*>(rows + pos * kPoolPitch + (blk * 128 + part * 8) * 2) =
           make_uint4(pk[0], pk[1], pk[2], pk[3]);
     }
