@@ -72,10 +72,11 @@ def _oracle(q, k_all, v_all, *, num_q, num_kv, start_pos, scale, k_splits=8):
 
 
 @pytest.mark.parametrize("start_pos,n_tok,num_q", [
-    (0, 40, 16),        # no history: the chunk attends to itself only
-    (1000, 70, 16),     # partial history tile, partial chunk tiles
+    (0, 40, 16),        # no history: the chunk attends to itself only (64-token workgroup, 8 + 32 tokens)
+    (1000, 70, 16),     # partial history tile, partial chunk tiles; the second workgroup's
+                        # second 32-token wave group holds no token
     (4096, 128, 16),    # whole tiles
-    (777, 33, 24),      # GQA 6 (two workgroups of three heads per kv head)
+    (777, 33, 24),      # GQA 6 (two workgroups of three heads x two token groups per kv head)
     (300, 1, 16),       # single-token chunk
     (64, 200, 24),
 ])
