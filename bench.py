@@ -284,18 +284,26 @@ def secondary(torch, kvcache, dev, stream):
         append16()
         kvcache.prefill_attn_tq3(qv, kb, vb, None, None, ov, wsp16, num_q=NUM_Q, num_kv=NUM_KV,
                                  start_pos=hist, scale=scale)
-    ms = _time(torch, stream, verify, 50)
+    def verify_one_call(i=0):
+        kvcache.decode_attn_tq3_append(qv, kv_, vv, kb, vb, ov, wsv, num_q=NUM_Q, num_kv=NUM_KV,
+                                       start_pos=hist, sub_n=nv, scale=scale)
+    ms_two = _time(torch, stream, verify, 50)
+    ms = _time(torch, stream, verify_one_call, 50)
     ms_pf = _time(torch, stream, verify_prefill_path, 50)
     vbytes = (hist + nv) * 2 * BLOCKS_PER_TOKEN * 52 + nv * NUM_Q * HD * 2 * 2
     out["config5_verify16"] = {
         "us": round(ms * 1e3, 3), "bytes": vbytes,
         "gbps": round(vbytes / (ms * 1e-3) / 1e9, 1),
         "frac": round(vbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+        "two_call_us": round(ms_two * 1e3, 3),
         "prefill_path_us": round(ms_pf * 1e3, 3),
         "note": "append of the 16 verify tokens, then causal attention of the 16 queries over "
-                "the TQ3 cache (131088 keys, the block's own keys read back quantized) through "
-                "qkv_decode_attn_tq3 with sub_n 16 (one pass over the cache: each tile decoded once for all 64 query-head columns); "
-                "prefill_path_us: the same through qkv_prefill_attn_tq3 in verify mode"}
+                "the TQ3 cache (131088 keys, the block's own keys read back quantized), in one "
+                "call and one launch: qkv_decode_attn_tq3_append, whose decode kernel encodes "
+                "the block's rows itself, writes them to the caches and decodes every tile once "
+                "for all 64 query-head columns (caches and output bit-identical to the two "
+                "calls); two_call_us: qkv_tq3_append_kv, then qkv_decode_attn_tq3 with sub_n 16; "
+                "prefill_path_us: the same step through qkv_prefill_attn_tq3 in verify mode"}
 
     # ---- f2: block-sparse verify of the same 16 queries (DFLASH_VERIFY_BLOCKSPARSE
     # defaults: top_k = 10% of the blocks capped at 64, beta 0.5, K_SPLITS 8) ----

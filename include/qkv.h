@@ -329,6 +329,27 @@ int qkv_decode_workspace_status_async(const void* workspace, int* status, hipStr
  * out, so the error path can be exercised without a GPU fault or hang. */
 int qkv_debug_set_merge_spin_limit(int limit);
 
+/* TQ3 append and decode of a multi-token (verify) block in one call.
+ * Replaces the reference's verify-step sequence: the block's K and V encoded
+ * into the cache (tq3_quantize_kernel, K then V, model.cuh:4566-4571;
+ * turboquant.cuh:112-165) followed by the split attention of its sub_n
+ * queries and the merge (model.cuh:4663-4687).  k_new, v_new are the block's
+ * fp16 K and V rows [sub_n][num_kv][256] (16-byte aligned); they are encoded
+ * exactly as qkv_tq3_append_kv encodes them and written to rows start_pos ..
+ * start_pos + sub_n - 1 of k and v, and the attention is that of
+ * qkv_decode_attn_tq3 with the same arguments.  When the call has more than
+ * 16 (query, head) columns and sub_n <= 64 it is ONE launch (the
+ * shared-decode kernel encodes the new rows it reads and writes them to the
+ * caches); otherwise the append's launch, then the decode's.  Caches and output equal those of
+ * qkv_tq3_append_kv followed by qkv_decode_attn_tq3; same workspace
+ * (qkv_decode_attn_tq3_workspace_bytes(num_q, num_kv, sub_n,
+ * start_pos + sub_n)) and errors. */
+int qkv_decode_attn_tq3_append(const uint16_t* q, const uint16_t* k_new, const uint16_t* v_new,
+                               qkv_block_tq3* k, qkv_block_tq3* v, uint16_t* out, int num_q,
+                               int num_kv, int head_dim, int start_pos, int sub_n, float scale,
+                               int sink_tok, int window_tok, const uint32_t* tree_mask,
+                               void* workspace, size_t workspace_bytes, hipStream_t stream);
+
 /* Allocation-free variant of qkv_decode_attn_tq3 (same arguments without the
  * workspace, same results).  No counterpart in the reference: it is for
  * callers that cannot allocate or own device memory (code under HIP graph

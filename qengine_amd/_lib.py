@@ -71,6 +71,8 @@ SIGNATURES = {
     "qkv_decode_attn_q8_workspace_bytes": (_SZ, [_I, _I, _I, _I]),
     "qkv_decode_attn_q8": (_I, [_P, _P, _P, _P, _I, _I, _I, _I, _I, _F, _P, _SZ, _P]),
     "qkv_decode_attn_q8_append": (_I, [_P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _F, _P, _SZ, _P]),
+    "qkv_decode_attn_tq3_append": (_I, [_P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _F, _I, _I, _P, _P,
+                                        _SZ, _P]),
     "qkv_decode_attn_q8k_tq3v_workspace_bytes": (_SZ, [_I, _I, _I, _I]),
     "qkv_decode_attn_q8k_tq3v": (_I, [_P, _P, _P, _P, _I, _I, _I, _I, _I, _F, _P, _SZ, _P]),
     "qkv_tq3_append_kv_paged": (_I, [_P, _P, _P, _P, _I, _I, _I, _I, _P, _I, _I, _I, _P, _P]),

@@ -49,6 +49,7 @@
 #include "attn_common.h"
 #include "attn_fastmerge.h"
 #include "qkv_launch.h"
+#include "tq3_encode.h"
 
 namespace qkv {
 
@@ -1057,6 +1058,10 @@ constexpr int kRawPitch = 112;
 constexpr int kLdsRawK = kLdsCorr + kWaves * 16 * 4;
 constexpr int kLdsRawV = kLdsRawK + 64 * kRawPitch;
 constexpr int kLdsEnd = kLdsRawV + 64 * kRawPitch + 16 * 16;
+// fused append: the encoded 13-dword blocks of this workgroup's new keys
+// (at most 64 keys x K, V x 2 blocks)
+constexpr int kLdsEnc = kLdsEnd;
+constexpr int kLdsEncEnd = kLdsEnc + 64 * 4 * 13 * 4;
 // setup: the rotated query's fp16 rounding and remainder, [64 columns][kKRow]
 // each (swizzled as the keys), over the decoded tile areas (read into
 // registers before tile 0)
@@ -1069,7 +1074,7 @@ constexpr int kLdsMl = kWaves * 16 * kMoPitch * 4;
 static_assert(kLdsQlo + 64 * kKRow <= kLdsNorm, "query scratch must fit the decoded tile areas");
 static_assert(kLdsMl + 2 * kWaves * 16 * 4 <= kLdsEnd && kLdsMl + 256 * 8 <= kLdsEnd, "merge area must fit");
 static_assert(kLdsMl >= kWaves * 128 * 4, "merger reduction area must not reach the merger scalars");
-static_assert(kLdsEnd <= 160 * 1024, "LDS");
+static_assert(kLdsEncEnd <= 160 * 1024, "LDS");
 __device__ __forceinline__ int raw_v_row(int r) { return kLdsRawV + r * kRawPitch + 16 * ((r >> 2) & 15); }
 }  // namespace mq
 
@@ -1178,7 +1183,7 @@ __device__ __forceinline__ void mq_decode(uint8_t* lds, uint32_t lane4, int lane
 __global__ __launch_bounds__(kThreads, 1) void tq3_mq_kernel(QKV_ATTN_LEAD_PARAMS, AttnArgs pin,
                                                               uint16_t* out) {
   QKV_ATTN_LEAD_APPLY(p, pin);
-  __shared__ __attribute__((aligned(16))) uint8_t lds[mq::kLdsEnd];
+  __shared__ __attribute__((aligned(16))) uint8_t lds[mq::kLdsEncEnd];
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -1239,6 +1244,34 @@ __global__ __launch_bounds__(kThreads, 1) void tq3_mq_kernel(QKV_ATTN_LEAD_PARAM
   lo = __builtin_amdgcn_readfirstlane(lo);
   hi = __builtin_amdgcn_readfirstlane(hi);
   hi_first = __builtin_amdgcn_readfirstlane(hi_first);
+  // ---- fused append (qkv_decode_attn_tq3_append): the new keys start_pos ..
+  // start_pos + sub_n - 1 that this workgroup reads, [new_lo, new_lo + n_new),
+  // are encoded here (tq3_encode_row16, the small append's arithmetic), 32
+  // blocks per round; the last query group's workgroups also store them to
+  // the caches.  Their cache rows are read (stale) like every other row and
+  // the encoded rows are written over them in the LDS staging before decode.
+  int new_lo = 0, n_new = 0;
+  if (p.k_new != nullptr && has_work && hi > max(lo, p.start_pos)) {
+    new_lo = max(lo, p.start_pos);
+    n_new = hi - new_lo;   // <= sub_n <= 64 (the host takes this path only then)
+  }
+  new_lo = __builtin_amdgcn_readfirstlane(new_lo);
+  n_new = __builtin_amdgcn_readfirstlane(n_new);
+  auto enc_input = [&](int round) {
+    const int j = 32 * round + (tid >> 4), t = tid & 15;
+    uint4 raw = make_uint4(0u, 0u, 0u, 0u);
+    if (j < 4 * n_new) {
+      const int tv = (j >> 1) & 1, blk = j & 1;
+      const uint16_t* src = (tv ? p.v_new : p.k_new) +
+                            ((long)(new_lo + (j >> 2) - p.start_pos) * p.num_kv + h) * kHD + blk * 128 + 8 * t;
+      raw = *reinterpret_cast<const uint4*>(src);
+    }
+    return raw;
+  };
+  // the inputs of the first two rounds (16 new keys) are requested now
+  uint4 enc_raw0 = make_uint4(0u, 0u, 0u, 0u), enc_raw1 = make_uint4(0u, 0u, 0u, 0u);
+  if (n_new > 0) enc_raw0 = enc_input(0);
+  if (n_new > 8) enc_raw1 = enc_input(1);
   // decode roles
   const int dj = wave & 1, dof = wave >> 1;              // keys: block, octet
   const int kq = lane & 15, vg = 4 * (wave >> 1) + (lane >> 4);   // values: key quad, code group
@@ -1289,6 +1322,25 @@ __global__ __launch_bounds__(kThreads, 1) void tq3_mq_kernel(QKV_ATTN_LEAD_PARAM
       *reinterpret_cast<uint4*>(lds + mq::kLdsQlo + qb) = make_uint4(pl[0], pl[1], pl[2], pl[3]);
     }
   }
+  if (n_new > 0) {
+    const bool put = t0 + nq == p.sub_n;   // the last query group stores the rows
+    uint32_t* enc = reinterpret_cast<uint32_t*>(lds + mq::kLdsEnc);
+    for (int round = 0; 32 * round < 4 * n_new; round++) {
+      const uint4 raw = round == 0 ? enc_raw0 : round == 1 ? enc_raw1 : enc_input(round);
+      const uint32_t word = tq3_encode_row16(raw, lane);
+      const int j = 32 * round + (tid >> 4), t = tid & 15;
+      if (j < 4 * n_new && t <= 12) {
+        const int w = t == 12 ? 0 : 1 + t;
+        enc[j * 13 + w] = word;
+        if (put) {
+          const int tv = (j >> 1) & 1, blk = j & 1;
+          uint32_t* dst = reinterpret_cast<uint32_t*>(tv ? p.v_w : p.k_w) +
+                          ((long)(new_lo + (j >> 2)) * p.num_kv + h) * 26 + blk * 13 + w;
+          *dst = word;
+        }
+      }
+    }
+  }
   if (n_tiles > 0) {   // tile 0 staged; its registers take tile 2
     mq_store_raw(lds, ra, tid);
     if (n_tiles > 2) mq_load(p, lo + 2 * kTile, p.num_kv, h, tid, ra);
@@ -1317,6 +1369,21 @@ __global__ __launch_bounds__(kThreads, 1) void tq3_mq_kernel(QKV_ATTN_LEAD_PARAM
   // that the two register sets stay fixed registers.
   auto tile_step = [&](int t, MqRaw& nxt) {
     const int ts = lo + t * kTile;
+    if (n_new > 0) {
+      // the encoded new keys of this tile over their staged (stale) rows
+      const int a0 = max(ts, new_lo), a1 = min(ts + kTile, new_lo + n_new);
+      if (a0 < a1) {
+        const uint32_t* enc = reinterpret_cast<const uint32_t*>(lds + mq::kLdsEnc);
+        for (int idx = tid; idx < (a1 - a0) * 52; idx += kThreads) {
+          const int kk = idx / 52, rem = idx - kk * 52, tv = rem / 26, w = rem - tv * 26;
+          const int key = a0 + kk, r = key - ts;
+          const uint32_t val = enc[((key - new_lo) * 4 + tv * 2 + w / 13) * 13 + w % 13];
+          *reinterpret_cast<uint32_t*>(lds + (tv ? mq::raw_v_row(r) : mq::kLdsRawK + r * mq::kRawPitch) +
+                                       4 * w) = val;
+        }
+        __syncthreads();
+      }
+    }
     mq_decode(lds, lane4, lane, dj, dof, kq, vg, scale2);
     __syncthreads();
     if (t + 1 < n_tiles) {

@@ -582,7 +582,8 @@ size_t qkv_decode_attn_tq3_workspace_bytes(int num_q, int num_kv, int sub_n, int
 static int decode_tq3(const uint16_t* q, const qkv_block_tq3* k, const qkv_block_tq3* v,
                       uint16_t* out, int num_q, int num_kv, int head_dim, int start_pos, int sub_n,
                       float scale, int sink_tok, int window_tok, const uint32_t* tree_mask,
-                      void* workspace, size_t workspace_bytes, bool noalloc, hipStream_t stream) {
+                      void* workspace, size_t workspace_bytes, bool noalloc, hipStream_t stream,
+                      const uint16_t* k_new = nullptr, const uint16_t* v_new = nullptr) {
   int st = check_attn_shape(num_q, num_kv, head_dim, start_pos, sub_n, tree_mask);
   if (st) return st;
   if (sink_tok < 0 || window_tok < 0) return QKV_ERR_INVALID;
@@ -634,6 +635,25 @@ static int decode_tq3(const uint16_t* q, const qkv_block_tq3* k, const qkv_block
   if (g.total > 0xffffffffULL) return QKV_ERR_UNSUPPORTED;   // 32-bit buffer offsets
   a.ws_ml_bytes = (uint32_t)(g.o_off - g.ml_off);
   a.ws_o_bytes = (uint32_t)(g.total - g.o_off);
+  if (k_new) {
+    // the block's rows start_pos .. start_pos + sub_n - 1: encoded inside the
+    // decode launch when it takes the shared-decode kernel (more than 16
+    // query-head columns) and the block has at most 64 rows (the kernel's
+    // encode area: a workgroup encodes the new rows it reads, at most
+    // min(sub_n, 64)), else appended by their own launch first
+    if (a.qpw * (num_q / num_kv) > 16 && sub_n <= 64) {
+      a.k_new = k_new;
+      a.v_new = v_new;
+      a.k_w = reinterpret_cast<uint8_t*>(const_cast<qkv_block_tq3*>(k));
+      a.v_w = reinterpret_cast<uint8_t*>(const_cast<qkv_block_tq3*>(v));
+    } else {
+      const long first = (long)start_pos * num_kv * 2;
+      const hipError_t e = qkv::launch_tq3_append(k_new, const_cast<qkv_block_tq3*>(k) + first, v_new,
+                                                  const_cast<qkv_block_tq3*>(v) + first, sub_n * num_kv * 2,
+                                                  2, stream);
+      if (e != hipSuccess) return launch_status(e);
+    }
+  }
   return launch_status(qkv::launch_tq3_attn(a, 0, out, stream));
 }
 
@@ -644,6 +664,17 @@ int qkv_decode_attn_tq3(const uint16_t* q, const qkv_block_tq3* k, const qkv_blo
                         hipStream_t stream) {
   return decode_tq3(q, k, v, out, num_q, num_kv, head_dim, start_pos, sub_n, scale, sink_tok,
                     window_tok, tree_mask, workspace, workspace_bytes, false, stream);
+}
+
+int qkv_decode_attn_tq3_append(const uint16_t* q, const uint16_t* k_new, const uint16_t* v_new,
+                               qkv_block_tq3* k, qkv_block_tq3* v, uint16_t* out, int num_q,
+                               int num_kv, int head_dim, int start_pos, int sub_n, float scale,
+                               int sink_tok, int window_tok, const uint32_t* tree_mask,
+                               void* workspace, size_t workspace_bytes, hipStream_t stream) {
+  if (!k_new || !v_new) return QKV_ERR_NULL;
+  if (!aligned(k_new, 16) || !aligned(v_new, 16)) return QKV_ERR_ALIGN;
+  return decode_tq3(q, k, v, out, num_q, num_kv, head_dim, start_pos, sub_n, scale, sink_tok,
+                    window_tok, tree_mask, workspace, workspace_bytes, false, stream, k_new, v_new);
 }
 
 int qkv_decode_attn_tq3_noalloc(const uint16_t* q, const qkv_block_tq3* k,

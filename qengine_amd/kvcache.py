@@ -328,6 +328,23 @@ def decode_attn_tq3(q, k, v, out, workspace, *, num_q, num_kv, start_pos, sub_n,
         workspace.numel() * workspace.element_size(), _stream(stream)), "qkv_decode_attn_tq3")
 
 
+def decode_attn_tq3_append(q, k_new, v_new, k, v, out, workspace, *, num_q, num_kv, start_pos,
+                           sub_n, scale, sink_tok=0, window_tok=0, tree_mask=None, head_dim=256,
+                           stream=None) -> None:
+    """decode_attn_tq3 of a block of sub_n new tokens whose K / V rows (fp16
+    [sub_n][num_kv][256]) are appended in the same call: encoded into rows
+    start_pos .. start_pos + sub_n - 1 of k / v (one launch when the call has
+    more than 16 query-head columns).  k and v must hold those rows."""
+    _attn_sizes(q, k, v, out, num_q, num_kv, start_pos + sub_n, sub_n, head_dim, TQ3_ROW, TQ3_ROW)
+    _need(k_new, sub_n * num_kv * head_dim * 2, "k_new", FP16)
+    _need(v_new, sub_n * num_kv * head_dim * 2, "v_new", FP16)
+    check(lib().qkv_decode_attn_tq3_append(
+        _dev_ptr(q, "q"), _dev_ptr(k_new, "k_new"), _dev_ptr(v_new, "v_new"), _dev_ptr(k, "k"),
+        _dev_ptr(v, "v"), _dev_ptr(out, "out"), num_q, num_kv, head_dim, start_pos, sub_n,
+        float(scale), sink_tok, window_tok, _opt_ptr(tree_mask), _dev_ptr(workspace, "workspace"),
+        workspace.numel() * workspace.element_size(), _stream(stream)), "qkv_decode_attn_tq3_append")
+
+
 def decode_attn_tq3_noalloc(q, k, v, out, *, num_q, num_kv, start_pos, sub_n, scale,
                             sink_tok=0, window_tok=0, tree_mask=None, head_dim=256,
                             stream=None) -> None:
