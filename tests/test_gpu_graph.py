@@ -129,3 +129,46 @@ def test_q8_append_and_decode_graph_replays(dev):
         torch.cuda.synchronize()
         assert torch.equal(out, ref), f"replay {i}"
         assert torch.equal(kb, kref) and torch.equal(vb, vref), f"replay {i}: appended rows"
+
+
+def test_tq3_verify_append_in_decode_graph_replays(dev):
+    """A 16-token verify block appended inside the decode launch
+    (qkv_decode_attn_tq3_append, one launch at 64 query-head columns) in a
+    graph: every replay rewrites the block's cache rows with the same bytes
+    and yields the eager output, with an eager decode of another shape on the
+    same workspace between the replays."""
+    import torch
+    from qengine_amd import kvcache
+    rng = np.random.default_rng(57)
+    hist, nv, nq, nkv = 6000, 16, 16, 4
+    n = hist + nv
+    kb = kvcache.tq3_blocks(n * nkv * 2, dev)
+    vb = kvcache.tq3_blocks(n * nkv * 2, dev)
+    kvcache.tq3_append_kv(_dev(kv_f16(rng, hist, nkv, 256), dev), _dev(kv_f16(rng, hist, nkv, 256), dev),
+                          kb[: hist * nkv * 2], vb[: hist * nkv * 2])
+    knew = _dev(kv_f16(rng, nv, nkv, 256), dev)
+    vnew = _dev(kv_f16(rng, nv, nkv, 256), dev)
+    q = _dev(q_f16(rng, nv, nq, 256).view(np.uint16), dev)
+    ws = kvcache.decode_attn_tq3_workspace(nq, nkv, nv, n, dev)
+    out = torch.zeros((nv, nq, 256), dtype=torch.float16, device=dev)
+    q1 = _dev(q_f16(rng, 1, nq, 256).view(np.uint16), dev)
+    out1 = torch.zeros((1, nq, 256), dtype=torch.float16, device=dev)
+
+    def call():
+        kvcache.decode_attn_tq3_append(q, knew, vnew, kb, vb, out, ws, num_q=nq, num_kv=nkv,
+                                       start_pos=hist, sub_n=nv, scale=1 / 16)
+    call()
+    torch.cuda.synchronize()
+    ref, kref, vref = out.clone(), kb.clone(), vb.clone()
+    g = _capture(call)
+    for i in range(4):
+        out.zero_()
+        kb[hist * nkv * 2:].zero_()
+        vb[hist * nkv * 2:].zero_()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, ref), f"replay {i}"
+        assert torch.equal(kb, kref) and torch.equal(vb, vref), f"replay {i}: appended rows"
+        kvcache.decode_attn_tq3(q1, kb, vb, out1, ws, num_q=nq, num_kv=nkv, start_pos=n - 1,
+                                sub_n=1, scale=1 / 16)
+        torch.cuda.synchronize()
