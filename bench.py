@@ -259,12 +259,17 @@ def secondary(torch, kvcache, dev, stream):
                                  start_pos=hist, scale=scale)
     ms = _time(torch, stream, prefill, 5)
     flop = sum(4 * NUM_Q * HD * (hist + t + 1) for t in range(chunk))
+    mfma_pf = mfma_sustained(torch, kvcache, dev, stream)
     out["config5_prefill_chunk"] = {
         "ms_per_chunk": round(ms, 3), "tflops": round(flop / (ms * 1e-3) / 1e12, 1),
         "frac_mfma_fp16": round(flop / (ms * 1e-3) / 1e12 / 2500.0, 4),
+        "mfma_sustained_pflops": round(mfma_pf, 3),
+        "frac_of_sustained_mfma": round(flop / (ms * 1e-3) / 1e15 / mfma_pf, 4),
         "note": "append of the 2048-token chunk + causal attention of the chunk over 131072 "
                 "history keys (TQ3) and its own 2048 fp16 keys; FLOPs 4*num_q*hd per "
-                "(query, visible key)"}
+                "(query, visible key); mfma_sustained_pflops: qkv_mfma_rate_bench, a register-only "
+                "loop of the same MFMA on random fp16 operands (the rate the part sustains on "
+                "data-like operands; 2.5 PFLOP/s nominal)"}
 
     nv = 16
     qv, kv_, vv = rnd(nv, NUM_Q, HD), rnd(nv, NUM_KV, HD), rnd(nv, NUM_KV, HD)
@@ -368,6 +373,24 @@ def secondary(torch, kvcache, dev, stream):
                 "keys Q8_0 (288 B per kv head and token), values TQ3 (104 B); 16 caches rotated"}
     del caches
     return out
+
+
+def mfma_sustained(torch, kvcache, dev, stream):
+    """Sustained fp16 MFMA rate on data-like operands: qkv_mfma_rate_bench,
+    256 workgroups x 8 waves x 16 * 8000 v_mfma_f32_32x32x16_f16 per wave
+    (a few ms per launch), 1 warm-up + 3 timed launches."""
+    sink = torch.zeros(1, dtype=torch.float32, device=dev)
+    wgs, iters = 256, 8000
+    kvcache.mfma_rate_bench(wgs, iters, sink)
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    a.record(stream)
+    for _ in range(3):
+        kvcache.mfma_rate_bench(wgs, iters, sink)
+    b.record(stream)
+    torch.cuda.synchronize()
+    ms = a.elapsed_time(b) / 3
+    return wgs * 8 * 16 * iters * 32768.0 / (ms * 1e-3) / 1e15
 
 
 def hbm_read_peak(torch, kvcache, dev, stream):

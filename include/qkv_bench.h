@@ -21,6 +21,15 @@ extern "C" {
  * (k_read_f4, lines 45-57). */
 int qkv_hbm_read_bench(const void* buf, size_t bytes, uint32_t* sink, hipStream_t stream);
 
+/* Measurement helper, not a cache operation: `workgroups` workgroups of 8
+ * waves, each wave issuing 16 x iters v_mfma_f32_32x32x16_f16 (32,768 flops
+ * each) on pseudo-random fp16 operands that rotate over four sets, nothing
+ * stored (sink, one float, is written only for a value no run produces).
+ * Timed over a few milliseconds it gives the fp16 matrix rate the part
+ * sustains on data-like operands, the ceiling the prefill's MFMA fraction is
+ * also quoted against. */
+int qkv_mfma_rate_bench(int workgroups, int iters, float* sink, hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

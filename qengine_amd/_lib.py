@@ -92,6 +92,7 @@ SIGNATURES = {
 
 BENCH_SIGNATURES = {
     "qkv_hbm_read_bench": (_I, [_P, _SZ, _P, _P]),
+    "qkv_mfma_rate_bench": (_I, [_I, _I, _P, _P]),
 }
 
 _lib = None
@@ -120,7 +121,7 @@ def lib() -> ctypes.CDLL:
 
 
 def bench_lib() -> ctypes.CDLL:
-    """libqkv_bench.so (include/qkv_bench.h): the benchmark's streaming read."""
+    """libqkv_bench.so (include/qkv_bench.h): the benchmark's streaming read and MFMA loop."""
     global _bench_lib
     if _bench_lib is None:
         if not os.path.exists(BENCH_LIB_PATH):

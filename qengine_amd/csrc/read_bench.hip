@@ -1,5 +1,6 @@
 // read_bench.hip -- the streaming-read kernels behind bench.py's HBM read
-// peak and single-launch read floor (libqkv_bench.so; not part of libqkv.so).
+// peak and single-launch read floor, and the MFMA loop behind its sustained
+// fp16 matrix rate (libqkv_bench.so; not part of libqkv.so).
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
@@ -51,8 +52,54 @@ hipError_t launch_stream_read(const void* p, size_t bytes, uint32_t* sink, hipSt
   return hipGetLastError();
 }
 
+typedef _Float16 mb_h8_t __attribute__((ext_vector_type(8)));
+typedef float mb_f16x_t __attribute__((ext_vector_type(16)));
+
+// Sustained fp16 MFMA rate on data-like operands: each wave runs 4 x iters
+// v_mfma_f32_32x32x16_f16 into four independent accumulators, its A and B
+// operands rotating over four sets of pseudo-random fp16 values per lane
+// (operands that never change draw less power and run faster than real
+// data).  The sums are written only for a value no run produces.
+__global__ __launch_bounds__(512) void mfma_rate_kernel(float* __restrict__ sink, int iters) {
+  mb_h8_t a[4], b[4];
+  uint32_t x = threadIdx.x * 2654435761u + blockIdx.x * 40503u + 12345u;
+#pragma unroll
+  for (int s = 0; s < 4; s++)
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+      x = x * 1664525u + 1013904223u;
+      a[s][i] = (_Float16)((float)((int)(x >> 16) - 32768) * (1.0f / 16384.0f));
+      x = x * 1664525u + 1013904223u;
+      b[s][i] = (_Float16)((float)((int)(x >> 16) - 32768) * (1.0f / 16384.0f));
+    }
+  mb_f16x_t acc[4];
+#pragma unroll
+  for (int j = 0; j < 4; j++) acc[j] = mb_f16x_t{};
+  for (int it = 0; it < iters; it++) {
+#pragma unroll
+    for (int k = 0; k < 4; k++)
+#pragma unroll
+      for (int j = 0; j < 4; j++)
+        acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[j], b[(j + k) & 3], acc[j], 0, 0, 0);
+  }
+  float sum = 0.f;
+#pragma unroll
+  for (int j = 0; j < 4; j++)
+#pragma unroll
+    for (int i = 0; i < 16; i++) sum += acc[j][i];
+  if (sum == 1.2345678f) sink[0] = sum;
+}
+
 }  // namespace
 }  // namespace qkv
+
+extern "C" int qkv_mfma_rate_bench(int workgroups, int iters, float* sink, hipStream_t stream) {
+  if (workgroups < 1 || iters < 1) return QKV_ERR_INVALID;
+  if (!sink) return QKV_ERR_NULL;
+  if (reinterpret_cast<uintptr_t>(sink) % 4) return QKV_ERR_ALIGN;
+  hipLaunchKernelGGL(qkv::mfma_rate_kernel, dim3((unsigned)workgroups), dim3(512), 0, stream, sink, iters);
+  return hipGetLastError() == hipSuccess ? QKV_OK : QKV_ERR_LAUNCH;
+}
 
 extern "C" int qkv_hbm_read_bench(const void* buf, size_t bytes, uint32_t* sink, hipStream_t stream) {
   if (bytes == 0) return QKV_OK;

@@ -219,6 +219,13 @@ def hbm_read_bench(buf, sink, stream=None) -> None:
                                    _dev_ptr(sink, "sink"), _stream(stream)), "qkv_hbm_read_bench")
 
 
+def mfma_rate_bench(workgroups, iters, sink, stream=None) -> None:
+    """One launch of the MFMA-rate loop (workgroups x 8 waves x 16 * iters
+    32x32x16 fp16 MFMAs on data-like operands; libqkv_bench.so)."""
+    check(bench_lib().qkv_mfma_rate_bench(int(workgroups), int(iters), _dev_ptr(sink, "sink"),
+                                          _stream(stream)), "qkv_mfma_rate_bench")
+
+
 def _opt_ptr(t):
     return 0 if t is None else _dev_ptr(t, "tensor")
 

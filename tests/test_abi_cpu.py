@@ -21,11 +21,11 @@ def test_exports_every_declared_function(L):
 
 
 def test_bench_library_exports_its_header():
-    """The benchmark's streaming read lives in libqkv_bench.so (include/qkv_bench.h),
-    not in the product library."""
+    """The benchmark's streaming read and MFMA loop live in libqkv_bench.so
+    (include/qkv_bench.h), not in the product library."""
     B = _lib.bench_lib()
     names = _lib.header_functions(_lib.BENCH_HEADER_PATH)
-    assert names == ["qkv_hbm_read_bench"]
+    assert names == ["qkv_hbm_read_bench", "qkv_mfma_rate_bench"]
     for n in names:
         assert hasattr(B, n) and n in _lib.BENCH_SIGNATURES
         assert not hasattr(_lib.lib(), n), f"libqkv.so still exports {n}"
@@ -35,6 +35,10 @@ def test_bench_library_exports_its_header():
     assert B.qkv_hbm_read_bench(p, 48, p, None) == -1        # multiples of 64 bytes
     assert B.qkv_hbm_read_bench(None, 64, p, None) == -2
     assert B.qkv_hbm_read_bench(p + 4, 64, p, None) == -4
+    assert B.qkv_mfma_rate_bench(0, 1, p, None) == -1        # no workgroup: refused, nothing launched
+    assert B.qkv_mfma_rate_bench(1, 0, p, None) == -1
+    assert B.qkv_mfma_rate_bench(1, 1, None, None) == -2
+    assert B.qkv_mfma_rate_bench(1, 1, p + 2, None) == -4
 
 
 def test_version_and_status_strings(L):
