@@ -242,6 +242,36 @@ def secondary(torch, kvcache, dev, stream):
                 "(2 launches); physical bytes count the shared prefix once"}
     del pools
 
+    # ---- config 3's decode step with its append: one layer, the new token's K
+    # and V encoded into row 32768, then the query over keys 0..32768 ----
+    ctx3 = 32768
+    k3 = kvcache.tq3_blocks((ctx3 + 1) * BLOCKS_PER_TOKEN, dev)
+    v3 = kvcache.tq3_blocks((ctx3 + 1) * BLOCKS_PER_TOKEN, dev)
+    kvcache.tq3_append_kv(rnd(ctx3, NUM_KV, HD), rnd(ctx3, NUM_KV, HD), k3[: ctx3 * BLOCKS_PER_TOKEN],
+                          v3[: ctx3 * BLOCKS_PER_TOKEN])
+    kn3, vn3, q3 = rnd(1, NUM_KV, HD), rnd(1, NUM_KV, HD), rnd(1, NUM_Q, HD)
+    o3 = torch.empty(1, NUM_Q, HD, dtype=torch.float16, device=dev)
+    ws3 = kvcache.decode_attn_tq3_workspace(NUM_Q, NUM_KV, 1, ctx3 + 1, dev)
+
+    def step_two_calls(i=0):
+        kvcache.tq3_append_kv(kn3, vn3, k3[ctx3 * BLOCKS_PER_TOKEN:], v3[ctx3 * BLOCKS_PER_TOKEN:])
+        kvcache.decode_attn_tq3(q3, k3, v3, o3, ws3, num_q=NUM_Q, num_kv=NUM_KV, start_pos=ctx3,
+                                sub_n=1, scale=scale)
+
+    def step_one_call(i=0):
+        kvcache.decode_attn_tq3_append(q3, kn3, vn3, k3, v3, o3, ws3, num_q=NUM_Q, num_kv=NUM_KV,
+                                       start_pos=ctx3, sub_n=1, scale=scale)
+    ms_two3 = _time(torch, stream, step_two_calls, 200)
+    ms_one3 = _time(torch, stream, step_one_call, 200)
+    out["config3_decode_step"] = {
+        "one_call_us": round(ms_one3 * 1e3, 3), "two_call_us": round(ms_two3 * 1e3, 3),
+        "note": "one layer of a decode step at 32K context: the new token's K and V appended "
+                "(row 32768) and the query attended over keys 0..32768, called one by one from "
+                "Python; one_call_us: qkv_decode_attn_tq3_append (one launch: the wave whose "
+                "tile holds the new key encodes it); two_call_us: qkv_tq3_append_kv, then "
+                "qkv_decode_attn_tq3"}
+    del k3, v3
+
     # ---- config 5: one slot, 16 q / 4 kv, 131072-token history ----
     hist, chunk = 131072, 2048
     kb = kvcache.tq3_blocks((hist + chunk) * 8, dev)

@@ -337,10 +337,11 @@ int qkv_debug_set_merge_spin_limit(int limit);
  * fp16 K and V rows [sub_n][num_kv][256] (16-byte aligned); they are encoded
  * exactly as qkv_tq3_append_kv encodes them and written to rows start_pos ..
  * start_pos + sub_n - 1 of k and v, and the attention is that of
- * qkv_decode_attn_tq3 with the same arguments.  When the call has more than
- * 16 (query, head) columns and sub_n <= 64 it is ONE launch (the
- * shared-decode kernel encodes the new rows it reads and writes them to the
- * caches); otherwise the append's launch, then the decode's.  Caches and output equal those of
+ * qkv_decode_attn_tq3 with the same arguments.  It is ONE launch for a
+ * decode step (sub_n = 1: the wave whose tile holds the new key encodes it)
+ * and for calls with more than 16 (query, head) columns and sub_n <= 64 (the
+ * shared-decode kernel encodes the new rows it reads); both write the rows to
+ * the caches.  Other shapes take the append's launch, then the decode's.  Caches and output equal those of
  * qkv_tq3_append_kv followed by qkv_decode_attn_tq3; same workspace
  * (qkv_decode_attn_tq3_workspace_bytes(num_q, num_kv, sub_n,
  * start_pos + sub_n)) and errors. */

@@ -120,7 +120,10 @@ constexpr int kLdsTileEnd = kLdsQ + 16 * 256 * 2;
 constexpr int kLdsMergeO = 0;                                // [waves][16 rows][256] f32
 constexpr int kLdsMergeML = kLdsMergeO + kWaves * 16 * kHD * 4;
 constexpr int kLdsMergeEnd = kLdsMergeML + 512 * 4;
-constexpr int kLdsTotal = kLdsTileEnd;
+// one-query step with its token appended in the launch: the new key's
+// encoded K and V blocks (4 x 13 dwords)
+constexpr int kLdsNewRow = kLdsTileEnd;
+constexpr int kLdsTotal = kLdsNewRow + 256;
 static_assert(kLdsMergeEnd <= kLdsQ, "merge area must not reach the query scratch");
 static_assert(kTracePolledByte >= kWaves * 128 * 4 && kTracePolledByte + 24 <= kLdsMergeML - kLdsMergeO,
               "the merger's trace slot lies in the merge area, past the reduction area");
@@ -342,6 +345,32 @@ __device__ __forceinline__ void load_tile(const AttnArgs& p, int prow, int nkv, 
   tr.vr6 = __builtin_amdgcn_raw_buffer_load_b64(rv, vrow + 96, 0, 0);
 }
 
+// The encoded new key (4 x 13 dwords at nr) written over the registers of
+// the tile that holds it, r = its index in the tile: lanes (row, col = r & 15)
+// of its 16-key group take its key code pieces and norms, lane r its value row
+// (constant register indices).
+__device__ __forceinline__ void patch_new_key(TileRegs& tr, const uint32_t* nr, int r, int lane, int row,
+                                              int col) {
+  const int g = r >> 4;
+  if (col == (r & 15)) {
+#pragma unroll
+    for (int G = 0; G < 4; G++) {
+#pragma unroll
+      for (int j = 0; j < 2; j++) {
+        tr.kq[G][j][0] = g == G ? nr[13 * j + 1 + 3 * row] : tr.kq[G][j][0];
+        tr.kq[G][j][1] = g == G ? nr[13 * j + 2 + 3 * row] : tr.kq[G][j][1];
+        tr.kq[G][j][2] = g == G ? nr[13 * j + 3 + 3 * row] : tr.kq[G][j][2];
+        tr.kn[G][j] = g == G ? __uint_as_float(nr[13 * j]) : tr.kn[G][j];
+      }
+    }
+  }
+  if (lane == r) {
+#pragma unroll
+    for (int i = 0; i < 6; i++) tr.vr[i] = u4_t{nr[26 + 4 * i], nr[27 + 4 * i], nr[28 + 4 * i], nr[29 + 4 * i]};
+    tr.vr6 = u2_t{nr[50], nr[51]};
+  }
+}
+
 // Key visibility of one query (attention.cuh:1923-1929, 2101-2105): the
 // sink/window rule on 32-key tiles, then the tree bits for keys of the block.
 // Branch-free: every key of a tile is tested with the same instructions.
@@ -456,7 +485,10 @@ __device__ void finish_rows(const uint8_t* lds, const AttnArgs& p, int h, int t,
 // CHAIN (fast path, several queries): 16 / GQA queries per workgroup, every
 // MFMA column a real (query, head); the remainders ride in a chained second
 // score product (see score_group).
-template <int MODE, bool CHAIN = false>
+// APPEND (MODE 0, one query): the step's new token is encoded in the launch
+// (qkv_decode_attn_tq3_append), a separate instance so that the plain decode
+// compiles without it.
+template <int MODE, bool CHAIN = false, bool APPEND = false>
 __global__ __launch_bounds__(kThreads, 1) void tq3_attn_kernel(QKV_ATTN_LEAD_PARAMS, AttnArgs pin,
                                                                 uint16_t* out) {
   QKV_ATTN_LEAD_APPLY(p, pin);
@@ -569,6 +601,22 @@ __global__ __launch_bounds__(kThreads, 1) void tq3_attn_kernel(QKV_ATTN_LEAD_PAR
   lo = __builtin_amdgcn_readfirstlane(lo);
   hi = __builtin_amdgcn_readfirstlane(hi);
   hi_first = __builtin_amdgcn_readfirstlane(hi_first);
+  // appended token (one-query launches of qkv_decode_attn_tq3_append): the
+  // wave whose tiles hold key start_pos (tile k of wave w starts at lo + 64w
+  // + k * 512), and its input, lane l: 16-byte piece l & 15 of block l >> 4
+  // (K block 0, K block 1, V block 0, V block 1 of kv head h)
+  int fa_wave = -1;
+  uint4 fa_raw = make_uint4(0u, 0u, 0u, 0u);
+  if constexpr (APPEND) {
+    if (p.k_new != nullptr && has_work && lo <= p.start_pos && p.start_pos < hi)
+      fa_wave = ((p.start_pos - lo) >> 6) & (kWaves - 1);
+    fa_wave = __builtin_amdgcn_readfirstlane(fa_wave);
+    if (fa_wave == wave) {
+      const int blk = lane >> 4;
+      fa_raw = *reinterpret_cast<const uint4*>((blk < 2 ? p.k_new : p.v_new) + h * kHD + (blk & 1) * 128 +
+                                               8 * (lane & 15));
+    }
+  }
   // A dead column has a zero query: its scores are 0 and its accumulator rows
   // are never stored, so it needs no mask of its own.
 
@@ -728,6 +776,26 @@ __global__ __launch_bounds__(kThreads, 1) void tq3_attn_kernel(QKV_ATTN_LEAD_PAR
           make_uint4(pk[0], pk[1], pk[2], pk[3]);
       *reinterpret_cast<uint4*>(qs + q_unit(q_col + 8, 4 * q_blk + u, o) * 8) =
           make_uint4(pl[0], pl[1], pl[2], pl[3]);
+    }
+  }
+  if constexpr (APPEND) {
+    // the step's new token appended in this launch (qkv_decode_attn_tq3_append
+    // with one query): the wave whose tile holds key start_pos encodes its
+    // K and V blocks (one 16-lane row each, tq3_encode_row16), stores them
+    // to the caches and keeps them in LDS for its tile registers
+    if (fa_wave == wave) {
+      const uint32_t word = tq3_encode_row16(fa_raw, lane);
+      const int blk = lane >> 4, t = lane & 15;
+      if (t <= 12) {
+        const int w = t == 12 ? 0 : 1 + t;
+        reinterpret_cast<uint32_t*>(lds + kLdsNewRow)[blk * 13 + w] = word;
+        uint32_t* dst = reinterpret_cast<uint32_t*>(blk < 2 ? p.k_w : p.v_w) +
+                        ((long)p.start_pos * p.num_kv + h) * 26 + (blk & 1) * 13 + w;
+        *dst = word;
+      }
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
     }
   }
   QKV_STAMP(kPhSetupWork);
@@ -914,9 +982,13 @@ __global__ __launch_bounds__(kThreads, 1) void tq3_attn_kernel(QKV_ATTN_LEAD_PAR
       for (int t = 0; t < 16; t++) acc[t] = f4_t{0.f, 0.f, 0.f, 0.f};
     }
   } else if (ts0 < hi) {
+    if (APPEND && fa_wave == wave && ts0 <= p.start_pos && p.start_pos < ts0 + kTile)
+      patch_new_key(tr, reinterpret_cast<const uint32_t*>(lds + kLdsNewRow), p.start_pos - ts0, lane, row, col);
     tile_body(std::true_type{}, ts0);
     for (int ts = ts0 + kStep; ts < hi; ts += kStep) {
       load_tile(p, wave_tile_row(ts), p.num_kv, h, lane, row, col, tr);
+      if (APPEND && fa_wave == wave && ts <= p.start_pos && p.start_pos < ts + kTile)
+        patch_new_key(tr, reinterpret_cast<const uint32_t*>(lds + kLdsNewRow), p.start_pos - ts, lane, row, col);
       tile_body(std::false_type{}, ts);
     }
   } else {
@@ -1603,6 +1675,8 @@ hipError_t launch_tq3_attn(const AttnArgs& a, int mode, uint16_t* out, hipStream
     hipLaunchKernelGGL(tq3_mq_kernel, grid, block, 0, stream, QKV_ATTN_LEAD_ARGS(a), a, out);
   else if (mode == 0 && a.qpw * (a.num_q / a.num_kv) > 8)
     hipLaunchKernelGGL((tq3_attn_kernel<0, true>), grid, block, 0, stream, QKV_ATTN_LEAD_ARGS(a), a, out);
+  else if (mode == 0 && a.k_new != nullptr)
+    hipLaunchKernelGGL((tq3_attn_kernel<0, false, true>), grid, block, 0, stream, QKV_ATTN_LEAD_ARGS(a), a, out);
   else if (mode == 0)
     hipLaunchKernelGGL((tq3_attn_kernel<0>), grid, block, 0, stream, QKV_ATTN_LEAD_ARGS(a), a, out);
   else if (mode == 1)

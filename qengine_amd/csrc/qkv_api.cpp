@@ -640,8 +640,10 @@ static int decode_tq3(const uint16_t* q, const qkv_block_tq3* k, const qkv_block
     // decode launch when it takes the shared-decode kernel (more than 16
     // query-head columns) and the block has at most 64 rows (the kernel's
     // encode area: a workgroup encodes the new rows it reads, at most
-    // min(sub_n, 64)), else appended by their own launch first
-    if (a.qpw * (num_q / num_kv) > 16 && sub_n <= 64) {
+    // min(sub_n, 64)), or when it is one query (a decode step: the wave whose
+    // tile holds the new key encodes it); else appended by their own launch
+    const int cols = a.qpw * (num_q / num_kv);
+    if ((cols > 16 && sub_n <= 64) || (sub_n == 1 && cols <= 8)) {
       a.k_new = k_new;
       a.v_new = v_new;
       a.k_w = reinterpret_cast<uint8_t*>(const_cast<qkv_block_tq3*>(k));

@@ -1,4 +1,5 @@
-"""A verify block appended inside the decode call (qkv_decode_attn_tq3_append).
+"""A verify block, or a decode step's token, appended inside the decode call
+(qkv_decode_attn_tq3_append).
 The reference encodes the block's K and V into the cache with
 tq3_quantize_kernel and then runs the split attention and its merge
 (model.cuh:4566-4571, 4663-4687).  Checked on identical seeded inputs: the
@@ -29,6 +30,11 @@ SHAPES = [
     (1800, 8, 33, False),     # 66 columns
     (0, 16, 16, False),       # no history: every key is new
     (900, 16, 3, False),      # 12 columns: the append's own launch, then the decode
+    # one query (a decode step): the wave whose tile holds the new key encodes it
+    (32767, 16, 1, False),    # config 3's step: the new key is the last of 32,768
+    (4100, 24, 1, False),     # GQA 6, the new key inside a partial last tile
+    (1000, 16, 1, False),
+    (0, 16, 1, False),        # the new key is the only key
 ]
 
 
