@@ -773,7 +773,7 @@ def main():
         "hbm_read_peak": read_peak,
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
-                     "traffic": traffic, "kernel": "tq3_attn_kernel<0, false>",
+                     "traffic": traffic, "kernel": "tq3_attn_kernel<0, false, false>",
                      "frac_of_measured_peak": round(achieved / read_peak["gbps"], 4),
                      "avg_launch_us": round(launch_ms * 1e3, 3),
                      "isolated_launch_median_us": round(durs[len(durs) // 2] * 1e3, 3),
