@@ -529,17 +529,29 @@ FastGeom fast_geom(int num_q, int num_kv, int sub_n, int n_keys, int base = kChu
   int tpw = (cb + 127) / 128;
   // chunks of base * t keys; from t = join_min on (0: never) a last chunk of
   // at most one 64-key tile joins the previous one (tq3_join_min)
-  auto chunks = [&](int t) {
+  auto chunks_from = [&](int t, int jmin) {
     const long ck = (long)base * t;
     int n = (int)((n_keys + ck - 1) / ck);
-    if (join_min > 0 && n > 1 && t >= join_min && n_keys - (n - 1) * ck <= 64) n--;
+    if (jmin > 0 && n > 1 && t >= jmin && n_keys - (n - 1) * ck <= 64) n--;
     return n;
   };
   // Long contexts and many queries: grow the chunks until the launch fits one
   // round of the GPU (kMaxFastWgs workgroups, one per CU), so that each
   // workgroup pays its setup and merge once for several tiles (config 4:
   // 189 -> 119 us per step; a 16-token verify over 131K keys: 148 -> 108 us).
-  while (groups > 0 && (long)groups * chunks(tpw) * num_kv > kMaxFastWgs && tpw < cb) tpw++;
+  auto fit = [&](int jmin) {
+    int t = tpw;
+    while (groups > 0 && (long)groups * chunks_from(t, jmin) * num_kv > kMaxFastWgs && t < cb) t++;
+    return t;
+  };
+  // A remainder of at most one tile also joins below join_min when leaving it
+  // alone would take longer chunks (a decode step over 32,769 keys: 64 chunks
+  // of 512 keys with one wave taking a second tile instead of 33 chunks of
+  // 1,024 on half the CUs, 20.8 -> 17.9 us); otherwise an extra chunk is the
+  // cheaper (4,097 keys: 9 chunks, 14.2 us, against 16.3 joined).
+  if (join_min > 1 && groups > 0 && fit(1) < fit(join_min)) join_min = 1;
+  auto chunks = [&](int t) { return chunks_from(t, join_min); };
+  tpw = fit(join_min);
   g.chunk_keys = base * tpw;
   g.n_chunks = chunks(tpw);
   g.n_slots = g.n_chunks;
